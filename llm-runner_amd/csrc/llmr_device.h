@@ -1,0 +1,79 @@
+// llmr_device.h - device-side types and helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llmr {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// 16-byte vector that is only guaranteed 4-byte aligned (GGUF Q8_0 rows are
+// dword-aligned but not 16-byte aligned); global_load_dwordx4 needs dword alignment.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+constexpr uint32_t kGgmlF32 = 0, kGgmlF16 = 1, kGgmlQ8_0 = 8, kGgmlQ4K = 12, kGgmlBF16 = 30;
+
+// fp16 bit pattern -> f32 exactly as unpack_f16 (llm.slang:235-251) and
+// cpu_f16_to_f32 (tensor.c3:130-147): exponent 31 (Inf and every NaN) -> +-Inf;
+// everything else is the exact value (the hardware widening is exact for
+// zero, subnormal and normal halves).
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    if (((bits >> 10) & 0x1fu) == 0x1fu) return __uint_as_float(((bits & 0x8000u) << 16) | 0x7f800000u);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    f16x2 h;
+    h.x = (_Float16)a;  // round to nearest even (v_cvt_pk_f16_f32)
+    h.y = (_Float16)b;
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Two bf16 halves of a dword -> their f16 roundings, packed.
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
+    return pack_f16x2(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
+}
+
+// Eight int8 values (two dwords) times an fp16 scale -> eight fp16 RN16(d*q),
+// the Q8_0 matrix operand of batch_matmul_q8 (llm.slang:1699-1703:
+// float16_t s * float16_t(q)). int8 -> fp16 is exact via the 1024+128+q bias
+// trick, the product is one IEEE fp16 multiply (round to nearest even).
+__device__ __forceinline__ f16x4 q8x4_to_f16(uint32_t w, f16x2 d2) {
+    const uint32_t x = w ^ 0x80808080u;                       // q + 128 in each byte
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);  // 0x64|b1, 0x64|b0
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);  // 0x64|b3, 0x64|b2
+    const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    f16x2 a = __builtin_bit_cast(f16x2, lo) - bias;  // exact q0, q1
+    f16x2 b = __builtin_bit_cast(f16x2, hi) - bias;  // exact q2, q3
+    a = a * d2;
+    b = b * d2;
+    f16x4 r;
+    r.x = a.x; r.y = a.y; r.z = b.x; r.w = b.y;
+    return r;
+}
+
+// get_scale_min_k4 (llm.slang:447-462) for sub-block index `is` (wave-uniform)
+// on the 12 scale bytes held in dwords s0 (bytes 0-3), s1 (4-7), s2 (8-11).
+__device__ __forceinline__ void q4k_scale_min(uint32_t is, uint32_t s0, uint32_t s1, uint32_t s2,
+                                              uint32_t& sc, uint32_t& mn) {
+    const uint32_t sh = 8u * (is & 3u);
+    if (is < 4) {
+        sc = (s0 >> sh) & 63u;
+        mn = (s1 >> sh) & 63u;
+    } else {
+        const uint32_t b_hi = (s2 >> sh) & 0xffu;  // byte is+4
+        const uint32_t b_lo = (s0 >> sh) & 0xffu;  // byte is-4
+        const uint32_t b_md = (s1 >> sh) & 0xffu;  // byte is
+        sc = (b_hi & 0xfu) | ((b_lo >> 6) << 4);
+        mn = (b_hi >> 4) | ((b_md >> 6) << 4);
+    }
+}
+
+}  // namespace llmr

@@ -1,0 +1,152 @@
+"""ctypes binding of the C-ABI in include/llmr_hip.h (libllmr_hip.so).
+
+The library is built in-tree by llm-runner_amd/Makefile (or
+__graft_entry__.build()). There is no fallback: if the library is missing or
+fails to load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(_PKG)                       # llm-runner_amd/
+REPO = os.path.dirname(ROOT)
+LIB_PATH = os.path.join(ROOT, "lib", "libllmr_hip.so")
+HEADER_PATH = os.path.join(REPO, "include", "llmr_hip.h")
+
+LLMR_OK = 0
+LLMR_ERR_INVALID_ARG = 1
+LLMR_ERR_UNSUPPORTED = 2
+LLMR_ERR_HIP = 3
+LLMR_ERR_NO_DEVICE = 4
+
+
+class LlmrError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"llmr error {code}: {msg}")
+        self.code = code
+
+
+class BatchMatMulParams(ctypes.Structure):
+    """BatchMatMulPC (dependencies/zimage.c3l/dit.c3:172-178)."""
+    _fields_ = [("out_dim", ctypes.c_uint32), ("in_dim", ctypes.c_uint32),
+                ("seq_len", ctypes.c_uint32), ("row_offset", ctypes.c_uint32)]
+
+
+class FlashAttentionParams(ctypes.Structure):
+    """FlashAttentionPC (dependencies/zimage.c3l/dit.c3:136-142)."""
+    _fields_ = [("head_dim", ctypes.c_uint32), ("n_heads", ctypes.c_uint32),
+                ("seq_len", ctypes.c_uint32), ("scale", ctypes.c_float)]
+
+
+_vp = ctypes.c_void_p
+_u32 = ctypes.c_uint32
+_SIGS = {
+    "llmr_create_context": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(_vp)]),
+    "llmr_destroy_context": (ctypes.c_int, [_vp]),
+    "llmr_set_stream": (ctypes.c_int, [_vp, _vp]),
+    "llmr_get_stream": (_vp, [_vp]),
+    "llmr_last_error": (ctypes.c_char_p, []),
+    "llmr_alloc": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "llmr_free": (ctypes.c_int, [_vp, _vp]),
+    "llmr_upload": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+    "llmr_download": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+    "llmr_sync": (ctypes.c_int, [_vp]),
+    "llmr_ggml_row_bytes": (ctypes.c_size_t, [_u32, _u32]),
+    "llmr_dequant": (ctypes.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "llmr_dequant_operand_f16": (ctypes.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "llmr_batch_matmul": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32]),
+    "llmr_batch_matmul_pc": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp,
+                                            ctypes.POINTER(BatchMatMulParams)]),
+    "llmr_flash_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32,
+                                            ctypes.c_float]),
+    "llmr_flash_attention_pc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _vp,
+                                               ctypes.POINTER(FlashAttentionParams)]),
+}
+
+_lib = None
+
+
+def header_symbols(path: str = HEADER_PATH) -> list[str]:
+    """Names of every LLMR_API function declared in include/llmr_hip.h."""
+    text = open(path).read()
+    return re.findall(r"LLMR_API\s+[\w\s\*]+?\b(llmr_\w+)\s*\(", text)
+
+
+def lib():
+    """The loaded libllmr_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise LlmrError(LLMR_ERR_NO_DEVICE,
+                            f"{LIB_PATH} is not built; run `make -C llm-runner_amd` "
+                            "or __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return (lib().llmr_last_error() or b"").decode()
+
+
+def check(rc: int) -> None:
+    if rc != LLMR_OK:
+        raise LlmrError(rc, last_error())
+
+
+class Context:
+    """One device + one in-order stream (createContext, lib/vulkan/context.c3:73)."""
+
+    def __init__(self, device: int = 0):
+        self._h = _vp()
+        check(lib().llmr_create_context(device, ctypes.byref(self._h)))
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self) -> None:
+        if self._h:
+            lib().llmr_destroy_context(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_stream(self, stream_ptr: int | None) -> None:
+        check(lib().llmr_set_stream(self._h, stream_ptr or None))  # 0/None: HIP null stream
+
+    def stream(self) -> int:
+        return lib().llmr_get_stream(self._h) or 0
+
+    def sync(self) -> None:
+        check(lib().llmr_sync(self._h))
+
+    def dequant(self, w_ptr: int, wtype: int, n_rows: int, in_dim: int, row_offset: int,
+                out_ptr: int) -> None:
+        check(lib().llmr_dequant(self._h, w_ptr, wtype, n_rows, in_dim, row_offset, out_ptr))
+
+    def dequant_operand_f16(self, w_ptr: int, wtype: int, n_rows: int, in_dim: int,
+                            row_offset: int, out_ptr: int) -> None:
+        check(lib().llmr_dequant_operand_f16(self._h, w_ptr, wtype, n_rows, in_dim, row_offset,
+                                             out_ptr))
+
+    def batch_matmul(self, w_ptr: int, wtype: int, x_ptr: int, xtype: int, y_ptr: int,
+                     out_dim: int, in_dim: int, seq_len: int, row_offset: int = 0) -> None:
+        check(lib().llmr_batch_matmul(self._h, w_ptr, wtype, x_ptr, xtype, y_ptr, out_dim, in_dim,
+                                      seq_len, row_offset))
+
+    def flash_attention(self, q_ptr: int, k_ptr: int, v_ptr: int, xtype: int, o_ptr: int,
+                        head_dim: int, n_heads: int, seq_len: int, scale: float) -> None:
+        check(lib().llmr_flash_attention(self._h, q_ptr, k_ptr, v_ptr, xtype, o_ptr, head_dim,
+                                         n_heads, seq_len, float(scale)))

@@ -1,0 +1,184 @@
+"""Host-side mirror of the reference's op interface for the DiT hot path.
+
+The reference's DiT blocks call
+    zimage::dispatch_batch_matmul(g, dk, weight, input, output,
+                                  out_dim, in_dim, seq_len, row_offset, lora...)
+        (dependencies/zimage.c3l/dit.c3:1198-1301, via flux::flux_matmul,
+         dependencies/flux.c3l/flux_dit.c3:533-551)
+and
+    g.dispatch(&dk.flash_attention, {Q, K, V, O}, &FlashAttentionPC, ceil(S/16), H)
+        (dependencies/zimage.c3l/dit.c3:1476-1483, flux_dit.c3:1042-1047)
+on a RenderGraph (lib/vulkan/graph.c3) over Tensors (lib/model/tensor.c3:8-14).
+This module keeps those names and argument meanings; device memory is held in
+torch tensors and every op goes through the C-ABI of libllmr_hip.so on the
+graph's stream (the caller's current torch stream).
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import torch
+
+from . import capi
+from .gguf import GGML_BF16, GGML_F16, GGML_F32, GGML_Q4_K, GGML_Q8_0, row_bytes
+
+_TORCH_GGML = {torch.float32: GGML_F32, torch.float16: GGML_F16, torch.bfloat16: GGML_BF16}
+
+
+@dataclasses.dataclass
+class Tensor:
+    """Device buffer + GGML dtype + logical shape (llm::Tensor, tensor.c3:8-14).
+
+    For quantized types `data` is a uint8 tensor of raw GGUF blocks and
+    `shape` is the logical [rows, cols] element shape."""
+    data: torch.Tensor
+    dtype: int
+    shape: tuple
+
+    @staticmethod
+    def from_torch(t: torch.Tensor) -> "Tensor":
+        return Tensor(t, _TORCH_GGML[t.dtype], tuple(t.shape))
+
+    @staticmethod
+    def quantized(blocks: torch.Tensor, ggml_type: int, rows: int, cols: int) -> "Tensor":
+        if blocks.dtype != torch.uint8 or blocks.numel() != rows * row_bytes(ggml_type, cols):
+            raise ValueError("quantized tensor bytes do not match [rows, cols]")
+        return Tensor(blocks, ggml_type, (rows, cols))
+
+    def ptr(self) -> int:
+        return self.data.data_ptr()
+
+
+@dataclasses.dataclass
+class FlashAttentionPC:
+    """FlashAttentionPC (dependencies/zimage.c3l/dit.c3:136-142)."""
+    head_dim: int
+    n_heads: int
+    seq_len: int
+    scale: float
+
+
+class RenderGraph:
+    """The ordering/sync surface of lib/vulkan/graph.c3 for the replaced ops:
+    dispatches run in issue order on one stream; checkpoint()/flush() wait
+    for them (graph.c3:94-107)."""
+
+    def __init__(self, ctx: capi.Context | None = None, device: int = 0):
+        self.ctx = ctx if ctx is not None else capi.Context(device)
+
+    def bind_stream(self) -> None:
+        self.ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+
+    def checkpoint(self) -> None:
+        self.bind_stream()
+        self.ctx.sync()
+
+    flush = checkpoint
+
+
+def _dev(t: Tensor, what: str) -> None:
+    if not t.data.is_cuda:
+        raise ValueError(f"{what} must be a device tensor")
+    if not t.data.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+
+
+def dispatch_batch_matmul(g: RenderGraph, weight: Tensor, input: Tensor, output: Tensor,
+                          out_dim: int, in_dim: int, seq_len: int, row_offset: int,
+                          lora=None) -> None:
+    """output[m, n] = sum_k input[m, k] * weight[row_offset + n, k] (f32, overwritten).
+
+    Mirrors zimage::dispatch_batch_matmul for Q8_0 / Q4_K weights. A present
+    LoRA is a caller-side second hop in the reference (dit.c3:1305-1364) and
+    is not part of this backend."""
+    if lora is not None and getattr(lora, "present", True):
+        raise NotImplementedError("runtime LoRA correction stays on the caller side")
+    if weight.dtype not in (GGML_Q8_0, GGML_Q4_K):
+        raise capi.LlmrError(capi.LLMR_ERR_UNSUPPORTED, f"weight type {weight.dtype}")
+    for t, n in ((weight, "weight"), (input, "input"), (output, "output")):
+        _dev(t, n)
+    if output.dtype != GGML_F32:
+        raise ValueError("output must be f32")
+    if weight.shape[1] != in_dim or row_offset + out_dim > weight.shape[0]:
+        raise ValueError("weight shape does not cover [row_offset, row_offset+out_dim) x in_dim")
+    if input.data.numel() < seq_len * in_dim or output.data.numel() < seq_len * out_dim:
+        raise ValueError("input/output smaller than [seq_len, in_dim] / [seq_len, out_dim]")
+    g.bind_stream()
+    g.ctx.batch_matmul(weight.ptr(), weight.dtype, input.ptr(), input.dtype, output.ptr(),
+                       out_dim, in_dim, seq_len, row_offset)
+
+
+def dispatch_flash_attention(g: RenderGraph, q: Tensor, k: Tensor, v: Tensor, out: Tensor,
+                             pc: FlashAttentionPC) -> None:
+    """out[s, h*D + d] = softmax(scale * q k^T) v per head; q/k/v [H, S, D], out f32 [S, H*D]."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out")):
+        _dev(t, n)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, v must share a dtype")
+    if out.dtype != GGML_F32:
+        raise ValueError("out must be f32")
+    n = pc.n_heads * pc.seq_len * pc.head_dim
+    if min(q.data.numel(), k.data.numel(), v.data.numel(), out.data.numel()) < n:
+        raise ValueError("buffers smaller than [n_heads, seq_len, head_dim]")
+    g.bind_stream()
+    g.ctx.flash_attention(q.ptr(), k.ptr(), v.ptr(), q.dtype, out.ptr(), pc.head_dim, pc.n_heads,
+                          pc.seq_len, pc.scale)
+
+
+# ---- torch-tensor conveniences (tests, bench) --------------------------------
+
+_default_graph: RenderGraph | None = None
+
+
+def default_graph() -> RenderGraph:
+    global _default_graph
+    if _default_graph is None:
+        _default_graph = RenderGraph()
+    return _default_graph
+
+
+def batch_matmul(w_blocks: torch.Tensor, wtype: int, x: torch.Tensor, out_dim: int,
+                 row_offset: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [M, K] (f32/f16/bf16, cuda) times rows [row_offset, row_offset+out_dim) of the
+    quantized weight -> f32 [M, out_dim]."""
+    M, K = x.shape
+    rows = w_blocks.numel() // row_bytes(wtype, K)
+    if out is None:
+        out = torch.empty((M, out_dim), dtype=torch.float32, device=x.device)
+    dispatch_batch_matmul(default_graph(), Tensor.quantized(w_blocks, wtype, rows, K),
+                          Tensor.from_torch(x), Tensor.from_torch(out), out_dim, K, M, row_offset)
+    return out
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """q, k, v [H, S, 128] -> f32 [S, H*128]."""
+    H, S, D = q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty((S, H * D), dtype=torch.float32, device=q.device)
+    dispatch_flash_attention(default_graph(), Tensor.from_torch(q), Tensor.from_torch(k),
+                             Tensor.from_torch(v), Tensor.from_torch(out),
+                             FlashAttentionPC(D, H, S, scale))
+    return out
+
+
+def dequant(w_blocks: torch.Tensor, wtype: int, n_rows: int, in_dim: int,
+            row_offset: int = 0) -> torch.Tensor:
+    out = torch.empty((n_rows, in_dim), dtype=torch.float32, device=w_blocks.device)
+    g = default_graph()
+    g.bind_stream()
+    g.ctx.dequant(w_blocks.data_ptr(), wtype, n_rows, in_dim, row_offset, out.data_ptr())
+    return out
+
+
+def dequant_operand_f16(w_blocks: torch.Tensor, wtype: int, n_rows: int, in_dim: int,
+                        row_offset: int = 0) -> torch.Tensor:
+    out = torch.empty((n_rows, in_dim), dtype=torch.int16, device=w_blocks.device)
+    g = default_graph()
+    g.bind_stream()
+    g.ctx.dequant_operand_f16(w_blocks.data_ptr(), wtype, n_rows, in_dim, row_offset,
+                              out.data_ptr())
+    return out

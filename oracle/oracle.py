@@ -1,0 +1,204 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP backend. Imported by tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg; never by the product.
+The C restatement and its reference citations live in oracle/oracle.c.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_u32 = ctypes.c_uint32
+_sz = ctypes.c_size_t
+
+
+def build() -> str:
+    """Compile liboracle.so from oracle.c (gcc, OpenMP)."""
+    subprocess.run(["make", "-s", "-B", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        sig = {
+            "orc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "orc_f16_to_f32_n": (None, [_u16p, _sz, _f32p]),
+            "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+            "orc_f32_to_f16_n": (None, [_f32p, _sz, _u16p]),
+            "orc_f64_to_f16": (ctypes.c_uint16, [ctypes.c_double]),
+            "orc_get_scale_min_k4": (None, [_u32, _u8p, _u32p, _u32p]),
+            "orc_dequant_q8_0": (None, [_u8p, _sz, _f32p]),
+            "orc_dequant_q4k": (None, [_u8p, _sz, _f32p]),
+            "orc_dequant_q8_0_operand": (None, [_u8p, _sz, _u16p]),
+            "orc_dequant_q4k_operand": (None, [_u8p, _sz, _u16p]),
+            "orc_quantize_q8_0": (None, [_f32p, _sz, _u8p]),
+            "orc_quantize_q4k": (None, [_f32p, _sz, _u8p]),
+            "orc_batch_matmul_q8": (None, [_u8p, _f32p, _f32p, _u32, _u32, _u32, _u32]),
+            "orc_batch_matmul_q4k": (None, [_u8p, _f32p, _f32p, _u32, _u32, _u32, _u32]),
+            "orc_batch_matmul_q8_rows": (None, [_u8p, _f32p, _f32p, _u32, _u32, _u32, _u32, _u32p, _u32]),
+            "orc_batch_matmul_q4k_rows": (None, [_u8p, _f32p, _f32p, _u32, _u32, _u32, _u32, _u32p, _u32]),
+            "orc_flash_attention": (None, [_f32p, _f32p, _f32p, _f32p, _u32, _u32, _u32, ctypes.c_float,
+                                           _u32, _u32, _u32, _u32]),
+            "orc_rope_tables": (None, [_u32p, _u32, _u32p, _u32, ctypes.c_float, _f32p, _f32p]),
+            "orc_rope_apply": (None, [_f32p, _u32, _u32, _f32p, _f32p]),
+            "orc_num_threads": (ctypes.c_int, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray, ptype):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ptype)
+
+
+def num_threads() -> int:
+    return lib().orc_num_threads()
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().orc_f16_to_f32_n(_p(bits, _u16p), bits.size, _p(out, _f32p))
+    return out
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_n(_p(x, _f32p), x.size, _p(out, _u16p))
+    return out
+
+
+def f64_to_f16(x: float) -> int:
+    return int(lib().orc_f64_to_f16(float(x)))
+
+
+def get_scale_min_k4(is_: int, scales12: np.ndarray):
+    s = np.ascontiguousarray(scales12, dtype=np.uint8)
+    sc, mn = ctypes.c_uint32(), ctypes.c_uint32()
+    lib().orc_get_scale_min_k4(is_, _p(s, _u8p), ctypes.byref(sc), ctypes.byref(mn))
+    return sc.value, mn.value
+
+
+def dequant_q8_0(blocks: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    n = b.size // 34
+    out = np.empty(n * 32, np.float32)
+    lib().orc_dequant_q8_0(_p(b, _u8p), n, _p(out, _f32p))
+    return out
+
+
+def dequant_q8_0_operand(blocks: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    n = b.size // 34
+    out = np.empty(n * 32, np.uint16)
+    lib().orc_dequant_q8_0_operand(_p(b, _u8p), n, _p(out, _u16p))
+    return out
+
+
+def dequant_q4k(blocks: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    n = b.size // 144
+    out = np.empty(n * 256, np.float32)
+    lib().orc_dequant_q4k(_p(b, _u8p), n, _p(out, _f32p))
+    return out
+
+
+def dequant_q4k_operand(blocks: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    n = b.size // 144
+    out = np.empty(n * 256, np.uint16)
+    lib().orc_dequant_q4k_operand(_p(b, _u8p), n, _p(out, _u16p))
+    return out
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size // 32 * 34, np.uint8)
+    lib().orc_quantize_q8_0(_p(x, _f32p), x.size, _p(out, _u8p))
+    return out
+
+
+def quantize_q4k(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty(x.size // 256 * 144, np.uint8)
+    lib().orc_quantize_q4k(_p(x, _f32p), x.size, _p(out, _u8p))
+    return out
+
+
+def batch_matmul(W: np.ndarray, wtype: int, X: np.ndarray, out_dim: int, in_dim: int,
+                 seq_len: int, row_offset: int = 0, rows=None) -> np.ndarray:
+    """Reference GEMM (wtype 8 = Q8_0, 12 = Q4_K) on f32 activations X [seq_len, in_dim].
+    With `rows`, only those output rows are computed (result [len(rows), out_dim])."""
+    W = np.ascontiguousarray(W, dtype=np.uint8).reshape(-1)
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    assert X.size == seq_len * in_dim
+    L = lib()
+    if rows is None:
+        Y = np.empty((seq_len, out_dim), np.float32)
+        fn = L.orc_batch_matmul_q8 if wtype == 8 else L.orc_batch_matmul_q4k
+        fn(_p(W, _u8p), _p(X, _f32p), _p(Y, _f32p), out_dim, in_dim, seq_len, row_offset)
+        return Y
+    r = np.ascontiguousarray(rows, dtype=np.uint32)
+    Y = np.empty((r.size, out_dim), np.float32)
+    fn = L.orc_batch_matmul_q8_rows if wtype == 8 else L.orc_batch_matmul_q4k_rows
+    fn(_p(W, _u8p), _p(X, _f32p), _p(Y, _f32p), out_dim, in_dim, seq_len, row_offset,
+       _p(r, _u32p), r.size)
+    return Y
+
+
+def flash_attention(Q: np.ndarray, K: np.ndarray, V: np.ndarray, scale: float,
+                    heads=None, qrange=None) -> np.ndarray:
+    """Reference attention on f32 [H, S, 128] inputs; returns O f32 [S, H*128]
+    (entries outside the sampled heads / query range are NaN)."""
+    H, S, D = Q.shape
+    Q = np.ascontiguousarray(Q, dtype=np.float32)
+    K = np.ascontiguousarray(K, dtype=np.float32)
+    V = np.ascontiguousarray(V, dtype=np.float32)
+    O = np.full((S, H * D), np.nan, np.float32)
+    h0, h1 = heads if heads is not None else (0, H)
+    q0, q1 = qrange if qrange is not None else (0, S)
+    lib().orc_flash_attention(_p(Q, _f32p), _p(K, _f32p), _p(V, _f32p), _p(O, _f32p), D, H, S,
+                              float(scale), h0, h1, q0, q1)
+    return O
+
+
+def rope_tables(pos: np.ndarray, axes_dims, theta: float):
+    pos = np.ascontiguousarray(pos, dtype=np.uint32)
+    S, n_axes = pos.shape
+    axes = np.ascontiguousarray(axes_dims, dtype=np.uint32)
+    cos_t = np.zeros((S, 64), np.float32)
+    sin_t = np.zeros((S, 64), np.float32)
+    lib().orc_rope_tables(_p(pos, _u32p), S, _p(axes, _u32p), n_axes, float(theta),
+                          _p(cos_t, _f32p), _p(sin_t, _f32p))
+    return cos_t, sin_t
+
+
+def rope_apply(x: np.ndarray, cos_t: np.ndarray, sin_t: np.ndarray) -> np.ndarray:
+    x = np.array(x, dtype=np.float32, copy=True, order="C")
+    H, S, D = x.shape
+    assert D == 128
+    lib().orc_rope_apply(_p(x, _f32p), H, S, _p(np.ascontiguousarray(cos_t, np.float32), _f32p),
+                         _p(np.ascontiguousarray(sin_t, np.float32), _f32p))
+    return x
