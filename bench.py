@@ -145,6 +145,20 @@ def cpu_baseline(name: str, budget_s: float = 10.0):
             "kind": "port", "sample": sample + f", {dt:.1f} s of oracle time"}
 
 
+def copy_calibration(steps: int, warmup: int) -> int:
+    """A plain device-to-device copy of 1 GiB (reads 1 GiB, writes 1 GiB): the
+    known-size kernel the HBM traffic counters are scaled by."""
+    import torch
+    n = 1 << 28
+    a = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    b = torch.empty_like(a)
+    total_ms, _ = _time_steps(lambda: b.copy_(a), steps, warmup)
+    ms = total_ms / steps
+    print(json.dumps({"calibration": "hbm_copy", "bytes_read": 4 * n, "bytes_written": 4 * n,
+                      "ms": round(ms, 4), "gbs": round(8 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -153,7 +167,11 @@ def main():
     ap.add_argument("--workload", default="flux_attention")
     ap.add_argument("--components", default="flux_linear1,flux_linear2,q8_linear,zimage_qkv")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--hbm-copy-calibration", action="store_true",
+                    help="time a plain 1 GiB device copy (reference for the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.hbm_copy_calibration:
+        return copy_calibration(args.steps, args.warmup)
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU; --gpus {args.gpus} is not supported "
               "(the hot path is single-GPU; sharding is design-only)", file=sys.stderr)

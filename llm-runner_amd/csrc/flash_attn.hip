@@ -20,10 +20,14 @@
 //    (swap of key-index bits 2 and 3) to match it.
 //  * K and V tiles of 64 keys are double buffered in LDS (K as [key][d],
 //    V transposed to [d][key] while staging), with XOR-swizzled 16-byte
-//    chunks; the next tile's global loads are issued before the current
-//    tile's matrix work. One barrier per tile.
+//    chunks, read from HBM through buffer descriptors that return zeros past
+//    the sequence end (no bounds branches), and software-pipelined so the
+//    score MFMAs of the next tile overlap the softmax of the current one
+//    (see flash_attn_fwd). One barrier per tile.
 //  * Workgroups are remapped so all query blocks of a head run on one XCD
 //    (its K/V stay in that XCD's L2).
+#include <type_traits>
+
 #include "llmr_device.h"
 #include "llmr_internal.h"
 
@@ -36,52 +40,19 @@ constexpr int kBQ = 128;  // queries per workgroup
 constexpr int kBKV = 64;  // keys per tile
 constexpr uint32_t kKBytes = kBKV * kD * 2;   // K tile [64][128] fp16
 constexpr uint32_t kVBytes = kD * kBKV * 2;   // V^T tile [128][64] fp16
-constexpr uint32_t kStage = kKBytes + kVBytes;
 
 // K tile: 256-byte rows (16 chunks), swizzle by key & 15.
 __device__ __forceinline__ uint32_t k_off(uint32_t key, uint32_t c) {
     return key * 256u + ((c ^ (key & 15u)) << 4);
 }
-// V^T tile: 128-byte rows (8 chunks), swizzle by d & 7.
+// V^T tile: 128-byte rows (8 chunks). gfx950's LDS has 64 four-byte banks
+// (two 128-byte rows per bank line). The swizzle (d & 7) ^ ((d >> 3) & 7)
+// keeps both access patterns spread over the banks: fragment reads (16
+// consecutive d, one chunk) hit 16 distinct bank quads, and the transposing
+// staging writes (rows 8 apart) no longer all land on one quad.
 __device__ __forceinline__ uint32_t v_off(uint32_t d, uint32_t c) {
-    return d * 128u + ((c ^ (d & 7u)) << 4);
+    return d * 128u + ((c ^ ((d & 7u) ^ ((d >> 3) & 7u))) << 4);
 }
-
-// 8 consecutive elements of a Q/K/V row as fp16.
-template <uint32_t XT>
-struct Row8;
-template <>
-struct Row8<kGgmlF16> {
-    u32x4 v;
-    __device__ __forceinline__ void load(const void* p, uint64_t e, bool ok) {
-        v = ok ? *(const u32x4*)((const uint16_t*)p + e) : u32x4{0, 0, 0, 0};
-    }
-    __device__ __forceinline__ u32x4 f16() const { return v; }
-};
-template <>
-struct Row8<kGgmlBF16> {
-    u32x4 v;
-    __device__ __forceinline__ void load(const void* p, uint64_t e, bool ok) {
-        v = ok ? *(const u32x4*)((const uint16_t*)p + e) : u32x4{0, 0, 0, 0};
-    }
-    __device__ __forceinline__ u32x4 f16() const {
-        return u32x4{bf16x2_to_f16x2(v.x), bf16x2_to_f16x2(v.y), bf16x2_to_f16x2(v.z),
-                     bf16x2_to_f16x2(v.w)};
-    }
-};
-template <>
-struct Row8<kGgmlF32> {
-    f32x4 a, b;
-    __device__ __forceinline__ void load(const void* p, uint64_t e, bool ok) {
-        const float* f = (const float*)p + e;
-        a = ok ? *(const f32x4*)f : f32x4{0, 0, 0, 0};
-        b = ok ? *(const f32x4*)(f + 4) : f32x4{0, 0, 0, 0};
-    }
-    __device__ __forceinline__ u32x4 f16() const {
-        return u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y),
-                     pack_f16x2(b.z, b.w)};
-    }
-};
 
 // Position of key r (0..15) of a 16-key chunk inside the V^T row: bits 2 and 3
 // swapped, so lane half kh finds its 8 keys {4kh..4kh+3, 8+4kh..8+4kh+3} at
@@ -90,11 +61,58 @@ __device__ __forceinline__ uint32_t vpos(uint32_t r) {
     return (r & 3u) | (((r >> 3) & 1u) << 2) | (((r >> 2) & 1u) << 3);
 }
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+// 8 consecutive elements of a row of one head, loaded through the head's
+// buffer descriptor (rows past the sequence end read as zero), as fp16.
+template <uint32_t XT>
+struct Row8B {
+    static constexpr int kN = (XT == kGgmlF32) ? 2 : 1;
+    u32x4 v[kN];
+    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t soff) {
+        v[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+        if constexpr (kN == 2)
+            v[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16u, soff, 0));
+    }
+    __device__ __forceinline__ u32x4 f16() const {
+        if constexpr (XT == kGgmlF32) {
+            const f32x4 a = __builtin_bit_cast(f32x4, v[0]), b = __builtin_bit_cast(f32x4, v[1]);
+            return u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y), pack_f16x2(b.z, b.w)};
+        } else if constexpr (XT == kGgmlBF16) {
+            return u32x4{bf16x2_to_f16x2(v[0].x), bf16x2_to_f16x2(v[0].y), bf16x2_to_f16x2(v[0].z),
+                         bf16x2_to_f16x2(v[0].w)};
+        } else {
+            return v[0];
+        }
+    }
+};
+
+// Software-pipelined tile loop. Per 64-key tile t a wave
+//   1. issues S(t+1) = K(t+1) Q^T on the matrix cores,
+//   2. runs the online softmax of S(t) on the vector ALU meanwhile,
+//   3. accumulates O^T += V(t)^T P(t)^T,
+//   4. stores the prefetched K(t+2) and V(t+1) into the free LDS buffers and
+//      issues the global loads of K(t+3) and V(t+2).
+// K and V have their own double buffers, phased one tile apart, so one
+// barrier per tile suffices. The running max used for the exponentials is
+// only raised when a new score exceeds it by more than 2^8 (log2 domain), so
+// most tiles skip rescaling O; p = exp2(s - m) then stays below 2^8, and the
+// final O / l is the same softmax.
 template <uint32_t XT>
 __global__ void __launch_bounds__(256, 2)
 flash_attn_fwd(const void* __restrict__ Q, const void* __restrict__ K, const void* __restrict__ V,
                float* __restrict__ O, uint32_t S, uint32_t H, float scale_log2, uint32_t n_qb) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * kStage];
+    __shared__ __attribute__((aligned(16))) uint8_t Kb0[kKBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t Kb1[kKBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t Vb0[kVBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t Vb1[kVBytes];
+    constexpr uint32_t XE = (XT == kGgmlF32) ? 4u : 2u;
+    constexpr uint32_t ROW = kD * XE;  // bytes per token row of one head
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t l32 = lane & 31u, kh = lane >> 5;
@@ -105,49 +123,47 @@ flash_attn_fwd(const void* __restrict__ Q, const void* __restrict__ K, const voi
     if (total % 8u == 0) L = (L % 8u) * (total / 8u) + L / 8u;
     const uint32_t head = L / n_qb, qb = L % n_qb;
 
-    const uint64_t hbase = (uint64_t)head * S * kD;
+    const uint64_t head_bytes = (uint64_t)S * ROW;
+    const rsrc_t qr = make_rsrc((const uint8_t*)Q + head * head_bytes, head_bytes);
+    const rsrc_t kr = make_rsrc((const uint8_t*)K + head * head_bytes, head_bytes);
+    const rsrc_t vr = make_rsrc((const uint8_t*)V + head * head_bytes, head_bytes);
     const uint32_t q_idx = qb * kBQ + wave * 32u + l32;
 
-    // Q fragments (B operand): d = 32*c + 16*kh + 8*st + 0..7
+    // Q fragments (B operand of S^T = K Q^T): d = 32c + 16kh + 8st + 0..7
     f16x8 qf[4][2];
 #pragma unroll
     for (int c = 0; c < 4; c++)
 #pragma unroll
         for (int st = 0; st < 2; st++) {
-            Row8<XT> r;
-            r.load(Q, hbase + (uint64_t)q_idx * kD + 32 * c + 16 * kh + 8 * st, q_idx < S);
+            Row8B<XT> r;
+            r.load(qr, q_idx * ROW + (32u * c + 16u * kh + 8u * st) * XE, 0);
             qf[c][st] = __builtin_bit_cast(f16x8, r.f16());
         }
 
-    // K/V staging: K thread -> (chunk tid&15, keys tid>>4 + 16i); V thread ->
-    // (8 dims 8*(tid&15).., 4 keys 4*(tid>>4)..)
-    Row8<XT> kr[4], vr[4];
+    // staging: K thread -> (16-byte chunk tid&15, keys tid>>4 + 16i);
+    // V thread -> (dims 8*(tid&15).., keys 4*(tid>>4)..+3)
     const uint32_t kc = tid & 15u, krow = tid >> 4;
     const uint32_t vdg = tid & 15u, vkg = tid >> 4;
-    auto load_tile = [&](uint32_t t) {
-        const uint32_t kv0 = t * kBKV;
+    Row8B<XT> kreg[4], vreg[4];
+    auto load_k = [&](uint32_t t) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t key = kv0 + krow + 16u * i;
-            kr[i].load(K, hbase + (uint64_t)key * kD + 8 * kc, key < S);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t key = kv0 + 4u * vkg + i;
-            vr[i].load(V, hbase + (uint64_t)key * kD + 8 * vdg, key < S);
-        }
+        for (int i = 0; i < 4; i++) kreg[i].load(kr, (krow + 16u * i) * ROW + kc * 8u * XE, t * kBKV * ROW);
     };
-    auto store_tile = [&](uint32_t buf) {
-        uint8_t* Ks = smem + buf * kStage;
-        uint8_t* Vs = Ks + kKBytes;
+    auto load_v = [&](uint32_t t) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) *(u32x4*)(Ks + k_off(krow + 16u * i, kc)) = kr[i].f16();
+        for (int i = 0; i < 4; i++) vreg[i].load(vr, (4u * vkg + i) * ROW + vdg * 8u * XE, t * kBKV * ROW);
+    };
+    auto store_k = [&](uint8_t* Ks) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) *(u32x4*)(Ks + k_off(krow + 16u * i, kc)) = kreg[i].f16();
+    };
+    auto store_v = [&](uint8_t* Vs) {
         u32x4 v[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = vr[i].f16();
-        // keys 4*vkg..+3 = chunk c16 = vkg/4, group g = vkg%4 -> positions 16*c16 + vpos(4g)..+3
+        for (int i = 0; i < 4; i++) v[i] = vreg[i].f16();
+        // keys 4*vkg..+3: 16-key chunk vkg/4, group vkg%4 -> positions 16*(vkg/4) + vpos(4*(vkg%4))..+3
         const uint32_t pos = 16u * (vkg >> 2) + vpos(4u * (vkg & 3u));
-        const uint32_t chunk = pos >> 3, sub = (pos & 7u) * 2u;  // byte offset inside the chunk
+        const uint32_t chunk = pos >> 3, sub = (pos & 7u) * 2u;
 #pragma unroll
         for (int dd = 0; dd < 8; dd++) {
             const uint32_t w0 = v[0][dd >> 1], w1 = v[1][dd >> 1], w2 = v[2][dd >> 1], w3 = v[3][dd >> 1];
@@ -155,8 +171,22 @@ flash_attn_fwd(const void* __restrict__ Q, const void* __restrict__ K, const voi
             u32x2 pr;
             pr.x = __builtin_amdgcn_perm(w1, w0, sel);
             pr.y = __builtin_amdgcn_perm(w3, w2, sel);
-            const uint32_t d = 8u * vdg + dd;
-            *(u32x2*)(Vs + v_off(d, chunk) + sub) = pr;
+            *(u32x2*)(Vs + v_off(8u * vdg + dd, chunk) + sub) = pr;
+        }
+    };
+    // S^T[key][query] for the two 32-key halves of the tile in Ks
+    auto qk = [&](const uint8_t* Ks, f32x16 (&s)[2]) {
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) s[kb][j] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int st = 0; st < 2; st++) {
+                    const f16x8 a = *(const f16x8*)(Ks + k_off(32u * kb + l32, 4u * c + 2u * kh + st));
+                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c][st], s[kb], 0, 0, 0);
+                }
         }
     };
 
@@ -165,68 +195,47 @@ flash_attn_fwd(const void* __restrict__ Q, const void* __restrict__ K, const voi
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 16; j++) o[i][j] = 0.0f;
-    float m_i = -1.0e30f;  // running max, log2 domain (reference starts at -1e30)
-    float l_i = 0.0f;      // this lane's partial row sum
+    float m_ref = -1.0e30f;  // max used by the exponentials (log2 domain); reference starts at -1e30
+    float l_i = 0.0f;        // this lane's partial row sum
 
-    const uint32_t n_tiles = (S + kBKV - 1) / kBKV;
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-
-    for (uint32_t t = 0; t < n_tiles; t++) {
-        const uint32_t buf = t & 1u;
-        if (t + 1 < n_tiles) load_tile(t + 1);
-        const uint8_t* Ks = smem + buf * kStage;
-        const uint8_t* Vs = Ks + kKBytes;
-
-        // S^T[key][query] for the two 32-key halves of the tile
-        f32x16 sacc[2];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-#pragma unroll
-            for (int j = 0; j < 16; j++) sacc[kb][j] = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-#pragma unroll
-                for (int st = 0; st < 2; st++) {
-                    const f16x8 a = *(const f16x8*)(Ks + k_off(32u * kb + l32, 4u * c + 2u * kh + st));
-                    sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c][st], sacc[kb], 0, 0, 0);
-                }
-        }
-        // keys past the end contribute nothing (reference: score -1e30, p = 0)
-        if ((t + 1) * kBKV > S) {
+    // softmax of S(t) and O^T += V(t)^T P(t)^T; keys >= S masked when kMask
+    auto softmax_pv = [&](f32x16 (&sc)[2], const uint8_t* Vs, uint32_t t, auto mask_tag) {
+        constexpr bool kMask = decltype(mask_tag)::value;
+        if constexpr (kMask) {
 #pragma unroll
             for (int kb = 0; kb < 2; kb++)
 #pragma unroll
                 for (int j = 0; j < 16; j++) {
                     const uint32_t key = t * kBKV + 32u * kb + 8u * (j >> 2) + 4u * kh + (j & 3);
-                    if (key >= S) sacc[kb][j] = -INFINITY;
+                    sc[kb][j] = key < S ? sc[kb][j] : -INFINITY;
                 }
         }
-        float mx = sacc[0][0];
+        float mx = sc[0][0];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-            for (int j = 0; j < 16; j++) mx = fmaxf(mx, sacc[kb][j]);
+            for (int j = 0; j < 16; j++) mx = fmaxf(mx, sc[kb][j]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_i, mx * scale_log2);
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-        m_i = m_new;
+        const float m_new = mx * scale_log2;
+        if (__builtin_amdgcn_ballot_w64(m_new > m_ref + 8.0f) != 0) {
+            const float m2 = fmaxf(m_ref, m_new);
+            const float alpha = __builtin_amdgcn_exp2f(m_ref - m2);
+            m_ref = m2;
+            l_i *= alpha;
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] *= alpha;
+        }
         float rs = 0.0f;
         f16x8 pf[2][2];
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
             for (int j = 0; j < 16; j++) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kb][j], scale_log2, -m_new));
+                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][j], scale_log2, -m_ref));
                 rs += p;
                 pf[kb][j >> 3][j & 7] = (_Float16)p;
             }
-        l_i = l_i * alpha + rs;
-#pragma unroll
-        for (int i = 0; i < 4; i++) o[i] *= alpha;
-
-        // O^T[d][query] += V^T[d][key] P^T[key][query]
+        l_i += rs;
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -236,10 +245,48 @@ flash_attn_fwd(const void* __restrict__ Q, const void* __restrict__ K, const voi
                     const f16x8 a = *(const f16x8*)(Vs + v_off(32u * dt + l32, 2u * (2u * kb + c) + kh));
                     o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[kb][c], o[dt], 0, 0, 0);
                 }
+    };
 
-        if (t + 1 < n_tiles) store_tile(buf ^ 1u);
+    // one pipelined tile: reads K(t+1) from Kr and V(t) from Vr, writes K(t+2)
+    // into Kw and V(t+1) into Vw
+    f32x16 sc[2];
+    auto body = [&](uint32_t t, const uint8_t* Kr, const uint8_t* Vr, uint8_t* Kw, uint8_t* Vw) {
+        f32x16 sn[2];
+        qk(Kr, sn);
+        softmax_pv(sc, Vr, t, std::false_type{});
+        store_k(Kw);
+        store_v(Vw);
+        load_k(t + 3);
+        load_v(t + 2);
         __syncthreads();
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) sc[kb] = sn[kb];
+    };
+
+    const uint32_t n_tiles = (S + kBKV - 1) / kBKV;
+    load_k(0);
+    load_v(0);
+    store_k(Kb0);
+    store_v(Vb0);
+    load_k(1);
+    store_k(Kb1);
+    load_k(2);
+    load_v(1);
+    __syncthreads();
+    qk(Kb0, sc);
+    __syncthreads();  // every wave has read K(0) before the first body() overwrites Kb0
+
+    uint32_t t = 0;
+    const uint32_t n_main = n_tiles - 1;  // the last tile may be partial: done below with masking
+    for (; t + 2 <= n_main; t += 2) {
+        body(t, Kb1, Vb0, Kb0, Vb1);
+        body(t + 1, Kb0, Vb1, Kb1, Vb0);
     }
+    if (t < n_main) {
+        body(t, Kb1, Vb0, Kb0, Vb1);
+        t++;
+    }
+    softmax_pv(sc, (t & 1u) ? Vb1 : Vb0, t, std::true_type{});
 
     const float l_tot = l_i + __shfl_xor(l_i, 32);
     const float inv_l = 1.0f / l_tot;

@@ -25,8 +25,9 @@ constexpr uint32_t kGgmlF32 = 0, kGgmlF16 = 1, kGgmlQ8_0 = 8, kGgmlQ4K = 12, kGg
 // everything else is the exact value (the hardware widening is exact for
 // zero, subnormal and normal halves).
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
-    if (((bits >> 10) & 0x1fu) == 0x1fu) return __uint_as_float(((bits & 0x8000u) << 16) | 0x7f800000u);
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+    const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+    const float inf = __uint_as_float(((bits & 0x8000u) << 16) | 0x7f800000u);
+    return ((bits & 0x7c00u) == 0x7c00u) ? inf : v;
 }
 
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
@@ -59,21 +60,31 @@ __device__ __forceinline__ f16x4 q8x4_to_f16(uint32_t w, f16x2 d2) {
     return r;
 }
 
+// Two 4-bit quants (bytes of `nib` picked by the v_perm selector `sel`, each
+// 0..15) -> packed fp16 RN16(dsc*q - dmn): 0x6400|q is the half 1024+q, one
+// packed subtract gives q exactly, and the mixed-precision FMA
+// (v_fma_mix{lo,hi}_f16) rounds the exact dsc*q - dmn once.
+__device__ __forceinline__ uint32_t q4_pair(uint32_t nib, uint32_t sel, float dsc, float dmn) {
+    const f16x2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const f16x2 q = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, nib, sel)) - bias;
+    f16x2 r;
+    r.x = (_Float16)__builtin_fmaf((float)q.x, dsc, -dmn);
+    r.y = (_Float16)__builtin_fmaf((float)q.y, dsc, -dmn);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 // get_scale_min_k4 (llm.slang:447-462) for sub-block index `is` (wave-uniform)
 // on the 12 scale bytes held in dwords s0 (bytes 0-3), s1 (4-7), s2 (8-11).
+// Branch-free (a mask select) so a loop calling it stays one basic block.
 __device__ __forceinline__ void q4k_scale_min(uint32_t is, uint32_t s0, uint32_t s1, uint32_t s2,
                                               uint32_t& sc, uint32_t& mn) {
     const uint32_t sh = 8u * (is & 3u);
-    if (is < 4) {
-        sc = (s0 >> sh) & 63u;
-        mn = (s1 >> sh) & 63u;
-    } else {
-        const uint32_t b_hi = (s2 >> sh) & 0xffu;  // byte is+4
-        const uint32_t b_lo = (s0 >> sh) & 0xffu;  // byte is-4
-        const uint32_t b_md = (s1 >> sh) & 0xffu;  // byte is
-        sc = (b_hi & 0xfu) | ((b_lo >> 6) << 4);
-        mn = (b_hi >> 4) | ((b_md >> 6) << 4);
-    }
+    const uint32_t x0 = (s0 >> sh) & 0xffu;  // byte is (is < 4) or byte is-4 (is >= 4)
+    const uint32_t x1 = (s1 >> sh) & 0xffu;  // byte is+4 (is < 4) or byte is (is >= 4)
+    const uint32_t x2 = (s2 >> sh) & 0xffu;  // byte is+4 (is >= 4)
+    const uint32_t hi = 0u - (is >> 2);      // all ones when is >= 4
+    sc = ((x0 & 63u) & ~hi) | (((x2 & 0xfu) | ((x0 >> 6) << 4)) & hi);
+    mn = ((x1 & 63u) & ~hi) | (((x2 >> 4) | ((x1 >> 6) << 4)) & hi);
 }
 
 }  // namespace llmr

@@ -127,9 +127,12 @@ def test_full_size_sampled_rows(orc, dev, name):
     err = rel_l2(got, ref)
     print(f"{name}: sampled rel_l2={err:.3e}")
     assert err <= TOL
-    # size-independent property over the whole output: each row equals the
-    # same computation done alone (row independence: no cross-token leakage)
+    # row independence: the same token computed alone (a one-token launch,
+    # which takes the small-tile kernel) agrees with the oracle and with its
+    # row of the full launch to within both kernels' operand rounding
     m = int(rows[5])
     y1 = ops.batch_matmul(w, g.wtype, xt[m:m + 1].contiguous(), g.N)
     torch.cuda.synchronize()
-    assert rel_l2(y1.cpu().numpy()[0], y[m].cpu().numpy()) <= 1e-5
+    y1 = y1.cpu().numpy()[0]
+    assert rel_l2(y1, ref[5]) <= TOL
+    assert rel_l2(y1, y[m].cpu().numpy()) <= 2 * TOL
