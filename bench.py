@@ -92,7 +92,22 @@ def setup_gemm(dev, name):
 
     cfg = {"workload": name, "M": g.M, "N": g.N, "K": g.K, "weight": gguf.TYPE_NAMES[g.wtype],
            "activations": gguf.TYPE_NAMES[g.xtype].lower(), "output": "f32"}
-    return step, g.flops, g.bytes, cfg, "f16"
+    # MFMA operand type: bf16 activations run bf16 MFMA, f32/f16 ones fp16 MFMA
+    return step, g.flops, g.bytes, cfg, "bf16" if g.xtype == gguf.GGML_BF16 else "f16"
+
+
+def gemm_kernel_name(name: str, num_cus: int) -> str:
+    """The kernel the library's dispatch picks for a GEMM workload: the
+    pipelined 256x256 kernel when 16-bit activations give at least 1.5
+    workgroups per CU, else the 4-wave tiled kernel."""
+    from llmr_amd import gguf, workloads
+    g = workloads.GEMMS[name]
+    tiles = ((g.M + 255) // 256) * ((g.N + 255) // 256)
+    if g.wtype == gguf.GGML_Q8_0 and g.K % 64:
+        return "gemm_q_generic"
+    if g.xtype != gguf.GGML_F32 and 2 * tiles >= 3 * num_cus:
+        return "gemm_q_pipe"
+    return "gemm_q_mfma"
 
 
 def measure(dev, name, steps, warmup):
@@ -197,7 +212,8 @@ def main():
     ach = main_r["tflops"]
     roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(ach / PEAK_TFLOPS, 4), "traffic": _traffic(args.workload),
-            "kernel": "flash_attn_fwd" if args.workload == "flux_attention" else "gemm_q_mfma",
+            "kernel": ("flash_attn_fwd" if args.workload == "flux_attention" else
+                       gemm_kernel_name(args.workload, torch.cuda.get_device_properties(dev).multi_processor_count)),
             "algorithmic_bytes": main_r["bytes"],
             "hbm_frac_algorithmic": round(main_r["bytes"] / (main_r["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
     line = {
