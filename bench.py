@@ -98,15 +98,15 @@ def setup_gemm(dev, name):
 
 def gemm_kernel_name(name: str, num_cus: int) -> str:
     """The kernel the library's dispatch picks for a GEMM workload: the
-    pipelined 256x256 kernel when 16-bit activations give at least 1.5
-    workgroups per CU, else the 4-wave tiled kernel."""
+    persistent 256x256 kernel for 16-bit activations with at least half the
+    CUs' worth of tiles (and N % 4 == 0), else the 4-wave tiled kernel."""
     from llmr_amd import gguf, workloads
     g = workloads.GEMMS[name]
     tiles = ((g.M + 255) // 256) * ((g.N + 255) // 256)
     if g.wtype == gguf.GGML_Q8_0 and g.K % 64:
         return "gemm_q_generic"
-    if g.xtype != gguf.GGML_F32 and 2 * tiles >= 3 * num_cus:
-        return "gemm_q_pipe"
+    if g.xtype != gguf.GGML_F32 and g.N % 4 == 0 and 2 * tiles >= num_cus:
+        return "gemm_q_persist"
     return "gemm_q_mfma"
 
 

@@ -26,6 +26,8 @@
 //    operands, so every fragment is one 16-byte LDS read.
 //  * Workgroups are remapped so the tiles one XCD runs concurrently share
 //    weight and activation rows in that XCD's L2.
+#include <type_traits>
+
 #include "llmr_device.h"
 #include "llmr_internal.h"
 
@@ -342,27 +344,7 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
 }
 
 // ---------------------------------------------------------------------------
-// 256 x 256 tile kernel for 16-bit activations, software pipelined.
-//
-// Same tile mapping, LDS row layout and MFMA k-permutation as gemm_q_mfma.
-// The activations are multiplied in their own type: bf16 activations with
-// v_mfma_f32_32x32x16_bf16 (converting them to fp16 would overflow above
-// 65504), f16 activations with the f16 instruction; the weights are
-// dequantized to that type (bf16: RN_bf16 of the reference's f32 dequant
-// value; f16: the fp16 operand of gemm_q_mfma). Restructured so the matrix
-// cores are not left waiting for the byte work:
-//  * the activation tile goes from HBM straight into LDS (buffer_load ... lds,
-//    16 bytes per lane; the per-lane source address is permuted so the fixed
-//    lane*16 LDS placement realizes the bank swizzle), into a 3-slot ring
-//    fetched two stages ahead - no registers, no VALU;
-//  * the weight tile is fetched into two register sets (two stages ahead),
-//    dequantized into a double-buffered LDS tile while the previous stage is
-//    multiplied (the VALU work is interleaved with the MFMAs);
-//  * all global reads use buffer descriptors whose size ends at the last
-//    valid row of the tile: the hardware returns zeros past it, so the loop
-//    has no bounds branches; reads past the last stage land in LDS that is
-//    never multiplied;
-//  * LDS is 3 x 32 KiB (activations) + 2 x 32 KiB (weights) = 160 KiB.
+// Buffer-resource helpers for the persistent kernel below.
 // ---------------------------------------------------------------------------
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -382,7 +364,7 @@ __device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t voff, uint32_t sof
 // (gfx9 encoding: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14).
 #define LLMR_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
 
-// Workgroup barrier for the pipelined loop: this wave's LDS writes are done
+// Workgroup barrier for a pipelined loop: this wave's LDS writes are done
 // (lgkmcnt(0)) and at most `n` of its global loads/DMAs are still in flight,
 // then s_barrier. __syncthreads() would instead wait for every outstanding
 // global load (vmcnt(0)), i.e. for the prefetches issued for later stages.
@@ -396,148 +378,11 @@ __device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t voff, uint32_t sof
         asm volatile("" ::: "memory");                                                     \
     } while (0)
 
-// Q4_K nibbles -> packed bf16 of the reference's f32 value d*sc*q - dmin*mn
-// (q exact via the 1024+q half, f32 FMA, then RNE to bf16).
-__device__ __forceinline__ uint32_t q4_pair_bf16(uint32_t nib, uint32_t sel, float dsc, float dmn) {
-    const f16x2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
-    const f16x2 q = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, nib, sel)) - bias;
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    bf16x2_t r;
-    r.x = (__bf16)__builtin_fmaf((float)q.x, dsc, -dmn);
-    r.y = (__bf16)__builtin_fmaf((float)q.y, dsc, -dmn);
-    return __builtin_bit_cast(uint32_t, r);
+// Eight Q8_0 quants (two dwords) -> one 16-byte chunk of fp16 operands RN16(d*q).
+__device__ __forceinline__ u32x4 q8x8_f16(uint32_t q0, uint32_t q1, f16x2 d2) {
+    const f16x4 lo = q8x4_to_f16(q0, d2), hi = q8x4_to_f16(q1, d2);
+    return __builtin_bit_cast(u32x4, f16x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
 }
-// Four Q8_0 quants -> two dwords of packed bf16 RN_bf16(d*q) (d*q exact in f32).
-__device__ __forceinline__ u32x2 q8x4_to_bf16(uint32_t w, float d) {
-    const uint32_t x = w ^ 0x80808080u;
-    const f16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const f16x2 a = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) - bias;
-    const f16x2 b = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) - bias;
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    bf16x2_t r0, r1;
-    r0.x = (__bf16)((float)a.x * d);
-    r0.y = (__bf16)((float)a.y * d);
-    r1.x = (__bf16)((float)b.x * d);
-    r1.y = (__bf16)((float)b.y * d);
-    return u32x2{__builtin_bit_cast(uint32_t, r0), __builtin_bit_cast(uint32_t, r1)};
-}
-
-// Eight Q8_0 quants (two dwords) -> one 16-byte chunk of operand type OT.
-template <uint32_t OT>
-__device__ __forceinline__ u32x4 q8x8_operand(uint32_t q0, uint32_t q1, float d, f16x2 d2) {
-    if constexpr (OT == kGgmlBF16) {
-        const u32x2 lo = q8x4_to_bf16(q0, d), hi = q8x4_to_bf16(q1, d);
-        return u32x4{lo.x, lo.y, hi.x, hi.y};
-    } else {
-        const f16x4 lo = q8x4_to_f16(q0, d2), hi = q8x4_to_f16(q1, d2);
-        return __builtin_bit_cast(u32x4, f16x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
-    }
-}
-
-// One thread's weight unit of one stage, dequantized to operand type OT
-// (kGgmlF16 or kGgmlBF16). 512 threads cover the 256-row tile; 16
-// consecutive lanes take 16 consecutive rows with the same chunk set, so
-// their 16-byte LDS writes hit 16 distinct bank quads:
-//   row = (tid & 15) + 16 * (tid >> 5), part = (tid >> 4) & 1.
-__device__ __forceinline__ uint32_t wunit_row(uint32_t tid) { return (tid & 15u) + 16u * (tid >> 5); }
-__device__ __forceinline__ uint32_t wunit_part(uint32_t tid) { return (tid >> 4) & 1u; }
-
-template <uint32_t WT, uint32_t OT>
-struct WUnit;
-
-// Q4_K: part p = half of the stage's 32 qs bytes of the row: 16 low nibbles
-// (k = 16p + 0..15, sub-block 2j) and 16 high nibbles (k = 32 + 16p + 0..15,
-// sub-block 2j+1), plus the 16-byte block header.
-template <uint32_t OT>
-struct WUnit<kGgmlQ4K, OT> {
-    static constexpr int kLoads = 2;
-    u32x4 hdr, qs;
-    // `end` (the descriptor size) replaces the stage offset of a padding stage
-    // past the last one, so every load of it returns zeros.
-    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t k0, bool live, uint32_t end) {
-        const uint32_t sh = live ? (k0 >> 8) * 144u : end;
-        const uint32_t sq = live ? sh + 16u + 32u * ((k0 >> 6) & 3u) : end;
-        hdr = bload16(r, voff, sh);
-        qs = bload16(r, voff + 16u * wunit_part(threadIdx.x), sq);
-    }
-    // LDS offsets of the 4 destination chunks 2p, 2p+1, 4+2p, 5+2p of the row
-    __device__ __forceinline__ static void offsets(uint32_t (&off)[4]) {
-        const uint32_t r = wunit_row(threadIdx.x), p = wunit_part(threadIdx.x);
-        off[0] = lds_off(r, 2u * p);
-        off[1] = lds_off(r, 2u * p + 1u);
-        off[2] = lds_off(r, 4u + 2u * p);
-        off[3] = lds_off(r, 5u + 2u * p);
-    }
-    __device__ __forceinline__ void store(uint8_t* lds, uint32_t k0, const uint32_t (&off)[4]) const {
-        const uint32_t j = (k0 >> 6) & 3u;
-        const float d = f16_bits_to_f32(hdr.x & 0xffffu);
-        const float dmin = f16_bits_to_f32(hdr.x >> 16);
-        uint32_t sc0, mn0, sc1, mn1;
-        q4k_scale_min(2 * j, hdr.y, hdr.z, hdr.w, sc0, mn0);
-        q4k_scale_min(2 * j + 1, hdr.y, hdr.z, hdr.w, sc1, mn1);
-        const float dsc0 = d * (float)sc0, dmn0 = dmin * (float)mn0;
-        const float dsc1 = d * (float)sc1, dmn1 = dmin * (float)mn1;
-        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w};
-        uint32_t lo[8], hi[8];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const uint32_t l4 = q[e] & 0x0f0f0f0fu;
-            const uint32_t h4 = (q[e] >> 4) & 0x0f0f0f0fu;
-            if constexpr (OT == kGgmlBF16) {
-                lo[2 * e] = q4_pair_bf16(l4, 0x04010400u, dsc0, dmn0);
-                lo[2 * e + 1] = q4_pair_bf16(l4, 0x04030402u, dsc0, dmn0);
-                hi[2 * e] = q4_pair_bf16(h4, 0x04010400u, dsc1, dmn1);
-                hi[2 * e + 1] = q4_pair_bf16(h4, 0x04030402u, dsc1, dmn1);
-            } else {
-                lo[2 * e] = q4_pair(l4, 0x04010400u, dsc0, dmn0);
-                lo[2 * e + 1] = q4_pair(l4, 0x04030402u, dsc0, dmn0);
-                hi[2 * e] = q4_pair(h4, 0x04010400u, dsc1, dmn1);
-                hi[2 * e + 1] = q4_pair(h4, 0x04030402u, dsc1, dmn1);
-            }
-        }
-        *(u32x4*)(lds + off[0]) = u32x4{lo[0], lo[1], lo[2], lo[3]};
-        *(u32x4*)(lds + off[1]) = u32x4{lo[4], lo[5], lo[6], lo[7]};
-        *(u32x4*)(lds + off[2]) = u32x4{hi[0], hi[1], hi[2], hi[3]};
-        *(u32x4*)(lds + off[3]) = u32x4{hi[4], hi[5], hi[6], hi[7]};
-    }
-};
-
-// Q8_0: part p = block p of the stage's two blocks (k = 32p + 0..31). The 9
-// dwords loaded from the dword-aligned start hold the block: p = 0 starts at
-// the stage's byte 0 (scale in the low half of dword 0, quants from byte 2),
-// p = 1 at byte 34 (loaded from byte 32: scale in the high half of dword 0,
-// quants in dwords 1..8).
-template <uint32_t OT>
-struct WUnit<kGgmlQ8_0, OT> {
-    static constexpr int kLoads = 3;
-    u32x4 a, b;
-    uint32_t c;
-    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t k0, bool live, uint32_t end) {
-        const uint32_t s = live ? (k0 >> 5) * 34u : end;
-        const uint32_t v = voff + 32u * wunit_part(threadIdx.x);
-        a = bload16(r, v, s);
-        b = bload16(r, v + 16u, s);
-        c = bload4(r, v + 32u, s);
-    }
-    __device__ __forceinline__ static void offsets(uint32_t (&off)[4]) {
-        const uint32_t r = wunit_row(threadIdx.x), p = wunit_part(threadIdx.x);
-#pragma unroll
-        for (int k = 0; k < 4; k++) off[k] = lds_off(r, 4u * p + k);
-    }
-    __device__ __forceinline__ void store(uint8_t* lds, uint32_t k0, const uint32_t (&off)[4]) const {
-        (void)k0;
-        const bool p1 = wunit_part(threadIdx.x) != 0;
-        const uint32_t wd[9] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c};
-        const float d = f16_bits_to_f32(p1 ? (wd[0] >> 16) : (wd[0] & 0xffffu));
-        const _Float16 h = (_Float16)d;
-        const f16x2 d2 = {h, h};
-        uint32_t qd[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) qd[i] = p1 ? wd[i + 1] : __builtin_amdgcn_alignbyte(wd[i + 1], wd[i], 2);
-#pragma unroll
-        for (int ch = 0; ch < 4; ch++) *(u32x4*)(lds + off[ch]) = q8x8_operand<OT>(qd[2 * ch], qd[2 * ch + 1], d, d2);
-    }
-};
 
 template <uint32_t XT>
 __device__ __forceinline__ f32x16 mfma16(f16x8 a, f16x8 b, f32x16 c) {
@@ -550,21 +395,232 @@ __device__ __forceinline__ f32x16 mfma16(f16x8 a, f16x8 b, f32x16 c) {
     }
 }
 
-// 512 threads = 8 waves = 2 per SIMD (one wave's LDS and barrier stalls are
-// covered by the other's MFMAs; on gfx950 vector ALU work does not overlap
-// matrix work on the same SIMD, so the dequant cost is kept to a minimum
-// instead). Wave tile 128 tokens x 64 features (wave grid 2 x 4).
+// ---------------------------------------------------------------------------
+// Persistent 256 x 256 tile kernel for 16-bit activations (gfx950).
+//
+// One workgroup per CU (grid = min(tiles, CUs)), 256 threads = one wave64
+// per SIMD, each wave a 128 (tokens) x 128 (features) sub-tile held in 16
+// v_mfma_f32_32x32x16 accumulators. A workgroup walks its tiles as one
+// continuous sequence of K stages (64 wide), so the loads of the next tile
+// start while the last stages of the current one are multiplied:
+//  * activations go HBM -> LDS by buffer_load ... lds (16 B per lane) into a
+//    3-slot ring, two stages ahead; each lane's source offset is permuted so
+//    the fixed lane*16 LDS placement realizes the bank swizzle;
+//  * each thread owns one weight row of the tile: its packed bytes for stage
+//    s+2 are fetched into registers, dequantized during stage s into a
+//    2-slot LDS ring (operand type = activation type);
+//  * per stage: fragment reads are double-buffered in registers across the
+//    four 16-wide k steps, and the one barrier sits after the third k step:
+//    the MFMAs of the fourth step run after it, covering the barrier wait;
+//  * a tile's f32 results are stored straight from the accumulators at the
+//    first stage of the next tile, right after that stage's loads went out.
+// Every row index lives in the per-lane buffer offset (rows past M or N read
+// as zero through the descriptor size); stages past K (the count is padded
+// to a multiple of 6 so the six ring-slot combinations are compile-time) and
+// tiles past the workgroup's last read through a zero-size descriptor.
+// ---------------------------------------------------------------------------
+
+// Tile order: in every full round of G = gridDim.x tiles the 32 workgroups
+// one XCD runs (dispatch is round-robin over the 8 XCDs) get 32 consecutive
+// indices, which the group-of-4-tile-rows order turns into a 4 x 8 block of
+// tiles (4 x 256 activation rows and 8 x 256 weight rows shared in the XCD's L2).
+__device__ __forceinline__ void map_tile_persist(uint32_t T, uint32_t G, uint32_t tiles_m, uint32_t tiles_n,
+                                                 uint32_t& tm, uint32_t& tn) {
+    constexpr uint32_t kXcd = 8, kGroupM = 4;
+    const uint32_t total = tiles_m * tiles_n;
+    uint32_t L = T;
+    if (G % kXcd == 0 && T / G < total / G) {
+        const uint32_t b = T % G;
+        L = (T - b) + (b % kXcd) * (G / kXcd) + b / kXcd;
+    }
+    const uint32_t per_group = kGroupM * tiles_n;
+    const uint32_t g = L / per_group;
+    const uint32_t first_m = g * kGroupM;
+    const uint32_t gsize = min(tiles_m - first_m, kGroupM);
+    const uint32_t in = L % per_group;
+    tm = first_m + in % gsize;
+    tn = in / gsize;
+}
+
+// Bytes 0,1 (SEL_LO) or 2,3 (SEL_HI) of `w` as two fp16 subnormals b * 2^-24
+// (exact: the byte is the mantissa of a zero-exponent half), so one mixed
+// FMA with a scale pre-multiplied by 2^24 forms scale * b + bias exactly
+// before its single rounding - no bias subtraction of the 1024+b encoding.
+constexpr uint32_t kSelLo = 0x0c010c00u, kSelHi = 0x0c030c02u;
+__device__ __forceinline__ f16x2 sub16x2(uint32_t w, uint32_t sel) {
+    return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, w, sel));
+}
+// Two operands RN(s * h + b) of type OT from the two halves of h, packed.
+template <uint32_t OT>
+__device__ __forceinline__ uint32_t fma_pair(f16x2 h, float s, float b) {
+    if constexpr (OT == kGgmlBF16) {
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+        bf16x2_t r;
+        r.x = (__bf16)__builtin_fmaf((float)h.x, s, b);
+        r.y = (__bf16)__builtin_fmaf((float)h.y, s, b);
+        return __builtin_bit_cast(uint32_t, r);
+    } else {
+        f16x2 r;
+        r.x = (_Float16)__builtin_fmaf((float)h.x, s, b);
+        r.y = (_Float16)__builtin_fmaf((float)h.y, s, b);
+        return __builtin_bit_cast(uint32_t, r);
+    }
+}
+
+template <uint32_t WT, uint32_t OT>
+struct WRow;
+
+// Q4_K row stage s: quarter s % 4 of superblock s / 4 = the 16-byte header
+// and qs bytes [32 (s%4), +32): low nibbles are k 0..31 of the stage
+// (sub-block 2j), high nibbles k 32..63 (sub-block 2j+1).
+// The dequantization is split in four parts (one per 16-wide k step of the
+// stage it overlaps): part p writes LDS chunks p and 4+p of the row.
+template <uint32_t OT>
+struct WRow<kGgmlQ4K, OT> {
+    static constexpr int kLoads = 3;
+    u32x4 hdr, qa, qb;
+    template <int L>
+    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t s) {
+        const uint32_t sh = (s >> 2) * 144u;
+        const uint32_t sq = sh + 16u + 32u * (s & 3u);
+        if constexpr (L == 0) hdr = bload16(r, voff, sh);
+        if constexpr (L == 1) qa = bload16(r, voff, sq);
+        if constexpr (L == 2) qb = bload16(r, voff + 16u, sq);
+    }
+    // Operand = RN(d*sc*q - dmin*mn) (products exact, one rounding): low
+    // nibbles are read as q * 2^-24, high nibbles (masked in place) as
+    // 16 q * 2^-24, so their scales carry 2^24 and 2^20.
+    struct Scale {
+        float s0, b0, s1, b1;
+    };
+    __device__ __forceinline__ Scale scale(uint32_t s) const {
+        const uint32_t j = s & 3u;
+        const float d = f16_bits_to_f32(hdr.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(hdr.x >> 16);
+        uint32_t sc0, mn0, sc1, mn1;
+        q4k_scale_min(2 * j, hdr.y, hdr.z, hdr.w, sc0, mn0);
+        q4k_scale_min(2 * j + 1, hdr.y, hdr.z, hdr.w, sc1, mn1);
+        return Scale{d * (float)sc0 * 16777216.0f, -(dmin * (float)mn0), d * (float)sc1 * 1048576.0f,
+                     -(dmin * (float)mn1)};
+    }
+    // `base` = LDS offset of chunk 0 of the row; chunk c is at base ^ (c << 4)
+    template <int P>
+    __device__ __forceinline__ void store(uint8_t* lds, const Scale& c, uint32_t base) const {
+        const uint32_t w0 = P < 2 ? qa[2 * P] : qb[2 * P - 4];
+        const uint32_t w1 = P < 2 ? qa[2 * P + 1] : qb[2 * P - 3];
+        const uint32_t l0 = w0 & 0x0f0f0f0fu, l1 = w1 & 0x0f0f0f0fu;
+        const uint32_t h0 = w0 & 0xf0f0f0f0u, h1 = w1 & 0xf0f0f0f0u;
+        const u32x4 lo = {fma_pair<OT>(sub16x2(l0, kSelLo), c.s0, c.b0), fma_pair<OT>(sub16x2(l0, kSelHi), c.s0, c.b0),
+                          fma_pair<OT>(sub16x2(l1, kSelLo), c.s0, c.b0), fma_pair<OT>(sub16x2(l1, kSelHi), c.s0, c.b0)};
+        const u32x4 hi = {fma_pair<OT>(sub16x2(h0, kSelLo), c.s1, c.b1), fma_pair<OT>(sub16x2(h0, kSelHi), c.s1, c.b1),
+                          fma_pair<OT>(sub16x2(h1, kSelLo), c.s1, c.b1), fma_pair<OT>(sub16x2(h1, kSelHi), c.s1, c.b1)};
+        *(u32x4*)(lds + (base ^ ((uint32_t)P << 4))) = lo;
+        *(u32x4*)(lds + (base ^ ((uint32_t)(4 + P) << 4))) = hi;
+    }
+};
+
+// Q8_0 row stage s: blocks 2s and 2s+1 = bytes [68 s, 68 s + 68) of the row
+// (dword-aligned: K % 64 == 0). Block 0: scale in the low half of dword 0,
+// quants from byte 2 (chunks 0..3); block 1: scale in the high half of dword
+// 8, quants in dwords 9..16 (chunks 4..7). Part p writes chunks p and 4+p.
+template <uint32_t OT>
+struct WRow<kGgmlQ8_0, OT> {
+    static constexpr int kLoads = 5;
+    u32x4 a, b, c, d;
+    uint32_t e;
+    template <int L>
+    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t s) {
+        const uint32_t so = 68u * s;
+        if constexpr (L == 0) a = bload16(r, voff, so);
+        if constexpr (L == 1) b = bload16(r, voff + 16u, so);
+        if constexpr (L == 2) c = bload16(r, voff + 32u, so);
+        if constexpr (L == 3) d = bload16(r, voff + 48u, so);
+        if constexpr (L == 4) e = bload4(r, voff + 64u, so);
+    }
+    struct Scale {
+        float s0, b0, s1, b1;  // bf16: (2^24 d, -128 d) per block; f16: (d, -) per block
+    };
+    __device__ __forceinline__ Scale scale(uint32_t s) const {
+        (void)s;
+        const float d0 = f16_bits_to_f32(a.x & 0xffffu);
+        const float d1 = f16_bits_to_f32(c.x >> 16);
+        if constexpr (OT == kGgmlBF16)
+            return Scale{d0 * 16777216.0f, -128.0f * d0, d1 * 16777216.0f, -128.0f * d1};
+        else
+            return Scale{d0, 0.0f, d1, 0.0f};
+    }
+    __device__ __forceinline__ uint32_t word(int i) const {
+        return i < 4 ? a[i] : i < 8 ? b[i - 4] : i < 12 ? c[i - 8] : i < 16 ? d[i - 12] : e;
+    }
+    // chunk ch of the stage from its two quant dwords q0, q1
+    __device__ __forceinline__ u32x4 chunk(uint32_t q0, uint32_t q1, float sc, float bi) const {
+        if constexpr (OT == kGgmlBF16) {
+            // RN_bf16(d*q): q + 128 read as a subnormal half, d*q = (2^24 d) h - 128 d
+            // exactly in f32, then one rounding to bf16
+            const uint32_t u0 = q0 ^ 0x80808080u, u1 = q1 ^ 0x80808080u;
+            return u32x4{fma_pair<OT>(sub16x2(u0, kSelLo), sc, bi), fma_pair<OT>(sub16x2(u0, kSelHi), sc, bi),
+                         fma_pair<OT>(sub16x2(u1, kSelLo), sc, bi), fma_pair<OT>(sub16x2(u1, kSelHi), sc, bi)};
+        } else {
+            const _Float16 h = (_Float16)sc;
+            return q8x8_f16(q0, q1, f16x2{h, h});
+        }
+    }
+    template <int P>
+    __device__ __forceinline__ void store(uint8_t* lds, const Scale& k, uint32_t base) const {
+        const uint32_t q0 = __builtin_amdgcn_alignbyte(word(2 * P + 1), word(2 * P), 2);
+        const uint32_t q1 = __builtin_amdgcn_alignbyte(word(2 * P + 2), word(2 * P + 1), 2);
+        *(u32x4*)(lds + (base ^ ((uint32_t)P << 4))) = chunk(q0, q1, k.s0, k.b0);
+        *(u32x4*)(lds + (base ^ ((uint32_t)(4 + P) << 4))) = chunk(word(9 + 2 * P), word(10 + 2 * P), k.s1, k.b1);
+    }
+};
+
+template <int I, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < E) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, E>(f);
+    }
+}
+
+// Schedule of one 16-wide k step inside a stage: its 16 MFMAs each followed
+// by a share of the stage's other work, so that work issues while the
+// matrix core is busy (on gfx950 a wave's VALU, LDS and buffer instructions
+// co-issue with its own MFMAs): the next step's fragment reads after the
+// first eight MFMAs, three VALU (the weight dequantization) after every one,
+// the two LDS writes of the dequantized weight chunks and the step's share
+// of the buffer loads spread in between.
+#define LLMR_SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+#define LLMR_SLOT_R LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x002, 3)
+#define LLMR_SLOT_V LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 3)
+#define LLMR_SLOT_L LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 3); LLMR_SGB(0x020, 1)
+#define LLMR_SLOT_W LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 3); LLMR_SGB(0x200, 1)
+#define LLMR_SLOT_RA LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x002, 5)
+#define LLMR_SLOT_VA LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 5)
+#define LLMR_SLOT_LA LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 5); LLMR_SGB(0x020, 1)
+#define LLMR_SLOT_WA LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 5); LLMR_SGB(0x200, 1)
+// the first step of a stage also computes the dequantization scales
+#define LLMR_STEP_SCHEDULE_A                                                                \
+    LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA;       \
+    LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_LA; LLMR_SLOT_VA; LLMR_SLOT_WA; LLMR_SLOT_LA;       \
+    LLMR_SLOT_VA; LLMR_SLOT_WA; LLMR_SLOT_LA; LLMR_SLOT_LA
+#define LLMR_STEP_SCHEDULE                                                                  \
+    LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R;             \
+    LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_L; LLMR_SLOT_V; LLMR_SLOT_W; LLMR_SLOT_L;             \
+    LLMR_SLOT_V; LLMR_SLOT_W; LLMR_SLOT_L; LLMR_SLOT_L
+
+struct Frags {
+    f16x8 x[4], w[4];
+};
+
 template <uint32_t WT, uint32_t XT>
-__global__ void __launch_bounds__(512, 1)
-gemm_q_pipe(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __restrict__ Y, uint32_t N,
-            uint32_t K, uint32_t M, uint32_t row_offset, uint32_t tiles_m, uint32_t tiles_n) {
+__global__ void __launch_bounds__(256, 1)
+gemm_q_persist(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __restrict__ Y, uint32_t N,
+               uint32_t K, uint32_t M, uint32_t row_offset, uint32_t tiles_m, uint32_t tiles_n) {
     static_assert(XT == kGgmlF16 || XT == kGgmlBF16, "16-bit activations only");
-    constexpr int BM = 256, BN = 256, WM = 128, WN = 64, TM = 4, TN = 2;
     constexpr uint32_t TILE = 256u * 128u;  // bytes of one 256-row x 64-wide 16-bit tile
-    constexpr int W_LOADS = WUnit<WT, XT>::kLoads;
-    constexpr int X_DMAS = 4;  // 1 KiB activation DMAs per wave per stage
-    // three separate arrays (not one indexed ring) so the compiler can prove a
-    // DMA into one slot does not alias reads of another and does not wait for it
+    constexpr int X_DMAS = 8;               // 1 KiB activation DMAs per wave per stage
+    constexpr int W_LOADS = WRow<WT, XT>::kLoads;
+    constexpr int IN_FLIGHT = X_DMAS + W_LOADS;  // one stage's loads
     __shared__ __attribute__((aligned(16))) uint8_t X0[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t X1[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t X2[TILE];
@@ -576,146 +632,243 @@ gemm_q_pipe(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
     const uint32_t l32 = lane & 31u, kh = lane >> 5;
     const uint32_t wm = wave & 1u, wn = wave >> 1;
 
-    uint32_t tile_m, tile_n;
-    map_tile(blockIdx.x, tiles_m, tiles_n, tile_m, tile_n);
-    const uint32_t m0 = tile_m * BM, n0 = tile_n * BN;
+    const uint32_t G = gridDim.x, total = tiles_m * tiles_n;
+    const uint32_t n_tiles = (total - blockIdx.x + G - 1) / G;  // >= 1: grid <= total
+    const uint32_t S = K / kBK;
+    const uint32_t SP = (S + 5u) / 6u * 6u;
     const uint32_t rb = (WT == kGgmlQ8_0) ? (K / 32u) * 34u : (K / 256u) * 144u;
-    // descriptor sizes end at the last valid row; the host guarantees they and
-    // every offset used below fit in 31 bits
-    const uint32_t x_end = (M - m0) * K * 2u;
-    const uint32_t w_end = (N - n0) * rb;
-    const rsrc_t xr = make_rsrc((const uint8_t*)X + (uint64_t)m0 * K * 2u, x_end);
-    const rsrc_t wr = make_rsrc(W + (uint64_t)(row_offset + n0) * rb, w_end);
-    const uint32_t n_stages = K / kBK;
+    const uint32_t xrow = K * 2u;
 
-    // activation DMA: wave w fills rows 32w .. 32w+31 of a slot, 8 rows (1 KiB)
-    // per instruction; lane l lands at byte 16l of the instruction's block,
-    // i.e. row 32w + 8i + l/8, physical chunk l%8, so it fetches logical chunk
-    // (l%8) ^ swizzle(row).
+    // per-lane offsets (tile independent)
+    // activation DMA i of wave w: rows 64w + 8i + lane/8, physical chunk lane%8,
+    // logical chunk (lane%8) ^ ((row >> 1) & 7) = (lane%8) ^ (lane/16) ^ 4(i&1)
     uint32_t xvoff[X_DMAS];
 #pragma unroll
     for (int i = 0; i < X_DMAS; i++) {
-        const uint32_t row = 32u * wave + 8u * i + (lane >> 3);
+        const uint32_t row = 64u * wave + 8u * i + (lane >> 3);
         const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
-        xvoff[i] = row * K * 2u + c * 16u;
+        xvoff[i] = row * xrow + c * 16u;
     }
-    auto dma_x = [&](uint32_t stage, uint8_t* Xslot) {
-        uint8_t* slot = Xslot + 32u * wave * 128u;
-        const uint32_t soff = stage < n_stages ? stage * kBK * 2u : x_end;
-#pragma unroll
-        for (int i = 0; i < X_DMAS; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(slot + 1024u * i), 16, xvoff[i], soff, 0, 0);
-    };
-
-    const uint32_t wvoff = wunit_row(tid) * rb;
-    WUnit<WT, XT> wu0, wu1;
-    auto wload = [&](WUnit<WT, XT>& u, uint32_t stage) {
-        u.load(wr, wvoff, stage * kBK, stage < n_stages, w_end);
-    };
-    uint32_t stoff[4];
-    WUnit<WT, XT>::offsets(stoff);
-
-    // Fragment addresses. Every row block starts at a multiple of 32 rows, so
-    // the swizzle term (row >> 1) & 7 depends only on the lane: each operand
-    // needs one lane offset per 16-wide k step t (chunk 4(t>>1) + 2kh + (t&1));
-    // the buffer and the row block are compile-time displacements.
+    const uint32_t wvoff = tid * rb;                                   // weight row tid of the tile
+    const uint32_t wbase = tid * 128u + ((((tid >> 1) & 7u)) << 4);    // its LDS chunk 0
+    // fragment offsets per 16-wide k step t: chunk 4(t>>1) + 2kh + (t&1) of
+    // rows (block) + l32; the swizzle term depends only on l32
     uint32_t xoff[4], woff[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const uint32_t ch = 4u * (t >> 1) + 2u * kh + (t & 1);
-        xoff[t] = lds_off(wm * WM + l32, ch);
-        woff[t] = lds_off(wn * WN + l32, ch);
+        xoff[t] = lds_off(wm * 128u + l32, ch);
+        woff[t] = lds_off(wn * 128u + l32, ch);
     }
 
-    f32x16 acc[TN][TM];
+    // Load side. Activations are fetched two stages ahead, weights three
+    // (their row-strided reads have the longer latency); each stream walks
+    // the workgroup's (tile, stage) sequence with its own cursor.
+    struct Cursor {
+        uint32_t s;               // stage within the tile
+        const uint8_t* base;      // the tile's first activation row / weight row
+        uint32_t size;            // bytes of valid rows from base (0 past the last tile)
+    };
+    auto tile_origin = [&](uint32_t k, uint32_t& m0, uint32_t& n0) {
+        uint32_t tm, tn;
+        map_tile_persist(blockIdx.x + k * G, G, tiles_m, tiles_n, tm, tn);
+        m0 = tm * 256u;
+        n0 = tn * 256u;
+    };
+    auto x_tile = [&](Cursor& c, uint32_t k) {
+        uint32_t m0, n0;
+        tile_origin(k, m0, n0);
+        c.s = 0;
+        c.base = (const uint8_t*)X + (uint64_t)m0 * xrow;
+        c.size = k < n_tiles ? (M - m0) * xrow : 0u;
+    };
+    auto w_tile = [&](Cursor& c, uint32_t k) {
+        uint32_t m0, n0;
+        tile_origin(k, m0, n0);
+        c.s = 0;
+        c.base = W + (uint64_t)(row_offset + n0) * rb;
+        c.size = k < n_tiles ? (N - n0) * rb : 0u;
+    };
+    Cursor cx{0, nullptr, 0}, cw{0, nullptr, 0};
+    // the tile after the one being multiplied, prepared once per tile: a
+    // cursor moving on to it only copies it (no per-stage tile arithmetic;
+    // a tile has at least 6 stages, more than the loads run ahead)
+    Cursor nx{0, nullptr, 0}, nw{0, nullptr, 0};
+    auto advance = [&](Cursor& c, const Cursor& next) {
+        if (++c.s == SP) c = next;
+    };
+    // one activation DMA (1 KiB: rows 64w + 8i .. +7 of the slot) of stage `so`/128
+    auto dma = [&](rsrc_t xr, uint8_t* Xs, int i, uint32_t so) {
+        uint8_t* dst = Xs + wave * (64u * 128u) + 1024u * i;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)dst, 16, xvoff[i], so, 0, 0);
+    };
+    WRow<WT, XT> R0, R1, R2;
+    // whole-stage loads (prologue): weights of the W cursor's stage into U,
+    // activations of the X cursor's stage into slot Xs
+    auto issue_w_all = [&](WRow<WT, XT>& U) {
+        const rsrc_t wr = make_rsrc(cw.base, cw.s < S ? cw.size : 0u);
+        static_for<0, W_LOADS>([&](auto L) { U.template load<decltype(L)::value>(wr, wvoff, cw.s); });
+        advance(cw, nw);
+    };
+    auto issue_x_all = [&](uint8_t* Xs) {
+        const rsrc_t xr = make_rsrc(cx.base, cx.s < S ? cx.size : 0u);
 #pragma unroll
-    for (int a = 0; a < TN; a++)
-#pragma unroll
-        for (int b = 0; b < TM; b++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) acc[a][b][i] = 0.0f;
-
-    // Multiply stage s (activations As, weights Bs) while dequantizing `u`
-    // (the weights of stage s+1) into Bn.
-    // The fragments of a k step are read right before its MFMAs: the other
-    // wave on the SIMD covers the LDS latency.
-    auto stage = [&](uint32_t s, const uint8_t* As, const uint8_t* Bs, const WUnit<WT, XT>& u, uint8_t* Bn) {
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            f16x8 xf[TM], wf[TN];
-#pragma unroll
-            for (int b = 0; b < TM; b++) xf[b] = *(const f16x8*)(As + b * 32 * 128 + xoff[t]);
-#pragma unroll
-            for (int a = 0; a < TN; a++) wf[a] = *(const f16x8*)(Bs + a * 32 * 128 + woff[t]);
-            if (t == 1) u.store(Bn, (s + 1) * kBK, stoff);
-#pragma unroll
-            for (int a = 0; a < TN; a++)
-#pragma unroll
-                for (int b = 0; b < TM; b++) acc[a][b] = mfma16<XT>(wf[a], xf[b], acc[a][b]);
-            // keep the next step's fragment reads below this step's MFMAs: at
-            // most one step of fragments is live (no spills, whose reloads
-            // would wait on every load in flight)
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int i = 0; i < X_DMAS; i++) dma(xr, Xs, i, cx.s * 128u);
+        advance(cx, nx);
+    };
+    // A stage's loads in issue order: the W_LOADS weight loads of W(g+3),
+    // then the X_DMAS activation DMAs of X(g+2); part p of 4 issues the
+    // slice [p n / 4, (p+1) n / 4) of that list.
+    constexpr int N_OPS = W_LOADS + X_DMAS;
+    auto issue_part = [&](auto PART, rsrc_t wr, uint32_t ws, rsrc_t xr, uint32_t xso, uint8_t* Xs,
+                          WRow<WT, XT>& U) {
+        constexpr int p = decltype(PART)::value;
+        static_for<p * N_OPS / 4, (p + 1) * N_OPS / 4>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            if constexpr (i < W_LOADS)
+                U.template load<i>(wr, wvoff, ws);
+            else
+                dma(xr, Xs, i - W_LOADS, xso);
+        });
     };
 
-    // prologue: activations of stages 0 and 1 in flight to LDS, weights of
-    // stage 0 dequantized into W0, weights of stages 1 and 2 in registers
-    dma_x(0, X0);
-    dma_x(1, X1);
-    wload(wu0, 0);
-    wload(wu1, 1);
-    wu0.store(W0, 0, stoff);
-    wload(wu0, 2);
-    LLMR_STAGE_BARRIER(X_DMAS + 2 * W_LOADS);  // stage-0 activations have landed
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = f32x16{};
 
-    // Stage t = s + i: DMA the activations of stage t+2 into the free slot,
-    // multiply stage t while storing the weights of stage t+1, fetch the
-    // weights of stage t+3; then wait until stage t+1's activations have
-    // landed (only the DMAs and weight fetches issued after them may stay in
-    // flight) and barrier. Unrolled by 6 = lcm(3 activation slots, 2 weight
-    // buffers) so every LDS buffer is a compile-time choice; the stage count
-    // is padded to a multiple of 6 with all-zero stages (their loads start at
-    // the descriptor end) instead of exiting mid-body.
-#define LLMR_PIPE_ITER(i, XC, XD, WC, WN_, U)                 \
-    dma_x(s + (i) + 2, XD);                                   \
-    stage(s + (i), XC, WC, U, WN_);                           \
-    wload(U, s + (i) + 3);                                    \
-    LLMR_STAGE_BARRIER(X_DMAS + 2 * W_LOADS);
-    for (uint32_t s = 0; s < n_stages; s += 6) {
-        LLMR_PIPE_ITER(0, X0, X2, W0, W1, wu1)
-        LLMR_PIPE_ITER(1, X1, X0, W1, W0, wu0)
-        LLMR_PIPE_ITER(2, X2, X1, W0, W1, wu1)
-        LLMR_PIPE_ITER(3, X0, X2, W1, W0, wu0)
-        LLMR_PIPE_ITER(4, X1, X0, W0, W1, wu1)
-        LLMR_PIPE_ITER(5, X2, X1, W1, W0, wu0)
-    }
-#undef LLMR_PIPE_ITER
-    LLMR_WAIT_VMCNT(0);  // no DMA may still be writing this workgroup's LDS when it exits
-
-    const bool vec_ok = (N % 4u) == 0u;
+    auto read_frags = [&](Frags& f, const uint8_t* Xs, const uint8_t* Ws, int t) {
 #pragma unroll
-    for (int a = 0; a < TN; a++)
+        for (int b = 0; b < 4; b++) f.x[b] = *(const f16x8*)(Xs + b * 32 * 128 + xoff[t]);
 #pragma unroll
-        for (int b = 0; b < TM; b++) {
-            const uint32_t m = m0 + wm * WM + b * 32 + l32;
-            if (m >= M) continue;
+        for (int a = 0; a < 4; a++) f.w[a] = *(const f16x8*)(Ws + a * 32 * 128 + woff[t]);
+    };
+    auto mfma_step = [&](const Frags& f) {
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const uint32_t n = n0 + wn * WN + a * 32 + 8 * g + 4 * kh;
-                float* yp = Y + (uint64_t)m * N + n;
-                const f32x4 v = {acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2],
-                                 acc[a][b][4 * g + 3]};
-                if (vec_ok && n + 3 < N) {
-                    *(f32x4*)yp = v;
-                } else {
-                    if (n < N) yp[0] = v.x;
-                    if (n + 1 < N) yp[1] = v.y;
-                    if (n + 2 < N) yp[2] = v.z;
-                    if (n + 3 < N) yp[3] = v.w;
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) acc[a][b] = mfma16<XT>(f.w[a], f.x[b], acc[a][b]);
+    };
+    // Store the accumulators as tile k's results and clear them (N % 4 == 0,
+    // host-checked: a lane's four consecutive features are all in range or
+    // all out).
+    auto store_tile = [&](uint32_t k) {
+        uint32_t tm, tn;
+        map_tile_persist(blockIdx.x + k * G, G, tiles_m, tiles_n, tm, tn);
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint32_t m = tm * 256u + wm * 128u + b * 32u + l32;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const uint32_t n = tn * 256u + wn * 128u + a * 32u + 8u * g + 4u * kh;
+                    if (m < M && n < N)
+                        *(f32x4*)(Y + (uint64_t)m * N + n) =
+                            f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
                 }
+                acc[a][b] = f32x16{};
             }
+    };
+
+    // prologue, issued in the steady state's order (a stage issues the
+    // weights of g+3, then the activations of g+2): W0 | W1 X0 | W2 X1; then
+    // stage 0's weights are dequantized and its activations have landed
+    x_tile(cx, 0);
+    w_tile(cw, 0);
+    x_tile(nx, 1);
+    w_tile(nw, 1);
+    issue_w_all(R0);
+    issue_w_all(R1);
+    issue_x_all(X0);
+    issue_w_all(R2);
+    issue_x_all(X1);
+    LLMR_WAIT_VMCNT(2 * W_LOADS + 2 * X_DMAS);
+    {
+        const auto sc0 = R0.scale(0);
+        R0.template store<0>(W0, sc0, wbase);
+        R0.template store<1>(W0, sc0, wbase);
+        R0.template store<2>(W0, sc0, wbase);
+        R0.template store<3>(W0, sc0, wbase);
+    }
+    LLMR_STAGE_BARRIER(IN_FLIGHT);
+
+    Frags F0, F1;
+
+    // Global stage g: slots X[g%3], W[g%2]; W(g+1) is in register row R[(g+1)%3].
+    //   wait for W(g+1) (issued first two stages ago: the activation DMAs of
+    //   that stage and all of last stage's loads may stay in flight);
+    //   k step A: MFMA (g-1,3), frags (g,0), dequant part 0, loads part 0
+    //   k step B: MFMA (g,0), frags (g,1), dequant part 1, loads part 1
+    //   k step C: MFMA (g,1), frags (g,2), dequant part 2, loads part 2
+    //   k step D: MFMA (g,2), frags (g,3), dequant part 3, loads part 3
+    //   (loads: weights of g+3 -> R[g%3], then activations of g+2 -> X[(g+2)%3]);
+    //   barrier once X(g+1) has landed (issued last in the previous stage:
+    //   this stage's loads may stay in flight) and the LDS writes are done.
+    // Loads run ahead across tile boundaries (each stream walks the
+    // workgroup's tiles on its own), so a tile's first stages are already in
+    // flight when its predecessor's results are stored.
+#define LLMR_PERSIST_STAGE(XC, WC, XD, WNX, RN, RL, NEXT)                                    \
+    {                                                                                       \
+        const rsrc_t wr_ = make_rsrc(cw.base, cw.s < S ? cw.size : 0u);                      \
+        const rsrc_t xr_ = make_rsrc(cx.base, cx.s < S ? cx.size : 0u);                      \
+        const uint32_t ws_ = cw.s, xso_ = cx.s * 128u;                                      \
+        LLMR_WAIT_VMCNT(X_DMAS + IN_FLIGHT);                                                \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        const auto sc_ = RN.scale(NEXT);                                                    \
+        issue_part(std::integral_constant<int, 0>{}, wr_, ws_, xr_, xso_, XD, RL);          \
+        read_frags(F0, XC, WC, 0);                                                          \
+        mfma_step(F1);                                                                      \
+        RN.template store<0>(WNX, sc_, wbase);                                              \
+        LLMR_STEP_SCHEDULE_A;                                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(std::integral_constant<int, 1>{}, wr_, ws_, xr_, xso_, XD, RL);          \
+        read_frags(F1, XC, WC, 1);                                                          \
+        mfma_step(F0);                                                                      \
+        RN.template store<1>(WNX, sc_, wbase);                                              \
+        LLMR_STEP_SCHEDULE;                                                                 \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(std::integral_constant<int, 2>{}, wr_, ws_, xr_, xso_, XD, RL);          \
+        read_frags(F0, XC, WC, 2);                                                          \
+        mfma_step(F1);                                                                      \
+        RN.template store<2>(WNX, sc_, wbase);                                              \
+        LLMR_STEP_SCHEDULE;                                                                 \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(std::integral_constant<int, 3>{}, wr_, ws_, xr_, xso_, XD, RL);          \
+        read_frags(F1, XC, WC, 3);                                                          \
+        mfma_step(F0);                                                                      \
+        RN.template store<3>(WNX, sc_, wbase);                                              \
+        LLMR_STEP_SCHEDULE;                                                                 \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        advance(cw, nw);                                                                    \
+        advance(cx, nx);                                                                    \
+        LLMR_STAGE_BARRIER(IN_FLIGHT);                                                      \
+    }
+    for (uint32_t k = 0; k < n_tiles; k++) {
+        if (k > 0) {  // the load cursors have moved on to tile k: prepare tile k+1
+            x_tile(nx, k + 1);
+            w_tile(nw, k + 1);
         }
+        // the first stage's "previous step" multiplies nothing
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            F1.x[i] = f16x8{};
+            F1.w[i] = f16x8{};
+        }
+        for (uint32_t s0 = 0; s0 < SP; s0 += 6) {
+            LLMR_PERSIST_STAGE(X0, W0, X2, W1, R1, R0, s0 + 1)
+            LLMR_PERSIST_STAGE(X1, W1, X0, W0, R2, R1, s0 + 2)
+            LLMR_PERSIST_STAGE(X2, W0, X1, W1, R0, R2, s0 + 3)
+            LLMR_PERSIST_STAGE(X0, W1, X2, W0, R1, R0, s0 + 4)
+            LLMR_PERSIST_STAGE(X1, W0, X0, W1, R2, R1, s0 + 5)
+            LLMR_PERSIST_STAGE(X2, W1, X1, W0, R0, R2, s0 + 6 == SP ? 0u : s0 + 6)
+        }
+        mfma_step(F1);
+        store_tile(k);
+    }
+#undef LLMR_PERSIST_STAGE
+    LLMR_WAIT_VMCNT(0);  // no DMA may still be writing this workgroup's LDS when it exits
 }
 
 // Generic path for shapes the tiled kernel does not take (Q8_0 with
@@ -789,27 +942,29 @@ hipError_t dispatch_x(const void* w, const void* x, float* y, uint32_t N, uint32
                            st, (const uint8_t*)w, x, y, N, K, M, row_offset);
         return hipGetLastError();
     }
-    // Largest tile that still gives every CU at least ~1.5 workgroups.
     auto wgs = [&](uint32_t bm, uint32_t bn) {
         return (uint64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     };
-    const uint64_t want = (uint64_t)num_cus * 3 / 2;
-    if (wgs(256, 256) >= want) {
-        // the pipelined kernel addresses activations and weight rows through
-        // 32-bit buffer offsets: it needs the whole X and the used weight rows
-        // to span less than 2 GiB
+    // 16-bit activations with at least half the CUs' worth of 256 x 256
+    // tiles: the persistent kernel. It addresses activations and weight rows
+    // through 32-bit buffer offsets (X and the used weight rows must span
+    // less than 2 GiB) and stores four features per lane (N % 4 == 0).
+    if constexpr (XT != kGgmlF32) {
         const uint64_t rb = (WT == kGgmlQ8_0) ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * 144;
         const bool fits31 = (uint64_t)M * K * 2u < (1ull << 31) && (uint64_t)N * rb < (1ull << 31);
-        if constexpr (XT == kGgmlF32) {
-            return launch_tiled<WT, XT, 256, 256>(w, x, y, N, K, M, row_offset, st);
-        } else {
-            if (!fits31) return launch_tiled<WT, XT, 256, 256>(w, x, y, N, K, M, row_offset, st);
+        const uint64_t tiles = wgs(256, 256);
+        if (fits31 && N % 4 == 0 && 2 * tiles >= (uint64_t)num_cus) {
             const uint32_t tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
-            hipLaunchKernelGGL((gemm_q_pipe<WT, XT>), dim3(tiles_m * tiles_n), dim3(512), 0, st,
+            const uint32_t grid = (uint32_t)min(tiles, (uint64_t)num_cus);
+            hipLaunchKernelGGL((gemm_q_persist<WT, XT>), dim3(grid), dim3(256), 0, st,
                                (const uint8_t*)w, x, y, N, K, M, row_offset, tiles_m, tiles_n);
             return hipGetLastError();
         }
     }
+    // Otherwise the largest 4-wave tile that still gives every CU at least
+    // ~1.5 workgroups.
+    const uint64_t want = (uint64_t)num_cus * 3 / 2;
+    if (wgs(256, 256) >= want) return launch_tiled<WT, XT, 256, 256>(w, x, y, N, K, M, row_offset, st);
     if (wgs(128, 128) >= want) return launch_tiled<WT, XT, 128, 128>(w, x, y, N, K, M, row_offset, st);
     return launch_tiled<WT, XT, 64, 64>(w, x, y, N, K, M, row_offset, st);
 }

@@ -109,6 +109,44 @@ def test_zero_and_nonfinite_scales(orc, dev):
     assert rel_l2(y[:, mask], ref[:, mask]) <= TOL
 
 
+# Shapes with at least 128 tiles of 256 x 256 take the persistent kernel
+# (16-bit activations, N % 4 == 0): ragged M and N, more tiles than CUs (two
+# per workgroup, some workgroups splitting their first tile in two K pieces),
+# stage counts that are not a multiple of 6 (zero-padded stages), row_offset
+# into a fused weight, both activation types.
+PERSIST_CASES = [
+    # (wtype, M, N, K, xtype, row_offset)
+    (12, 4100, 4100, 768, 30, 0),
+    (8, 4100, 4100, 768, 30, 16),
+    (8, 4100, 4100, 320, 1, 0),
+    (12, 2000, 4352, 1024, 1, 256),
+    (8, 2560, 3332, 640, 1, 4),
+]
+
+
+@pytest.mark.parametrize("wtype,M,N,K,xtype,row_offset", PERSIST_CASES)
+def test_persistent_kernel_sampled_rows(orc, dev, wtype, M, N, K, xtype, row_offset):
+    import torch
+    from llmr_amd import gguf, ops, synth
+    blk = gguf.quantize(synth.normal(13, 2, (N + row_offset + 3) * K, 0.02), wtype)
+    x = synth.normal(13, 1, M * K).reshape(M, K)
+    w = torch.from_numpy(blk).to(dev)
+    xt = _torch_x(x, xtype, dev)
+    y = ops.batch_matmul(w, wtype, xt, N, row_offset=row_offset)
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, 31, 32, 255, 256, 511, 1024 + 7, M // 2, M - 257, M - 256, M - 2, M - 1],
+                    np.uint32)
+    ref = orc.batch_matmul(blk, wtype, _x_as_f32(xt), N, K, M, row_offset, rows=rows)
+    got = y[torch.from_numpy(rows.astype(np.int64)).to(dev)].cpu().numpy()
+    err = rel_l2(got, ref)
+    print(f"persistent wtype={wtype} M={M} N={N} K={K} xtype={xtype}: sampled rel_l2={err:.3e}")
+    assert np.all(np.isfinite(got))
+    assert err <= TOL
+    # every column block of every sampled row is right (no tile left unwritten)
+    for c0 in range(0, N, 256):
+        assert rel_l2(got[:, c0:c0 + 256], ref[:, c0:c0 + 256]) <= 2 * TOL
+
+
 @pytest.mark.parametrize("name", ["flux_linear1", "flux_linear2", "zimage_qkv"])
 def test_full_size_sampled_rows(orc, dev, name):
     """Full-size launches; the oracle checks a sample of tokens (every column)."""
