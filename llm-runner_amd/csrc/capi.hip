@@ -232,6 +232,9 @@ int llmr_flash_attention(llmr_context* ctx, const void* q, const void* k, const 
         return fail(LLMR_ERR_INVALID_ARG, "q/k/v/out pointers must be 16-byte aligned");
     if ((uint64_t)n_heads * ((seq_len + 127) / 128) > 0x7fffffffull)
         return fail(LLMR_ERR_INVALID_ARG, "grid too large");
+    // one head's [S, 128] slab is addressed with 32-bit byte offsets
+    if ((uint64_t)seq_len * 128u * (xtype == 0 ? 4u : 2u) > 0xffffffffull)
+        return fail(LLMR_ERR_INVALID_ARG, "seq_len %u too large: one head must span < 4 GiB", seq_len);
     hipError_t e = llmr::launch_flash_attention(q, k, v, xtype, out, n_heads, seq_len, scale, ctx->cur);
     if (e != hipSuccess) return fail(LLMR_ERR_HIP, "flash_attention launch: %s", hipGetErrorString(e));
     return ok();

@@ -61,12 +61,6 @@ __device__ __forceinline__ uint32_t vpos(uint32_t r) {
     return (r & 3u) | (((r >> 3) & 1u) << 2) | (((r >> 2) & 1u) << 3);
 }
 
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint64_t bytes) {
-    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
-}
 
 // 8 consecutive elements of a row of one head, loaded through the head's
 // buffer descriptor (rows past the sequence end read as zero), as fp16.
@@ -303,15 +297,320 @@ flash_attn_fwd(const void* __restrict__ Q, const void* __restrict__ K, const voi
     }
 }
 
+// ---------------------------------------------------------------------------
+// fp16 fast path: 64 queries per wave, one wave per SIMD.
+//
+// A workgroup of 4 waves takes 256 queries of one head; each wave owns 64
+// (two 32-query blocks). Every K or V fragment read from LDS then feeds two
+// MFMAs (one per query block), halving the LDS bytes per MFMA of the
+// 32-query design. K and V tiles of 64 keys go HBM -> LDS by buffer DMA
+// (no staging registers, no VALU) into 3-slot rings, two tiles (K) and one
+// tile (V) ahead of use; V stays row-major in LDS and the V^T operand is
+// read with the transposing ds_read_b64_tr_b16 (lane i of a 16-lane group
+// gets V[key0 + e][d0 + i], e = 0..3).
+//
+// Per tile t a wave: DMAs K(t+3) and V(t+2); exponentiates S(t) one 32-key
+// block at a time, refilling the block's registers with S(t+1) = K(t+1) Q^T
+// (the VALU work co-issues with the MFMAs);
+// accumulates O^T += V(t)^T P(t)^T while taking the row max of S(t+1);
+// rescales O if a running max grew (lazily, as in flash_attn_fwd); then one
+// barrier. The loop is unrolled by 3 (the LDS slots) over a tile count
+// padded to a multiple of 3; the bodies from the one computing the scores
+// of the first tile with keys past the sequence end run a copy that masks
+// them (padding tiles are fully masked).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kBQ64 = 256;            // queries per workgroup
+constexpr uint32_t kTile64 = 64u * 256u;   // one K or V tile: 64 keys x 128 fp16
+
+// LDS rows are 256 bytes (16 chunks of 8 fp16). K: chunk c of key r at
+// c ^ (r & 15) (a 16-lane fragment read touches 16 distinct bank quads).
+// V: chunk c of key r at c ^ vswz(r); a transposing read touches 8
+// consecutive keys x 4 chunks, and vswz spreads those 32 cells evenly over
+// the 16 chunk positions (two each: the minimum for 512 bytes).
+__device__ __forceinline__ uint32_t kswz(uint32_t r) { return r & 15u; }
+__device__ __forceinline__ uint32_t vswz(uint32_t r) { return ((r & 3u) << 2) | ((r >> 2) & 1u); }
+
+__device__ __forceinline__ float xhalf_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(256, 1)
+flash_attn_fwd64(const _Float16* __restrict__ Q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
+                 float* __restrict__ O, uint32_t S, uint32_t H, float scale_log2, uint32_t n_qb) {
+    __shared__ __attribute__((aligned(16))) uint8_t K0[kTile64];
+    __shared__ __attribute__((aligned(16))) uint8_t K1[kTile64];
+    __shared__ __attribute__((aligned(16))) uint8_t K2[kTile64];
+    __shared__ __attribute__((aligned(16))) uint8_t V0[kTile64];
+    __shared__ __attribute__((aligned(16))) uint8_t V1[kTile64];
+    __shared__ __attribute__((aligned(16))) uint8_t V2[kTile64];
+    constexpr uint32_t ROW = kD * 2u;  // bytes per token row of one head
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t l32 = lane & 31u, kh = lane >> 5;
+
+    // workgroup -> (head, query block), all blocks of a head on one XCD
+    const uint32_t total = n_qb * H;
+    uint32_t L = blockIdx.x;
+    if (total % 8u == 0) L = (L % 8u) * (total / 8u) + L / 8u;
+    const uint32_t head = L / n_qb, qb = L % n_qb;
+    const uint64_t head_bytes = (uint64_t)S * ROW;
+    const uint8_t* Qh = (const uint8_t*)Q + head * head_bytes;
+    const uint8_t* Kh = (const uint8_t*)K + head * head_bytes;
+    const uint8_t* Vh = (const uint8_t*)V + head * head_bytes;
+    const uint32_t q0 = qb * kBQ64 + wave * 64u;  // first query of this wave
+
+    // Q fragments (B operand of S^T = K Q^T) of the two query blocks:
+    // d = 32c + 16kh + 8st + 0..7 of query q0 + 32b + l32
+    f16x8 qf[2][4][2];
+    {
+        const rsrc_t qr = make_rsrc(Qh, head_bytes);
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int st = 0; st < 2; st++)
+                    qf[b][c][st] = __builtin_bit_cast(
+                        f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                   qr, (q0 + 32u * b + l32) * ROW + (32u * c + 16u * kh + 8u * st) * 2u, 0, 0));
+    }
+
+    // DMA lane offsets: instruction i of wave w fills keys 16w + 4i + lane/16
+    // of a slot, lane l landing in physical chunk l % 16 of its key
+    uint32_t kvo[4], vvo[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t r = 16u * wave + 4u * i + (lane >> 4), p = lane & 15u;
+        kvo[i] = r * ROW + ((p ^ kswz(r)) << 4);
+        vvo[i] = r * ROW + ((p ^ vswz(r)) << 4);
+    }
+    // tile t's keys through a descriptor ending at the sequence end (keys
+    // past it, and tiles past the last, read as zero)
+    auto dma = [&](const uint8_t* base, const uint32_t (&vo)[4], uint32_t t, uint8_t* slot) {
+        const uint32_t k0 = t * 64u;
+        // S * ROW < 2^32 (checked by the host); readfirstlane keeps the
+        // descriptor in scalar registers
+        const uint32_t bytes = __builtin_amdgcn_readfirstlane(k0 < S ? (S - k0) * ROW : 0u);
+        const rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base) + (uint64_t)k0 * ROW,
+                                                           (short)0, (int)bytes, 0x00020000);
+        uint8_t* dst = slot + wave * (16u * ROW);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024u * i), 16, vo[i], 0, 0, 0);
+    };
+
+    // K fragment offsets (A operand of S^T): key 32kb + l32 (+ 32kb*ROW at use),
+    // chunk 4c + 2kh + st
+    uint32_t kfo[4][2];
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+#pragma unroll
+        for (int st = 0; st < 2; st++) kfo[c][st] = l32 * ROW + (((4u * c + 2u * kh + st) ^ kswz(l32)) << 4);
+    // V^T fragment offsets (transposing reads): lane (group g, index j)
+    // addresses key R + 4(g/2) + j/4 (R = 32kb + 16c + 8h at use), dims
+    // 32dt + 16(g%2) + 4(j%4) .. +3
+    uint32_t vto[4];
+    {
+        const uint32_t g = lane >> 4, j = lane & 15u;
+        const uint32_t kr = 4u * (g >> 1) + (j >> 2);
+        const uint32_t x = 2u * (g & 1u) + ((j & 3u) >> 1), half = j & 1u;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) vto[dt] = kr * ROW + (((4u * dt + x) ^ vswz(kr)) << 4) + 8u * half;
+    }
+
+    // S^T of key block kb (32 keys) of the tile in Ks, both query blocks
+    auto qk = [&](const uint8_t* Ks, int kb, f32x16 (&s)[2][2]) {
+#pragma unroll
+        for (int b = 0; b < 2; b++) s[kb][b] = f32x16{};
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int st = 0; st < 2; st++) {
+                const f16x8 a = *(const f16x8*)(Ks + 32u * kb * ROW + kfo[c][st]);
+#pragma unroll
+                for (int b = 0; b < 2; b++)
+                    s[kb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[b][c][st], s[kb][b], 0, 0, 0);
+            }
+    };
+
+    f32x16 o[4][2];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) o[dt][b] = f32x16{};
+    float m_ref[2] = {-1.0e30f, -1.0e30f};  // max used by the exponentials (log2 domain)
+    float l_i[2] = {0.0f, 0.0f};             // this lane's partial row sums
+
+    // keys >= S of tile t to -inf (masked copy of the loop only)
+    auto mask = [&](f32x16 (&s)[2][2], uint32_t t) {
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t key = t * 64u + 32u * kb + 8u * (i >> 2) + 4u * kh + (i & 3);
+#pragma unroll
+                for (int b = 0; b < 2; b++) s[kb][b][i] = key < S ? s[kb][b][i] : -INFINITY;
+            }
+    };
+    // row max of a score tile (log2 domain), both halves of the wave combined
+    auto rowmax = [&](const f32x16 (&s)[2][2], float (&mx)[2]) {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            float m = s[0][b][0];
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) m = fmaxf(m, s[kb][b][i]);
+            mx[b] = xhalf_max(m) * scale_log2;
+        }
+    };
+    // raise the running max where a tile exceeds it by more than 2^8
+    auto rescale = [&](const float (&mx)[2]) {
+        if (__builtin_amdgcn_ballot_w64(mx[0] > m_ref[0] + 8.0f || mx[1] > m_ref[1] + 8.0f) != 0) {
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const float m2 = fmaxf(m_ref[b], mx[b]);
+                const float alpha = __builtin_amdgcn_exp2f(m_ref[b] - m2);
+                m_ref[b] = m2;
+                l_i[b] *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++) o[dt][b] *= alpha;
+            }
+        }
+    };
+    // P = exp2(S scale - m_ref) of key block kb as fp16 B operands [b][kb][c]; row sums
+    auto softmax_exp = [&](const f32x16 (&s)[2][2], int kb, f16x8 (&p)[2][2][2]) {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            float rs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][b][i], scale_log2, -m_ref[b]));
+                rs += e;
+                p[b][kb][i >> 3][i & 7] = (_Float16)e;
+            }
+            l_i[b] += rs;
+        }
+    };
+    // O^T += V^T P^T for the tile in Vs
+    auto pv = [&](const uint8_t* Vs, const f16x8 (&p)[2][2][2]) {
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int c = 0; c < 2; c++) {
+                    const uint32_t R = 32u * kb + 16u * c;
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)(Vs + R * ROW + vto[dt]));
+                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)(Vs + (R + 8u) * ROW + vto[dt]));
+                    const f16x8 a = __builtin_bit_cast(
+                        f16x8, (short __attribute__((ext_vector_type(8)))){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
+#pragma unroll
+                    for (int b = 0; b < 2; b++)
+                        o[dt][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, p[b][kb][c], o[dt][b], 0, 0, 0);
+                }
+    };
+
+    const uint32_t n_tiles = (S + 63u) / 64u;
+    const uint32_t T = (n_tiles + 2u) / 3u * 3u;  // padded: whole unrolled bodies
+
+    // prologue: K0 V0 K1 V1 K2 in flight; S(0) and its max
+    dma(Kh, kvo, 0, K0);
+    dma(Vh, vvo, 0, V0);
+    dma(Kh, kvo, 1, K1);
+    dma(Vh, vvo, 1, V1);
+    dma(Kh, kvo, 2, K2);
+    LLMR_STAGE_BARRIER(16);  // K(0) has landed
+    f32x16 sc[2][2];
+    float mx[2];
+    qk(K0, 0, sc);
+    qk(K0, 1, sc);
+    if (S < 64u) mask(sc, 0);
+    rowmax(sc, mx);
+    rescale(mx);
+    LLMR_STAGE_BARRIER(8);  // K(1), V(0) have landed; every wave is done with K(0)
+
+    // tile t: the scores of tile t (in sc) are exponentiated one key block
+    // at a time and that block's registers refilled with tile t+1's scores
+    // (K slot KQ) - the exponentials of block 1 overlap the QK MFMAs of
+    // block 0; then O^T += V(t)^T P(t)^T (V slot VP) while the new scores'
+    // row max is taken; DMAs of K(t+3) -> KD and V(t+2) -> VD
+#define LLMR_FA_TILE(t, KQ, VP, KD, VD, MASKED)                                \
+    {                                                                         \
+        dma(Kh, kvo, (t) + 3u, KD);                                           \
+        dma(Vh, vvo, (t) + 2u, VD);                                           \
+        f16x8 p[2][2][2];                                                     \
+        softmax_exp(sc, 0, p);                                                \
+        qk(KQ, 0, sc);                                                        \
+        softmax_exp(sc, 1, p);                                                \
+        qk(KQ, 1, sc);                                                        \
+        if (MASKED) mask(sc, (t) + 1u);                                       \
+        pv(VP, p);                                                            \
+        rowmax(sc, mx);                                                       \
+        rescale(mx);                                                          \
+        LLMR_STAGE_BARRIER(8);                                                \
+    }
+#define LLMR_FA_BODY(t0, MASKED)                                              \
+    {                                                                         \
+        LLMR_FA_TILE((t0) + 0u, K1, V0, K0, V2, MASKED)                       \
+        LLMR_FA_TILE((t0) + 1u, K2, V1, K1, V0, MASKED)                       \
+        LLMR_FA_TILE((t0) + 2u, K0, V2, K2, V1, MASKED)                       \
+    }
+    // the first tile holding keys past S, and the first body whose QKs
+    // reach it (tile u's scores are computed in iteration u-1)
+    const uint32_t u_m = (S % 64u) != 0u ? n_tiles - 1u : n_tiles;
+    const uint32_t t_m = u_m == 0u ? 0u : (u_m - 1u) / 3u * 3u;
+    uint32_t t0 = 0;
+    for (; t0 < t_m; t0 += 3u) LLMR_FA_BODY(t0, false)
+    for (; t0 < T; t0 += 3u) LLMR_FA_BODY(t0, true)
+#undef LLMR_FA_BODY
+#undef LLMR_FA_TILE
+    LLMR_WAIT_VMCNT(0);  // no DMA may still be writing LDS when the wave exits
+
+    // O = O^T / l, rows of this wave's queries
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        const float inv_l = 1.0f / xhalf_sum(l_i[b]);
+        const uint32_t q = q0 + 32u * b + l32;
+        if (q < S) {
+            float* orow = O + (uint64_t)q * H * kD + (uint64_t)head * kD;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const uint32_t d = 32u * dt + 8u * g + 4u * kh;
+                    *(f32x4*)(orow + d) = f32x4{o[dt][b][4 * g] * inv_l, o[dt][b][4 * g + 1] * inv_l,
+                                                 o[dt][b][4 * g + 2] * inv_l, o[dt][b][4 * g + 3] * inv_l};
+                }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_flash_attention(const void* q, const void* k, const void* v, uint32_t xtype,
                                   float* o, uint32_t n_heads, uint32_t seq_len, float scale,
                                   hipStream_t st) {
     if (seq_len == 0 || n_heads == 0) return hipSuccess;
+    const float scale_log2 = scale * 1.4426950408889634f;
+    if (xtype == kGgmlF16) {
+        const uint32_t n_qb64 = (seq_len + kBQ64 - 1) / kBQ64;
+        hipLaunchKernelGGL(flash_attn_fwd64, dim3(n_qb64 * n_heads), dim3(256), 0, st, (const _Float16*)q,
+                           (const _Float16*)k, (const _Float16*)v, o, seq_len, n_heads, scale_log2, n_qb64);
+        return hipGetLastError();
+    }
     const uint32_t n_qb = (seq_len + kBQ - 1) / kBQ;
     const dim3 grid(n_qb * n_heads);
-    const float scale_log2 = scale * 1.4426950408889634f;
     switch (xtype) {
         case kGgmlF16:
             hipLaunchKernelGGL(flash_attn_fwd<kGgmlF16>, grid, dim3(256), 0, st, q, k, v, o, seq_len, n_heads,

@@ -347,37 +347,12 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
 // Buffer-resource helpers for the persistent kernel below.
 // ---------------------------------------------------------------------------
 
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint64_t bytes) {
-    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
-}
 __device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 __device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
 }
-// s_waitcnt vmcnt(n) leaving the LDS and export counters unconstrained
-// (gfx9 encoding: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14).
-#define LLMR_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
-
-// Workgroup barrier for a pipelined loop: this wave's LDS writes are done
-// (lgkmcnt(0)) and at most `n` of its global loads/DMAs are still in flight,
-// then s_barrier. __syncthreads() would instead wait for every outstanding
-// global load (vmcnt(0)), i.e. for the prefetches issued for later stages.
-// The empty asm statements keep the compiler from moving memory operations
-// across the barrier.
-#define LLMR_STAGE_BARRIER(n)                                                              \
-    do {                                                                                   \
-        asm volatile("" ::: "memory");                                                     \
-        __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (0 << 8) | (((n) >> 4) << 14)); \
-        __builtin_amdgcn_s_barrier();                                                      \
-        asm volatile("" ::: "memory");                                                     \
-    } while (0)
-
 // Eight Q8_0 quants (two dwords) -> one 16-byte chunk of fp16 operands RN16(d*q).
 __device__ __forceinline__ u32x4 q8x8_f16(uint32_t q0, uint32_t q1, f16x2 d2) {
     const f16x4 lo = q8x4_to_f16(q0, d2), hi = q8x4_to_f16(q1, d2);

@@ -20,6 +20,34 @@ typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr uint32_t kGgmlF32 = 0, kGgmlF16 = 1, kGgmlQ8_0 = 8, kGgmlQ4K = 12, kGgmlBF16 = 30;
 
+// Buffer resource over [base, base + bytes): loads past the end return zero
+// and stores past it are dropped (raw buffer, dword format word 3).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+// s_waitcnt vmcnt(n) leaving the LDS and export counters unconstrained
+// (gfx9 encoding: vmcnt[3:0] | expcnt << 4 | lgkmcnt << 8 | vmcnt[5:4] << 14).
+#define LLMR_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+
+// Workgroup barrier for a pipelined loop: this wave's LDS accesses are done
+// (lgkmcnt(0)) and at most `n` of its global loads/DMAs are still in flight,
+// then s_barrier. __syncthreads() would instead wait for every outstanding
+// global load (vmcnt(0)), i.e. for the prefetches issued for later stages.
+// The empty asm statements keep the compiler from moving memory operations
+// across the barrier.
+#define LLMR_STAGE_BARRIER(n)                                                              \
+    do {                                                                                   \
+        asm volatile("" ::: "memory");                                                     \
+        __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (0 << 8) | (((n) >> 4) << 14)); \
+        __builtin_amdgcn_s_barrier();                                                      \
+        asm volatile("" ::: "memory");                                                     \
+    } while (0)
+
 // fp16 bit pattern -> f32 exactly as unpack_f16 (llm.slang:235-251) and
 // cpu_f16_to_f32 (tensor.c3:130-147): exponent 31 (Inf and every NaN) -> +-Inf;
 // everything else is the exact value (the hardware widening is exact for

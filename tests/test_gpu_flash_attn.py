@@ -29,8 +29,13 @@ def _fa(dev, q, k, v, xtype, scale=None):
     return o.cpu().numpy(), back
 
 
+# f16 inputs take the 64-query-per-wave kernel: sequence lengths cover a
+# partial last tile at each position relative to its 3-tile unroll (the
+# masked loop copy starting in the first, second or third body position),
+# S < 64, S = 64, and a whole-tile end (S = 4352: one padding tile).
 @pytest.mark.parametrize("H,S,xtype", [(2, 200, 1), (1, 64, 1), (1, 1, 1), (3, 63, 0), (2, 129, 30),
-                                       (1, 257, 0), (4, 512, 1), (2, 1000, 30)])
+                                       (1, 257, 0), (4, 512, 1), (2, 1000, 30), (1, 65, 1), (2, 257, 1),
+                                       (1, 383, 1), (3, 1000, 1), (2, 1089, 1), (1, 4352, 1)])
 def test_fa_parity_small(orc, dev, H, S, xtype):
     from llmr_amd import synth
     n = H * S * 128
@@ -41,6 +46,24 @@ def test_fa_parity_small(orc, dev, H, S, xtype):
     ref = orc.flash_attention(qr, kr, vr, 1.0 / math.sqrt(128))
     err = rel_l2(o, ref)
     print(f"H={H} S={S} xtype={xtype}: rel_l2={err:.3e}")
+    assert np.all(np.isfinite(o))
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("xtype", [1, 0])
+def test_fa_large_scores(orc, dev, xtype):
+    """Scores of magnitude ~100 (scaled Q and K): the running max is raised
+    many times along the keys, exercising the lazy rescaling of O and l."""
+    from llmr_amd import synth
+    H, S = 2, 700
+    n = H * S * 128
+    q = synth.normal(6, 3, n).reshape(H, S, 128) * 3
+    k = synth.normal(6, 4, n).reshape(H, S, 128) * 3
+    v = synth.normal(6, 5, n).reshape(H, S, 128)
+    o, (qr, kr, vr) = _fa(dev, q, k, v, xtype)
+    ref = orc.flash_attention(qr, kr, vr, 1.0 / math.sqrt(128))
+    err = rel_l2(o, ref)
+    print(f"large scores xtype={xtype}: rel_l2={err:.3e}")
     assert np.all(np.isfinite(o))
     assert err <= TOL
 
