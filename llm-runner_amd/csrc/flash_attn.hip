@@ -304,20 +304,21 @@ flash_attn_fwd(const void* __restrict__ Q, const void* __restrict__ K, const voi
 // (two 32-query blocks). Every K or V fragment read from LDS then feeds two
 // MFMAs (one per query block), halving the LDS bytes per MFMA of the
 // 32-query design. K and V tiles of 64 keys go HBM -> LDS by buffer DMA
-// (no staging registers, no VALU) into 3-slot rings, two tiles (K) and one
-// tile (V) ahead of use; V stays row-major in LDS and the V^T operand is
-// read with the transposing ds_read_b64_tr_b16 (lane i of a 16-lane group
-// gets V[key0 + e][d0 + i], e = 0..3).
+// (no staging registers, no VALU) into 3-slot rings, K three tiles and V two
+// tiles ahead of use; V stays row-major in LDS and the V^T operand is read
+// with the transposing ds_read_b64_tr_b16 (lane i of a 16-lane group gets
+// V[key0 + e][d0 + i], e = 0..3).
 //
-// Per tile t a wave: DMAs K(t+3) and V(t+2); exponentiates S(t) one 32-key
-// block at a time, refilling the block's registers with S(t+1) = K(t+1) Q^T
-// (the VALU work co-issues with the MFMAs);
-// accumulates O^T += V(t)^T P(t)^T while taking the row max of S(t+1);
-// rescales O if a running max grew (lazily, as in flash_attn_fwd); then one
-// barrier. The loop is unrolled by 3 (the LDS slots) over a tile count
-// padded to a multiple of 3; the bodies from the one computing the scores
-// of the first tile with keys past the sequence end run a copy that masks
-// them (padding tiles are fully masked).
+// Scores live in two register sets used alternately, so the MFMAs of
+// S(t+1) = K(t+1) Q^T do not wait for the exponentials of S(t). Per tile t
+// a wave: DMAs K(t+3) and V(t+2); computes S(t+1) on the matrix cores while
+// the vector ALU exponentiates S(t) into the fp16 P(t); accumulates
+// O^T += V(t)^T P(t)^T while taking the row max of S(t+1); rescales O if a
+// running max grew by more than 2^8 (lazily, as in flash_attn_fwd); then one
+// barrier. The main loop is unrolled by 2 (the score sets) and walks the
+// LDS rings with scalar slot offsets. It runs while S(t+1) has no keys past
+// the sequence end; one masked iteration follows when the last tile is
+// partial, then a final iteration that only exponentiates and accumulates.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kBQ64 = 256;            // queries per workgroup
 constexpr uint32_t kTile64 = 64u * 256u;   // one K or V tile: 64 keys x 128 fp16
@@ -341,15 +342,12 @@ __device__ __forceinline__ float xhalf_sum(float x) {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
+
 __global__ void __launch_bounds__(256, 1)
 flash_attn_fwd64(const _Float16* __restrict__ Q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
                  float* __restrict__ O, uint32_t S, uint32_t H, float scale_log2, uint32_t n_qb) {
-    __shared__ __attribute__((aligned(16))) uint8_t K0[kTile64];
-    __shared__ __attribute__((aligned(16))) uint8_t K1[kTile64];
-    __shared__ __attribute__((aligned(16))) uint8_t K2[kTile64];
-    __shared__ __attribute__((aligned(16))) uint8_t V0[kTile64];
-    __shared__ __attribute__((aligned(16))) uint8_t V1[kTile64];
-    __shared__ __attribute__((aligned(16))) uint8_t V2[kTile64];
+    // K ring in slots 0..2, V ring in slots 3..5
+    __shared__ __attribute__((aligned(16))) uint8_t lds[6u * kTile64];
     constexpr uint32_t ROW = kD * 2u;  // bytes per token row of one head
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -393,15 +391,15 @@ flash_attn_fwd64(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
         vvo[i] = r * ROW + ((p ^ vswz(r)) << 4);
     }
     // tile t's keys through a descriptor ending at the sequence end (keys
-    // past it, and tiles past the last, read as zero)
-    auto dma = [&](const uint8_t* base, const uint32_t (&vo)[4], uint32_t t, uint8_t* slot) {
+    // past it, and tiles past the last, read as zero) into LDS slot `slot`
+    auto dma = [&](const uint8_t* base, const uint32_t (&vo)[4], uint32_t t, uint32_t slot) {
         const uint32_t k0 = t * 64u;
         // S * ROW < 2^32 (checked by the host); readfirstlane keeps the
         // descriptor in scalar registers
         const uint32_t bytes = __builtin_amdgcn_readfirstlane(k0 < S ? (S - k0) * ROW : 0u);
         const rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base) + (uint64_t)k0 * ROW,
                                                            (short)0, (int)bytes, 0x00020000);
-        uint8_t* dst = slot + wave * (16u * ROW);
+        uint8_t* dst = lds + slot * kTile64 + wave * (16u * ROW);
 #pragma unroll
         for (int i = 0; i < 4; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024u * i), 16, vo[i], 0, 0, 0);
@@ -426,21 +424,6 @@ flash_attn_fwd64(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
         for (int dt = 0; dt < 4; dt++) vto[dt] = kr * ROW + (((4u * dt + x) ^ vswz(kr)) << 4) + 8u * half;
     }
 
-    // S^T of key block kb (32 keys) of the tile in Ks, both query blocks
-    auto qk = [&](const uint8_t* Ks, int kb, f32x16 (&s)[2][2]) {
-#pragma unroll
-        for (int b = 0; b < 2; b++) s[kb][b] = f32x16{};
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-#pragma unroll
-            for (int st = 0; st < 2; st++) {
-                const f16x8 a = *(const f16x8*)(Ks + 32u * kb * ROW + kfo[c][st]);
-#pragma unroll
-                for (int b = 0; b < 2; b++)
-                    s[kb][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[b][c][st], s[kb][b], 0, 0, 0);
-            }
-    };
-
     f32x16 o[4][2];
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
@@ -449,26 +432,59 @@ flash_attn_fwd64(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
     float m_ref[2] = {-1.0e30f, -1.0e30f};  // max used by the exponentials (log2 domain)
     float l_i[2] = {0.0f, 0.0f};             // this lane's partial row sums
 
-    // keys >= S of tile t to -inf (masked copy of the loop only)
-    auto mask = [&](f32x16 (&s)[2][2], uint32_t t) {
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const uint32_t key = t * 64u + 32u * kb + 8u * (i >> 2) + 4u * kh + (i & 3);
-#pragma unroll
-                for (int b = 0; b < 2; b++) s[kb][b][i] = key < S ? s[kb][b][i] : -INFINITY;
-            }
+    // Score halves: the scores of one 32-key block of a tile for both query
+    // blocks; h[b] at lane l holds key 32kb + 8(i/4) + 4kh + i%4 of the
+    // tile (kb = the block), query 32b + l32.
+    //
+    // K fragment f = 0..15 of the tile at Ks: key block f/8, d chunk
+    // (c, st) = ((f%8)/2, f%2)
+    auto kfrag = [&](const uint8_t* Ks, int f) -> f16x8 {
+        return *(const f16x8*)(Ks + 32u * (uint32_t)(f / 8) * ROW + kfo[(f % 8) / 2][f % 2]);
     };
-    // row max of a score tile (log2 domain), both halves of the wave combined
-    auto rowmax = [&](const f32x16 (&s)[2][2], float (&mx)[2]) {
+    // V^T fragment f = 0..15 of the tile at Vs: key block kb = f/8, keys
+    // 32kb + 16c + {4kh..4kh+3, 8+4kh..8+4kh+3} with c = (f%8)/4, dims
+    // 32dt + l32 with dt = f%4
+    auto vfrag = [&](const uint8_t* Vs, int f) -> f16x8 {
+        const uint32_t R = 32u * (uint32_t)(f / 8) + 16u * (uint32_t)((f % 8) / 4);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(Vs + R * ROW + vto[f % 4]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(Vs + (R + 8u) * ROW + vto[f % 4]));
+        return __builtin_bit_cast(
+            f16x8, (short __attribute__((ext_vector_type(8)))){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
+    };
+    // S of the tile at Ks into the halves (h0: keys 0..31, h1: keys 32..63)
+    auto qk_all = [&](const uint8_t* Ks, f32x16 (&h0)[2], f32x16 (&h1)[2]) {
+        static_for<0, 16>([&](auto F) {
+            constexpr int f = F, kb = f / 8, c = (f % 8) / 2, st = f % 2;
+            const f16x8 a = kfrag(Ks, f);
+            static_for<0, 2>([&](auto B) {
+                constexpr int b = B;
+                f32x16& s = kb == 0 ? h0[b] : h1[b];
+                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[b][c][st], (c == 0 && st == 0) ? f32x16{} : s,
+                                                           0, 0, 0);
+            });
+        });
+    };
+    // keys >= S of tile t (halves h0, h1) to -inf
+    auto mask = [&](f32x16 (&h0)[2], f32x16 (&h1)[2], uint32_t t) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t key = t * 64u + 8u * (i >> 2) + 4u * kh + (i & 3);
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                h0[b][i] = key < S ? h0[b][i] : -INFINITY;
+                h1[b][i] = key + 32u < S ? h1[b][i] : -INFINITY;
+            }
+        }
+    };
+    // row max of a tile (log2 domain), both halves of the wave combined
+    auto rowmax = [&](const f32x16 (&h0)[2], const f32x16 (&h1)[2], float (&mx)[2]) {
 #pragma unroll
         for (int b = 0; b < 2; b++) {
-            float m = s[0][b][0];
+            float m = h0[b][0];
 #pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) m = fmaxf(m, s[kb][b][i]);
+            for (int i = 0; i < 16; i++) m = fmaxf(fmaxf(m, h0[b][i]), h1[b][i]);
             mx[b] = xhalf_max(m) * scale_log2;
         }
     };
@@ -486,95 +502,143 @@ flash_attn_fwd64(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
             }
         }
     };
-    // P = exp2(S scale - m_ref) of key block kb as fp16 B operands [b][kb][c]; row sums
-    auto softmax_exp = [&](const f32x16 (&s)[2][2], int kb, f16x8 (&p)[2][2][2]) {
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            float rs = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][b][i], scale_log2, -m_ref[b]));
-                rs += e;
-                p[b][kb][i >> 3][i & 7] = (_Float16)e;
-            }
-            l_i[b] += rs;
-        }
+    // P = exp2(S scale - m_ref) of score pair `item` (query block item/8,
+    // keys 2(item%8), +1) of half h (key block kb) into the fp16 operand p
+    // (p[b][kb][c] holds keys 16c..16c+15 of the block); row sums into rs
+    auto exp_pair = [&](const f32x16 (&h)[2], int kb, int item, f16x8 (&p)[2][2][2], float (&rs)[2]) {
+        const int b = item / 8, i = 2 * (item % 8);
+        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(h[b][i], scale_log2, -m_ref[b]));
+        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(h[b][i + 1], scale_log2, -m_ref[b]));
+        rs[b] += e0 + e1;
+        p[b][kb][i >> 3][i & 7] = (_Float16)e0;
+        p[b][kb][i >> 3][(i & 7) + 1] = (_Float16)e1;
     };
-    // O^T += V^T P^T for the tile in Vs
-    auto pv = [&](const uint8_t* Vs, const f16x8 (&p)[2][2][2]) {
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int c = 0; c < 2; c++) {
-                    const uint32_t R = 32u * kb + 16u * c;
-                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4*)(Vs + R * ROW + vto[dt]));
-                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4*)(Vs + (R + 8u) * ROW + vto[dt]));
-                    const f16x8 a = __builtin_bit_cast(
-                        f16x8, (short __attribute__((ext_vector_type(8)))){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
-#pragma unroll
-                    for (int b = 0; b < 2; b++)
-                        o[dt][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, p[b][kb][c], o[dt][b], 0, 0, 0);
-                }
+
+    // One tile t. S(t) is in (c0, c1); S(t+1) = K(t+1) Q^T goes to (n0, c0)
+    // (n0 free; c0's block-0 scores are exponentiated before its first
+    // write). K(t+1) is in LDS slot ks, V(t) in V slot vs; K(t+3) is DMAed
+    // to K slot kd and V(t+2) to V slot vd.
+    // The 64 MFMAs (32 for S(t+1), then 32 for O^T += V(t)^T P(t)^T) are
+    // issued in a fixed order with the vector work spread between them:
+    // the exponentials of block 0 under the first 16, those of block 1 under
+    // the next 32 (P's block 0 is complete before its accumulation starts),
+    // then the row max of S(t+1) under the accumulation MFMAs. Fragment
+    // reads run PF fragments ahead of their MFMAs. sched_barrier fences
+    // keep that order.
+    auto tile = [&](f32x16 (&c0)[2], f32x16 (&c1)[2], f32x16 (&n0)[2], uint32_t t, uint32_t ks, uint32_t vs,
+                    uint32_t kd, uint32_t vd, auto masked) {
+        dma(Kh, kvo, t + 3u, kd);
+        dma(Vh, vvo, t + 2u, 3u + vd);
+        const uint8_t* Ks = lds + ks * kTile64;
+        const uint8_t* Vs = lds + (3u + vs) * kTile64;
+        f16x8 p[2][2][2];
+        constexpr int PF = 3;  // fragments in flight ahead of their MFMAs
+        f16x8 kf[PF + 1], vf[PF + 1];
+        float rs[2] = {0.0f, 0.0f}, mt[2] = {-INFINITY, -INFINITY};
+        static_for<0, PF>([&](auto F) { kf[F] = kfrag(Ks, F); });
+        static_for<0, 64>([&](auto J) {
+            constexpr int j = J;
+            if constexpr (j < 32) {
+                constexpr int f = j / 2, b = j % 2, kb = f / 8, c = (f % 8) / 2, st = f % 2;
+                if constexpr (b == 0 && f + PF < 16) kf[(f + PF) % (PF + 1)] = kfrag(Ks, f + PF);
+                f32x16& s = kb == 0 ? n0[b] : c0[b];
+                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[f % (PF + 1)], qf[b][c][st],
+                                                           (c == 0 && st == 0) ? f32x16{} : s, 0, 0, 0);
+            } else {
+                constexpr int f = (j - 32) / 2, b = j % 2, kb = f / 8, c = (f % 8) / 4, dt = f % 4;
+                if constexpr (b == 0 && f + PF < 16) vf[(f + PF) % (PF + 1)] = vfrag(Vs, f + PF);
+                o[dt][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[f % (PF + 1)], p[b][kb][c], o[dt][b], 0, 0, 0);
+            }
+            if constexpr (j >= 32 - 2 * PF && j < 32 && j % 2 == 0) vf[(j - (32 - 2 * PF)) / 2] = vfrag(Vs, (j - (32 - 2 * PF)) / 2);
+            if constexpr (j < 16) exp_pair(c0, 0, j, p, rs);
+            if constexpr (j >= 16 && j < 48 && j % 2 == 0) exp_pair(c1, 1, (j - 16) / 2, p, rs);
+            if constexpr (decltype(masked)::value && j == 31) mask(n0, c0, t + 1u);
+            if constexpr (j >= 32 && j % 2 == 0) {
+                // row max item k: half k/8 (n0, then c0), query block (k%8)/4, scores 4(k%4)..+3
+                constexpr int k = (j - 32) / 2, b = (k % 8) / 4, i = 4 * (k % 4);
+                const f32x16& s = k < 8 ? n0[b] : c0[b];
+                mt[b] = fmaxf(fmaxf(mt[b], s[i]), s[i + 1]);
+                mt[b] = fmaxf(fmaxf(mt[b], s[i + 2]), s[i + 3]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        l_i[0] += rs[0];
+        l_i[1] += rs[1];
+        const float mx[2] = {xhalf_max(mt[0]) * scale_log2, xhalf_max(mt[1]) * scale_log2};
+        rescale(mx);
+        LLMR_STAGE_BARRIER(8);
     };
 
     const uint32_t n_tiles = (S + 63u) / 64u;
-    const uint32_t T = (n_tiles + 2u) / 3u * 3u;  // padded: whole unrolled bodies
+    const bool partial = (S % 64u) != 0u;
+    // iterations t whose S(t+1) has no key past the sequence end
+    const uint32_t n_plain = partial ? (n_tiles >= 2u ? n_tiles - 2u : 0u) : n_tiles - 1u;
 
-    // prologue: K0 V0 K1 V1 K2 in flight; S(0) and its max
-    dma(Kh, kvo, 0, K0);
-    dma(Vh, vvo, 0, V0);
-    dma(Kh, kvo, 1, K1);
-    dma(Vh, vvo, 1, V1);
-    dma(Kh, kvo, 2, K2);
+    // prologue: K(0) V(0) K(1) V(1) K(2) in flight; S(0) and its max
+    dma(Kh, kvo, 0, 0);
+    dma(Vh, vvo, 0, 3);
+    dma(Kh, kvo, 1, 1);
+    dma(Vh, vvo, 1, 4);
+    dma(Kh, kvo, 2, 2);
     LLMR_STAGE_BARRIER(16);  // K(0) has landed
-    f32x16 sc[2][2];
-    float mx[2];
-    qk(K0, 0, sc);
-    qk(K0, 1, sc);
-    if (S < 64u) mask(sc, 0);
-    rowmax(sc, mx);
-    rescale(mx);
+    f32x16 h0[2], h1[2], h2[2];
+    {
+        float mx[2];
+        qk_all(lds, h0, h1);
+        if (n_tiles == 1u && partial) mask(h0, h1, 0);
+        rowmax(h0, h1, mx);
+        rescale(mx);
+    }
     LLMR_STAGE_BARRIER(8);  // K(1), V(0) have landed; every wave is done with K(0)
 
-    // tile t: the scores of tile t (in sc) are exponentiated one key block
-    // at a time and that block's registers refilled with tile t+1's scores
-    // (K slot KQ) - the exponentials of block 1 overlap the QK MFMAs of
-    // block 0; then O^T += V(t)^T P(t)^T (V slot VP) while the new scores'
-    // row max is taken; DMAs of K(t+3) -> KD and V(t+2) -> VD
-#define LLMR_FA_TILE(t, KQ, VP, KD, VD, MASKED)                                \
-    {                                                                         \
-        dma(Kh, kvo, (t) + 3u, KD);                                           \
-        dma(Vh, vvo, (t) + 2u, VD);                                           \
-        f16x8 p[2][2][2];                                                     \
-        softmax_exp(sc, 0, p);                                                \
-        qk(KQ, 0, sc);                                                        \
-        softmax_exp(sc, 1, p);                                                \
-        qk(KQ, 1, sc);                                                        \
-        if (MASKED) mask(sc, (t) + 1u);                                       \
-        pv(VP, p);                                                            \
-        rowmax(sc, mx);                                                       \
-        rescale(mx);                                                          \
-        LLMR_STAGE_BARRIER(8);                                                \
+    // t % 3 = r0 names the ring slots: K(t+1) in r1, V(t) in r0; K(t+3) to
+    // r0 (K(t), last read in iteration t-1), V(t+2) to r2 (V(t-1)). The
+    // score halves rotate with period 3: S(t) in (h0, h1), (h2, h0), (h1, h2).
+    uint32_t t = 0, r0 = 0;
+    auto step = [&](f32x16 (&c0)[2], f32x16 (&c1)[2], f32x16 (&n0)[2], auto masked) {
+        const uint32_t r1 = r0 == 2u ? 0u : r0 + 1u;
+        const uint32_t r2 = r0 == 0u ? 2u : r0 - 1u;
+        tile(c0, c1, n0, t, r1, r0, r0, r2, masked);
+        t++;
+        r0 = r1;
+    };
+    // S(t) back into (h0, h1) after one step from (h0, h1)
+    auto rotate = [&]() {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            h1[b] = h0[b];
+            h0[b] = h2[b];
+        }
+    };
+    while (t + 3u <= n_plain) {
+        step(h0, h1, h2, std::false_type{});
+        step(h2, h0, h1, std::false_type{});
+        step(h1, h2, h0, std::false_type{});
     }
-#define LLMR_FA_BODY(t0, MASKED)                                              \
-    {                                                                         \
-        LLMR_FA_TILE((t0) + 0u, K1, V0, K0, V2, MASKED)                       \
-        LLMR_FA_TILE((t0) + 1u, K2, V1, K1, V0, MASKED)                       \
-        LLMR_FA_TILE((t0) + 2u, K0, V2, K2, V1, MASKED)                       \
+    while (t < n_plain) {
+        step(h0, h1, h2, std::false_type{});
+        rotate();
     }
-    // the first tile holding keys past S, and the first body whose QKs
-    // reach it (tile u's scores are computed in iteration u-1)
-    const uint32_t u_m = (S % 64u) != 0u ? n_tiles - 1u : n_tiles;
-    const uint32_t t_m = u_m == 0u ? 0u : (u_m - 1u) / 3u * 3u;
-    uint32_t t0 = 0;
-    for (; t0 < t_m; t0 += 3u) LLMR_FA_BODY(t0, false)
-    for (; t0 < T; t0 += 3u) LLMR_FA_BODY(t0, true)
-#undef LLMR_FA_BODY
-#undef LLMR_FA_TILE
+    if (partial && n_tiles >= 2u) {
+        step(h0, h1, h2, std::true_type{});
+        rotate();
+    }
+    {   // last tile: S(n-1) is in (h0, h1), V(n-1) in V slot r0
+        f16x8 p[2][2][2];
+        float rs[2] = {0.0f, 0.0f};
+        static_for<0, 16>([&](auto I) { exp_pair(h0, 0, I, p, rs); });
+        static_for<0, 16>([&](auto I) { exp_pair(h1, 1, I, p, rs); });
+        l_i[0] += rs[0];
+        l_i[1] += rs[1];
+        const uint8_t* Vs = lds + (3u + r0) * kTile64;
+        static_for<0, 16>([&](auto F) {
+            constexpr int f = F, kb = f / 8, c = (f % 8) / 4, dt = f % 4;
+            const f16x8 a = vfrag(Vs, f);
+            static_for<0, 2>([&](auto B) {
+                o[dt][B] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, p[B][kb][c], o[dt][B], 0, 0, 0);
+            });
+        });
+    }
     LLMR_WAIT_VMCNT(0);  // no DMA may still be writing LDS when the wave exits
 
     // O = O^T / l, rows of this wave's queries
@@ -595,7 +659,6 @@ flash_attn_fwd64(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
         }
     }
 }
-
 }  // namespace
 
 hipError_t launch_flash_attention(const void* q, const void* k, const void* v, uint32_t xtype,

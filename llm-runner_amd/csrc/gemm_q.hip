@@ -549,13 +549,6 @@ struct WRow<kGgmlQ8_0, OT> {
     }
 };
 
-template <int I, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-    if constexpr (I < E) {
-        f(std::integral_constant<int, I>{});
-        static_for<I + 1, E>(f);
-    }
-}
 
 // Schedule of one 16-wide k step inside a stage: its 16 MFMAs each followed
 // by a share of the stage's other work, so that work issues while the

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace llmr {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -19,6 +21,16 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr uint32_t kGgmlF32 = 0, kGgmlF16 = 1, kGgmlQ8_0 = 8, kGgmlQ4K = 12, kGgmlBF16 = 30;
+
+// f(std::integral_constant<int, I>) for I = B .. E-1, unrolled at compile time
+// (every index derived from I is a constant expression).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
 
 // Buffer resource over [base, base + bytes): loads past the end return zero
 // and stores past it are dropped (raw buffer, dword format word 3).
