@@ -212,7 +212,7 @@ def main():
     ach = main_r["tflops"]
     roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(ach / PEAK_TFLOPS, 4), "traffic": _traffic(args.workload),
-            "kernel": ("flash_attn_fwd" if args.workload == "flux_attention" else
+            "kernel": ("flash_attn_fwd64_w8" if args.workload == "flux_attention" else
                        gemm_kernel_name(args.workload, torch.cuda.get_device_properties(dev).multi_processor_count)),
             "algorithmic_bytes": main_r["bytes"],
             "hbm_frac_algorithmic": round(main_r["bytes"] / (main_r["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
