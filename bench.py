@@ -96,6 +96,24 @@ def setup_gemm(dev, name):
     return step, g.flops, g.bytes, cfg, "bf16" if g.xtype == gguf.GGML_BF16 else "f16"
 
 
+def setup_swiglu(dev, name):
+    import torch
+    from llmr_amd import gguf, ops, workloads
+    g = workloads.SWIGLUS[name]
+    wg = torch.from_numpy(workloads.gemm_weight_blocks(g)).to(dev)
+    wu = torch.from_numpy(workloads.swiglu_up_blocks(g)).to(dev)
+    xt = torch.from_numpy(workloads.gemm_activations_f32(g))
+    xt = {gguf.GGML_F32: xt, gguf.GGML_F16: xt.half(), gguf.GGML_BF16: xt.bfloat16()}[g.xtype].to(dev)
+    out = torch.empty((g.M, g.N), dtype=torch.float32, device=dev)
+
+    def step():
+        ops.batch_matmul_swiglu(wg, wu, xt, g.N, out=out)
+
+    cfg = {"workload": name, "M": g.M, "N": g.N, "K": g.K, "weight": "Q8_0 gate + up",
+           "activations": gguf.TYPE_NAMES[g.xtype].lower(), "output": "f32 silu(gate) * up"}
+    return step, g.flops, g.bytes, cfg, "bf16" if g.xtype == gguf.GGML_BF16 else "f16"
+
+
 def gemm_kernel_name(name: str, num_cus: int) -> str:
     """The kernel the library's dispatch picks for a GEMM workload: the
     persistent 256x256 kernel for 16-bit activations with at least half the
@@ -111,8 +129,13 @@ def gemm_kernel_name(name: str, num_cus: int) -> str:
 
 
 def measure(dev, name, steps, warmup):
-    step, flops, nbytes, cfg, dtype = (setup_attention(dev) if name == "flux_attention"
-                                       else setup_gemm(dev, name))
+    from llmr_amd import workloads
+    if name == "flux_attention":
+        step, flops, nbytes, cfg, dtype = setup_attention(dev)
+    elif name in workloads.SWIGLUS:
+        step, flops, nbytes, cfg, dtype = setup_swiglu(dev, name)
+    else:
+        step, flops, nbytes, cfg, dtype = setup_gemm(dev, name)
     total_ms, per = _time_steps(step, steps, warmup)
     ms = total_ms / steps
     per.sort()
@@ -180,7 +203,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="flux_attention")
-    ap.add_argument("--components", default="flux_linear1,flux_linear2,q8_linear,zimage_qkv")
+    ap.add_argument("--components", default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--hbm-copy-calibration", action="store_true",
                     help="time a plain 1 GiB device copy (reference for the FETCH_SIZE/WRITE_SIZE counters)")

@@ -169,6 +169,27 @@ LLMR_API int llmr_batch_matmul_pc(llmr_context* ctx, const void* weight, uint32_
                                   const void* input, uint32_t input_type, float* output,
                                   const llmr_batch_matmul_params* pc);
 
+/* SwiGLU feed-forward in-projection, both matmuls and the activation in one op:
+ *   g = input · weight_gate^T,  u = input · weight_up^T,
+ *   output[s, o] = silu(g[s, o]) * u[s, o],  silu(g) = g / (1 + e^-g)
+ * weight_gate and weight_up Q8_0 [out_dim, in_dim] (rows from 0), input
+ * [seq_len, in_dim] of input_type F32, F16 or BF16, output f32 [seq_len,
+ * out_dim], overwritten. Replaces the batch_matmul_swiglu_q8 dispatch
+ * (dependencies/zimage.c3l/dit.c3:1562-1580; kernel
+ * dependencies/llm_text.c3l/shaders/llm.slang:1769-1911). F32 input is
+ * rounded to bf16 for the matrix cores (the reference keeps it in f32); that
+ * path, and shapes the fused kernel does not take (out_dim % 4 != 0), use a
+ * workspace the context allocates on first use and keeps (grow-only). */
+LLMR_API int llmr_batch_matmul_swiglu(llmr_context* ctx, const void* weight_gate, const void* weight_up,
+                                      uint32_t weight_type, const void* input, uint32_t input_type,
+                                      float* output, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len);
+
+/* Same op with the reference's push constants (dit.c3:1567-1579); row_offset
+ * must be 0 (the reference kernel reads rows from 0). */
+LLMR_API int llmr_batch_matmul_swiglu_pc(llmr_context* ctx, const void* weight_gate, const void* weight_up,
+                                         uint32_t weight_type, const void* input, uint32_t input_type,
+                                         float* output, const llmr_batch_matmul_params* pc);
+
 /* Non-causal attention, no mask:
  *   out[s, h*D + d] = sum_j softmax_j(scale * <q[h,s,:], k[h,j,:]>) * v[h,j,d]
  * q, k, v [n_heads, seq_len, head_dim] of qkv_type F32, F16 or BF16 (values are

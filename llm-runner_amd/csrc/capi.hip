@@ -16,6 +16,8 @@ struct llmr_context {
     int num_cus;
     hipStream_t own;
     hipStream_t cur;
+    void* ws;         // library workspace (the SwiGLU's f32-input and fallback paths), grow-only
+    size_t ws_bytes;
 };
 
 namespace {
@@ -91,6 +93,8 @@ int llmr_create_context(int device_index, llmr_context** out_ctx) {
         return fail(LLMR_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
     }
     c->cur = c->own;
+    c->ws = nullptr;
+    c->ws_bytes = 0;
     *out_ctx = c;
     return ok();
 }
@@ -101,6 +105,7 @@ int llmr_destroy_context(llmr_context* ctx) {
     (void)hipStreamSynchronize(ctx->cur);
     (void)hipStreamSynchronize(ctx->own);
     (void)hipStreamDestroy(ctx->own);
+    if (ctx->ws) (void)hipFree(ctx->ws);
     delete ctx;
     return ok();
 }
@@ -214,6 +219,47 @@ int llmr_batch_matmul_pc(llmr_context* ctx, const void* weight, uint32_t wtype, 
     if (!pc) return fail(LLMR_ERR_INVALID_ARG, "null push constants");
     return llmr_batch_matmul(ctx, weight, wtype, input, xtype, output, pc->out_dim, pc->in_dim,
                              pc->seq_len, pc->row_offset);
+}
+
+int llmr_batch_matmul_swiglu(llmr_context* ctx, const void* weight_gate, const void* weight_up,
+                              uint32_t wtype, const void* input, uint32_t xtype, float* output,
+                              uint32_t out_dim, uint32_t in_dim, uint32_t seq_len) {
+    if (int r = check_ctx(ctx)) return r;
+    if (wtype != LLMR_GGML_Q8_0)
+        return fail(LLMR_ERR_UNSUPPORTED, "SwiGLU GEMM needs Q8_0 gate and up weights (llm.slang:1777), got type %u",
+                    wtype);
+    if (int r = check_weight(weight_gate, wtype, in_dim)) return r;
+    if (int r = check_weight(weight_up, wtype, in_dim)) return r;
+    if (!is_act_type(xtype))
+        return fail(LLMR_ERR_UNSUPPORTED, "input type %u not supported (F32=0, F16=1, BF16=30)", xtype);
+    if (seq_len == 0 || out_dim == 0) return ok();
+    if (!input || !output) return fail(LLMR_ERR_INVALID_ARG, "null input/output pointer");
+    if (!aligned(input, 16) || !aligned(output, 16))
+        return fail(LLMR_ERR_INVALID_ARG, "input/output pointers must be 16-byte aligned");
+    const size_t need = llmr::swiglu_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len);
+    if (need > ctx->ws_bytes) {
+        // hipFree waits for every launch that may still read the old workspace
+        if (ctx->ws) LLMR_HIP_CHECK(hipFree(ctx->ws));
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+        LLMR_HIP_CHECK(hipMalloc(&ctx->ws, need));
+        ctx->ws_bytes = need;
+    }
+    hipError_t e = llmr::launch_batch_matmul_swiglu(weight_gate, weight_up, wtype, input, xtype, output, out_dim,
+                                                    in_dim, seq_len, ctx->num_cus, ctx->ws, ctx->cur);
+    if (e != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul_swiglu launch: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int llmr_batch_matmul_swiglu_pc(llmr_context* ctx, const void* weight_gate, const void* weight_up,
+                                 uint32_t wtype, const void* input, uint32_t xtype, float* output,
+                                 const llmr_batch_matmul_params* pc) {
+    if (!pc) return fail(LLMR_ERR_INVALID_ARG, "null push constants");
+    if (pc->row_offset != 0)
+        return fail(LLMR_ERR_INVALID_ARG, "SwiGLU GEMM reads weight rows from 0 (row_offset must be 0, got %u)",
+                    pc->row_offset);
+    return llmr_batch_matmul_swiglu(ctx, weight_gate, weight_up, wtype, input, xtype, output, pc->out_dim,
+                                    pc->in_dim, pc->seq_len);
 }
 
 int llmr_flash_attention(llmr_context* ctx, const void* q, const void* k, const void* v,

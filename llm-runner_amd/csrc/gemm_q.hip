@@ -45,6 +45,19 @@ __device__ __forceinline__ uint32_t lds_off(uint32_t r, uint32_t c) {
     return r * 128u + ((c ^ ((r >> 1) & 7u)) << 4);
 }
 
+// 32x32x16 MFMA on 16-bit operand bits: bf16 operands for bf16 activations
+// (fp16 cannot hold bf16's range), fp16 otherwise.
+template <uint32_t XT>
+__device__ __forceinline__ f32x16 mfma16(f16x8 a, f16x8 b, f32x16 c) {
+    if constexpr (XT == kGgmlBF16) {
+        typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+}
+
 template <uint32_t XT>
 struct XLoad;
 
@@ -55,10 +68,8 @@ struct XLoad<kGgmlBF16> {
     __device__ __forceinline__ void load(const void* x, uint64_t elem, bool ok) {
         v = ok ? *(const u32x4*)((const uint16_t*)x + elem) : u32x4{0, 0, 0, 0};
     }
-    __device__ __forceinline__ u32x4 to_f16() const {
-        return u32x4{bf16x2_to_f16x2(v.x), bf16x2_to_f16x2(v.y), bf16x2_to_f16x2(v.z),
-                     bf16x2_to_f16x2(v.w)};
-    }
+    // bf16 activations are used as bf16 operands (bf16 MFMA)
+    __device__ __forceinline__ u32x4 to_op() const { return v; }
 };
 template <>
 struct XLoad<kGgmlF16> {
@@ -66,7 +77,7 @@ struct XLoad<kGgmlF16> {
     __device__ __forceinline__ void load(const void* x, uint64_t elem, bool ok) {
         v = ok ? *(const u32x4*)((const uint16_t*)x + elem) : u32x4{0, 0, 0, 0};
     }
-    __device__ __forceinline__ u32x4 to_f16() const { return v; }
+    __device__ __forceinline__ u32x4 to_op() const { return v; }
 };
 // f32 activations: two 16-byte loads per LDS chunk, rounded to fp16 as the
 // reference's float16_t(v) (llm.slang:1673).
@@ -78,7 +89,7 @@ struct XLoad<kGgmlF32> {
         a = ok ? *(const f32x4*)p : f32x4{0, 0, 0, 0};
         b = ok ? *(const f32x4*)(p + 4) : f32x4{0, 0, 0, 0};
     }
-    __device__ __forceinline__ u32x4 to_f16() const {
+    __device__ __forceinline__ u32x4 to_op() const {
         return u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y),
                      pack_f16x2(b.z, b.w)};
     }
@@ -112,10 +123,33 @@ struct WLoad<kGgmlQ8_0> {
         e = *(const uint32_t*)(p + 64);
     }
     // Writes chunks 0..7 of LDS row r (k 0..31 from block 0, 32..63 from block 1).
+    // bf16 operands: RN_bf16(d*q) (the product is exact in f32).
+    template <uint32_t OT>
     __device__ __forceinline__ void store(uint8_t* lds, uint32_t r, uint32_t unit) const {
         (void)unit;
         const uint32_t wd[17] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x,
                                  c.y, c.z, c.w, d.x, d.y, d.z, d.w, e};
+        if constexpr (OT == kGgmlBF16) {
+            typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+            auto chunk = [](uint32_t q0, uint32_t q1, float dd) {
+                bf16x8_t v;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    v[i] = (__bf16)(dd * (float)(int8_t)(q0 >> (8 * i)));
+                    v[4 + i] = (__bf16)(dd * (float)(int8_t)(q1 >> (8 * i)));
+                }
+                return __builtin_bit_cast(u32x4, v);
+            };
+            const float d0 = f16_bits_to_f32(wd[0] & 0xffffu), d1 = f16_bits_to_f32(wd[8] >> 16);
+#pragma unroll
+            for (int ch = 0; ch < 4; ch++) {
+                const uint32_t q0 = __builtin_amdgcn_alignbyte(wd[2 * ch + 1], wd[2 * ch], 2);
+                const uint32_t q1 = __builtin_amdgcn_alignbyte(wd[2 * ch + 2], wd[2 * ch + 1], 2);
+                *(u32x4*)(lds + lds_off(r, ch)) = chunk(q0, q1, d0);
+                *(u32x4*)(lds + lds_off(r, 4 + ch)) = chunk(wd[9 + 2 * ch], wd[10 + 2 * ch], d1);
+            }
+            return;
+        }
         // block 0: scale = bytes 0-1, quants = bytes 2..33 (re-aligned by 2 bytes)
         const _Float16 d0 = (_Float16)f16_bits_to_f32(wd[0] & 0xffffu);
         const f16x2 d02 = {d0, d0};
@@ -163,6 +197,8 @@ struct WLoad<kGgmlQ4K> {
         hdr = *(const u32x4*)p;
         qs = *(const u32x4*)(p + 16 + 32 * j + 16 * unit);
     }
+    // operands RN(d*sc*q - dmin*mn) of type OT (fp16 or bf16)
+    template <uint32_t OT>
     __device__ __forceinline__ void store(uint8_t* lds, uint32_t r, uint32_t unit, uint32_t k0) const {
         const uint32_t j = (k0 % 256) / 64;
         const float d = f16_bits_to_f32(hdr.x & 0xffffu);
@@ -178,10 +214,17 @@ struct WLoad<kGgmlQ4K> {
         for (int i = 0; i < 4; i++) {
             const uint32_t l4 = q[i] & 0x0f0f0f0fu;
             const uint32_t h4 = (q[i] >> 4) & 0x0f0f0f0fu;
-            lo[2 * i] = q4_pair(l4, 0x04010400u, dsc0, dmn0);
-            lo[2 * i + 1] = q4_pair(l4, 0x04030402u, dsc0, dmn0);
-            hi[2 * i] = q4_pair(h4, 0x04010400u, dsc1, dmn1);
-            hi[2 * i + 1] = q4_pair(h4, 0x04030402u, dsc1, dmn1);
+            if constexpr (OT == kGgmlBF16) {
+                lo[2 * i] = q4_pair_bf16(l4, 0x04010400u, dsc0, dmn0);
+                lo[2 * i + 1] = q4_pair_bf16(l4, 0x04030402u, dsc0, dmn0);
+                hi[2 * i] = q4_pair_bf16(h4, 0x04010400u, dsc1, dmn1);
+                hi[2 * i + 1] = q4_pair_bf16(h4, 0x04030402u, dsc1, dmn1);
+            } else {
+                lo[2 * i] = q4_pair(l4, 0x04010400u, dsc0, dmn0);
+                lo[2 * i + 1] = q4_pair(l4, 0x04030402u, dsc0, dmn0);
+                hi[2 * i] = q4_pair(h4, 0x04010400u, dsc1, dmn1);
+                hi[2 * i + 1] = q4_pair(h4, 0x04030402u, dsc1, dmn1);
+            }
         }
         *(u32x4*)(lds + lds_off(r, 2 * unit)) = u32x4{lo[0], lo[1], lo[2], lo[3]};
         *(u32x4*)(lds + lds_off(r, 2 * unit + 1)) = u32x4{lo[4], lo[5], lo[6], lo[7]};
@@ -213,6 +256,7 @@ __global__ void __launch_bounds__(256, (BM * BN >= 256 * 256) ? 1 : 2)
 gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __restrict__ Y,
             uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset, uint32_t tiles_m,
             uint32_t tiles_n) {
+    constexpr uint32_t OT = (XT == kGgmlBF16) ? kGgmlBF16 : kGgmlF16;  // MFMA operand type
     constexpr int WM = BM / 2, WN = BN / 2;  // per-wave tile (tokens x features)
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr uint32_t A_BYTES = BM * kBK * 2, B_BYTES = BN * kBK * 2;
@@ -258,7 +302,7 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
 #pragma unroll
         for (int i = 0; i < X_PER_T; i++) {
             const uint32_t r = (tid >> 3) + 32u * i, c = tid & 7u;
-            *(u32x4*)(As + lds_off(r, c)) = xl[i].to_f16();
+            *(u32x4*)(As + lds_off(r, c)) = xl[i].to_op();
         }
 #pragma unroll
         for (int i = 0; i < W_PER_T; i++) {
@@ -266,9 +310,9 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
             if (u < (uint32_t)W_UNITS) {
                 const uint32_t r = u / WLoad<WT>::kUnitsPerRow, unit = u % WLoad<WT>::kUnitsPerRow;
                 if constexpr (WT == kGgmlQ4K)
-                    wl[i].store(Bs, r, unit, s * kBK);
+                    wl[i].template store<OT>(Bs, r, unit, s * kBK);
                 else
-                    wl[i].store(Bs, r, unit);
+                    wl[i].template store<OT>(Bs, r, unit);
             }
         }
     };
@@ -310,7 +354,7 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
                 for (int a = 0; a < TN; a++)
 #pragma unroll
                     for (int b = 0; b < TM; b++)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[a], xf[b], acc[a][b], 0, 0, 0);
+                        acc[a][b] = mfma16<OT>(wf[a], xf[b], acc[a][b]);
             }
         }
         if (s + 1 < n_stages) store_stage(s + 1, buf ^ 1u);
@@ -359,16 +403,6 @@ __device__ __forceinline__ u32x4 q8x8_f16(uint32_t q0, uint32_t q1, f16x2 d2) {
     return __builtin_bit_cast(u32x4, f16x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
 }
 
-template <uint32_t XT>
-__device__ __forceinline__ f32x16 mfma16(f16x8 a, f16x8 b, f32x16 c) {
-    if constexpr (XT == kGgmlBF16) {
-        typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-    } else {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Persistent 256 x 256 tile kernel for 16-bit activations (gfx950).
@@ -580,11 +614,24 @@ struct Frags {
     f16x8 x[4], w[4];
 };
 
-template <uint32_t WT, uint32_t XT>
+// silu(g) = g / (1 + e^-g) (llm.slang:1903), e^-g as 2^(-g log2 e)
+__device__ __forceinline__ float silu(float g) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
+
+// SW (SwiGLU, batch_matmul_swiglu_q8, llm.slang:1769-1911): W holds the gate
+// rows and W2 the up rows (N each, row_offset unused); a tile covers 128
+// output features, whose 128 gate and 128 up rows form its 256 weight rows
+// arranged so that each wave's 128 feature columns are 64 gate features
+// followed by the same 64 up features: the epilogue writes
+// silu(gate) * up from two accumulators of the same lane.
+template <uint32_t WT, uint32_t XT, bool SW>
 __global__ void __launch_bounds__(256, 1)
-gemm_q_persist(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __restrict__ Y, uint32_t N,
-               uint32_t K, uint32_t M, uint32_t row_offset, uint32_t tiles_m, uint32_t tiles_n) {
+gemm_q_persist(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2, const void* __restrict__ X,
+               float* __restrict__ Y, uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset, uint32_t tiles_m,
+               uint32_t tiles_n) {
     static_assert(XT == kGgmlF16 || XT == kGgmlBF16, "16-bit activations only");
+    constexpr uint32_t NT = SW ? 128u : 256u;  // output features per tile
     constexpr uint32_t TILE = 256u * 128u;  // bytes of one 256-row x 64-wide 16-bit tile
     constexpr int X_DMAS = 8;               // 1 KiB activation DMAs per wave per stage
     constexpr int W_LOADS = WRow<WT, XT>::kLoads;
@@ -617,8 +664,13 @@ gemm_q_persist(const uint8_t* __restrict__ W, const void* __restrict__ X, float*
         const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
         xvoff[i] = row * xrow + c * 16u;
     }
-    const uint32_t wvoff = tid * rb;                                   // weight row tid of the tile
-    const uint32_t wbase = tid * 128u + ((((tid >> 1) & 7u)) << 4);    // its LDS chunk 0
+    // Thread tid loads one weight row of the tile. SW: waves 0-1 the gate rows
+    // 0..127 and waves 2-3 the up rows 0..127 of the tile's features (one
+    // descriptor per wave), placed at LDS rows gate 0-63 | up 0-63 | gate
+    // 64-127 | up 64-127 (waves 1 and 2 swap places).
+    const uint32_t wvoff = (SW ? (tid & 127u) : tid) * rb;
+    const uint32_t wrow = SW ? (wave == 1u ? tid + 64u : wave == 2u ? tid - 64u : tid) : tid;
+    const uint32_t wbase = wrow * 128u + ((((wrow >> 1) & 7u)) << 4);  // its LDS chunk 0
     // fragment offsets per 16-wide k step t: chunk 4(t>>1) + 2kh + (t&1) of
     // rows (block) + l32; the swizzle term depends only on l32
     uint32_t xoff[4], woff[4];
@@ -641,7 +693,7 @@ gemm_q_persist(const uint8_t* __restrict__ W, const void* __restrict__ X, float*
         uint32_t tm, tn;
         map_tile_persist(blockIdx.x + k * G, G, tiles_m, tiles_n, tm, tn);
         m0 = tm * 256u;
-        n0 = tn * 256u;
+        n0 = tn * NT;
     };
     auto x_tile = [&](Cursor& c, uint32_t k) {
         uint32_t m0, n0;
@@ -654,7 +706,10 @@ gemm_q_persist(const uint8_t* __restrict__ W, const void* __restrict__ X, float*
         uint32_t m0, n0;
         tile_origin(k, m0, n0);
         c.s = 0;
-        c.base = W + (uint64_t)(row_offset + n0) * rb;
+        if constexpr (SW)
+            c.base = (wave < 2u ? W : W2) + (uint64_t)n0 * rb;
+        else
+            c.base = W + (uint64_t)(row_offset + n0) * rb;
         c.size = k < n_tiles ? (N - n0) * rb : 0u;
     };
     Cursor cx{0, nullptr, 0}, cw{0, nullptr, 0};
@@ -724,6 +779,26 @@ gemm_q_persist(const uint8_t* __restrict__ W, const void* __restrict__ X, float*
     auto store_tile = [&](uint32_t k) {
         uint32_t tm, tn;
         map_tile_persist(blockIdx.x + k * G, G, tiles_m, tiles_n, tm, tn);
+        if constexpr (SW) {
+            // acc[a] (gate) and acc[a + 2] (up) hold the same features
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const uint32_t m = tm * 256u + wm * 128u + b * 32u + l32;
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const uint32_t n = tn * 128u + wn * 64u + a * 32u + 8u * g + 4u * kh;
+                        f32x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) v[e] = silu(acc[a][b][4 * g + e]) * acc[a + 2][b][4 * g + e];
+                        if (m < M && n < N) *(f32x4*)(Y + (uint64_t)m * N + n) = v;
+                    }
+                    acc[a][b] = f32x16{};
+                    acc[a + 2][b] = f32x16{};
+                }
+            return;
+        }
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
@@ -840,8 +915,9 @@ gemm_q_persist(const uint8_t* __restrict__ W, const void* __restrict__ X, float*
 }
 
 // Generic path for shapes the tiled kernel does not take (Q8_0 with
-// K % 64 == 32): one thread per output, operands and order as the MFMA path
-// (fp16 activations, fp16 weight operands, f32 accumulation).
+// K % 64 == 32): one thread per output, operands as the MFMA paths (bf16
+// activations and weight operands for bf16 inputs, fp16 otherwise; f32
+// accumulation).
 template <uint32_t WT, uint32_t XT>
 __global__ void __launch_bounds__(256) gemm_q_generic(const uint8_t* __restrict__ W,
                                                       const void* __restrict__ X,
@@ -861,12 +937,15 @@ __global__ void __launch_bounds__(256) gemm_q_generic(const uint8_t* __restrict_
             xv = (float)((const _Float16*)X)[(uint64_t)m * K + k];
         else
             xv = __uint_as_float((uint32_t)((const uint16_t*)X)[(uint64_t)m * K + k] << 16);
-        const float a = (float)(_Float16)xv;
+        constexpr bool bf = XT == kGgmlBF16;
+        const float a = bf ? xv : (float)(_Float16)xv;
         float b;
         if (WT == kGgmlQ8_0) {
             const uint8_t* blk = wr + (uint64_t)(k / 32) * 34;
-            const _Float16 d = (_Float16)f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-            b = (float)(_Float16)(d * (_Float16)(float)(int8_t)blk[2 + k % 32]);
+            const float df = f16_bits_to_f32((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+            const _Float16 d = (_Float16)df;
+            const float q = (float)(int8_t)blk[2 + k % 32];
+            b = bf ? (float)(__bf16)(df * q) : (float)(_Float16)(d * (_Float16)q);
         } else {
             const uint8_t* blk = wr + (uint64_t)(k / 256) * 144;
             const uint32_t e = k % 256, j = e >> 6, h = (e >> 5) & 1u, l = e & 31u;
@@ -877,7 +956,8 @@ __global__ void __launch_bounds__(256) gemm_q_generic(const uint8_t* __restrict_
                           *(const uint32_t*)(blk + 12), sc, mn);
             const uint32_t qb = blk[16 + j * 32 + l];
             const uint32_t q = h ? (qb >> 4) : (qb & 0xfu);
-            b = (float)(_Float16)((d * (float)sc) * (float)q - dmin * (float)mn);
+            const float v = __builtin_fmaf((float)q, d * (float)sc, -(dmin * (float)mn));
+            b = bf ? (float)(__bf16)v : (float)(_Float16)v;
         }
         acc += a * b;
     }
@@ -924,8 +1004,9 @@ hipError_t dispatch_x(const void* w, const void* x, float* y, uint32_t N, uint32
         if (fits31 && N % 4 == 0 && 2 * tiles >= (uint64_t)num_cus) {
             const uint32_t tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
             const uint32_t grid = (uint32_t)min(tiles, (uint64_t)num_cus);
-            hipLaunchKernelGGL((gemm_q_persist<WT, XT>), dim3(grid), dim3(256), 0, st,
-                               (const uint8_t*)w, x, y, N, K, M, row_offset, tiles_m, tiles_n);
+            hipLaunchKernelGGL((gemm_q_persist<WT, XT, false>), dim3(grid), dim3(256), 0, st,
+                               (const uint8_t*)w, (const uint8_t*)nullptr, x, y, N, K, M, row_offset, tiles_m,
+                               tiles_n);
             return hipGetLastError();
         }
     }
@@ -947,7 +1028,82 @@ hipError_t dispatch_w(const void* w, uint32_t xtype, const void* x, float* y, ui
     }
 }
 
+// f32 -> bf16 with round to nearest even (NaN stays NaN), 4 values per thread
+__global__ void __launch_bounds__(256) f32_to_bf16_kernel(const float* __restrict__ x, uint32_t* __restrict__ y,
+                                                          size_t n4) {
+    const size_t i = (size_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= n4) return;
+    const u32x4 v = *(const u32x4*)(x + 4 * i);
+    auto rn = [](uint32_t b) -> uint32_t {
+        if ((b & 0x7fffffffu) > 0x7f800000u) return (b >> 16) | 0x40u;  // quiet NaN
+        return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+    };
+    *(u32x2*)(y + 2 * i) = u32x2{rn(v.x) | (rn(v.y) << 16), rn(v.z) | (rn(v.w) << 16)};
+}
+
+// y = silu(g) * u elementwise (the SwiGLU of two separately computed GEMMs)
+__global__ void __launch_bounds__(256) swiglu_combine_kernel(const float* __restrict__ g,
+                                                             const float* __restrict__ u, float* __restrict__ y,
+                                                             size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256u + threadIdx.x;
+    if (i < n) y[i] = silu(g[i]) * u[i];
+}
+
+// Whether the fused SwiGLU kernel takes this launch: four features per
+// lane store (N % 4 == 0) and 32-bit buffer offsets for the 16-bit
+// activations and each weight.
+bool swiglu_fused(uint32_t wtype, uint32_t N, uint32_t K, uint32_t M) {
+    const uint64_t rb = (wtype == kGgmlQ8_0) ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * 144;
+    return N % 4 == 0 && (K % kBK) == 0 && (uint64_t)M * K * 2u < (1ull << 31) && (uint64_t)N * rb < (1ull << 31);
+}
+
 }  // namespace
+
+size_t swiglu_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
+                              uint32_t seq_len) {
+    if (!swiglu_fused(wtype, out_dim, in_dim, seq_len))
+        return 2 * (((size_t)seq_len * out_dim + 63) / 64 * 64) * sizeof(float);
+    return xtype == kGgmlF32 ? (size_t)seq_len * in_dim * 2u : 0u;
+}
+
+hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t wtype, const void* x,
+                                      uint32_t xtype, float* y, uint32_t out_dim, uint32_t in_dim,
+                                      uint32_t seq_len, int num_cus, void* ws, hipStream_t st) {
+    if (seq_len == 0 || out_dim == 0) return hipSuccess;
+    const uint32_t N = out_dim, K = in_dim, M = seq_len;
+    if (!swiglu_fused(wtype, N, K, M)) {
+        // two GEMMs into the workspace, then the elementwise SwiGLU
+        float* g = (float*)ws;
+        float* u = g + ((size_t)M * N + 63) / 64 * 64;  // 256-byte aligned
+        hipError_t e = launch_batch_matmul(wg, wtype, x, xtype, g, N, K, M, 0, num_cus, st);
+        if (e == hipSuccess) e = launch_batch_matmul(wu, wtype, x, xtype, u, N, K, M, 0, num_cus, st);
+        if (e != hipSuccess) return e;
+        const size_t n = (size_t)M * N;
+        hipLaunchKernelGGL(swiglu_combine_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, g, u, y, n);
+        return hipGetLastError();
+    }
+    const void* x16 = x;
+    uint32_t xt = xtype;
+    if (xtype == kGgmlF32) {  // activations rounded to bf16 once (range of f32 kept)
+        const size_t n4 = (size_t)M * K / 4;
+        hipLaunchKernelGGL(f32_to_bf16_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, st,
+                           (const float*)x, (uint32_t*)ws, n4);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        x16 = ws;
+        xt = kGgmlBF16;
+    }
+    const uint32_t tiles_m = (M + 255) / 256, tiles_n = (N + 127) / 128;
+    const uint32_t grid = (uint32_t)min((uint64_t)tiles_m * tiles_n, (uint64_t)num_cus);
+    if (wtype != kGgmlQ8_0) return hipErrorInvalidValue;
+    if (xt == kGgmlF16)
+        hipLaunchKernelGGL((gemm_q_persist<kGgmlQ8_0, kGgmlF16, true>), dim3(grid), dim3(256), 0, st,
+                           (const uint8_t*)wg, (const uint8_t*)wu, x16, y, N, K, M, 0u, tiles_m, tiles_n);
+    else
+        hipLaunchKernelGGL((gemm_q_persist<kGgmlQ8_0, kGgmlBF16, true>), dim3(grid), dim3(256), 0, st,
+                           (const uint8_t*)wg, (const uint8_t*)wu, x16, y, N, K, M, 0u, tiles_m, tiles_n);
+    return hipGetLastError();
+}
 
 hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uint32_t xtype,
                                float* y, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,

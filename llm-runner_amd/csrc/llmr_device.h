@@ -113,6 +113,17 @@ __device__ __forceinline__ uint32_t q4_pair(uint32_t nib, uint32_t sel, float ds
     return __builtin_bit_cast(uint32_t, r);
 }
 
+// The same two quants as packed bf16: the reference's f32 value d*sc*q - dmin*mn
+// (both products exact, one rounding in the FMA) rounded to bf16.
+__device__ __forceinline__ uint32_t q4_pair_bf16(uint32_t nib, uint32_t sel, float dsc, float dmn) {
+    const uint32_t q = __builtin_amdgcn_perm(0u, nib, sel);  // q0 in bits 0-7, q1 in bits 16-23
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    bf16x2_t r;
+    r.x = (__bf16)__builtin_fmaf((float)(q & 0xffu), dsc, -dmn);
+    r.y = (__bf16)__builtin_fmaf((float)(q >> 16), dsc, -dmn);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 // get_scale_min_k4 (llm.slang:447-462) for sub-block index `is` (wave-uniform)
 // on the 12 scale bytes held in dwords s0 (bytes 0-3), s1 (4-7), s2 (8-11).
 // Branch-free (a mask select) so a loop calling it stays one basic block.

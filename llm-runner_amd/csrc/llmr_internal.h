@@ -19,6 +19,14 @@ hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uin
                                float* y, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,
                                uint32_t row_offset, int num_cus, hipStream_t st);
 
+// SwiGLU of two Q8_0 GEMMs (batch_matmul_swiglu_q8). `ws` must hold
+// swiglu_workspace_bytes(...) bytes (may be 0).
+size_t swiglu_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
+                              uint32_t seq_len);
+hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t wtype, const void* x,
+                                      uint32_t xtype, float* y, uint32_t out_dim, uint32_t in_dim,
+                                      uint32_t seq_len, int num_cus, void* ws, hipStream_t st);
+
 hipError_t launch_flash_attention(const void* q, const void* k, const void* v, uint32_t xtype,
                                   float* o, uint32_t n_heads, uint32_t seq_len, float scale,
                                   hipStream_t st);

@@ -60,6 +60,9 @@ _SIGS = {
     "llmr_batch_matmul": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32]),
     "llmr_batch_matmul_pc": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp,
                                             ctypes.POINTER(BatchMatMulParams)]),
+    "llmr_batch_matmul_swiglu": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32]),
+    "llmr_batch_matmul_swiglu_pc": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp,
+                                                   ctypes.POINTER(BatchMatMulParams)]),
     "llmr_flash_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32,
                                             ctypes.c_float]),
     "llmr_flash_attention_pc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _vp,
@@ -145,6 +148,11 @@ class Context:
                      out_dim: int, in_dim: int, seq_len: int, row_offset: int = 0) -> None:
         check(lib().llmr_batch_matmul(self._h, w_ptr, wtype, x_ptr, xtype, y_ptr, out_dim, in_dim,
                                       seq_len, row_offset))
+
+    def batch_matmul_swiglu(self, wg_ptr: int, wu_ptr: int, wtype: int, x_ptr: int, xtype: int,
+                            y_ptr: int, out_dim: int, in_dim: int, seq_len: int) -> None:
+        check(lib().llmr_batch_matmul_swiglu(self._h, wg_ptr, wu_ptr, wtype, x_ptr, xtype, y_ptr,
+                                             out_dim, in_dim, seq_len))
 
     def flash_attention(self, q_ptr: int, k_ptr: int, v_ptr: int, xtype: int, o_ptr: int,
                         head_dim: int, n_heads: int, seq_len: int, scale: float) -> None:

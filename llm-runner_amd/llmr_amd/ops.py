@@ -109,6 +109,32 @@ def dispatch_batch_matmul(g: RenderGraph, weight: Tensor, input: Tensor, output:
                        out_dim, in_dim, seq_len, row_offset)
 
 
+def dispatch_batch_matmul_swiglu(g: RenderGraph, weight_gate: Tensor, weight_up: Tensor,
+                                 input: Tensor, output: Tensor, out_dim: int, in_dim: int,
+                                 seq_len: int) -> None:
+    """output[s, o] = silu(input . weight_gate[o]) * (input . weight_up[o]) (f32, overwritten).
+
+    Mirrors the batch_matmul_swiglu_q8 dispatch of dit_transformer_layer
+    (dit.c3:1562-1580): both weights Q8_0 [out_dim, in_dim], rows from 0. The
+    reference takes this path only without LoRA on gate/up; a present LoRA
+    keeps the caller's two-matmul fallback (dit.c3:1582-1592)."""
+    if weight_gate.dtype != GGML_Q8_0 or weight_up.dtype != GGML_Q8_0:
+        raise capi.LlmrError(capi.LLMR_ERR_UNSUPPORTED, "SwiGLU GEMM needs Q8_0 gate and up weights")
+    for t, n in ((weight_gate, "weight_gate"), (weight_up, "weight_up"), (input, "input"),
+                 (output, "output")):
+        _dev(t, n)
+    if output.dtype != GGML_F32:
+        raise ValueError("output must be f32")
+    for w in (weight_gate, weight_up):
+        if w.shape[1] != in_dim or out_dim > w.shape[0]:
+            raise ValueError("weight shape does not cover out_dim x in_dim")
+    if input.data.numel() < seq_len * in_dim or output.data.numel() < seq_len * out_dim:
+        raise ValueError("input/output smaller than [seq_len, in_dim] / [seq_len, out_dim]")
+    g.bind_stream()
+    g.ctx.batch_matmul_swiglu(weight_gate.ptr(), weight_up.ptr(), weight_gate.dtype, input.ptr(),
+                              input.dtype, output.ptr(), out_dim, in_dim, seq_len)
+
+
 def dispatch_flash_attention(g: RenderGraph, q: Tensor, k: Tensor, v: Tensor, out: Tensor,
                              pc: FlashAttentionPC) -> None:
     """out[s, h*D + d] = softmax(scale * q k^T) v per head; q/k/v [H, S, D], out f32 [S, H*D]."""
@@ -148,6 +174,21 @@ def batch_matmul(w_blocks: torch.Tensor, wtype: int, x: torch.Tensor, out_dim: i
         out = torch.empty((M, out_dim), dtype=torch.float32, device=x.device)
     dispatch_batch_matmul(default_graph(), Tensor.quantized(w_blocks, wtype, rows, K),
                           Tensor.from_torch(x), Tensor.from_torch(out), out_dim, K, M, row_offset)
+    return out
+
+
+def batch_matmul_swiglu(wg_blocks: torch.Tensor, wu_blocks: torch.Tensor, x: torch.Tensor,
+                        out_dim: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [M, K] (f32/f16/bf16, cuda) and Q8_0 gate/up weights [out_dim, K] ->
+    f32 [M, out_dim] = silu(x Wg^T) * (x Wu^T)."""
+    M, K = x.shape
+    if out is None:
+        out = torch.empty((M, out_dim), dtype=torch.float32, device=x.device)
+    rows_g = wg_blocks.numel() // row_bytes(GGML_Q8_0, K)
+    rows_u = wu_blocks.numel() // row_bytes(GGML_Q8_0, K)
+    dispatch_batch_matmul_swiglu(default_graph(), Tensor.quantized(wg_blocks, GGML_Q8_0, rows_g, K),
+                                 Tensor.quantized(wu_blocks, GGML_Q8_0, rows_u, K),
+                                 Tensor.from_torch(x), Tensor.from_torch(out), out_dim, K, M)
     return out
 
 

@@ -8,6 +8,8 @@ Shapes are in GEMM form: M = tokens (seq_len), N = out_dim, K = in_dim.
   flux_linear1    Flux single-stream fused QKV+MLP-in, Q4_K, bf16 [4608, 3072] -> 21504
   flux_linear2    Flux single-stream output projection, Q4_K, bf16 [4608, 15360] -> 3072
   zimage_*        Z-Image block GEMMs (Q8_0, bf16 activations, S = 4096 + 256)
+  zimage_swiglu   Z-Image FFN in-projection: silu(x Wg^T) * (x Wu^T), Q8_0 gate and
+                  up [10240, 3840], bf16 [4352, 3840] (batch_matmul_swiglu_q8)
 Weights are N(0, 0.02), activations N(0, 1), all from llmr_amd.synth streams.
 """
 from __future__ import annotations
@@ -44,6 +46,21 @@ class Gemm:
 
 
 @dataclasses.dataclass(frozen=True)
+class SwiGLU(Gemm):
+    """Two GEMMs sharing the activations (gate weight from w_stream, up weight
+    from w_stream + 1) and one f32 output."""
+
+    @property
+    def flops(self) -> float:
+        return 4.0 * self.M * self.N * self.K
+
+    @property
+    def bytes(self) -> int:
+        xb = 4 if self.xtype == gguf.GGML_F32 else 2
+        return 2 * self.N * gguf.row_bytes(self.wtype, self.K) + self.M * self.K * xb + self.M * self.N * 4
+
+
+@dataclasses.dataclass(frozen=True)
 class Attention:
     name: str
     H: int
@@ -71,9 +88,11 @@ FLUX_LINEAR2 = Gemm("flux_linear2", 4608, 3072, 15360, gguf.GGML_Q4_K, gguf.GGML
 ZIMAGE_QKV = Gemm("zimage_qkv", 4352, 11520, 3840, gguf.GGML_Q8_0, gguf.GGML_BF16, 10, 11)
 ZIMAGE_O = Gemm("zimage_o", 4352, 3840, 3840, gguf.GGML_Q8_0, gguf.GGML_BF16, 12, 13)
 ZIMAGE_DOWN = Gemm("zimage_down", 4352, 3840, 10240, gguf.GGML_Q8_0, gguf.GGML_BF16, 14, 15)
+ZIMAGE_SWIGLU = SwiGLU("zimage_swiglu", 4352, 10240, 3840, gguf.GGML_Q8_0, gguf.GGML_BF16, 16, 17)
 ZIMAGE_ATTENTION = Attention("zimage_attention", 30, 4352, 128, 256, 64, 64, (32, 48, 48), 256.0)
 
 GEMMS = {g.name: g for g in (Q8_LINEAR, FLUX_LINEAR1, FLUX_LINEAR2, ZIMAGE_QKV, ZIMAGE_O, ZIMAGE_DOWN)}
+SWIGLUS = {g.name: g for g in (ZIMAGE_SWIGLU,)}
 
 
 def gemm_weight_f32(g: Gemm) -> np.ndarray:
@@ -82,6 +101,12 @@ def gemm_weight_f32(g: Gemm) -> np.ndarray:
 
 def gemm_weight_blocks(g: Gemm) -> np.ndarray:
     return gguf.quantize(gemm_weight_f32(g), g.wtype)
+
+
+def swiglu_up_blocks(g: SwiGLU) -> np.ndarray:
+    """The up weight of a SwiGLU workload (gemm_weight_blocks gives the gate)."""
+    w = synth.normal(SEED, g.w_stream + 1, g.N * g.K, 0.02).reshape(g.N, g.K)
+    return gguf.quantize(w, g.wtype)
 
 
 def gemm_activations_f32(g: Gemm) -> np.ndarray:

@@ -34,6 +34,9 @@
  *   orc_batch_matmul_q8/q4k  float64 brute force on small shapes (tolerance
  *                            from the fp16 operand rounding), identity weights,
  *                            linearity in X, row_offset slicing == fused call.
+ *   orc_batch_matmul_swiglu_q8  float64 brute force (dequantized weights,
+ *                            silu(g) * u) on small shapes; gate/up swapped or
+ *                            sigmoid-instead-of-silu restatements must fail it.
  *   orc_flash_attention      float64 textbook softmax attention on small shapes;
  *                            constant V -> O = V; S = 1 -> O = V; key permutation
  *                            invariance.
@@ -424,6 +427,65 @@ void orc_batch_matmul_q8(const uint8_t* W, const float* X, float* Y, uint32_t N,
     uint32_t* rows = (uint32_t*)malloc(sizeof(uint32_t) * (M ? M : 1));
     for (uint32_t i = 0; i < M; i++) rows[i] = i;
     orc_batch_matmul_q8_rows(W, X, Y, N, K, M, row_offset, rows, M);
+    free(rows);
+}
+
+/* batch_matmul_swiglu_q8 (llm.slang:1769-1911), restricted to output rows
+ * `rows`. Unlike batch_matmul_q8 everything is f32: the activations are not
+ * rounded and the weight is dequant_q8_at = f32(d) * q (llm.slang:1797-1813,
+ * exact in f32). Per output: g = u = 0; for t in 0..K/32-1: for k in 0..31:
+ *   g += a_k * bg_k;  u += a_k * bu_k       (one rounding per mul and add here;
+ * the reference leaves contraction of these to its shader compiler, so an
+ * FMA there differs by an ulp per step, far inside the GEMM tolerance)
+ * then out = silu(g) * u with silu(g) = g / (1 + exp(-g)) (llm.slang:1901-1904). */
+void orc_batch_matmul_swiglu_q8_rows(const uint8_t* Wg, const uint8_t* Wu, const float* X, float* Y,
+                                     uint32_t N, uint32_t K, uint32_t M, const uint32_t* rows,
+                                     uint32_t n_rows) {
+    (void)M;
+    const size_t bpr = K / 32;
+    uint32_t nblk = (N + ORC_NB - 1) / ORC_NB;
+#pragma omp parallel for schedule(dynamic)
+    for (uint32_t jb = 0; jb < nblk; jb++) {
+        uint32_t n0 = jb * ORC_NB;
+        uint32_t nn = N - n0 < ORC_NB ? N - n0 : ORC_NB;
+        float* BG = (float*)calloc((size_t)K * ORC_NB, sizeof(float));
+        float* BU = (float*)calloc((size_t)K * ORC_NB, sizeof(float));
+        float* tmp = (float*)malloc(sizeof(float) * K);
+        for (uint32_t j = 0; j < nn; j++) {
+            orc_dequant_q8_0(Wg + (size_t)(n0 + j) * bpr * 34, bpr, tmp);
+            for (uint32_t k = 0; k < K; k++) BG[(size_t)k * ORC_NB + j] = tmp[k];
+            orc_dequant_q8_0(Wu + (size_t)(n0 + j) * bpr * 34, bpr, tmp);
+            for (uint32_t k = 0; k < K; k++) BU[(size_t)k * ORC_NB + j] = tmp[k];
+        }
+        float g[ORC_NB], u[ORC_NB];
+        for (uint32_t r = 0; r < n_rows; r++) {
+            const float* a = X + (size_t)rows[r] * K;
+            for (int j = 0; j < ORC_NB; j++) g[j] = u[j] = 0.0f;
+            for (uint32_t k = 0; k < K; k++) {
+                const float ak = a[k];
+                const float* bg = BG + (size_t)k * ORC_NB;
+                const float* bu = BU + (size_t)k * ORC_NB;
+                for (int j = 0; j < ORC_NB; j++) {
+                    g[j] += ak * bg[j];
+                    u[j] += ak * bu[j];
+                }
+            }
+            for (uint32_t j = 0; j < nn; j++) {
+                const float silu = g[j] / (1.0f + expf(-g[j]));
+                Y[(size_t)r * N + n0 + j] = silu * u[j];
+            }
+        }
+        free(tmp);
+        free(BU);
+        free(BG);
+    }
+}
+
+void orc_batch_matmul_swiglu_q8(const uint8_t* Wg, const uint8_t* Wu, const float* X, float* Y, uint32_t N,
+                                uint32_t K, uint32_t M) {
+    uint32_t* rows = (uint32_t*)malloc(sizeof(uint32_t) * (M ? M : 1));
+    for (uint32_t i = 0; i < M; i++) rows[i] = i;
+    orc_batch_matmul_swiglu_q8_rows(Wg, Wu, X, Y, N, K, M, rows, M);
     free(rows);
 }
 

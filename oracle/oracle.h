@@ -73,6 +73,15 @@ void orc_batch_matmul_q4k_rows(const uint8_t* W, const float* X, float* Y, uint3
                                uint32_t K, uint32_t M, uint32_t row_offset,
                                const uint32_t* rows, uint32_t n_rows);
 
+/* batch_matmul_swiglu_q8 (llm.slang:1769-1911): Wg, Wu Q8_0 [N, K] (rows from
+ * 0), all f32 (a = x, b = f32(d)*q), out = silu(g) * u, silu(g) = g/(1+exp(-g));
+ * X f32 [M, K], Y f32 [M, N] (the _rows form: [n_rows, N]). */
+void orc_batch_matmul_swiglu_q8(const uint8_t* Wg, const uint8_t* Wu, const float* X, float* Y, uint32_t N,
+                                uint32_t K, uint32_t M);
+void orc_batch_matmul_swiglu_q8_rows(const uint8_t* Wg, const uint8_t* Wu, const float* X, float* Y,
+                                     uint32_t N, uint32_t K, uint32_t M, const uint32_t* rows,
+                                     uint32_t n_rows);
+
 /* flash_attention_v2 (flash_attn.slang:38-241): Q/K/V f32 [H,S,D] rounded to
  * fp16, BR=16 query rows, BC=32 key tiles, f32 online softmax, tree-reduced
  * tile sums; O f32 [S, H*D]. Restricted to heads [h0, h1) and query rows

@@ -52,6 +52,8 @@ def lib():
             "orc_batch_matmul_q8": (None, [_u8p, _f32p, _f32p, _u32, _u32, _u32, _u32]),
             "orc_batch_matmul_q4k": (None, [_u8p, _f32p, _f32p, _u32, _u32, _u32, _u32]),
             "orc_batch_matmul_q8_rows": (None, [_u8p, _f32p, _f32p, _u32, _u32, _u32, _u32, _u32p, _u32]),
+            "orc_batch_matmul_swiglu_q8": (None, [_u8p, _u8p, _f32p, _f32p, _u32, _u32, _u32]),
+            "orc_batch_matmul_swiglu_q8_rows": (None, [_u8p, _u8p, _f32p, _f32p, _u32, _u32, _u32, _u32p, _u32]),
             "orc_batch_matmul_q4k_rows": (None, [_u8p, _f32p, _f32p, _u32, _u32, _u32, _u32, _u32p, _u32]),
             "orc_flash_attention": (None, [_f32p, _f32p, _f32p, _f32p, _u32, _u32, _u32, ctypes.c_float,
                                            _u32, _u32, _u32, _u32]),
@@ -165,6 +167,28 @@ def batch_matmul(W: np.ndarray, wtype: int, X: np.ndarray, out_dim: int, in_dim:
     fn = L.orc_batch_matmul_q8_rows if wtype == 8 else L.orc_batch_matmul_q4k_rows
     fn(_p(W, _u8p), _p(X, _f32p), _p(Y, _f32p), out_dim, in_dim, seq_len, row_offset,
        _p(r, _u32p), r.size)
+    return Y
+
+
+def batch_matmul_swiglu_q8(Wg: np.ndarray, Wu: np.ndarray, X: np.ndarray, out_dim: int, in_dim: int,
+                           seq_len: int, rows=None) -> np.ndarray:
+    """Reference SwiGLU GEMM (batch_matmul_swiglu_q8, llm.slang:1769-1911) on f32
+    activations X [seq_len, in_dim] and Q8_0 gate/up weights [out_dim, in_dim].
+    With `rows`, only those output rows are computed (result [len(rows), out_dim])."""
+    Wg = np.ascontiguousarray(Wg, dtype=np.uint8).reshape(-1)
+    Wu = np.ascontiguousarray(Wu, dtype=np.uint8).reshape(-1)
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    assert X.size == seq_len * in_dim
+    L = lib()
+    if rows is None:
+        Y = np.empty((seq_len, out_dim), np.float32)
+        L.orc_batch_matmul_swiglu_q8(_p(Wg, _u8p), _p(Wu, _u8p), _p(X, _f32p), _p(Y, _f32p), out_dim, in_dim,
+                                     seq_len)
+        return Y
+    r = np.ascontiguousarray(rows, dtype=np.uint32)
+    Y = np.empty((r.size, out_dim), np.float32)
+    L.orc_batch_matmul_swiglu_q8_rows(_p(Wg, _u8p), _p(Wu, _u8p), _p(X, _f32p), _p(Y, _f32p), out_dim, in_dim,
+                                      seq_len, _p(r, _u32p), r.size)
     return Y
 
 

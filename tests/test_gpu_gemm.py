@@ -174,3 +174,108 @@ def test_full_size_sampled_rows(orc, dev, name):
     y1 = y1.cpu().numpy()[0]
     assert rel_l2(y1, ref[5]) <= TOL
     assert rel_l2(y1, y[m].cpu().numpy()) <= 2 * TOL
+
+
+SWIGLU_CASES = [
+    # (M, N, K, xtype)
+    (100, 256, 512, 30),   # bf16, fused kernel, ragged M
+    (300, 520, 1024, 1),   # f16, fused, N not a multiple of 128
+    (65, 260, 256, 0),     # f32 activations: rounded to bf16, then fused
+    (7, 34, 96, 30),       # N % 4 != 0 and K % 64 == 32: two GEMMs + elementwise SwiGLU
+    (1, 64, 64, 30),       # one token
+    (513, 1032, 768, 30),  # more tiles than workgroups in one round on small GPUs
+]
+
+
+@pytest.mark.parametrize("M,N,K,xtype", SWIGLU_CASES)
+def test_swiglu_parity(orc, dev, M, N, K, xtype):
+    from llmr_amd import gguf, ops, synth
+    wg = gguf.quantize_q8_0(synth.normal(21, 1, N * K, 0.05))
+    wu = gguf.quantize_q8_0(synth.normal(21, 2, N * K, 0.05))
+    x = synth.normal(21, 3, M * K).reshape(M, K)
+    import torch
+    xt = _torch_x(x, xtype, dev)
+    y = ops.batch_matmul_swiglu(torch.from_numpy(wg).to(dev), torch.from_numpy(wu).to(dev), xt, N)
+    torch.cuda.synchronize()
+    ref = orc.batch_matmul_swiglu_q8(wg, wu, _x_as_f32(xt), N, K, M)
+    err = rel_l2(y.cpu().numpy(), ref)
+    print(f"swiglu M={M} N={N} K={K} xtype={xtype}: rel_l2={err:.3e}")
+    assert np.all(np.isfinite(y.cpu().numpy()))
+    assert err <= TOL
+    # gate and up are not interchangeable: the swapped product is far off
+    swapped = orc.batch_matmul_swiglu_q8(wu, wg, _x_as_f32(xt), N, K, M)
+    assert rel_l2(y.cpu().numpy(), swapped) > 10 * TOL
+
+
+def test_swiglu_matches_two_gemms(dev):
+    """The fused kernel equals silu(gate GEMM) * up GEMM from the plain entry point
+    (f16 activations: the same fp16 operands on both paths) to f32 rounding."""
+    import torch
+    from llmr_amd import gguf, ops, synth
+    M, N, K = 512, 512, 1024
+    wg = torch.from_numpy(gguf.quantize_q8_0(synth.normal(22, 1, N * K, 0.05))).to(dev)
+    wu = torch.from_numpy(gguf.quantize_q8_0(synth.normal(22, 2, N * K, 0.05))).to(dev)
+    x = _torch_x(synth.normal(22, 3, M * K).reshape(M, K), 1, dev)
+    y = ops.batch_matmul_swiglu(wg, wu, x, N)
+    g = ops.batch_matmul(wg, 8, x, N)
+    u = ops.batch_matmul(wu, 8, x, N)
+    torch.cuda.synchronize()
+    ref = (g / (1 + torch.exp(-g)) * u).cpu().numpy()
+    assert rel_l2(y.cpu().numpy(), ref) < 1e-5
+
+
+def test_swiglu_pc_rejects_row_offset(dev):
+    import ctypes
+    import torch
+    from llmr_amd import capi, gguf, ops, synth
+    N, K, M = 64, 64, 4
+    w = torch.from_numpy(gguf.quantize_q8_0(synth.normal(23, 1, N * K, 0.05))).to(dev)
+    x = torch.zeros((M, K), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    g = ops.default_graph()
+    g.bind_stream()
+    pc = capi.BatchMatMulParams(N, K, M, 1)
+    rc = capi.lib().llmr_batch_matmul_swiglu_pc(g.ctx.handle, w.data_ptr(), w.data_ptr(), 8, x.data_ptr(), 30,
+                                                y.data_ptr(), ctypes.byref(pc))
+    assert rc == capi.LLMR_ERR_INVALID_ARG
+    rc = capi.lib().llmr_batch_matmul_swiglu(g.ctx.handle, w.data_ptr(), w.data_ptr(), 12, x.data_ptr(), 30,
+                                             y.data_ptr(), N, K, M)
+    assert rc == capi.LLMR_ERR_UNSUPPORTED
+
+
+def test_swiglu_full_size_sampled(orc, dev):
+    """The Z-Image FFN in-projection at full size; sampled tokens vs the oracle."""
+    import torch
+    from llmr_amd import ops, workloads
+    g = workloads.ZIMAGE_SWIGLU
+    wg_np = workloads.gemm_weight_blocks(g)
+    wg = torch.from_numpy(wg_np).to(dev)
+    wu_np = workloads.swiglu_up_blocks(g)
+    wu = torch.from_numpy(wu_np).to(dev)
+    x = workloads.gemm_activations_f32(g)
+    xt = _torch_x(x, g.xtype, dev)
+    y = ops.batch_matmul_swiglu(wg, wu, xt, g.N)
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, 255, 256, 2049, g.M - 2, g.M - 1], np.uint32)
+    ref = orc.batch_matmul_swiglu_q8(wg_np, wu_np, x, g.N, g.K, g.M, rows=rows)
+    got = y[torch.from_numpy(rows.astype(np.int64)).to(dev)].cpu().numpy()
+    err = rel_l2(got, ref)
+    print(f"zimage_swiglu: sampled rel_l2={err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 128, 512), (2304, 2304, 512)])
+def test_bf16_activations_beyond_fp16_range(orc, dev, M, N, K):
+    """bf16 activations of magnitude ~1e5 (past fp16's 65504) stay finite: every
+    kernel uses bf16 operands for bf16 inputs (small launch: 4-wave tiles;
+    large: the persistent kernel). Q4_K keeps the reference's all-f32 operand."""
+    import torch
+    from llmr_amd import gguf, ops, synth
+    blk = gguf.quantize_q4k(synth.normal(24, 1, N * K, 0.02))
+    x = synth.normal(24, 2, M * K).reshape(M, K) * np.float32(1.0e5)
+    y, xr = _run(dev, blk, 12, x, 30, N)
+    rows = np.array([0, M // 2, M - 1], np.uint32)
+    ref = orc.batch_matmul(blk, 12, xr, N, K, M, 0, rows=rows)
+    assert np.all(np.isfinite(y))
+    assert np.abs(xr).max() > 65504.0
+    assert rel_l2(y[rows.astype(np.int64)], ref) <= TOL

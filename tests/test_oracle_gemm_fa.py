@@ -63,6 +63,51 @@ def test_gemm_row_offset_is_column_slice(orc, wtype):
     assert np.array_equal(rows, full[[2, 0]])
 
 
+def _silu64(g):
+    return g / (1.0 + np.exp(-g))
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 7, 64), (3, 40, 320), (1, 9, 512)])
+def test_swiglu_gemm_vs_float64(orc, M, N, K):
+    """silu(x Wg^T) * (x Wu^T) with f32 activations and the exact f32 dequant
+    (batch_matmul_swiglu_q8), against float64; a gate/up swap, a missing g
+    factor (sigmoid instead of silu) or fp16-rounded operands all fail it."""
+    wg = gguf.quantize_q8_0(synth.normal(4, 1, N * K, 0.05))
+    wu = gguf.quantize_q8_0(synth.normal(4, 2, N * K, 0.05))
+    x = synth.normal(4, 3, M * K).reshape(M, K)
+    got = orc.batch_matmul_swiglu_q8(wg, wu, x, N, K, M)
+    bg = orc.dequant_q8_0(wg).astype(np.float64).reshape(N, K)
+    bu = orc.dequant_q8_0(wu).astype(np.float64).reshape(N, K)
+    x64 = x.astype(np.float64)
+    g, u = x64 @ bg.T, x64 @ bu.T
+    exp = _silu64(g) * u
+    # f32 accumulation of K products each rounded once, then silu and the product
+    eg = 2 * K * 2.0**-24 * (np.abs(x64) @ np.abs(bg).T)
+    eu = 2 * K * 2.0**-24 * (np.abs(x64) @ np.abs(bu).T)
+    bound = eg * np.abs(u) * 1.2 + eu * np.abs(_silu64(g)) + 8 * 2.0**-24 * np.abs(exp) + 1e-30
+    assert np.all(np.abs(got - exp) <= bound)
+    for wrong in (_silu64(u) * g, g / (1.0 + np.exp(-g)) / np.where(g == 0, 1, g) * u):
+        assert rel_l2(got, wrong) > 1e-2
+    rows = orc.batch_matmul_swiglu_q8(wg, wu, x, N, K, M, rows=[M - 1, 0])
+    assert np.array_equal(rows, got[[M - 1, 0]])
+
+
+def test_swiglu_special_values(orc):
+    """g = 0 gives 0 whatever u; a large negative g gives -0 * u; u = 0 gives 0."""
+    N, K = 4, 32
+    w0 = np.zeros((N, K), np.float32)
+    wg = w0.copy()
+    wg[1, 0] = -60.0  # g = -60 x0
+    wg[2, 0] = 1.0
+    wu = np.ones((N, K), np.float32)
+    wu[2] = 0.0
+    x = np.zeros((1, K), np.float32)
+    x[0, 0] = 1.0
+    got = orc.batch_matmul_swiglu_q8(gguf.quantize_q8_0(wg), gguf.quantize_q8_0(wu), x, N, K, 1)[0]
+    assert got[0] == 0.0 and got[2] == 0.0 and got[3] == 0.0
+    assert abs(got[1]) < 1e-20
+
+
 def _attn64(q, k, v, scale):
     q, k, v = (_f16(t) for t in (q, k, v))
     H, S, D = q.shape
