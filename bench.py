@@ -10,8 +10,9 @@ for a GEMM workload one dequant-GEMM launch. Rank 0 prints one JSON line:
 `value` is the workload's TFLOP/s (4*H*S^2*D or 2*M*N*K per step), timed
 with HIP events on the stream the kernels run on; `components` carries the
 same measurement for the other configurations (Q4_K Flux linears, the Q8_0
-linear, the Z-Image QKV projection) so the three-part headline metric is
-reported in one line. `roofline` describes the workload's kernel,
+linear, the Z-Image QKV and SwiGLU projections) and the composed ones: one
+full Z-Image block and one Flux-dev-shaped denoising step (ms/step), so the
+three-part headline metric is reported in one line. `roofline` describes the workload's kernel,
 `cpu_baseline` the oracle timed on a bounded sample on the host cores.
 """
 from __future__ import annotations
@@ -114,6 +115,58 @@ def setup_swiglu(dev, name):
     return step, g.flops, g.bytes, cfg, "bf16" if g.xtype == gguf.GGML_BF16 else "f16"
 
 
+def setup_zimage_block(dev):
+    """One Z-Image DiT block at full size (hidden 3840, 30 heads, FFN 10240,
+    4096 image + 256 text tokens), Q8_0 weights, bf16 activations."""
+    import torch
+    from llmr_amd import dit, synth, workloads
+    dim, H, ffn = 3840, 30, 10240
+    a = workloads.ZIMAGE_ATTENTION
+    S = a.S
+    w = dit.zimage_layer_weights(dim, H, ffn, device=dev)
+    cos_t, sin_t = workloads.rope_tables(workloads.attention_positions(a), a.axes, a.theta)
+    rope = (torch.from_numpy(cos_t).to(dev), torch.from_numpy(sin_t).to(dev))
+    h0 = workloads.round_bf16(synth.normal(workloads.SEED, 10, S * dim).reshape(S, dim))
+    hidden = torch.from_numpy(h0).to(dev)
+    blk = dit.ZImageBlock(dim, H, ffn, S, act_dtype=torch.bfloat16, device=dev)
+
+    def step():
+        blk.forward(w, hidden, *rope)
+
+    flops = 2.0 * S * dim * (3 * dim + dim + 2 * ffn + ffn) + a.flops
+    cfg = {"workload": "zimage_block", "hidden": dim, "heads": H, "head_dim": 128, "ffn": ffn, "seq_len": S,
+           "weights": "Q8_0", "activations": "bf16", "sequence": "rmsnorm*scale, qkv, headnorm+rope, attention, "
+           "o-proj, postnorm+tanh-gated residual, rmsnorm*scale, swiglu, down, postnorm+tanh-gated residual"}
+    return step, flops, None, cfg, "bf16"
+
+
+def setup_flux_step(dev):
+    """One denoising forward of the Flux-dev-shaped DiT (19 double + 38 single
+    blocks, hidden 3072, 24 heads, MLP 12288, Q4_K weights generated on the
+    device, 4096 image tokens from 16x128x128 latents + 512 text tokens)."""
+    import torch
+    from llmr_amd import dit, synth, workloads
+    cfg_m = dit.FLUX_DEV
+    glob, doubles, singles = dit.flux_weights(cfg_m, device=dev)
+    model = dit.FluxDiT(cfg_m, glob, doubles, singles, act_dtype=torch.bfloat16, device=dev)
+    lat = torch.from_numpy(synth.normal(workloads.SEED, 30, cfg_m.latent_ch * cfg_m.latent_h * cfg_m.latent_w)
+                           .reshape(cfg_m.latent_ch, cfg_m.latent_h, cfg_m.latent_w)).to(dev)
+    txt = torch.from_numpy(synth.normal(workloads.SEED, 31, cfg_m.n_txt * cfg_m.text_dim)
+                           .reshape(cfg_m.n_txt, cfg_m.text_dim)).to(dev).to(torch.bfloat16)
+
+    def step():
+        model.forward(lat, txt, 0.5)
+
+    cfg = {"workload": "flux_step", "double_blocks": cfg_m.n_double, "single_blocks": cfg_m.n_single,
+           "hidden": cfg_m.dim, "heads": cfg_m.n_heads, "mlp": cfg_m.mlp, "img_tokens": cfg_m.n_img,
+           "txt_tokens": cfg_m.n_txt, "weights": "Q4_K (img_in Q8_0)", "activations": "bf16",
+           "timestep": 0.5, "mlp_act": "gelu-tanh", "modulation": "per block"}
+    return step, cfg_m.gemm_flops(), None, cfg, "bf16"
+
+
+MODEL_SETUPS = {"zimage_block": setup_zimage_block, "flux_step": setup_flux_step}
+
+
 def gemm_kernel_name(name: str, num_cus: int) -> str:
     """The kernel the library's dispatch picks for a GEMM workload: the
     persistent 256x256 kernel for 16-bit activations with at least half the
@@ -132,6 +185,8 @@ def measure(dev, name, steps, warmup):
     from llmr_amd import workloads
     if name == "flux_attention":
         step, flops, nbytes, cfg, dtype = setup_attention(dev)
+    elif name in MODEL_SETUPS:
+        step, flops, nbytes, cfg, dtype = MODEL_SETUPS[name](dev)
     elif name in workloads.SWIGLUS:
         step, flops, nbytes, cfg, dtype = setup_swiglu(dev, name)
     else:
@@ -203,7 +258,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="flux_attention")
-    ap.add_argument("--components", default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu")
+    ap.add_argument("--components",
+                    default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu,zimage_block,flux_step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--hbm-copy-calibration", action="store_true",
                     help="time a plain 1 GiB device copy (reference for the FETCH_SIZE/WRITE_SIZE counters)")
@@ -226,11 +282,18 @@ def main():
     main_r = measure(dev, args.workload, args.steps, args.warmup)
     comps = {}
     for c in [c for c in args.components.split(",") if c and c != args.workload]:
-        r = measure(dev, c, max(5, args.steps // 2), args.warmup)
-        comps[c] = {"tflops": round(r["tflops"], 2), "ms_per_call": round(r["ms"], 4),
-                    "frac_of_peak": round(r["tflops"] / PEAK_TFLOPS, 4),
-                    "hbm_gbs_algorithmic": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1),
-                    "config": r["cfg"]}
+        if c in MODEL_SETUPS:  # whole blocks / steps: fewer, longer steps
+            r = measure(dev, c, max(3, args.steps // 10), max(1, args.warmup // 2))
+            comps[c] = {"ms_per_step": round(r["ms"], 3), "median_ms": round(r["median_ms"], 3),
+                        "tflops_gemm_attention": round(r["tflops"], 2),
+                        "frac_of_peak": round(r["tflops"] / PEAK_TFLOPS, 4), "config": r["cfg"]}
+        else:
+            r = measure(dev, c, max(5, args.steps // 2), args.warmup)
+            comps[c] = {"tflops": round(r["tflops"], 2), "ms_per_call": round(r["ms"], 4),
+                        "frac_of_peak": round(r["tflops"] / PEAK_TFLOPS, 4),
+                        "hbm_gbs_algorithmic": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1),
+                        "config": r["cfg"]}
+        print(f"# {c}: {json.dumps(comps[c])}", file=sys.stderr, flush=True)
 
     ach = main_r["tflops"]
     roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",

@@ -209,6 +209,119 @@ LLMR_API int llmr_flash_attention_pc(llmr_context* ctx, const void* q, const voi
                                      const void* v, uint32_t qkv_type, float* out,
                                      const llmr_flash_attention_params* pc);
 
+/* ---------------------------------------------------------------------------
+ * Block glue: the row reductions and elementwise ops the DiT blocks run
+ * between the GEMMs and attention. Each replaces a chain of the reference's
+ * dispatches over one tensor with one pass, and writes its result directly in
+ * the type the next GEMM or attention call reads (out_type F32, F16 or BF16),
+ * so a block never round-trips f32 activations through memory just to convert
+ * them. All math is f32 in the reference's operation order.
+ * Shared preconditions: dims, row strides and column offsets are in elements
+ * and multiples of 4 (8-byte / 16-byte vector accesses); pointers 16-byte
+ * aligned; row widths (dim) at most 8192. Strides let a call address a row
+ * range or column slice of a larger buffer (e.g. the image rows of a joint
+ * text+image sequence) without a copy.
+ * ------------------------------------------------------------------------- */
+
+enum { LLMR_ACT_COPY = 0, LLMR_ACT_SILU = 1, LLMR_ACT_GELU_TANH = 2, LLMR_ACT_SILU_MUL = 3 };
+enum { LLMR_GATE_NONE = 0, LLMR_GATE_LINEAR = 1, LLMR_GATE_TANH = 2 };
+
+/* out[r, d] = x[r, d] * (1 / sqrt(sum_d x[r, d]^2 / dim + eps)) * weight[d],
+ * then *= 1 + mod_scale[d] and += mod_shift[d] where those are non-null.
+ * x f32 [n_rows, x_stride], out [n_rows, out_stride] of out_type.
+ * Replaces batch_rmsnorm followed by scale_modulate
+ * (dependencies/zimage.c3l/dit.c3:1424-1432, 1546-1554; kernels
+ * dependencies/zimage.c3l/shaders/zimage.slang:449-500, 356-373). */
+LLMR_API int llmr_batch_rmsnorm(llmr_context* ctx, const float* x, uint32_t x_stride, const float* weight,
+                                const float* mod_scale, const float* mod_shift, void* out, uint32_t out_type,
+                                uint32_t out_stride, uint32_t dim, uint32_t n_rows, float eps);
+
+/* out[r, d] = (x[r, d] - mean_r) * (1 / sqrt(var_r + eps)) (no affine;
+ * two-pass mean and variance), then *= 1 + mod_scale[d] and += mod_shift[d]
+ * where non-null. Replaces batch_layernorm followed by adaln_modulate
+ * (dependencies/flux.c3l/flux_dit.c3:767-770, 992-995, 1186-1191; kernels
+ * zimage.slang:502-561, 98-117). */
+LLMR_API int llmr_batch_layernorm(llmr_context* ctx, const float* x, uint32_t x_stride, const float* mod_scale,
+                                  const float* mod_shift, void* out, uint32_t out_type, uint32_t out_stride,
+                                  uint32_t dim, uint32_t n_rows, float eps);
+
+/* Per-head RMSNorm + rotary embedding + head-major transpose of a QKV GEMM
+ * output. qkv f32 [n_rows, qkv_stride] holds Q | K | V, each n_heads*128
+ * wide, starting at column 0. For row r (sequence position t = row0 + r),
+ * head h, pair j < 64:
+ *   x = qkv[r, slot*n_heads*128 + h*128 + 2j .. 2j+1]
+ *   Q, K: x *= (1 / sqrt(sum_head x^2 / 128 + eps)) * norm[2j .. 2j+1]   (norm non-null)
+ *   Q, K: (x0, x1) -> (x0*c - x1*s, x0*s + x1*c), c/s = rope_cos/sin[t, j]
+ *         (tables f32 [seq_len, 64], both null for no rotation)
+ *   out_slot[h, t, 2j .. 2j+1] = x    (q, k, v [n_heads, seq_len, 128] of out_type)
+ * row0 + n_rows <= seq_len; the tables must hold seq_len rows. Replaces
+ * batch_head_norm x2 + transpose_heads x3 + mrope x2
+ * (dependencies/zimage.c3l/dit.c3:1448-1473, dependencies/flux.c3l/flux_dit.c3:
+ * 814-863, 1022-1040; kernels zimage.slang:563-667,
+ * dependencies/zimage.c3l/shaders/mrope.slang:33-54). Two calls with
+ * different norms and row0 fill the text and image rows of a joint sequence. */
+LLMR_API int llmr_qkv_heads(llmr_context* ctx, const float* qkv, uint32_t qkv_stride, uint32_t n_rows,
+                            uint32_t n_heads, const float* q_norm, const float* k_norm, float eps,
+                            const float* rope_cos, const float* rope_sin, void* q, void* k, void* v,
+                            uint32_t out_type, uint32_t seq_len, uint32_t row0);
+
+/* residual[r, d] += g * y with y = input[r, d], RMS-normalised with
+ * norm_weight first when that is non-null (eps as batch_rmsnorm), and
+ *   LLMR_GATE_NONE:   g * y = y                          (residual_add)
+ *   LLMR_GATE_LINEAR: g * y = gate[d] * y                (gated_residual_linear)
+ *   LLMR_GATE_TANH:   clamp(tanh(gate[d]) * y, +-1e10)   (gated_residual, scale 1)
+ * residual f32 [n_rows, residual_stride] updated in place, input f32.
+ * Replaces the post-norm + gated residual pairs of the Z-Image block
+ * (dependencies/zimage.c3l/dit.c3:1495-1503, 1602-1610) and Flux's
+ * gated_residual_linear (dependencies/flux.c3l/flux_dit.c3:891-898, 1067-1068;
+ * kernels zimage.slang:382-424, lib/shaders/diffusion.slang:1713-1716). */
+LLMR_API int llmr_gated_residual(llmr_context* ctx, float* residual, uint32_t residual_stride, const float* input,
+                                 uint32_t input_stride, const float* norm_weight, const float* gate,
+                                 uint32_t gate_mode, uint32_t dim, uint32_t n_rows, float eps);
+
+/* dst[r, dst_col + c] = f(src[r, src_col + c]) for c < n_cols with
+ *   LLMR_ACT_COPY      x                         (a cast / column copy)
+ *   LLMR_ACT_SILU      x / (1 + exp(-x))
+ *   LLMR_ACT_GELU_TANH 0.5*x*(1 + tanh(0.7978845608*(x + 0.044715*x^3)))
+ *   LLMR_ACT_SILU_MUL  silu(x) * src[r, src2_col + c]
+ * src f32 [n_rows, src_stride]; dst [n_rows, dst_stride] of dst_type.
+ * Replaces silu + elemwise_mul (dependencies/flux.c3l/flux_dit.c3:929-931,
+ * 1051-1053; kernels lib/shaders/diffusion.slang:1082-1086, 1733-1736), gelu
+ * (diffusion.slang:1092-1107) and the single-stream concat_rows_copy
+ * (flux_dit.c3:625-660, 1057): the
+ * attention output and the activated MLP half are written into the column
+ * ranges [0, dim) and [dim, dim + mlp) of linear2's input. */
+LLMR_API int llmr_activation(llmr_context* ctx, const float* src, uint32_t src_stride, uint32_t src_col,
+                             uint32_t src2_col, void* dst, uint32_t dst_type, uint32_t dst_stride, uint32_t dst_col,
+                             uint32_t n_rows, uint32_t n_cols, uint32_t act);
+
+/* out[i] = cos(t * f_i) for i < dim/2 and sin(t * f_(i - dim/2)) above, with
+ * f_j = exp(-ln(10000) * j / (dim/2)); dim even. Replaces dit_timestep_embed
+ * (dependencies/flux.c3l/flux_dit.c3:1121-1123; kernel zimage.slang:284-307). */
+LLMR_API int llmr_timestep_embed(llmr_context* ctx, float* out, uint32_t dim, float timestep);
+
+/* latent f32 [channels, height, width] -> out [(height/p)*(width/p),
+ * channels*p*p] of out_type, element (py*p + px)*channels + c of each patch.
+ * Replaces patchify (dependencies/flux.c3l/flux_dit.c3:1096-1100; kernel
+ * zimage.slang:11-51). */
+LLMR_API int llmr_patchify(llmr_context* ctx, const float* latent, void* out, uint32_t out_type,
+                           uint32_t channels, uint32_t height, uint32_t width, uint32_t patch_size);
+
+/* The inverse permutation, f32 (unpatchify, flux_dit.c3:1196-1202; kernel
+ * zimage.slang:56-93). */
+LLMR_API int llmr_unpatchify(llmr_context* ctx, const float* patches, float* out, uint32_t channels,
+                             uint32_t height, uint32_t width, uint32_t patch_size);
+
+/* Synthetic Q4_K weights generated on the device: out receives
+ * n_rows * in_dim/256 blocks (144 B each) of values ~N(0, std^2) drawn from
+ * the counter-based stream (seed, stream) and quantized per superblock.
+ * Byte-identical to the host-side generator + quantizer of the Python
+ * package (llmr_amd.synth.normal, llmr_amd.gguf.quantize_q4k). Test and
+ * benchmark setup only; the reference loads real GGUF weights instead
+ * (lib/model/tensor.c3:48-66). in_dim % 256 == 0. */
+LLMR_API int llmr_synth_q4k(llmr_context* ctx, void* out, uint64_t n_rows, uint32_t in_dim, uint64_t seed,
+                            uint64_t stream, double std);
+
 #ifdef __cplusplus
 }
 #endif

@@ -294,3 +294,187 @@ int llmr_flash_attention_pc(llmr_context* ctx, const void* q, const void* k, con
 }
 
 }  // extern "C"
+
+// --- block glue ---------------------------------------------------------------
+
+namespace {
+
+// A row-major [rows, stride] operand accessed in 4-element vectors over `width` columns.
+int check_rows(const void* p, const char* what, uint32_t stride, uint32_t width) {
+    if (!p) return fail(LLMR_ERR_INVALID_ARG, "null %s pointer", what);
+    if (!aligned(p, 16)) return fail(LLMR_ERR_INVALID_ARG, "%s pointer must be 16-byte aligned", what);
+    if (stride % 4) return fail(LLMR_ERR_INVALID_ARG, "%s row stride must be a multiple of 4 (got %u)", what, stride);
+    if (stride < width) return fail(LLMR_ERR_INVALID_ARG, "%s row stride %u < row width %u", what, stride, width);
+    return LLMR_OK;
+}
+
+int check_vec(const void* p, const char* what, bool required) {
+    if (!p) return required ? fail(LLMR_ERR_INVALID_ARG, "null %s pointer", what) : LLMR_OK;
+    if (!aligned(p, 16)) return fail(LLMR_ERR_INVALID_ARG, "%s pointer must be 16-byte aligned", what);
+    return LLMR_OK;
+}
+
+int check_dim(uint32_t dim) {
+    if (dim == 0 || dim % 4 || dim > llmr::kRowNormMaxDim)
+        return fail(LLMR_ERR_INVALID_ARG, "dim must be a positive multiple of 4 and <= %u (got %u)",
+                    llmr::kRowNormMaxDim, dim);
+    return LLMR_OK;
+}
+
+int launched(hipError_t e, const char* op) {
+    if (e != hipSuccess) return fail(LLMR_ERR_HIP, "%s launch: %s", op, hipGetErrorString(e));
+    return ok();
+}
+
+int row_norm_common(llmr_context* ctx, bool ln, const float* x, uint32_t x_stride, const float* weight,
+                    const float* mod_scale, const float* mod_shift, void* out, uint32_t out_type,
+                    uint32_t out_stride, uint32_t dim, uint32_t n_rows, float eps) {
+    if (int r = check_ctx(ctx)) return r;
+    if (!is_act_type(out_type)) return fail(LLMR_ERR_UNSUPPORTED, "output type %u not supported", out_type);
+    if (int r = check_dim(dim)) return r;
+    if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(LLMR_ERR_INVALID_ARG, "eps must be finite and >= 0");
+    if (n_rows == 0) return ok();
+    if (int r = check_rows(x, "x", x_stride, dim)) return r;
+    if (int r = check_rows(out, "out", out_stride, dim)) return r;
+    if (int r = check_vec(weight, "weight", !ln)) return r;
+    if (ln && weight) return fail(LLMR_ERR_INVALID_ARG, "batch_layernorm has no affine weight (pass null)");
+    if (int r = check_vec(mod_scale, "mod_scale", false)) return r;
+    if (int r = check_vec(mod_shift, "mod_shift", false)) return r;
+    llmr::RowNormArgs a{x, weight, mod_scale, mod_shift, out, x_stride, out_stride, n_rows, dim, eps};
+    return launched(llmr::launch_row_norm(a, ln, out_type, ctx->cur), ln ? "batch_layernorm" : "batch_rmsnorm");
+}
+
+}  // namespace
+
+extern "C" {
+
+int llmr_batch_rmsnorm(llmr_context* ctx, const float* x, uint32_t x_stride, const float* weight,
+                       const float* mod_scale, const float* mod_shift, void* out, uint32_t out_type,
+                       uint32_t out_stride, uint32_t dim, uint32_t n_rows, float eps) {
+    return row_norm_common(ctx, false, x, x_stride, weight, mod_scale, mod_shift, out, out_type, out_stride, dim,
+                           n_rows, eps);
+}
+
+int llmr_batch_layernorm(llmr_context* ctx, const float* x, uint32_t x_stride, const float* mod_scale,
+                         const float* mod_shift, void* out, uint32_t out_type, uint32_t out_stride, uint32_t dim,
+                         uint32_t n_rows, float eps) {
+    return row_norm_common(ctx, true, x, x_stride, nullptr, mod_scale, mod_shift, out, out_type, out_stride, dim,
+                           n_rows, eps);
+}
+
+int llmr_qkv_heads(llmr_context* ctx, const float* qkv, uint32_t qkv_stride, uint32_t n_rows, uint32_t n_heads,
+                   const float* q_norm, const float* k_norm, float eps, const float* rope_cos, const float* rope_sin,
+                   void* q, void* k, void* v, uint32_t out_type, uint32_t seq_len, uint32_t row0) {
+    if (int r = check_ctx(ctx)) return r;
+    if (!is_act_type(out_type)) return fail(LLMR_ERR_UNSUPPORTED, "output type %u not supported", out_type);
+    if (n_heads == 0 || n_heads > 1024) return fail(LLMR_ERR_INVALID_ARG, "n_heads must be in [1, 1024]");
+    if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(LLMR_ERR_INVALID_ARG, "eps must be finite and >= 0");
+    if ((uint64_t)row0 + n_rows > seq_len)
+        return fail(LLMR_ERR_INVALID_ARG, "row0 + n_rows (%llu) > seq_len %u",
+                    (unsigned long long)row0 + n_rows, seq_len);
+    if (n_rows == 0) return ok();
+    if (int r = check_rows(qkv, "qkv", qkv_stride, 3u * n_heads * 128u)) return r;
+    if (int r = check_vec(q_norm, "q_norm", false)) return r;
+    if (int r = check_vec(k_norm, "k_norm", false)) return r;
+    if ((rope_cos == nullptr) != (rope_sin == nullptr))
+        return fail(LLMR_ERR_INVALID_ARG, "rope_cos and rope_sin must both be given or both be null");
+    if (int r = check_vec(rope_cos, "rope_cos", false)) return r;
+    if (int r = check_vec(rope_sin, "rope_sin", false)) return r;
+    if (int r = check_vec(q, "q", true)) return r;
+    if (int r = check_vec(k, "k", true)) return r;
+    if (int r = check_vec(v, "v", true)) return r;
+    llmr::QkvHeadsArgs a{qkv, q_norm, k_norm, rope_cos, rope_sin, q, k, v, qkv_stride, n_rows, n_heads, seq_len,
+                         row0, eps};
+    return launched(llmr::launch_qkv_heads(a, out_type, ctx->cur), "qkv_heads");
+}
+
+int llmr_gated_residual(llmr_context* ctx, float* residual, uint32_t residual_stride, const float* input,
+                        uint32_t input_stride, const float* norm_weight, const float* gate, uint32_t gate_mode,
+                        uint32_t dim, uint32_t n_rows, float eps) {
+    if (int r = check_ctx(ctx)) return r;
+    if (gate_mode > LLMR_GATE_TANH) return fail(LLMR_ERR_INVALID_ARG, "unknown gate mode %u", gate_mode);
+    if (int r = check_dim(dim)) return r;
+    if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(LLMR_ERR_INVALID_ARG, "eps must be finite and >= 0");
+    if (n_rows == 0) return ok();
+    if (int r = check_rows(residual, "residual", residual_stride, dim)) return r;
+    if (int r = check_rows(input, "input", input_stride, dim)) return r;
+    if (int r = check_vec(norm_weight, "norm_weight", false)) return r;
+    if (int r = check_vec(gate, "gate", gate_mode != LLMR_GATE_NONE)) return r;
+    llmr::ResidualArgs a{residual, input, norm_weight, gate_mode == LLMR_GATE_NONE ? nullptr : gate,
+                         residual_stride, input_stride, n_rows, dim, eps};
+    return launched(llmr::launch_residual(a, gate_mode == LLMR_GATE_TANH, ctx->cur), "gated_residual");
+}
+
+int llmr_activation(llmr_context* ctx, const float* src, uint32_t src_stride, uint32_t src_col, uint32_t src2_col,
+                    void* dst, uint32_t dst_type, uint32_t dst_stride, uint32_t dst_col, uint32_t n_rows,
+                    uint32_t n_cols, uint32_t act) {
+    if (int r = check_ctx(ctx)) return r;
+    if (!is_act_type(dst_type)) return fail(LLMR_ERR_UNSUPPORTED, "output type %u not supported", dst_type);
+    if (act > LLMR_ACT_SILU_MUL) return fail(LLMR_ERR_INVALID_ARG, "unknown activation %u", act);
+    if (n_cols % 4 || src_col % 4 || src2_col % 4 || dst_col % 4)
+        return fail(LLMR_ERR_INVALID_ARG, "n_cols and column offsets must be multiples of 4");
+    if (n_rows == 0 || n_cols == 0) return ok();
+    const uint64_t src_w = (uint64_t)src_col + n_cols;
+    const uint64_t src2_w = act == LLMR_ACT_SILU_MUL ? (uint64_t)src2_col + n_cols : 0;
+    const uint64_t dst_w = (uint64_t)dst_col + n_cols;
+    if (src_w > src_stride || src2_w > src_stride)
+        return fail(LLMR_ERR_INVALID_ARG, "source columns exceed the row stride %u", src_stride);
+    if (dst_w > dst_stride) return fail(LLMR_ERR_INVALID_ARG, "destination columns exceed the row stride %u", dst_stride);
+    if (int r = check_rows(src, "src", src_stride, 0)) return r;
+    if (int r = check_rows(dst, "dst", dst_stride, 0)) return r;
+    if ((uint64_t)((n_cols / 4u + 255u) / 256u) * n_rows > 0x7fffffffull)
+        return fail(LLMR_ERR_INVALID_ARG, "grid too large");
+    llmr::ActColsArgs a{src, dst, src_stride, src_col, src2_col, dst_stride, dst_col, n_rows, n_cols};
+    return launched(llmr::launch_act_cols(a, (int)act, dst_type, ctx->cur), "activation");
+}
+
+int llmr_timestep_embed(llmr_context* ctx, float* out, uint32_t dim, float timestep) {
+    if (int r = check_ctx(ctx)) return r;
+    if (dim == 0 || dim % 2) return fail(LLMR_ERR_INVALID_ARG, "dim must be even and > 0 (got %u)", dim);
+    if (!out) return fail(LLMR_ERR_INVALID_ARG, "null output pointer");
+    if (!std::isfinite(timestep)) return fail(LLMR_ERR_INVALID_ARG, "timestep must be finite");
+    return launched(llmr::launch_timestep_embed(out, dim, timestep, ctx->cur), "timestep_embed");
+}
+
+static int patch_shape(uint32_t channels, uint32_t height, uint32_t width, uint32_t patch_size) {
+    if (channels == 0 || height == 0 || width == 0 || patch_size == 0)
+        return fail(LLMR_ERR_INVALID_ARG, "channels, height, width and patch_size must be > 0");
+    if (height % patch_size || width % patch_size)
+        return fail(LLMR_ERR_INVALID_ARG, "height and width must be multiples of patch_size");
+    if ((uint64_t)channels * height * width > 0x7fffffffull)
+        return fail(LLMR_ERR_INVALID_ARG, "latent too large");
+    return LLMR_OK;
+}
+
+int llmr_patchify(llmr_context* ctx, const float* latent, void* out, uint32_t out_type, uint32_t channels,
+                  uint32_t height, uint32_t width, uint32_t patch_size) {
+    if (int r = check_ctx(ctx)) return r;
+    if (!is_act_type(out_type)) return fail(LLMR_ERR_UNSUPPORTED, "output type %u not supported", out_type);
+    if (int r = patch_shape(channels, height, width, patch_size)) return r;
+    if (!latent || !out) return fail(LLMR_ERR_INVALID_ARG, "null pointer");
+    return launched(llmr::launch_patchify(latent, out, out_type, channels, height, width, patch_size, ctx->cur),
+                    "patchify");
+}
+
+int llmr_unpatchify(llmr_context* ctx, const float* patches, float* out, uint32_t channels, uint32_t height,
+                    uint32_t width, uint32_t patch_size) {
+    if (int r = check_ctx(ctx)) return r;
+    if (int r = patch_shape(channels, height, width, patch_size)) return r;
+    if (!patches || !out) return fail(LLMR_ERR_INVALID_ARG, "null pointer");
+    return launched(llmr::launch_unpatchify(patches, out, channels, height, width, patch_size, ctx->cur),
+                    "unpatchify");
+}
+
+int llmr_synth_q4k(llmr_context* ctx, void* out, uint64_t n_rows, uint32_t in_dim, uint64_t seed, uint64_t stream,
+                   double std) {
+    if (int r = check_ctx(ctx)) return r;
+    if (in_dim == 0 || in_dim % 256) return fail(LLMR_ERR_INVALID_ARG, "in_dim must be a positive multiple of 256");
+    if (!(std >= 0.0) || !std::isfinite(std)) return fail(LLMR_ERR_INVALID_ARG, "std must be finite and >= 0");
+    if (n_rows == 0) return ok();
+    if (!out || !aligned(out, 16)) return fail(LLMR_ERR_INVALID_ARG, "output must be non-null and 16-byte aligned");
+    if (n_rows > (1ull << 33) / (in_dim / 256u))  // superblocks must fit the kernel's 2^31 x 4 waves
+        return fail(LLMR_ERR_INVALID_ARG, "n_rows * in_dim / 256 too large");
+    return launched(llmr::launch_synth_q4k(out, n_rows, in_dim, seed, stream, std, ctx->cur), "synth_q4k");
+}
+
+}  // extern "C"

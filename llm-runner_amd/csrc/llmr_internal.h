@@ -31,4 +31,65 @@ hipError_t launch_flash_attention(const void* q, const void* k, const void* v, u
                                   float* o, uint32_t n_heads, uint32_t seq_len, float scale,
                                   hipStream_t st);
 
+// --- block glue (glue.hip). Strides are in elements; the C-ABI layer checks
+// that every vector access is aligned (dims, strides and column offsets % 4,
+// pointers 16-byte aligned) and that dims fit the kernels' register rows.
+
+struct RowNormArgs {
+    const float* x;       // [rows, x_stride] f32
+    const float* w;       // [dim] RMS weight (unused by LayerNorm)
+    const float* scale;   // [dim] or null: y *= 1 + scale
+    const float* shift;   // [dim] or null: y += shift
+    void* out;            // [rows, out_stride] of the output type
+    uint32_t x_stride, out_stride, rows, dim;
+    float eps;
+};
+constexpr uint32_t kRowNormMaxDim = 8192;
+
+struct QkvHeadsArgs {
+    const float* src;          // [rows, src_stride] f32: Q | K | V, each n_heads * 128 wide
+    const float* q_norm;       // [128] or null
+    const float* k_norm;       // [128] or null
+    const float* rope_cos;     // [dst_seq, 64] or null
+    const float* rope_sin;
+    void* q;                   // [n_heads, dst_seq, 128] of the output type
+    void* k;
+    void* v;
+    uint32_t src_stride, rows, n_heads, dst_seq, dst_row0;
+    float eps;
+};
+
+struct ResidualArgs {
+    float* h;               // [rows, h_stride] f32, updated in place
+    const float* x;         // [rows, x_stride] f32
+    const float* norm_w;    // [dim] or null: no RMSNorm of x
+    const float* gate;      // [dim] or null: plain add
+    uint32_t h_stride, x_stride, rows, dim;
+    float eps;
+};
+
+constexpr int kActCopy = 0, kActSilu = 1, kActGelu = 2, kActSiluMul = 3;
+struct ActColsArgs {
+    const float* src;   // [rows, src_stride] f32
+    void* dst;          // [rows, dst_stride] of the output type
+    uint32_t src_stride, src_col, src2_col, dst_stride, dst_col, rows, cols;
+};
+
+hipError_t launch_row_norm(const RowNormArgs& a, bool layernorm, uint32_t otype, hipStream_t st);
+hipError_t launch_qkv_heads(const QkvHeadsArgs& a, uint32_t otype, hipStream_t st);
+hipError_t launch_residual(const ResidualArgs& a, bool tanh_gate, hipStream_t st);
+hipError_t launch_act_cols(const ActColsArgs& a, int act, uint32_t otype, hipStream_t st);
+hipError_t launch_timestep_embed(float* out, uint32_t dim, float t, hipStream_t st);
+hipError_t launch_patchify(const float* in, void* out, uint32_t otype, uint32_t C, uint32_t H, uint32_t W,
+                           uint32_t ps, hipStream_t st);
+hipError_t launch_unpatchify(const float* in, float* out, uint32_t C, uint32_t H, uint32_t W, uint32_t ps,
+                             hipStream_t st);
+
+// Synthetic Q4_K weights generated on the device (synth.hip): n_rows x in_dim
+// values ~N(0, std^2) from a counter-based generator keyed by (seed, stream),
+// quantized per 256-element superblock with the float64 min/max rule of
+// llmr_amd.gguf.quantize_q4k.
+hipError_t launch_synth_q4k(void* out, uint64_t n_rows, uint32_t in_dim, uint64_t seed, uint64_t stream,
+                            double std, hipStream_t st);
+
 }  // namespace llmr

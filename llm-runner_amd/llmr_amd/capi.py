@@ -67,7 +67,25 @@ _SIGS = {
                                             ctypes.c_float]),
     "llmr_flash_attention_pc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _vp,
                                                ctypes.POINTER(FlashAttentionParams)]),
+    "llmr_batch_rmsnorm": (ctypes.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                          ctypes.c_float]),
+    "llmr_batch_layernorm": (ctypes.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                            ctypes.c_float]),
+    "llmr_qkv_heads": (ctypes.c_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, ctypes.c_float, _vp, _vp,
+                                      _vp, _vp, _vp, _u32, _u32, _u32]),
+    "llmr_gated_residual": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32,
+                                           ctypes.c_float]),
+    "llmr_activation": (ctypes.c_int, [_vp, _vp, _u32, _u32, _u32, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "llmr_timestep_embed": (ctypes.c_int, [_vp, _vp, _u32, ctypes.c_float]),
+    "llmr_patchify": (ctypes.c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32]),
+    "llmr_unpatchify": (ctypes.c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
+    "llmr_synth_q4k": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, _u32, ctypes.c_uint64, ctypes.c_uint64,
+                                      ctypes.c_double]),
 }
+
+# Activation and gate selectors of llmr_activation / llmr_gated_residual.
+ACT_COPY, ACT_SILU, ACT_GELU_TANH, ACT_SILU_MUL = 0, 1, 2, 3
+GATE_NONE, GATE_LINEAR, GATE_TANH = 0, 1, 2
 
 _lib = None
 
@@ -158,3 +176,38 @@ class Context:
                         head_dim: int, n_heads: int, seq_len: int, scale: float) -> None:
         check(lib().llmr_flash_attention(self._h, q_ptr, k_ptr, v_ptr, xtype, o_ptr, head_dim,
                                          n_heads, seq_len, float(scale)))
+
+    # --- block glue (pointers are device addresses, strides in elements) ---
+
+    def batch_rmsnorm(self, x, x_stride, w, scale, shift, out, otype, out_stride, dim, rows, eps):
+        check(lib().llmr_batch_rmsnorm(self._h, x, x_stride, w, scale, shift, out, otype, out_stride, dim,
+                                       rows, float(eps)))
+
+    def batch_layernorm(self, x, x_stride, scale, shift, out, otype, out_stride, dim, rows, eps):
+        check(lib().llmr_batch_layernorm(self._h, x, x_stride, scale, shift, out, otype, out_stride, dim,
+                                         rows, float(eps)))
+
+    def qkv_heads(self, qkv, qkv_stride, rows, n_heads, q_norm, k_norm, eps, cos_t, sin_t, q, k, v, otype,
+                  seq_len, row0):
+        check(lib().llmr_qkv_heads(self._h, qkv, qkv_stride, rows, n_heads, q_norm, k_norm, float(eps), cos_t,
+                                   sin_t, q, k, v, otype, seq_len, row0))
+
+    def gated_residual(self, h, h_stride, x, x_stride, norm_w, gate, mode, dim, rows, eps):
+        check(lib().llmr_gated_residual(self._h, h, h_stride, x, x_stride, norm_w, gate, mode, dim, rows,
+                                        float(eps)))
+
+    def activation(self, src, src_stride, src_col, src2_col, dst, dtype, dst_stride, dst_col, rows, cols, act):
+        check(lib().llmr_activation(self._h, src, src_stride, src_col, src2_col, dst, dtype, dst_stride,
+                                    dst_col, rows, cols, act))
+
+    def timestep_embed(self, out, dim, t):
+        check(lib().llmr_timestep_embed(self._h, out, dim, float(t)))
+
+    def patchify(self, latent, out, otype, C, H, W, ps):
+        check(lib().llmr_patchify(self._h, latent, out, otype, C, H, W, ps))
+
+    def unpatchify(self, patches, out, C, H, W, ps):
+        check(lib().llmr_unpatchify(self._h, patches, out, C, H, W, ps))
+
+    def synth_q4k(self, out, n_rows, in_dim, seed, stream, std):
+        check(lib().llmr_synth_q4k(self._h, out, n_rows, in_dim, seed, stream, float(std)))

@@ -1,0 +1,409 @@
+"""DiT blocks composed from the backend's entry points: the call sequences of
+the reference's block functions, with its dispatch chains replaced by the
+fused glue calls.
+
+  ZImageBlock   dit_transformer_layer with adaLN
+                (dependencies/zimage.c3l/dit.c3:1372-1627): RMSNorm + scale,
+                QKV GEMM, head norm + RoPE + FA, O-proj, post-norm + tanh-gated
+                residual, RMSNorm + scale, SwiGLU GEMM, down GEMM, post-norm +
+                tanh-gated residual.
+  FluxDiT       FluxDiTModel.forward (dependencies/flux.c3l/flux_dit.c3:1075-
+                1210) over flux_dual_stream_block (:746-971) and
+                flux_single_stream_block (:975-1071), at Flux.1-dev shapes:
+                GELU (tanh) MLPs where the reference's Klein variant has SwiGLU
+                halves, and per-block modulation projections where Klein shares
+                one per block type.
+
+Layout decisions (MI355X side, not the reference's):
+  - the text and image streams live in one joint [n_txt + n_img, dim] f32
+    residual buffer, text rows first (the reference's joint order), so the
+    reference's stream concatenation and split copies (flux_dit.c3:1152-1153,
+    880-887) disappear: each stream is a row range;
+  - a fused weight is multiplied in one call over its full row range
+    (Q | K | V, or Q | K | V | MLP-in for linear1) instead of one call per
+    slot; the output columns are the slots side by side, exactly what the
+    slot calls produce;
+  - every GEMM and attention input is written by the glue in the activation
+    type the kernels read (act_dtype, bf16 by default; Q/K/V in fp16).
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import numpy as np
+import torch
+
+from . import capi, glue, workloads
+from .gguf import GGML_Q4_K, GGML_Q8_0
+from .ops import FlashAttentionPC, RenderGraph, Tensor, default_graph, dispatch_batch_matmul, \
+    dispatch_batch_matmul_swiglu, dispatch_flash_attention
+
+HEAD_DIM = 128
+
+
+def _qt(blocks: torch.Tensor, wtype: int, rows: int, cols: int) -> Tensor:
+    return Tensor.quantized(blocks, wtype, rows, cols)
+
+
+def _t(x: torch.Tensor) -> Tensor:
+    return Tensor.from_torch(x)
+
+
+# ---------------------------------------------------------------------------
+# Z-Image block
+# ---------------------------------------------------------------------------
+
+@dataclasses.dataclass
+class ZImageLayerWeights:
+    """The DiTLayerWeights a block reads (Q8_0 GEMM weights as raw blocks)."""
+    wqkv: torch.Tensor      # [3*dim, dim]
+    wo: torch.Tensor        # [dim, dim]
+    w_gate: torch.Tensor    # [ffn, dim]
+    w_up: torch.Tensor      # [ffn, dim]
+    w_down: torch.Tensor    # [dim, ffn]
+    attn_norm1: torch.Tensor  # f32 [dim]
+    attn_norm2: torch.Tensor
+    ffn_norm1: torch.Tensor
+    ffn_norm2: torch.Tensor
+    q_norm: torch.Tensor    # f32 [128]
+    k_norm: torch.Tensor
+    adaln: torch.Tensor     # f32 [4, dim]: scale_msa, gate_msa, scale_mlp, gate_mlp
+
+
+class ZImageBlock:
+    """One Z-Image transformer layer with adaLN, on preallocated buffers for a
+    fixed (dim, n_heads, ffn_dim, seq_len). The per-layer adaLN projection of
+    the timestep embedding (an M=1 linear_proj, dit.c3:1398-1417) is an input
+    here: `weights.adaln` holds its four chunks."""
+
+    EPS = 1e-5  # batch_rmsnorm and batch_head_norm eps (dit.c3:1423, 1447)
+
+    def __init__(self, dim: int, n_heads: int, ffn_dim: int, seq_len: int, act_dtype=torch.bfloat16,
+                 device="cuda", g: RenderGraph | None = None):
+        if dim != n_heads * HEAD_DIM:
+            raise ValueError("dim must be n_heads * 128")
+        self.dim, self.n_heads, self.ffn, self.S = dim, n_heads, ffn_dim, seq_len
+        self.g = g or default_graph()
+        S = seq_len
+        e = dict(device=device)
+        self.xa = torch.empty(S, dim, dtype=act_dtype, **e)          # GEMM inputs of width dim
+        self.qkv = torch.empty(S, 3 * dim, dtype=torch.float32, **e)
+        self.q = torch.empty(n_heads, S, HEAD_DIM, dtype=torch.float16, **e)
+        self.k = torch.empty_like(self.q)
+        self.v = torch.empty_like(self.q)
+        self.o = torch.empty(S, dim, dtype=torch.float32, **e)
+        self.t = torch.empty(S, dim, dtype=torch.float32, **e)      # O-proj / down outputs
+        self.f = torch.empty(S, ffn_dim, dtype=torch.float32, **e)  # SwiGLU output
+        self.fa = torch.empty(S, ffn_dim, dtype=act_dtype, **e)     # down-projection input
+
+    def forward(self, w: ZImageLayerWeights, hidden: torch.Tensor, rope_cos: torch.Tensor,
+                rope_sin: torch.Tensor) -> torch.Tensor:
+        """hidden f32 [seq_len, dim], updated in place (and returned)."""
+        g, S, dim, H, ffn, eps = self.g, self.S, self.dim, self.n_heads, self.ffn, self.EPS
+        if hidden.shape != (S, dim) or hidden.dtype != torch.float32:
+            raise ValueError("hidden must be f32 [seq_len, dim]")
+        # A: pre-attention RMSNorm, * (1 + scale_msa)                 (dit.c3:1421-1432)
+        glue.batch_rmsnorm(hidden, w.attn_norm1, self.xa, eps, mod_scale=w.adaln[0], g=g)
+        # B: Q | K | V in one call over the fused weight               (dit.c3:1435-1443)
+        dispatch_batch_matmul(g, _qt(w.wqkv, GGML_Q8_0, 3 * dim, dim), _t(self.xa), _t(self.qkv), 3 * dim, dim,
+                              S, 0)
+        # C: head norm, RoPE, head-major fp16 Q/K/V; attention         (dit.c3:1446-1483)
+        glue.qkv_heads(self.qkv, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, eps, (rope_cos, rope_sin), g=g)
+        dispatch_flash_attention(g, _t(self.q), _t(self.k), _t(self.v), _t(self.o),
+                                 FlashAttentionPC(HEAD_DIM, H, S, 1.0 / math.sqrt(HEAD_DIM)))
+        # D: O-proj; hidden += tanh(gate_msa) * rmsnorm(o-proj)        (dit.c3:1488-1503)
+        glue.activation(self.o, self.xa, capi.ACT_COPY, g=g)
+        dispatch_batch_matmul(g, _qt(w.wo, GGML_Q8_0, dim, dim), _t(self.xa), _t(self.t), dim, dim, S, 0)
+        glue.gated_residual(hidden, self.t, w.adaln[1], capi.GATE_TANH, w.attn_norm2, eps, g=g)
+        # E: FFN pre-norm, * (1 + scale_mlp)                           (dit.c3:1545-1554)
+        glue.batch_rmsnorm(hidden, w.ffn_norm1, self.xa, eps, mod_scale=w.adaln[2], g=g)
+        # F: SwiGLU in-projection, down-projection                     (dit.c3:1562-1596)
+        dispatch_batch_matmul_swiglu(g, _qt(w.w_gate, GGML_Q8_0, ffn, dim), _qt(w.w_up, GGML_Q8_0, ffn, dim),
+                                     _t(self.xa), _t(self.f), ffn, dim, S)
+        glue.activation(self.f, self.fa, capi.ACT_COPY, g=g)
+        dispatch_batch_matmul(g, _qt(w.w_down, GGML_Q8_0, dim, ffn), _t(self.fa), _t(self.t), dim, ffn, S, 0)
+        # G: hidden += tanh(gate_mlp) * rmsnorm(down)                  (dit.c3:1600-1610)
+        glue.gated_residual(hidden, self.t, w.adaln[3], capi.GATE_TANH, w.ffn_norm2, eps, g=g)
+        return hidden
+
+
+def zimage_layer_weights(dim: int, n_heads: int, ffn: int, device="cuda", seed: int = workloads.SEED,
+                         base_stream: int = 10) -> ZImageLayerWeights:
+    """Synthetic Z-Image layer weights: Q8_0 GEMM weights ~N(0, 0.02) quantized
+    on the host (the same streams as the zimage_* GEMM workloads when the
+    shapes are the full block's), norm weights 1 + N(0, 0.1), adaLN chunks
+    N(0, 0.5)."""
+    from . import gguf, synth
+
+    def q8(rows, cols, stream):
+        w = synth.normal(seed, stream, rows * cols, 0.02).reshape(rows, cols)
+        return torch.from_numpy(gguf.quantize(w, GGML_Q8_0)).to(device)
+
+    def vec(n, stream, mean, std):
+        return torch.from_numpy(mean + synth.normal(seed, stream, n, std)).to(device)
+
+    b = base_stream
+    return ZImageLayerWeights(
+        wqkv=q8(3 * dim, dim, b + 1), wo=q8(dim, dim, b + 3), w_gate=q8(ffn, dim, b + 6),
+        w_up=q8(ffn, dim, b + 7), w_down=q8(dim, ffn, b + 5),
+        attn_norm1=vec(dim, b + 20, 1.0, 0.1), attn_norm2=vec(dim, b + 21, 1.0, 0.1),
+        ffn_norm1=vec(dim, b + 22, 1.0, 0.1), ffn_norm2=vec(dim, b + 23, 1.0, 0.1),
+        q_norm=vec(HEAD_DIM, b + 24, 1.0, 0.1), k_norm=vec(HEAD_DIM, b + 25, 1.0, 0.1),
+        adaln=vec(4 * dim, b + 26, 0.0, 0.5).reshape(4, dim))
+
+
+# ---------------------------------------------------------------------------
+# Flux (Flux.1-dev shapes)
+# ---------------------------------------------------------------------------
+
+@dataclasses.dataclass(frozen=True)
+class FluxConfig:
+    dim: int = 3072
+    n_heads: int = 24
+    mlp: int = 12288
+    n_double: int = 19
+    n_single: int = 38
+    text_dim: int = 4096
+    n_txt: int = 512
+    latent_ch: int = 16
+    latent_h: int = 128
+    latent_w: int = 128
+    patch: int = 2
+    t_emb_dim: int = 256
+    axes: tuple = (16, 56, 56)
+    theta: float = 10000.0
+
+    @property
+    def patch_dim(self) -> int:
+        return self.latent_ch * self.patch * self.patch
+
+    @property
+    def n_img(self) -> int:
+        return (self.latent_h // self.patch) * (self.latent_w // self.patch)
+
+    @property
+    def seq(self) -> int:
+        return self.n_txt + self.n_img
+
+    def gemm_flops(self) -> float:
+        """2MNK over every token-wise GEMM plus 4*H*S^2*D per attention (the
+        modulation and timestep projections, M = 1, are not counted)."""
+        d, m, ni, nt, S = self.dim, self.mlp, self.n_img, self.n_txt, self.seq
+        per_stream = 3 * d * d + d * d + 2 * d * m
+        double = 2.0 * (ni + nt) * per_stream + 4.0 * self.n_heads * S * S * HEAD_DIM
+        single = 2.0 * S * ((3 * d + m) * d + d * (d + m)) + 4.0 * self.n_heads * S * S * HEAD_DIM
+        io = 2.0 * ni * self.patch_dim * d + 2.0 * nt * self.text_dim * d + 2.0 * ni * d * self.patch_dim
+        return self.n_double * double + self.n_single * single + io
+
+
+FLUX_DEV = FluxConfig()
+
+
+@dataclasses.dataclass
+class FluxDoubleWeights:
+    img_mod: torch.Tensor   # Q4_K [6*dim, dim]
+    txt_mod: torch.Tensor
+    img_qkv: torch.Tensor   # Q4_K [3*dim, dim]
+    txt_qkv: torch.Tensor
+    img_proj: torch.Tensor  # Q4_K [dim, dim]
+    txt_proj: torch.Tensor
+    img_mlp0: torch.Tensor  # Q4_K [mlp, dim]
+    txt_mlp0: torch.Tensor
+    img_mlp2: torch.Tensor  # Q4_K [dim, mlp]
+    txt_mlp2: torch.Tensor
+    img_q_norm: torch.Tensor  # f32 [128]
+    img_k_norm: torch.Tensor
+    txt_q_norm: torch.Tensor
+    txt_k_norm: torch.Tensor
+
+
+@dataclasses.dataclass
+class FluxSingleWeights:
+    mod: torch.Tensor       # Q4_K [3*dim, dim]
+    linear1: torch.Tensor   # Q4_K [3*dim + mlp, dim]
+    linear2: torch.Tensor   # Q4_K [dim, dim + mlp]
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+
+
+@dataclasses.dataclass
+class FluxGlobalWeights:
+    img_in: torch.Tensor      # Q8_0 [dim, patch_dim] (patch_dim = 64 is not a Q4_K row)
+    txt_in: torch.Tensor      # Q4_K [dim, text_dim]
+    time_in0: torch.Tensor    # Q4_K [dim, t_emb_dim]
+    time_in1: torch.Tensor    # Q4_K [dim, dim]
+    final_mod: torch.Tensor   # Q4_K [2*dim, dim]
+    final_linear: torch.Tensor  # Q4_K [patch_dim, dim]
+
+
+def flux_weights(cfg: FluxConfig, device="cuda", seed: int = workloads.SEED, g: RenderGraph | None = None):
+    """Random-init Flux weights: Q4_K tensors ~N(0, 0.02) generated and
+    quantized on the device (llmr_synth_q4k), one stream per tensor; norm
+    weights 1 + N(0, 0.1); img_in Q8_0 quantized on the host."""
+    from . import gguf, synth
+    g = g or default_graph()
+    d, m = cfg.dim, cfg.mlp
+    counter = [1000]
+
+    def q4(rows, cols):
+        counter[0] += 1
+        return glue.synth_q4k(rows, cols, counter[0], 0.02, seed, device, g)
+
+    def norm():
+        counter[0] += 1
+        return torch.from_numpy(1.0 + synth.normal(seed, counter[0], HEAD_DIM, 0.1)).to(device)
+
+    doubles = [FluxDoubleWeights(q4(6 * d, d), q4(6 * d, d), q4(3 * d, d), q4(3 * d, d), q4(d, d), q4(d, d),
+                                 q4(m, d), q4(m, d), q4(d, m), q4(d, m), norm(), norm(), norm(), norm())
+               for _ in range(cfg.n_double)]
+    singles = [FluxSingleWeights(q4(3 * d, d), q4(3 * d + m, d), q4(d, d + m), norm(), norm())
+               for _ in range(cfg.n_single)]
+    w_in = synth.normal(seed, 999, d * cfg.patch_dim, 0.02).reshape(d, cfg.patch_dim)
+    glob = FluxGlobalWeights(torch.from_numpy(gguf.quantize(w_in, GGML_Q8_0)).to(device), q4(d, cfg.text_dim),
+                             q4(d, cfg.t_emb_dim), q4(d, d), q4(2 * d, d), q4(cfg.patch_dim, d))
+    return glob, doubles, singles
+
+
+def flux_rope(cfg: FluxConfig, device="cuda"):
+    """cos/sin [seq, 64] for text ids (0,0,0) then image ids (0, row, col)
+    (precompute_flux_mrope, flux_dit.c3:396-529), computed on the host."""
+    att = workloads.Attention("flux", cfg.n_heads, cfg.seq, HEAD_DIM, cfg.n_txt, cfg.latent_h // cfg.patch,
+                              cfg.latent_w // cfg.patch, cfg.axes, cfg.theta)
+    cos_t, sin_t = workloads.rope_tables(workloads.attention_positions(att), cfg.axes, cfg.theta)
+    return torch.from_numpy(cos_t).to(device), torch.from_numpy(sin_t).to(device)
+
+
+class FluxDiT:
+    """One denoising forward of a Flux-shaped DiT on preallocated buffers."""
+
+    LN_EPS = 1e-6   # batch_layernorm eps (flux_dit.c3:766)
+    HN_EPS = 1e-6   # batch_head_norm eps (flux_dit.c3:813)
+
+    def __init__(self, cfg: FluxConfig, glob: FluxGlobalWeights, doubles, singles, act_dtype=torch.bfloat16,
+                 device="cuda", g: RenderGraph | None = None):
+        self.cfg, self.glob, self.doubles, self.singles = cfg, glob, doubles, singles
+        self.g = g or default_graph()
+        c, e = cfg, dict(device=device)
+        S, d, m, nt = c.seq, c.dim, c.mlp, c.n_txt
+        self.rope = flux_rope(cfg, device)
+        self.hidden = torch.empty(S, d, dtype=torch.float32, **e)   # joint residual stream, text rows first
+        self.xa = torch.empty(S, d, dtype=act_dtype, **e)
+        self.patches = torch.empty(c.n_img, c.patch_dim, dtype=act_dtype, **e)
+        self.l1 = torch.empty(S, 3 * d + m, dtype=torch.float32, **e)  # linear1 out; its first 3d cols are QKV
+        self.q = torch.empty(c.n_heads, S, HEAD_DIM, dtype=torch.float16, **e)
+        self.k = torch.empty_like(self.q)
+        self.v = torch.empty_like(self.q)
+        self.o = torch.empty(S, d, dtype=torch.float32, **e)
+        self.t = torch.empty(S, d, dtype=torch.float32, **e)
+        self.cat = torch.empty(S, d + m, dtype=act_dtype, **e)  # linear2 input [attention | MLP]
+        self.f = torch.empty(c.n_img, m, dtype=torch.float32, **e)  # double-block MLP up-projection
+        # dense views over the single block's buffers for the double block (GEMM
+        # outputs and inputs are dense [M, N]): QKV [S, 3d] and the MLP
+        # activations [n_img, mlp]; the two block types never overlap in time
+        self.qkv = self.l1.view(-1)[:S * 3 * d].view(S, 3 * d)
+        self.fa = self.cat.view(-1)[:c.n_img * m].view(c.n_img, m)
+        self.t_emb = torch.empty(1, c.t_emb_dim, dtype=torch.float32, **e)
+        self.vec0 = torch.empty(1, d, dtype=torch.float32, **e)
+        self.vec = torch.empty(1, d, dtype=torch.float32, **e)
+        n_mod = (12 * c.n_double + 3 * c.n_single + 2) * d
+        self.mods = torch.empty(1, n_mod, dtype=torch.float32, **e)
+        self.velocity = torch.empty(c.n_img, c.patch_dim, dtype=torch.float32, **e)
+        self.out = torch.empty(c.latent_ch, c.latent_h, c.latent_w, dtype=torch.float32, **e)
+
+    # GEMM helper: rows [r0, r0+M) of x (activation type) times weight -> rows of y (f32)
+    def _mm(self, w: torch.Tensor, wtype: int, N: int, K: int, x: torch.Tensor, y: torch.Tensor) -> None:
+        dispatch_batch_matmul(self.g, _qt(w, wtype, N, K), _t(x), _t(y), N, K, x.shape[0], 0)
+
+    def _mod(self, i: int, n: int) -> torch.Tensor:
+        d = self.cfg.dim
+        return self.mods[0, i * d:(i + n) * d].view(n, d)
+
+    def forward(self, latent: torch.Tensor, txt: torch.Tensor, sigma: float) -> torch.Tensor:
+        """latent f32 [C, H, W], txt [n_txt, text_dim] (activation type) ->
+        velocity f32 [C, H, W] (self.out)."""
+        c, g = self.cfg, self.g
+        d, nt = c.dim, c.n_txt
+        S = c.seq
+        hid_t, hid_i = self.hidden[:nt], self.hidden[nt:]
+        # 1-3: patchify; img_in and txt_in straight into the joint stream (flux_dit.c3:1093-1114)
+        glue.patchify(latent, self.patches, c.patch, g=g)
+        self._mm(self.glob.img_in, GGML_Q8_0, d, c.patch_dim, self.patches, hid_i)
+        self._mm(self.glob.txt_in, GGML_Q4_K, d, c.text_dim, txt, hid_t)
+        # 4: timestep embedding (sigma * 1000) -> MLP (flux_dit.c3:1121-1129)
+        glue.timestep_embed(self.t_emb, sigma * 1000.0, g=g)
+        self._mm(self.glob.time_in0, GGML_Q4_K, d, c.t_emb_dim, self.t_emb, self.vec0)
+        glue.activation(self.vec0, self.vec0, capi.ACT_SILU, g=g)
+        self._mm(self.glob.time_in1, GGML_Q4_K, d, d, self.vec0, self.vec)
+        glue.activation(self.vec, self.vec, capi.ACT_SILU, g=g)
+        # 5: modulation vectors of every block from silu(vec) (flux_dit.c3:1131-1140)
+        mi = 0
+        for w in self.doubles:
+            self._mm(w.img_mod, GGML_Q4_K, 6 * d, d, self.vec, self.mods[:, mi * d:(mi + 6) * d])
+            self._mm(w.txt_mod, GGML_Q4_K, 6 * d, d, self.vec, self.mods[:, (mi + 6) * d:(mi + 12) * d])
+            mi += 12
+        for w in self.singles:
+            self._mm(w.mod, GGML_Q4_K, 3 * d, d, self.vec, self.mods[:, mi * d:(mi + 3) * d])
+            mi += 3
+        self._mm(self.glob.final_mod, GGML_Q4_K, 2 * d, d, self.vec, self.mods[:, mi * d:(mi + 2) * d])
+        # 6-8: blocks (flux_dit.c3:1146-1162)
+        mi = 0
+        for w in self.doubles:
+            self._double(w, self._mod(mi, 6), self._mod(mi + 6, 6))
+            mi += 12
+        for w in self.singles:
+            self._single(w, self._mod(mi, 3))
+            mi += 3
+        # 9: final LayerNorm + adaLN (shift, scale) on the image rows, projection, unpatchify
+        fm = self._mod(mi, 2)
+        glue.batch_layernorm(hid_i, self.xa[nt:], self.LN_EPS, mod_scale=fm[1], mod_shift=fm[0], g=g)
+        self._mm(self.glob.final_linear, GGML_Q4_K, c.patch_dim, d, self.xa[nt:], self.velocity)
+        glue.unpatchify(self.velocity, self.out, c.patch, g=g)
+        return self.out
+
+    def _attention(self, S: int) -> None:
+        dispatch_flash_attention(self.g, _t(self.q), _t(self.k), _t(self.v), _t(self.o),
+                                 FlashAttentionPC(HEAD_DIM, self.cfg.n_heads, S, 1.0 / math.sqrt(HEAD_DIM)))
+
+    def _double(self, w: FluxDoubleWeights, mi: torch.Tensor, mt: torch.Tensor) -> None:
+        """flux_dual_stream_block (flux_dit.c3:746-971). mi / mt: [6, dim]
+        (shift1, scale1, gate1, shift2, scale2, gate2) of the image / text stream."""
+        c, g = self.cfg, self.g
+        d, m, nt, H, S = c.dim, c.mlp, c.n_txt, c.n_heads, c.seq
+        streams = ((slice(nt, S), mi, w.img_qkv, w.img_proj, w.img_mlp0, w.img_mlp2, w.img_q_norm, w.img_k_norm),
+                   (slice(0, nt), mt, w.txt_qkv, w.txt_proj, w.txt_mlp0, w.txt_mlp2, w.txt_q_norm, w.txt_k_norm))
+        # LayerNorm + modulation, QKV, head norm + RoPE into the joint Q/K/V   (flux_dit.c3:761-863)
+        for sl, mod, wqkv, _, _, _, qn, kn in streams:
+            glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0],
+                                 g=g)
+            self._mm(wqkv, GGML_Q4_K, 3 * d, d, self.xa[sl], self.qkv[sl])
+            glue.qkv_heads(self.qkv[sl], H, self.q, self.k, self.v, sl.start, qn, kn, self.HN_EPS, self.rope, g=g)
+        self._attention(S)
+        # per-stream output projection, gated residual                       (flux_dit.c3:875-898)
+        glue.activation(self.o, self.xa, capi.ACT_COPY, g=g)
+        for sl, mod, _, wproj, _, _, _, _ in streams:
+            self._mm(wproj, GGML_Q4_K, d, d, self.xa[sl], self.t[sl])
+            glue.gated_residual(self.hidden[sl], self.t[sl], mod[2], capi.GATE_LINEAR, g=g)
+        # per-stream MLP: LayerNorm + modulation, up, GELU, down, gated residual (flux_dit.c3:902-967)
+        for sl, mod, _, _, wm0, wm2, _, _ in streams:
+            n = sl.stop - sl.start
+            glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[4], mod_shift=mod[3],
+                                 g=g)
+            self._mm(wm0, GGML_Q4_K, m, d, self.xa[sl], self.f[:n])
+            glue.activation(self.f[:n], self.fa[:n], capi.ACT_GELU_TANH, g=g)
+            self._mm(wm2, GGML_Q4_K, d, m, self.fa[:n], self.t[sl])
+            glue.gated_residual(self.hidden[sl], self.t[sl], mod[5], capi.GATE_LINEAR, g=g)
+
+    def _single(self, w: FluxSingleWeights, mod: torch.Tensor) -> None:
+        """flux_single_stream_block (flux_dit.c3:975-1071). mod: [3, dim] (shift, scale, gate)."""
+        c, g = self.cfg, self.g
+        d, m, H, S = c.dim, c.mlp, c.n_heads, c.seq
+        glue.batch_layernorm(self.hidden, self.xa, self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0], g=g)
+        self._mm(w.linear1, GGML_Q4_K, 3 * d + m, d, self.xa, self.l1)
+        glue.qkv_heads(self.l1, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, self.HN_EPS, self.rope, g=g)
+        self._attention(S)
+        # linear2 input = [attention out | gelu(MLP half)]          (flux_dit.c3:1049-1057)
+        glue.activation(self.o, self.cat[:, :d], capi.ACT_COPY, g=g)
+        glue.activation(self.l1[:, 3 * d:], self.cat[:, d:], capi.ACT_GELU_TANH, g=g)
+        self._mm(w.linear2, GGML_Q4_K, d, d + m, self.cat, self.t)
+        glue.gated_residual(self.hidden, self.t, mod[2], capi.GATE_LINEAR, g=g)

@@ -670,3 +670,155 @@ void orc_rope_apply(float* x, uint32_t H, uint32_t S, const float* cos_t, const 
             }
         }
 }
+
+/* ---------------------------------------------------------------------------
+ * DiT block glue (the dispatches between the GEMMs and attention), each as
+ * its own op exactly as the reference dispatches it, f32, in place where the
+ * reference works in place.
+ * ------------------------------------------------------------------------- */
+
+/* The shared-memory reduction of a 256-thread workgroup: thread gi first sums
+ * its strided elements in order (i = gi, gi+256, ...), then the tree
+ * s = 128, 64, ..., 1: part[gi] += part[gi + s]. */
+static float wg_tree_sum(float part[256]) {
+    for (uint32_t s = 128; s > 0; s >>= 1)
+        for (uint32_t gi = 0; gi < s; gi++) part[gi] += part[gi + s];
+    return part[0];
+}
+
+/* batch_rmsnorm (zimage.slang:449-500): out = x * (1/sqrt(sum/dim + eps)) * w. */
+void orc_batch_rmsnorm(const float* x, const float* w, float* out, uint32_t dim, uint32_t n_rows, float eps) {
+#pragma omp parallel for schedule(static)
+    for (uint32_t r = 0; r < n_rows; r++) {
+        const float* xr = x + (size_t)r * dim;
+        float part[256];
+        for (uint32_t gi = 0; gi < 256; gi++) {
+            float s = 0.0f;
+            for (uint32_t i = gi; i < dim; i += 256) s += xr[i] * xr[i];
+            part[gi] = s;
+        }
+        float rms = 1.0f / sqrtf(wg_tree_sum(part) / (float)dim + eps);
+        for (uint32_t i = 0; i < dim; i++) out[(size_t)r * dim + i] = xr[i] * rms * w[i];
+    }
+}
+
+/* batch_layernorm (zimage.slang:502-561): two passes, no affine. */
+void orc_batch_layernorm(const float* x, float* out, uint32_t dim, uint32_t n_rows, float eps) {
+#pragma omp parallel for schedule(static)
+    for (uint32_t r = 0; r < n_rows; r++) {
+        const float* xr = x + (size_t)r * dim;
+        float part[256];
+        for (uint32_t gi = 0; gi < 256; gi++) {
+            float s = 0.0f;
+            for (uint32_t i = gi; i < dim; i += 256) s += xr[i];
+            part[gi] = s;
+        }
+        float mean = wg_tree_sum(part) / (float)dim;
+        for (uint32_t gi = 0; gi < 256; gi++) {
+            float s = 0.0f;
+            for (uint32_t i = gi; i < dim; i += 256) {
+                float d = xr[i] - mean;
+                s += d * d;
+            }
+            part[gi] = s;
+        }
+        float inv_std = 1.0f / sqrtf(wg_tree_sum(part) / (float)dim + eps);
+        for (uint32_t i = 0; i < dim; i++) out[(size_t)r * dim + i] = (xr[i] - mean) * inv_std;
+    }
+}
+
+/* scale_modulate (zimage.slang:356-373): x[i] = x[i] * (1 + scale[i % dim]), and
+ * adaln_modulate (zimage.slang:98-117): x[i] = x[i] * (1 + scale[d]) + shift[d];
+ * shift == NULL selects the former. In place over n elements. */
+void orc_modulate(float* x, const float* scale, const float* shift, uint32_t dim, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        uint32_t d = (uint32_t)(i % dim);
+        x[i] = shift ? x[i] * (1.0f + scale[d]) + shift[d] : x[i] * (1.0f + scale[d]);
+    }
+}
+
+/* batch_head_norm (zimage.slang:609-667): per (pos, head) RMSNorm over D, in place. */
+void orc_batch_head_norm(float* x, const float* w, uint32_t n_heads, uint32_t D, uint32_t seq_len, float eps) {
+#pragma omp parallel for schedule(static)
+    for (uint32_t g = 0; g < seq_len * n_heads; g++) {
+        float* row = x + (size_t)g * D;
+        float part[256];
+        for (uint32_t gi = 0; gi < 256; gi++) {
+            float s = 0.0f;
+            for (uint32_t i = gi; i < D; i += 256) s += row[i] * row[i];
+            part[gi] = s;
+        }
+        float rms = 1.0f / sqrtf(wg_tree_sum(part) / (float)D + eps);
+        for (uint32_t i = 0; i < D; i++) row[i] = row[i] * rms * w[i];
+    }
+}
+
+/* transpose_heads direction 0 (zimage.slang:563-601): [S, H, D] -> [H, S, D]. */
+void orc_transpose_heads(const float* in, float* out, uint32_t S, uint32_t H, uint32_t D) {
+    for (uint32_t s = 0; s < S; s++)
+        for (uint32_t h = 0; h < H; h++)
+            memcpy(out + ((size_t)h * S + s) * D, in + ((size_t)s * H + h) * D, D * sizeof(float));
+}
+
+/* gated_residual (zimage.slang:382-410) with scale <= 0 -> 1 and clip <= 0 ->
+ * 1e10, and gated_residual_linear (zimage.slang:414-424) when tanh_gate == 0:
+ * residual[i] += g(d) * input[i], d = i % dim. */
+void orc_gated_residual(float* residual, const float* gate, const float* input, uint32_t dim, size_t n,
+                        int tanh_gate, float scale, float clip_thresh) {
+    float rs = scale > 0.0f ? scale : 1.0f;
+    float ct = clip_thresh > 0.0f ? clip_thresh : 1e10f;
+    for (size_t i = 0; i < n; i++) {
+        uint32_t d = (uint32_t)(i % dim);
+        if (tanh_gate) {
+            float v = rs * tanhf(gate[d]) * input[i];
+            v = v < -ct ? -ct : (v > ct ? ct : v);
+            residual[i] += v;
+        } else {
+            residual[i] += gate[d] * input[i];
+        }
+    }
+}
+
+/* silu (diffusion.slang:1082-1086), gelu (tanh form, diffusion.slang:1092-1107),
+ * in place over n elements. */
+void orc_silu(float* x, size_t n) {
+    for (size_t i = 0; i < n; i++) x[i] = x[i] / (1.0f + expf(-x[i]));
+}
+void orc_gelu(float* x, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        float v = x[i];
+        float c = 0.7978845608f;
+        x[i] = 0.5f * v * (1.0f + tanhf(c * (v + 0.044715f * v * v * v)));
+    }
+}
+
+/* dit_timestep_embed (zimage.slang:284-307). */
+void orc_timestep_embed(float* out, uint32_t dim, float t) {
+    uint32_t half = dim / 2;
+    for (uint32_t i = 0; i < dim; i++) {
+        uint32_t j = i < half ? i : i - half;
+        float freq = expf(-logf(10000.0f) * (float)j / (float)half);
+        out[i] = i < half ? cosf(t * freq) : sinf(t * freq);
+    }
+}
+
+/* patchify (zimage.slang:11-51): [C, H, W] -> [n_patches, C*ps*ps]. */
+void orc_patchify(const float* in, float* out, uint32_t C, uint32_t H, uint32_t W, uint32_t ps) {
+    uint32_t pd = C * ps * ps, pw = W / ps, n = (H / ps) * pw * pd;
+    for (uint32_t t = 0; t < n; t++) {
+        uint32_t p = t / pd, e = t % pd;
+        uint32_t py = e / (ps * C), px = (e % (ps * C)) / C, c = e % C;
+        uint32_t ih = (p / pw) * ps + py, iw = (p % pw) * ps + px;
+        out[t] = in[(size_t)c * H * W + (size_t)ih * W + iw];
+    }
+}
+
+/* unpatchify (zimage.slang:56-93): [n_patches, C*ps*ps] -> [C, H, W]. */
+void orc_unpatchify(const float* in, float* out, uint32_t C, uint32_t H, uint32_t W, uint32_t ps) {
+    for (uint32_t t = 0; t < C * H * W; t++) {
+        uint32_t c = t / (H * W), rem = t % (H * W), h = rem / W, w = rem % W;
+        uint32_t p = (h / ps) * (W / ps) + w / ps;
+        uint32_t e = (h % ps) * ps * C + (w % ps) * C + c;
+        out[t] = in[(size_t)p * C * ps * ps + e];
+    }
+}

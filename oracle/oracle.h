@@ -96,6 +96,23 @@ void orc_rope_tables(const uint32_t* pos /* [S, n_axes] */, uint32_t S, const ui
                      uint32_t n_axes, float theta, float* cos_out, float* sin_out);
 void orc_rope_apply(float* x, uint32_t H, uint32_t S, const float* cos_t, const float* sin_t);
 
+/* DiT block glue, one function per reference dispatch (zimage.slang,
+ * diffusion.slang), f32, reference reduction order (256 strided partial sums,
+ * then the shared-memory tree). */
+void orc_batch_rmsnorm(const float* x, const float* w, float* out, uint32_t dim, uint32_t n_rows, float eps);
+void orc_batch_layernorm(const float* x, float* out, uint32_t dim, uint32_t n_rows, float eps);
+void orc_modulate(float* x, const float* scale, const float* shift /* NULL: scale_modulate */, uint32_t dim,
+                  size_t n);
+void orc_batch_head_norm(float* x, const float* w, uint32_t n_heads, uint32_t D, uint32_t seq_len, float eps);
+void orc_transpose_heads(const float* in, float* out, uint32_t S, uint32_t H, uint32_t D);
+void orc_gated_residual(float* residual, const float* gate, const float* input, uint32_t dim, size_t n,
+                        int tanh_gate, float scale, float clip_thresh);
+void orc_silu(float* x, size_t n);
+void orc_gelu(float* x, size_t n);
+void orc_timestep_embed(float* out, uint32_t dim, float t);
+void orc_patchify(const float* in, float* out, uint32_t C, uint32_t H, uint32_t W, uint32_t ps);
+void orc_unpatchify(const float* in, float* out, uint32_t C, uint32_t H, uint32_t W, uint32_t ps);
+
 /* Number of OpenMP threads the oracle uses. */
 int orc_num_threads(void);
 

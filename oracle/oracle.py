@@ -60,6 +60,18 @@ def lib():
             "orc_rope_tables": (None, [_u32p, _u32, _u32p, _u32, ctypes.c_float, _f32p, _f32p]),
             "orc_rope_apply": (None, [_f32p, _u32, _u32, _f32p, _f32p]),
             "orc_num_threads": (ctypes.c_int, []),
+            "orc_batch_rmsnorm": (None, [_f32p, _f32p, _f32p, _u32, _u32, ctypes.c_float]),
+            "orc_batch_layernorm": (None, [_f32p, _f32p, _u32, _u32, ctypes.c_float]),
+            "orc_modulate": (None, [_f32p, _f32p, _f32p, _u32, _sz]),
+            "orc_batch_head_norm": (None, [_f32p, _f32p, _u32, _u32, _u32, ctypes.c_float]),
+            "orc_transpose_heads": (None, [_f32p, _f32p, _u32, _u32, _u32]),
+            "orc_gated_residual": (None, [_f32p, _f32p, _f32p, _u32, _sz, ctypes.c_int, ctypes.c_float,
+                                          ctypes.c_float]),
+            "orc_silu": (None, [_f32p, _sz]),
+            "orc_gelu": (None, [_f32p, _sz]),
+            "orc_timestep_embed": (None, [_f32p, _u32, ctypes.c_float]),
+            "orc_patchify": (None, [_f32p, _f32p, _u32, _u32, _u32, _u32]),
+            "orc_unpatchify": (None, [_f32p, _f32p, _u32, _u32, _u32, _u32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -226,3 +238,99 @@ def rope_apply(x: np.ndarray, cos_t: np.ndarray, sin_t: np.ndarray) -> np.ndarra
     lib().orc_rope_apply(_p(x, _f32p), H, S, _p(np.ascontiguousarray(cos_t, np.float32), _f32p),
                          _p(np.ascontiguousarray(sin_t, np.float32), _f32p))
     return x
+
+
+# --- DiT block glue: one function per reference dispatch (f32 in, f32 out) ---
+
+def _f32c(a) -> np.ndarray:
+    return np.array(a, dtype=np.float32, copy=True, order="C")
+
+
+def batch_rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """batch_rmsnorm (zimage.slang:449-500) on [rows, dim]."""
+    x = _f32c(x)
+    rows, dim = x.shape
+    out = np.empty_like(x)
+    lib().orc_batch_rmsnorm(_p(x, _f32p), _p(_f32c(w), _f32p), _p(out, _f32p), dim, rows, float(eps))
+    return out
+
+
+def batch_layernorm(x: np.ndarray, eps: float) -> np.ndarray:
+    """batch_layernorm (zimage.slang:502-561) on [rows, dim]."""
+    x = _f32c(x)
+    rows, dim = x.shape
+    out = np.empty_like(x)
+    lib().orc_batch_layernorm(_p(x, _f32p), _p(out, _f32p), dim, rows, float(eps))
+    return out
+
+
+def modulate(x: np.ndarray, scale: np.ndarray, shift=None) -> np.ndarray:
+    """scale_modulate (shift None) / adaln_modulate over the last axis."""
+    x = _f32c(x)
+    dim = x.shape[-1]
+    sh = _f32c(shift) if shift is not None else None
+    lib().orc_modulate(_p(x, _f32p), _p(_f32c(scale), _f32p), _p(sh, _f32p) if sh is not None else None,
+                       dim, x.size)
+    return x
+
+
+def batch_head_norm(x: np.ndarray, w: np.ndarray, n_heads: int, eps: float) -> np.ndarray:
+    """batch_head_norm (zimage.slang:609-667) on [seq, n_heads*D]."""
+    x = _f32c(x)
+    S = x.shape[0]
+    D = x.shape[1] // n_heads
+    lib().orc_batch_head_norm(_p(x, _f32p), _p(_f32c(w), _f32p), n_heads, D, S, float(eps))
+    return x
+
+
+def transpose_heads(x: np.ndarray, n_heads: int) -> np.ndarray:
+    """transpose_heads direction 0: [S, H*D] -> [H, S, D]."""
+    x = _f32c(x)
+    S = x.shape[0]
+    D = x.shape[1] // n_heads
+    out = np.empty((n_heads, S, D), np.float32)
+    lib().orc_transpose_heads(_p(x, _f32p), _p(out, _f32p), S, n_heads, D)
+    return out
+
+
+def gated_residual(residual: np.ndarray, gate: np.ndarray, inp: np.ndarray, tanh_gate: bool,
+                   scale: float = 1.0, clip_thresh: float = 0.0) -> np.ndarray:
+    """gated_residual (tanh_gate) / gated_residual_linear; returns the updated residual."""
+    r = _f32c(residual)
+    x = _f32c(inp)
+    lib().orc_gated_residual(_p(r, _f32p), _p(_f32c(gate), _f32p), _p(x, _f32p), r.shape[-1], r.size,
+                             1 if tanh_gate else 0, float(scale), float(clip_thresh))
+    return r
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    x = _f32c(x)
+    lib().orc_silu(_p(x, _f32p), x.size)
+    return x
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    x = _f32c(x)
+    lib().orc_gelu(_p(x, _f32p), x.size)
+    return x
+
+
+def timestep_embed(dim: int, t: float) -> np.ndarray:
+    out = np.empty(dim, np.float32)
+    lib().orc_timestep_embed(_p(out, _f32p), dim, float(t))
+    return out
+
+
+def patchify(latent: np.ndarray, ps: int) -> np.ndarray:
+    x = _f32c(latent)
+    C, H, W = x.shape
+    out = np.empty(((H // ps) * (W // ps), C * ps * ps), np.float32)
+    lib().orc_patchify(_p(x, _f32p), _p(out, _f32p), C, H, W, ps)
+    return out
+
+
+def unpatchify(patches: np.ndarray, C: int, H: int, W: int, ps: int) -> np.ndarray:
+    x = _f32c(patches)
+    out = np.empty((C, H, W), np.float32)
+    lib().orc_unpatchify(_p(x, _f32p), _p(out, _f32p), C, H, W, ps)
+    return out

@@ -1,0 +1,83 @@
+"""Composed DiT blocks (llmr_amd.dit) vs the oracle's restatement of the
+reference's dispatch sequence (oracle/blocks.py), at small shapes.
+
+The bar is the GEMM/attention one, relative L2 <= 1e-2, applied to what a
+block contributes (the residual update) and to the Flux velocity; the
+activation type sets how close they get (fp16 activations reproduce the
+reference's fp16 GEMM operands, bf16 carries 3 fewer mantissa bits)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_zimage_block_vs_oracle(dev, act):
+    from llmr_amd import dit, synth, workloads
+    from oracle import blocks
+    dim, H, ffn, S = 256, 2, 512, 200
+    w = dit.zimage_layer_weights(dim, H, ffn, device=dev, base_stream=300)
+    att = workloads.Attention("z", H, S, 128, 24, 11, 16, (32, 48, 48), 256.0)
+    cos_t, sin_t = workloads.rope_tables(workloads.attention_positions(att), att.axes, att.theta)
+    h0 = synth.normal(42, 399, S * dim).reshape(S, dim)
+    blk = dit.ZImageBlock(dim, H, ffn, S, act_dtype=act, device=dev)
+    h = torch.from_numpy(h0.copy()).to(dev)
+    blk.forward(w, h, torch.from_numpy(cos_t).to(dev), torch.from_numpy(sin_t).to(dev))
+    torch.cuda.synchronize()
+    wn = {k: _np(getattr(w, k)) for k in w.__dataclass_fields__}
+    ref = blocks.zimage_layer(wn, h0, H, cos_t, sin_t)
+    got = _np(h)
+    err = rel_l2(got - h0, ref - h0)
+    print(f"zimage block act={act}: rel L2 of the update {err:.2e}, of hidden {rel_l2(got, ref):.2e}")
+    assert err < (3e-3 if act == torch.float16 else 1e-2)
+
+
+def _small_flux():
+    from llmr_amd import dit
+    return dit.FluxConfig(dim=256, n_heads=2, mlp=512, n_double=2, n_single=2, text_dim=256, n_txt=40,
+                          latent_ch=16, latent_h=16, latent_w=16, patch=2)
+
+
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_flux_forward_vs_oracle(dev, act):
+    from llmr_amd import dit, synth
+    from oracle import blocks
+    cfg = _small_flux()
+    glob, doubles, singles = dit.flux_weights(cfg, device=dev)
+    model = dit.FluxDiT(cfg, glob, doubles, singles, act_dtype=act, device=dev)
+    lat = synth.normal(42, 501, cfg.latent_ch * cfg.latent_h * cfg.latent_w).reshape(
+        cfg.latent_ch, cfg.latent_h, cfg.latent_w)
+    txt = synth.normal(42, 502, cfg.n_txt * cfg.text_dim).reshape(cfg.n_txt, cfg.text_dim)
+    txt_t = torch.from_numpy(txt).to(dev).to(act)
+    out = model.forward(torch.from_numpy(lat).to(dev), txt_t, 0.5)
+    torch.cuda.synchronize()
+    as_np = lambda o: {k: _np(getattr(o, k)) for k in o.__dataclass_fields__}  # noqa: E731
+    cos_t, sin_t = (_np(t) for t in model.rope)
+    ref = blocks.flux_forward(cfg, as_np(glob), [as_np(d) for d in doubles], [as_np(s) for s in singles], lat,
+                              txt_t.float().cpu().numpy(), 0.5, cos_t, sin_t)
+    got = _np(out)
+    err = rel_l2(got, ref)
+    print(f"flux forward act={act}: velocity rel L2 {err:.2e}")
+    assert np.isfinite(got).all()
+    assert err < (5e-3 if act == torch.float16 else 2e-2)
+
+
+def test_flux_forward_is_deterministic(dev):
+    """Two forwards on the same inputs give identical bits (no state leaks
+    between calls through the shared buffers)."""
+    from llmr_amd import dit, synth
+    cfg = _small_flux()
+    model = dit.FluxDiT(cfg, *dit.flux_weights(cfg, device=dev), device=dev)
+    lat = torch.from_numpy(synth.normal(42, 503, 16 * 16 * 16).reshape(16, 16, 16)).to(dev)
+    txt = torch.from_numpy(synth.normal(42, 504, cfg.n_txt * cfg.text_dim).reshape(cfg.n_txt, -1)).to(dev)
+    a = model.forward(lat, txt.to(torch.bfloat16), 0.5).clone()
+    b = model.forward(lat, txt.to(torch.bfloat16), 0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

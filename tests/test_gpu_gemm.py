@@ -121,6 +121,7 @@ PERSIST_CASES = [
     (8, 4100, 4100, 320, 1, 0),
     (12, 2000, 4352, 1024, 1, 256),
     (8, 2560, 3332, 640, 1, 4),
+    (8, 4096, 3072, 64, 30, 0),   # Flux img_in: one real K stage of six
 ]
 
 

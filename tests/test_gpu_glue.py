@@ -1,0 +1,225 @@
+"""Block-glue entry points (C-ABI through llmr_amd.glue) vs the oracle's
+per-dispatch restatements.
+
+Tolerances: f32 outputs differ from the oracle only by reduction order and
+transcendental ulps (rtol 1e-5); 16-bit outputs are the f32 value rounded once,
+so they must sit within half an ulp of the 16-bit type of the oracle's value
+plus that f32 slack."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+ULP = {torch.float32: 2.0 ** -23, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
+
+
+def _close(got: torch.Tensor, ref: np.ndarray, dtype, atol=1e-6):
+    g = got.float().cpu().numpy()
+    tol = (0.5 * ULP[dtype] + 1e-5) * np.abs(ref) + atol
+    bad = np.abs(g - ref) > tol
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside tolerance; max err {np.abs(g - ref).max()}"
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dim,rows", [(3840, 37), (3072, 5), (100, 9)])
+def test_rmsnorm_modulate(orc, dev, dtype, dim, rows):
+    from llmr_amd import glue
+    r = _rng(dim + rows)
+    xf = r.standard_normal((rows, dim + 12)).astype(np.float32)  # rows of a wider buffer
+    w = (1 + 0.1 * r.standard_normal(dim)).astype(np.float32)
+    sc = (0.5 * r.standard_normal(dim)).astype(np.float32)
+    x_t = _dev(xf, dev)[:, :dim]
+    out = torch.empty(rows, dim, dtype=dtype, device=dev)
+    glue.batch_rmsnorm(x_t, _dev(w, dev), out, 1e-5, mod_scale=_dev(sc, dev))
+    torch.cuda.synchronize()
+    ref = orc.modulate(orc.batch_rmsnorm(xf[:, :dim], w, 1e-5), sc)
+    _close(out, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_layernorm_adaln_on_row_range(orc, dev, dtype):
+    from llmr_amd import glue
+    r = _rng(11)
+    S, nt, dim = 300, 44, 3072
+    h = (r.standard_normal((S, dim)) * 3 + 1.5).astype(np.float32)
+    sc = (0.3 * r.standard_normal(dim)).astype(np.float32)
+    sh = (0.3 * r.standard_normal(dim)).astype(np.float32)
+    h_t = _dev(h, dev)
+    out = torch.full((S, dim), 7.0, dtype=dtype, device=dev)
+    glue.batch_layernorm(h_t[nt:], out[nt:], 1e-6, mod_scale=_dev(sc, dev), mod_shift=_dev(sh, dev))
+    torch.cuda.synchronize()
+    ref = orc.modulate(orc.batch_layernorm(h[nt:], 1e-6), sc, sh)
+    _close(out[nt:], ref, dtype, atol=1e-5)
+    assert (out[:nt].float() == 7.0).all()  # rows outside the range untouched
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_qkv_heads_joint_rows(orc, dev, dtype):
+    """Image rows of a linear1-shaped buffer (stride > 3*H*128) into rows
+    row0.. of the joint Q/K/V, with head norm and RoPE; V unrotated."""
+    from llmr_amd import glue, workloads
+    r = _rng(12)
+    H, S, row0, rows, extra = 3, 70, 20, 50, 256
+    src = r.standard_normal((rows, 3 * H * 128 + extra)).astype(np.float32)
+    qn = (1 + 0.1 * r.standard_normal(128)).astype(np.float32)
+    kn = (1 + 0.1 * r.standard_normal(128)).astype(np.float32)
+    att = workloads.Attention("t", H, S, 128, 6, 8, 8, (16, 56, 56), 10000.0)
+    cos_t, sin_t = workloads.rope_tables(workloads.attention_positions(att), att.axes, att.theta)
+    q = torch.zeros(H, S, 128, dtype=dtype, device=dev)
+    k = torch.zeros_like(q)
+    v = torch.zeros_like(q)
+    glue.qkv_heads(_dev(src, dev), H, q, k, v, row0, _dev(qn, dev), _dev(kn, dev), 1e-6,
+                   (_dev(cos_t, dev), _dev(sin_t, dev)))
+    torch.cuda.synchronize()
+    D = H * 128
+    sl = slice(row0, row0 + rows)
+    rq = orc.rope_apply(orc.transpose_heads(orc.batch_head_norm(src[:, :D], qn, H, 1e-6), H), cos_t[sl], sin_t[sl])
+    rk = orc.rope_apply(orc.transpose_heads(orc.batch_head_norm(src[:, D:2 * D], kn, H, 1e-6), H), cos_t[sl],
+                        sin_t[sl])
+    rv = orc.transpose_heads(src[:, 2 * D:3 * D], H)
+    _close(q[:, sl], rq, dtype, atol=1e-5)
+    _close(k[:, sl], rk, dtype, atol=1e-5)
+    _close(v[:, sl], rv, dtype)
+    assert (q[:, :row0].float() == 0).all() and (v[:, row0 + rows:].float() == 0).all()
+
+
+def test_qkv_heads_plain_transpose(orc, dev):
+    from llmr_amd import glue
+    r = _rng(13)
+    H, S = 2, 33
+    src = r.standard_normal((S, 3 * H * 128)).astype(np.float32)
+    q = torch.empty(H, S, 128, dtype=torch.float32, device=dev)
+    k, v = torch.empty_like(q), torch.empty_like(q)
+    glue.qkv_heads(_dev(src, dev), H, q, k, v)
+    torch.cuda.synchronize()
+    for i, t in enumerate((q, k, v)):
+        np.testing.assert_array_equal(t.cpu().numpy(), orc.transpose_heads(src[:, i * H * 128:(i + 1) * H * 128], H))
+
+
+@pytest.mark.parametrize("mode,norm", [(2, True), (1, False), (0, False), (2, False)])
+def test_gated_residual_modes(orc, dev, mode, norm):
+    from llmr_amd import glue
+    r = _rng(14 + mode)
+    S, nt, dim = 200, 40, 3840
+    h = r.standard_normal((S, dim)).astype(np.float32)
+    x = r.standard_normal((S - nt, dim)).astype(np.float32) * 2
+    gate = r.standard_normal(dim).astype(np.float32)
+    nw = (1 + 0.1 * r.standard_normal(dim)).astype(np.float32)
+    h_t = _dev(h, dev)
+    glue.gated_residual(h_t[nt:], _dev(x, dev), _dev(gate, dev) if mode else None, mode,
+                        _dev(nw, dev) if norm else None, 1e-5)
+    torch.cuda.synchronize()
+    y = orc.batch_rmsnorm(x, nw, 1e-5) if norm else x
+    if mode == 0:
+        ref = h[nt:] + y
+    else:
+        ref = orc.gated_residual(h[nt:], gate, y, mode == 2)
+    got = h_t.cpu().numpy()
+    np.testing.assert_allclose(got[nt:], ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_array_equal(got[:nt], h[:nt])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_activation_concat_gelu_silu_mul(orc, dev, dtype):
+    """The single-stream concat: attention output -> cat[:, :d], gelu(linear1
+    MLP half) -> cat[:, d:]; and silu(gate) * up from one buffer."""
+    from llmr_amd import capi, glue
+    r = _rng(15)
+    S, d, m = 65, 256, 512
+    o = r.standard_normal((S, d)).astype(np.float32)
+    l1 = (3 * r.standard_normal((S, 3 * d + m))).astype(np.float32)
+    l1_t = _dev(l1, dev)
+    cat = torch.empty(S, d + m, dtype=dtype, device=dev)
+    glue.activation(_dev(o, dev), cat[:, :d], capi.ACT_COPY)
+    glue.activation(l1_t[:, 3 * d:], cat[:, d:], capi.ACT_GELU_TANH)
+    gu = (3 * r.standard_normal((S, 2 * m))).astype(np.float32)
+    gu_t = _dev(gu, dev)
+    sm = torch.empty(S, m, dtype=dtype, device=dev)
+    glue.activation(gu_t[:, :m], sm, capi.ACT_SILU_MUL, src2=gu_t[:, m:])
+    torch.cuda.synchronize()
+    _close(cat[:, :d], o, dtype)
+    _close(cat[:, d:], orc.gelu(l1[:, 3 * d:]), dtype, atol=1e-6)
+    _close(sm, orc.silu(gu[:, :m]) * gu[:, m:], dtype, atol=1e-6)
+
+
+def test_activation_in_place_single_row(orc, dev):
+    from llmr_amd import capi, glue
+    x = np.linspace(-9, 9, 3072, dtype=np.float32)[None, :]
+    t = _dev(x, dev)
+    glue.activation(t, t, capi.ACT_SILU)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(t.cpu().numpy(), orc.silu(x), rtol=1e-6, atol=1e-7)
+
+
+def test_timestep_patchify_unpatchify(orc, dev):
+    from llmr_amd import glue
+    emb = torch.empty(256, dtype=torch.float32, device=dev)
+    glue.timestep_embed(emb, 500.0)
+    r = _rng(16)
+    lat = r.standard_normal((16, 32, 48)).astype(np.float32)
+    p = torch.empty(16 * 24, 64, dtype=torch.bfloat16, device=dev)
+    glue.patchify(_dev(lat, dev), p, 2)
+    pf = _dev(orc.patchify(lat, 2), dev)
+    back = torch.empty(16, 32, 48, dtype=torch.float32, device=dev)
+    glue.unpatchify(pf, back, 2)
+    torch.cuda.synchronize()
+    # freq = exp(...) may differ by an ulp between device and host exp; the
+    # angle t * freq then moves by up to t * ulp(1) = 500 * 1.2e-7 = 6e-5
+    np.testing.assert_allclose(emb.cpu().numpy(), orc.timestep_embed(256, 500.0), rtol=0, atol=1.5e-4)
+    _close(p, orc.patchify(lat, 2), torch.bfloat16)
+    np.testing.assert_array_equal(back.cpu().numpy(), lat)
+
+
+def test_glue_rejects_bad_arguments(dev):
+    from llmr_amd import capi, glue
+    x = torch.zeros(4, 8192 + 4, device=dev)
+    out = torch.zeros(4, 8192 + 4, device=dev)
+    w = torch.ones(8192 + 4, device=dev)
+    with pytest.raises(capi.LlmrError) as e:  # wider than the register-resident row
+        glue.batch_rmsnorm(x, w, out, 1e-5)
+    assert e.value.code == capi.LLMR_ERR_INVALID_ARG
+    x = torch.zeros(4, 130, device=dev)
+    with pytest.raises(capi.LlmrError):  # dim % 4 != 0
+        glue.batch_rmsnorm(x[:, :126], w, torch.zeros(4, 126, device=dev), 1e-5)
+    ctx = glue.default_graph().ctx
+    base = torch.zeros(64, device=dev)
+    with pytest.raises(capi.LlmrError):  # misaligned pointer
+        ctx.gated_residual(base.data_ptr() + 4, 8, base.data_ptr(), 8, None, None, 0, 8, 2, 1e-5)
+    with pytest.raises(capi.LlmrError):  # row0 + rows beyond the sequence
+        q = torch.zeros(1, 8, 128, device=dev, dtype=torch.float16)
+        glue.qkv_heads(torch.zeros(8, 384, device=dev), 1, q, q.clone(), q.clone(), row0=1)
+    with pytest.raises(capi.LlmrError):  # destination columns beyond its stride
+        ctx.activation(base.data_ptr(), 8, 0, 0, base.data_ptr(), 0, 8, 4, 2, 8, capi.ACT_COPY)
+
+
+def test_synth_q4k_matches_host_quantizer(dev):
+    """The device generator + quantizer is byte-identical to the package's host
+    path (synth.normal + gguf.quantize_q4k) on the same stream."""
+    from llmr_amd import glue, gguf, synth
+    rows, K, stream = 96, 768, 4242
+    blk = glue.synth_q4k(rows, K, stream, 0.02, seed=42, device=dev)
+    torch.cuda.synchronize()
+    host = gguf.quantize_q4k(synth.normal(42, stream, rows * K, 0.02).reshape(rows, K))
+    got = blk.cpu().numpy()
+    assert got.size == host.size
+    diff = np.flatnonzero(got != host)
+    assert diff.size == 0, f"{diff.size} bytes differ, first at {diff[:8]}"
+
+
+def test_synth_q4k_distribution(orc, dev):
+    from llmr_amd import glue
+    rows, K = 1024, 3072
+    blk = glue.synth_q4k(rows, K, 77, 0.02, device=dev)
+    torch.cuda.synchronize()
+    w = orc.dequant_q4k(blk.cpu().numpy())
+    assert np.isfinite(w).all()
+    assert abs(w.mean()) < 1e-4 and abs(w.std() / 0.02 - 1) < 0.02
