@@ -169,6 +169,56 @@ LLMR_API int llmr_batch_matmul_pc(llmr_context* ctx, const void* weight, uint32_
                                   const void* input, uint32_t input_type, float* output,
                                   const llmr_batch_matmul_params* pc);
 
+/* One GEMM of llmr_batch_matmul_multi: output = input · W[row_offset ..]^T as
+ * llmr_batch_matmul, written through the call's epilogue. */
+typedef struct llmr_matmul_job {
+    const void* weight; /* raw GGUF blocks; row row_offset is output feature 0 */
+    const void* input;  /* [seq_len, in_dim] of input_type, 16-byte aligned */
+    float* output;      /* f32 rows, row stride ldy (GATED_RESIDUAL: read and updated) */
+    const float* gate;  /* GATED_RESIDUAL: per-feature gate [out_dim], or NULL for 1 */
+    void* output2;      /* SPLIT_GELU: 16-bit rows, row stride ldy2 */
+    uint32_t seq_len;
+    uint32_t row_offset;
+} llmr_matmul_job;
+
+enum { LLMR_EPI_STORE = 0, LLMR_EPI_GATED_RESIDUAL = 1, LLMR_EPI_SPLIT_GELU = 2 };
+
+/* How the f32 result r[m, n] of a job reaches memory:
+ *   STORE            output[m*ldy + n] = r
+ *   GATED_RESIDUAL   output[m*ldy + n] += gate[n] * r      (out_dim <= 8192)
+ *   SPLIT_GELU       n <  split: output[m*ldy + n] = r
+ *                    n >= split: output2[m*ldy2 + n - split] = gelu_tanh(r)
+ *                    rounded to output2_type (split % 8 == 0)
+ * ldy 0 means out_dim (SPLIT_GELU: split); ldy2 0 means out_dim - split.
+ * Strides are multiples of 4; out_dim % 4 == 0 unless the epilogue is a
+ * STORE with ldy == out_dim. */
+typedef struct llmr_matmul_epilogue {
+    uint32_t kind;
+    uint32_t ldy;
+    uint32_t split;
+    uint32_t ldy2;
+    uint32_t output2_type; /* LLMR_GGML_BF16 or LLMR_GGML_F16 */
+} llmr_matmul_epilogue;
+
+/* n_jobs GEMMs of one shape and type (out_dim, in_dim, weight_type,
+ * input_type) with a shared epilogue (NULL: STORE, ldy = out_dim). Equivalent
+ * to n_jobs llmr_batch_matmul calls each followed by its epilogue; the jobs'
+ * outputs must not overlap. Replaces the reference's per-stream and per-slot
+ * dispatch_batch_matmul calls and the glue dispatches that follow them:
+ *   - the image and text stream projections of a Flux double block
+ *     (dependencies/flux.c3l/flux_dit.c3:786-804, 875-887, 917-964), run as
+ *     one launch: pairs of jobs share the device as one grid of tiles;
+ *   - gated_residual_linear after a projection (flux_dit.c3:891-898, 1064-1068);
+ *   - the single block's linear1 slots plus silu/gelu and concat_rows_copy
+ *     (flux_dit.c3:1005-1018, 1049-1058): Q | K | V to `output`, the
+ *     activated MLP half straight into linear2's input.
+ * A job pair that cannot run as one persistent launch (f32 input, too few
+ * tiles, ...) runs job by job through a context workspace (grow-only, like
+ * the SwiGLU's). No reference counterpart as a single call. */
+LLMR_API int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t weight_type, uint32_t input_type,
+                                     uint32_t out_dim, uint32_t in_dim, const llmr_matmul_job* jobs,
+                                     uint32_t n_jobs, const llmr_matmul_epilogue* epilogue);
+
 /* SwiGLU feed-forward in-projection, both matmuls and the activation in one op:
  *   g = input · weight_gate^T,  u = input · weight_up^T,
  *   output[s, o] = silu(g[s, o]) * u[s, o],  silu(g) = g / (1 + e^-g)

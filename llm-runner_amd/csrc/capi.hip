@@ -221,6 +221,75 @@ int llmr_batch_matmul_pc(llmr_context* ctx, const void* weight, uint32_t wtype, 
                              pc->seq_len, pc->row_offset);
 }
 
+// Grows the context workspace to `need` bytes (hipFree waits for every
+// launch that may still use the old one).
+static int grow_workspace(llmr_context* ctx, size_t need) {
+    if (need <= ctx->ws_bytes) return LLMR_OK;
+    if (ctx->ws) LLMR_HIP_CHECK(hipFree(ctx->ws));
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+    LLMR_HIP_CHECK(hipMalloc(&ctx->ws, need));
+    ctx->ws_bytes = need;
+    return LLMR_OK;
+}
+
+int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
+                            const llmr_matmul_job* jobs, uint32_t n_jobs, const llmr_matmul_epilogue* epilogue) {
+    if (int r = check_ctx(ctx)) return r;
+    if (!is_act_type(xtype))
+        return fail(LLMR_ERR_UNSUPPORTED, "input type %u not supported (F32=0, F16=1, BF16=30)", xtype);
+    if (n_jobs == 0) return ok();
+    if (!jobs) return fail(LLMR_ERR_INVALID_ARG, "null jobs");
+    if (n_jobs > 64) return fail(LLMR_ERR_INVALID_ARG, "at most 64 jobs per call (got %u)", n_jobs);
+    if (out_dim == 0) return ok();
+    llmr_matmul_epilogue e = epilogue ? *epilogue : llmr_matmul_epilogue{LLMR_EPI_STORE, 0, 0, 0, 0};
+    if (e.kind > LLMR_EPI_SPLIT_GELU) return fail(LLMR_ERR_INVALID_ARG, "unknown epilogue kind %u", e.kind);
+    const bool split = e.kind == LLMR_EPI_SPLIT_GELU;
+    if (!split) e.split = out_dim;
+    if (split && (e.split > out_dim || e.split % 8))
+        return fail(LLMR_ERR_INVALID_ARG, "split must be a multiple of 8 and <= out_dim (got %u)", e.split);
+    if (e.ldy == 0) e.ldy = split ? e.split : out_dim;
+    if (e.ldy2 == 0) e.ldy2 = out_dim - e.split;
+    const uint32_t width = split ? e.split : out_dim;
+    const bool plain = e.kind == LLMR_EPI_STORE && e.ldy == out_dim;
+    if (!plain && out_dim % 4) return fail(LLMR_ERR_INVALID_ARG, "this epilogue needs out_dim %% 4 == 0");
+    if (!plain && (e.ldy % 4 || e.ldy < width))
+        return fail(LLMR_ERR_INVALID_ARG, "ldy must be a multiple of 4 and >= %u (got %u)", width, e.ldy);
+    if (e.kind == LLMR_EPI_GATED_RESIDUAL && out_dim > llmr::kRowNormMaxDim)
+        return fail(LLMR_ERR_INVALID_ARG, "GATED_RESIDUAL needs out_dim <= %u", llmr::kRowNormMaxDim);
+    const bool has2 = split && e.split < out_dim;
+    if (has2 && (e.ldy2 % 4 || e.ldy2 < out_dim - e.split))
+        return fail(LLMR_ERR_INVALID_ARG, "ldy2 must be a multiple of 4 and >= out_dim - split");
+    if (has2 && e.output2_type != LLMR_GGML_BF16 && e.output2_type != LLMR_GGML_F16)
+        return fail(LLMR_ERR_UNSUPPORTED, "output2_type must be BF16 or F16 (got %u)", e.output2_type);
+    if ((uint64_t)e.ldy > 0xffffffffull / 4) return fail(LLMR_ERR_INVALID_ARG, "ldy too large");
+    llmr::GemmJob gj[64];
+    for (uint32_t i = 0; i < n_jobs; i++) {
+        const llmr_matmul_job& j = jobs[i];
+        if (int r = check_weight(j.weight, wtype, in_dim)) return r;
+        if (j.seq_len && (!j.input || !j.output))
+            return fail(LLMR_ERR_INVALID_ARG, "job %u: null input/output pointer", i);
+        if (!aligned(j.input, 16) || !aligned(j.output, 16))
+            return fail(LLMR_ERR_INVALID_ARG, "job %u: input/output pointers must be 16-byte aligned", i);
+        if ((uint64_t)j.row_offset + out_dim > 0xffffffffull)
+            return fail(LLMR_ERR_INVALID_ARG, "job %u: row_offset + out_dim overflows", i);
+        if (e.kind == LLMR_EPI_GATED_RESIDUAL && j.gate && !aligned(j.gate, 16))
+            return fail(LLMR_ERR_INVALID_ARG, "job %u: gate must be 16-byte aligned", i);
+        if (has2 && j.seq_len && (!j.output2 || !aligned(j.output2, 16)))
+            return fail(LLMR_ERR_INVALID_ARG, "job %u: output2 must be non-null and 16-byte aligned", i);
+        gj[i] = llmr::GemmJob{j.weight, j.input, j.output, e.kind == LLMR_EPI_GATED_RESIDUAL ? j.gate : nullptr,
+                              has2 ? j.output2 : nullptr, j.seq_len, j.row_offset};
+    }
+    const llmr::GemmEpilogue ge{e.kind, e.ldy, e.ldy2, e.split, has2 ? e.output2_type : (uint32_t)LLMR_GGML_BF16};
+    const size_t need = llmr::batch_matmul_multi_workspace_bytes(wtype, xtype, out_dim, in_dim, gj, n_jobs, ge,
+                                                                 ctx->num_cus);
+    if (int r = grow_workspace(ctx, need)) return r;
+    hipError_t err = llmr::launch_batch_matmul_multi(wtype, xtype, out_dim, in_dim, gj, n_jobs, ge, ctx->num_cus,
+                                                     ctx->ws, ctx->cur);
+    if (err != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul_multi launch: %s", hipGetErrorString(err));
+    return ok();
+}
+
 int llmr_batch_matmul_swiglu(llmr_context* ctx, const void* weight_gate, const void* weight_up,
                               uint32_t wtype, const void* input, uint32_t xtype, float* output,
                               uint32_t out_dim, uint32_t in_dim, uint32_t seq_len) {
@@ -236,15 +305,7 @@ int llmr_batch_matmul_swiglu(llmr_context* ctx, const void* weight_gate, const v
     if (!input || !output) return fail(LLMR_ERR_INVALID_ARG, "null input/output pointer");
     if (!aligned(input, 16) || !aligned(output, 16))
         return fail(LLMR_ERR_INVALID_ARG, "input/output pointers must be 16-byte aligned");
-    const size_t need = llmr::swiglu_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len);
-    if (need > ctx->ws_bytes) {
-        // hipFree waits for every launch that may still read the old workspace
-        if (ctx->ws) LLMR_HIP_CHECK(hipFree(ctx->ws));
-        ctx->ws = nullptr;
-        ctx->ws_bytes = 0;
-        LLMR_HIP_CHECK(hipMalloc(&ctx->ws, need));
-        ctx->ws_bytes = need;
-    }
+    if (int r = grow_workspace(ctx, llmr::swiglu_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len))) return r;
     hipError_t e = llmr::launch_batch_matmul_swiglu(weight_gate, weight_up, wtype, input, xtype, output, out_dim,
                                                     in_dim, seq_len, ctx->num_cus, ctx->ws, ctx->cur);
     if (e != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul_swiglu launch: %s", hipGetErrorString(e));

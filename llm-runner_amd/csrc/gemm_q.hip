@@ -619,17 +619,72 @@ __device__ __forceinline__ float silu(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
 }
 
+// gelu (tanh form, lib/shaders/diffusion.slang:1103-1107) as
+// 0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)), u = 0.7978845608 (x + 0.044715 x^3)
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float u = 0.7978845608f * (x + 0.044715f * x * x * x);
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u));
+}
+
+// Output of the persistent kernel's tile accumulators (host-selected):
+//   kEpiStore      Y[m, n] = acc
+//   kEpiResidual   Y[m, n] += gate[n] * acc  (gate 1 when null)
+//   kEpiSplitGelu  n < split: Y[m, n] = acc; n >= split: Y2[m, n - split] =
+//                  16-bit gelu(acc)   (split % 8 == 0)
+// with row strides ldy (Y) and ldy2 (Y2).
+constexpr uint32_t kEpiStore = 0, kEpiResidual = 1, kEpiSplitGelu = 2;
+
+// One GEMM of a persistent launch. A launch multiplies up to two problems
+// that share N and K (e.g. the text and image rows of a block with their own
+// weights); their 256-row tiles are stacked along M, problem 0 first.
+struct PersistProblem {
+    const uint8_t* W;   // weight blocks; row row_offset is output feature 0
+    const void* X;      // [M, K] 16-bit activations
+    float* Y;           // f32 output (kEpiResidual: read and updated)
+    const float* gate;  // kEpiResidual: [N] or null
+    void* Y2;           // kEpiSplitGelu: 16-bit output
+    uint32_t M, row_offset, tiles_m;
+};
+struct PersistArgs {
+    PersistProblem p[2];
+    const uint8_t* W2;  // SwiGLU: the up weight (p[0].W is the gate)
+    uint32_t N, K, tiles_m, tiles_n;  // tiles_m of both problems
+    uint32_t epi, ldy, ldy2, split, y2_bf16;
+};
+
+template <typename T>
+__device__ __forceinline__ T pick(uint32_t p, T a, T b) {
+    return p ? b : a;
+}
+
 // SW (SwiGLU, batch_matmul_swiglu_q8, llm.slang:1769-1911): W holds the gate
 // rows and W2 the up rows (N each, row_offset unused); a tile covers 128
 // output features, whose 128 gate and 128 up rows form its 256 weight rows
 // arranged so that each wave's 128 feature columns are 64 gate features
 // followed by the same 64 up features: the epilogue writes
 // silu(gate) * up from two accumulators of the same lane.
-template <uint32_t WT, uint32_t XT, bool SW>
-__global__ void __launch_bounds__(256, 1)
-gemm_q_persist(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2, const void* __restrict__ X,
-               float* __restrict__ Y, uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset, uint32_t tiles_m,
-               uint32_t tiles_n) {
+template <uint32_t WT, uint32_t XT, bool SW, uint32_t EPI = kEpiStore, bool GROUPED = false>
+__global__ void __launch_bounds__(256, 1) gemm_q_persist(const PersistArgs args) {
+    static_assert(!(SW && GROUPED) && (!SW || EPI == kEpiStore), "SwiGLU launches are single, plain stores");
+    // every argument the kernel uses as a scalar local (the lambdas below
+    // capture these, never the argument struct, which would otherwise be
+    // addressed through private memory)
+    const uint32_t N = args.N, K = args.K, tiles_m = args.tiles_m, tiles_n = args.tiles_n;
+    const uint32_t ldy = args.ldy, ldy2 = args.ldy2, split = args.split, y2_bf16 = args.y2_bf16;
+    const uint8_t* const W2 = args.W2;
+    const uint8_t* const Wp0 = args.p[0].W;
+    const uint8_t* const Wp1 = GROUPED ? args.p[1].W : nullptr;
+    const void* const Xp0 = args.p[0].X;
+    const void* const Xp1 = GROUPED ? args.p[1].X : nullptr;
+    float* const Yp0 = args.p[0].Y;
+    float* const Yp1 = GROUPED ? args.p[1].Y : nullptr;
+    const float* const Gp0 = args.p[0].gate;
+    const float* const Gp1 = GROUPED ? args.p[1].gate : nullptr;
+    void* const Y2p0 = args.p[0].Y2;
+    void* const Y2p1 = GROUPED ? args.p[1].Y2 : nullptr;
+    const uint32_t Mp0 = args.p[0].M, Mp1 = GROUPED ? args.p[1].M : 0u;
+    const uint32_t Rp0 = args.p[0].row_offset, Rp1 = GROUPED ? args.p[1].row_offset : 0u;
+    const uint32_t Tp0 = args.p[0].tiles_m;
     static_assert(XT == kGgmlF16 || XT == kGgmlBF16, "16-bit activations only");
     constexpr uint32_t NT = SW ? 128u : 256u;  // output features per tile
     constexpr uint32_t TILE = 256u * 128u;  // bytes of one 256-row x 64-wide 16-bit tile
@@ -689,27 +744,30 @@ gemm_q_persist(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2, co
         const uint8_t* base;      // the tile's first activation row / weight row
         uint32_t size;            // bytes of valid rows from base (0 past the last tile)
     };
-    auto tile_origin = [&](uint32_t k, uint32_t& m0, uint32_t& n0) {
+    // tile k of this workgroup: its problem, its first row in that problem,
+    // its first output feature
+    auto tile_origin = [&](uint32_t k, uint32_t& p, uint32_t& m0, uint32_t& n0) {
         uint32_t tm, tn;
         map_tile_persist(blockIdx.x + k * G, G, tiles_m, tiles_n, tm, tn);
-        m0 = tm * 256u;
+        p = GROUPED && tm >= Tp0 ? 1u : 0u;
+        m0 = (tm - (p ? Tp0 : 0u)) * 256u;
         n0 = tn * NT;
     };
     auto x_tile = [&](Cursor& c, uint32_t k) {
-        uint32_t m0, n0;
-        tile_origin(k, m0, n0);
+        uint32_t p, m0, n0;
+        tile_origin(k, p, m0, n0);
         c.s = 0;
-        c.base = (const uint8_t*)X + (uint64_t)m0 * xrow;
-        c.size = k < n_tiles ? (M - m0) * xrow : 0u;
+        c.base = (const uint8_t*)pick(p, Xp0, Xp1) + (uint64_t)m0 * xrow;
+        c.size = k < n_tiles ? (pick(p, Mp0, Mp1) - m0) * xrow : 0u;
     };
     auto w_tile = [&](Cursor& c, uint32_t k) {
-        uint32_t m0, n0;
-        tile_origin(k, m0, n0);
+        uint32_t p, m0, n0;
+        tile_origin(k, p, m0, n0);
         c.s = 0;
         if constexpr (SW)
-            c.base = (wave < 2u ? W : W2) + (uint64_t)n0 * rb;
+            c.base = (wave < 2u ? Wp0 : W2) + (uint64_t)n0 * rb;
         else
-            c.base = W + (uint64_t)(row_offset + n0) * rb;
+            c.base = pick(p, Wp0, Wp1) + (uint64_t)(pick(p, Rp0, Rp1) + n0) * rb;
         c.size = k < n_tiles ? (N - n0) * rb : 0u;
     };
     Cursor cx{0, nullptr, 0}, cw{0, nullptr, 0};
@@ -777,42 +835,82 @@ gemm_q_persist(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2, co
     // host-checked: a lane's four consecutive features are all in range or
     // all out).
     auto store_tile = [&](uint32_t k) {
-        uint32_t tm, tn;
-        map_tile_persist(blockIdx.x + k * G, G, tiles_m, tiles_n, tm, tn);
+        uint32_t p, m0, n0;
+        tile_origin(k, p, m0, n0);
+        const uint32_t M = pick(p, Mp0, Mp1);
+        float* const Y = pick(p, Yp0, Yp1);
         if constexpr (SW) {
             // acc[a] (gate) and acc[a + 2] (up) hold the same features
 #pragma unroll
             for (int a = 0; a < 2; a++)
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
-                    const uint32_t m = tm * 256u + wm * 128u + b * 32u + l32;
+                    const uint32_t m = m0 + wm * 128u + b * 32u + l32;
 #pragma unroll
                     for (int g = 0; g < 4; g++) {
-                        const uint32_t n = tn * 128u + wn * 64u + a * 32u + 8u * g + 4u * kh;
+                        const uint32_t n = n0 + wn * 64u + a * 32u + 8u * g + 4u * kh;
                         f32x4 v;
 #pragma unroll
                         for (int e = 0; e < 4; e++) v[e] = silu(acc[a][b][4 * g + e]) * acc[a + 2][b][4 * g + e];
-                        if (m < M && n < N) *(f32x4*)(Y + (uint64_t)m * N + n) = v;
+                        if (m < M && n < N) *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
                     }
                     acc[a][b] = f32x16{};
                     acc[a + 2][b] = f32x16{};
                 }
             return;
         }
+        // the lane's four consecutive features n .. n+3 of row m (N % 4 == 0,
+        // host-checked: all four in range or none). nw = n - 4 kh is the same
+        // for the whole wave; with split % 8 == 0 (host-checked) nw < split
+        // decides the side of split for both kh, as a uniform branch.
+        auto each = [&](auto&& f) __attribute__((always_inline)) {
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+            for (int a = 0; a < 4; a++)
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const uint32_t m = tm * 256u + wm * 128u + b * 32u + l32;
+                for (int b = 0; b < 4; b++) {
+                    const uint32_t m = m0 + wm * 128u + b * 32u + l32;
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const uint32_t n = tn * 256u + wn * 128u + a * 32u + 8u * g + 4u * kh;
-                    if (m < M && n < N)
-                        *(f32x4*)(Y + (uint64_t)m * N + n) =
-                            f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
+                    for (int g = 0; g < 4; g++) {
+                        const uint32_t nw = n0 + wn * 128u + a * 32u + 8u * g;
+                        const uint32_t n = nw + 4u * kh;
+                        if (m < M && n < N)
+                            f(m, n, nw, f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2],
+                                              acc[a][b][4 * g + 3]});
+                    }
+                    acc[a][b] = f32x16{};
                 }
-                acc[a][b] = f32x16{};
-            }
+        };
+        if constexpr (EPI == kEpiResidual) {
+            const float* const gate = pick(p, Gp0, Gp1);
+            each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
+                f32x4* const h = (f32x4*)(Y + (uint64_t)m * ldy + n);
+                const f32x4 gv = gate ? *(const f32x4*)(gate + n) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+                *h = *h + gv * v;
+            });
+        } else if constexpr (EPI == kEpiSplitGelu) {
+            uint16_t* const Y2 = (uint16_t*)pick(p, Y2p0, Y2p1);
+            const uint32_t bf = y2_bf16;
+            each([&](uint32_t m, uint32_t n, uint32_t nw, f32x4 v) __attribute__((always_inline)) {
+                if (nw < split) {
+                    *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
+                } else {
+                    const f32x4 gl{gelu_tanh(v.x), gelu_tanh(v.y), gelu_tanh(v.z), gelu_tanh(v.w)};
+                    u32x2 o;
+                    if (bf) {
+                        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+                        o.x = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.x, (__bf16)gl.y});
+                        o.y = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.z, (__bf16)gl.w});
+                    } else {
+                        o = u32x2{pack_f16x2(gl.x, gl.y), pack_f16x2(gl.z, gl.w)};
+                    }
+                    *(u32x2*)(Y2 + (uint64_t)m * ldy2 + (n - split)) = o;
+                }
+            });
+        } else {
+            each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
+                *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
+            });
+        }
     };
 
     // prologue, issued in the steady state's order (a stage issues the
@@ -1004,9 +1102,15 @@ hipError_t dispatch_x(const void* w, const void* x, float* y, uint32_t N, uint32
         if (fits31 && N % 4 == 0 && 2 * tiles >= (uint64_t)num_cus) {
             const uint32_t tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
             const uint32_t grid = (uint32_t)min(tiles, (uint64_t)num_cus);
-            hipLaunchKernelGGL((gemm_q_persist<WT, XT, false>), dim3(grid), dim3(256), 0, st,
-                               (const uint8_t*)w, (const uint8_t*)nullptr, x, y, N, K, M, row_offset, tiles_m,
-                               tiles_n);
+            PersistArgs a{};
+            a.p[0] = PersistProblem{(const uint8_t*)w, x, y, nullptr, nullptr, M, row_offset, tiles_m};
+            a.N = N;
+            a.K = K;
+            a.tiles_m = tiles_m;
+            a.tiles_n = tiles_n;
+            a.epi = kEpiStore;
+            a.ldy = N;
+            hipLaunchKernelGGL((gemm_q_persist<WT, XT, false>), dim3(grid), dim3(256), 0, st, a);
             return hipGetLastError();
         }
     }
@@ -1096,12 +1200,19 @@ hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t w
     const uint32_t tiles_m = (M + 255) / 256, tiles_n = (N + 127) / 128;
     const uint32_t grid = (uint32_t)min((uint64_t)tiles_m * tiles_n, (uint64_t)num_cus);
     if (wtype != kGgmlQ8_0) return hipErrorInvalidValue;
+    PersistArgs a{};
+    a.p[0] = PersistProblem{(const uint8_t*)wg, x16, y, nullptr, nullptr, M, 0u, tiles_m};
+    a.W2 = (const uint8_t*)wu;
+    a.N = N;
+    a.K = K;
+    a.tiles_m = tiles_m;
+    a.tiles_n = tiles_n;
+    a.epi = kEpiStore;
+    a.ldy = N;
     if (xt == kGgmlF16)
-        hipLaunchKernelGGL((gemm_q_persist<kGgmlQ8_0, kGgmlF16, true>), dim3(grid), dim3(256), 0, st,
-                           (const uint8_t*)wg, (const uint8_t*)wu, x16, y, N, K, M, 0u, tiles_m, tiles_n);
+        hipLaunchKernelGGL((gemm_q_persist<kGgmlQ8_0, kGgmlF16, true>), dim3(grid), dim3(256), 0, st, a);
     else
-        hipLaunchKernelGGL((gemm_q_persist<kGgmlQ8_0, kGgmlBF16, true>), dim3(grid), dim3(256), 0, st,
-                           (const uint8_t*)wg, (const uint8_t*)wu, x16, y, N, K, M, 0u, tiles_m, tiles_n);
+        hipLaunchKernelGGL((gemm_q_persist<kGgmlQ8_0, kGgmlBF16, true>), dim3(grid), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
@@ -1109,9 +1220,120 @@ hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uin
                                float* y, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,
                                uint32_t row_offset, int num_cus, hipStream_t st) {
     if (seq_len == 0 || out_dim == 0) return hipSuccess;
+    if (wtype == kGgmlQ4K && seq_len <= kGemvMaxTokens)
+        return launch_gemv_q4k(w, xtype, x, y, out_dim, in_dim, seq_len, row_offset, st);
     if (wtype == kGgmlQ8_0)
         return dispatch_w<kGgmlQ8_0>(w, xtype, x, y, out_dim, in_dim, seq_len, row_offset, num_cus, st);
     return dispatch_w<kGgmlQ4K>(w, xtype, x, y, out_dim, in_dim, seq_len, row_offset, num_cus, st);
+}
+
+namespace {
+
+// Whether jobs [j0, j0 + n) (n <= 2) run as one persistent launch: 16-bit
+// activations, N % 4 == 0, whole 64-wide K stages, 32-bit buffer offsets for
+// every job's activations and used weight rows, and at least half the CUs'
+// worth of 256 x 256 tiles between them.
+bool multi_persistent(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n,
+                      int num_cus) {
+    if (xtype == kGgmlF32 || N % 4 || K % kBK) return false;
+    const uint64_t rb = (wtype == kGgmlQ8_0) ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * 144;
+    uint64_t tiles = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        if ((uint64_t)jobs[i].M * K * 2u >= (1ull << 31) || (uint64_t)N * rb >= (1ull << 31)) return false;
+        tiles += (uint64_t)((jobs[i].M + 255) / 256) * ((N + 255) / 256);
+    }
+    return 2 * tiles >= (uint64_t)num_cus;
+}
+
+template <uint32_t WT, uint32_t XT>
+hipError_t launch_persist_multi(uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n, const GemmEpilogue& epi,
+                                int num_cus, hipStream_t st) {
+    PersistArgs a{};
+    const uint32_t tiles_n = (N + 255) / 256;
+    uint32_t tiles_m = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        const GemmJob& j = jobs[i];
+        const uint32_t tm = (j.M + 255) / 256;
+        a.p[i] = PersistProblem{(const uint8_t*)j.w, j.x, j.y, j.gate, j.y2, j.M, j.row_offset, tm};
+        tiles_m += tm;
+    }
+    a.N = N;
+    a.K = K;
+    a.tiles_m = tiles_m;
+    a.tiles_n = tiles_n;
+    a.epi = epi.kind;
+    a.ldy = epi.ldy;
+    a.ldy2 = epi.ldy2;
+    a.split = epi.kind == kEpiSplitGelu ? epi.split : N;
+    a.y2_bf16 = epi.y2_type == kGgmlBF16 ? 1u : 0u;
+    const uint32_t grid = (uint32_t)min((uint64_t)tiles_m * tiles_n, (uint64_t)num_cus);
+    auto kern = epi.kind == kEpiResidual    ? gemm_q_persist<WT, XT, false, kEpiResidual, true>
+                : epi.kind == kEpiSplitGelu ? gemm_q_persist<WT, XT, false, kEpiSplitGelu, true>
+                                            : gemm_q_persist<WT, XT, false, kEpiStore, true>;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// One job the persistent kernel does not take: the plain GEMM into the
+// workspace `t` (directly into the output for an unstrided store), then
+// the epilogue as glue passes.
+hipError_t run_job_fallback(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob& j,
+                            const GemmEpilogue& epi, int num_cus, float* t, hipStream_t st) {
+    if (epi.kind == kEpiStore && epi.ldy == N)
+        return launch_batch_matmul(j.w, wtype, j.x, xtype, j.y, N, K, j.M, j.row_offset, num_cus, st);
+    hipError_t e = launch_batch_matmul(j.w, wtype, j.x, xtype, t, N, K, j.M, j.row_offset, num_cus, st);
+    if (e != hipSuccess) return e;
+    if (epi.kind == kEpiResidual) {
+        const ResidualArgs r{j.y, t, nullptr, j.gate, epi.ldy, N, j.M, N, 0.0f};
+        return launch_residual(r, false, st);
+    }
+    const uint32_t split = epi.kind == kEpiSplitGelu ? epi.split : N;
+    if (split > 0) {
+        const ActColsArgs c{t, j.y, N, 0u, 0u, epi.ldy, 0u, j.M, split};
+        if ((e = launch_act_cols(c, kActCopy, kGgmlF32, st)) != hipSuccess) return e;
+    }
+    if (split < N) {
+        const ActColsArgs c{t, j.y2, N, split, 0u, epi.ldy2, 0u, j.M, N - split};
+        e = launch_act_cols(c, kActGelu, epi.y2_type, st);
+    }
+    return e;
+}
+
+}  // namespace
+
+size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K,
+                                          const GemmJob* jobs, uint32_t n_jobs, const GemmEpilogue& epi,
+                                          int num_cus) {
+    size_t need = 0;
+    for (uint32_t i = 0; i < n_jobs; i += 2) {
+        const uint32_t n = min(2u, n_jobs - i);
+        if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) continue;
+        if (epi.kind == kEpiStore && epi.ldy == N) continue;
+        for (uint32_t q = i; q < i + n; q++) need = max(need, (size_t)jobs[q].M * N * sizeof(float));
+    }
+    return need;
+}
+
+hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs,
+                                     uint32_t n_jobs, const GemmEpilogue& epi, int num_cus, void* ws,
+                                     hipStream_t st) {
+    for (uint32_t i = 0; i < n_jobs; i += 2) {
+        const uint32_t n = min(2u, n_jobs - i);
+        hipError_t e = hipSuccess;
+        if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) {
+            if (wtype == kGgmlQ8_0)
+                e = xtype == kGgmlF16 ? launch_persist_multi<kGgmlQ8_0, kGgmlF16>(N, K, jobs + i, n, epi, num_cus, st)
+                                      : launch_persist_multi<kGgmlQ8_0, kGgmlBF16>(N, K, jobs + i, n, epi, num_cus, st);
+            else
+                e = xtype == kGgmlF16 ? launch_persist_multi<kGgmlQ4K, kGgmlF16>(N, K, jobs + i, n, epi, num_cus, st)
+                                      : launch_persist_multi<kGgmlQ4K, kGgmlBF16>(N, K, jobs + i, n, epi, num_cus, st);
+        } else {
+            for (uint32_t q = i; q < i + n && e == hipSuccess; q++)
+                e = run_job_fallback(wtype, xtype, N, K, jobs[q], epi, num_cus, (float*)ws, st);
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace llmr

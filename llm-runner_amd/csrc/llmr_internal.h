@@ -19,6 +19,35 @@ hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uin
                                float* y, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,
                                uint32_t row_offset, int num_cus, hipStream_t st);
 
+// Several GEMMs of one shape (N, K, weight and activation types) with a
+// shared epilogue (kind kEpi* of gemm_q.hip: 0 store, 1 gated residual
+// accumulate, 2 f32 | 16-bit gelu column split). Pairs of jobs run as one
+// persistent launch when they fill the device; other jobs run as a plain
+// GEMM into `ws` (batch_matmul_multi_workspace_bytes) plus glue passes.
+struct GemmJob {
+    const void* w;
+    const void* x;
+    float* y;
+    const float* gate;
+    void* y2;
+    uint32_t M, row_offset;
+};
+struct GemmEpilogue {
+    uint32_t kind, ldy, ldy2, split, y2_type;
+};
+size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K,
+                                          const GemmJob* jobs, uint32_t n_jobs, const GemmEpilogue& epi,
+                                          int num_cus);
+hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs,
+                                     uint32_t n_jobs, const GemmEpilogue& epi, int num_cus, void* ws,
+                                     hipStream_t st);
+
+// Q4_K weights times at most kGemvMaxTokens tokens (gemv_q.hip): an
+// HBM-bound weight stream, taken by launch_batch_matmul for such M.
+constexpr uint32_t kGemvMaxTokens = 8;
+hipError_t launch_gemv_q4k(const void* w, uint32_t xtype, const void* x, float* y, uint32_t N, uint32_t K,
+                           uint32_t M, uint32_t row_offset, hipStream_t st);
+
 // SwiGLU of two Q8_0 GEMMs (batch_matmul_swiglu_q8). `ws` must hold
 // swiglu_workspace_bytes(...) bytes (may be 0).
 size_t swiglu_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,

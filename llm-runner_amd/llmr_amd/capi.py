@@ -41,6 +41,21 @@ class FlashAttentionParams(ctypes.Structure):
                 ("seq_len", ctypes.c_uint32), ("scale", ctypes.c_float)]
 
 
+class MatmulJob(ctypes.Structure):
+    """llmr_matmul_job: one GEMM of llmr_batch_matmul_multi."""
+    _fields_ = [("weight", ctypes.c_void_p), ("input", ctypes.c_void_p), ("output", ctypes.c_void_p),
+                ("gate", ctypes.c_void_p), ("output2", ctypes.c_void_p), ("seq_len", ctypes.c_uint32),
+                ("row_offset", ctypes.c_uint32)]
+
+
+class MatmulEpilogue(ctypes.Structure):
+    """llmr_matmul_epilogue."""
+    _fields_ = [("kind", ctypes.c_uint32), ("ldy", ctypes.c_uint32), ("split", ctypes.c_uint32),
+                ("ldy2", ctypes.c_uint32), ("output2_type", ctypes.c_uint32)]
+
+
+EPI_STORE, EPI_GATED_RESIDUAL, EPI_SPLIT_GELU = 0, 1, 2
+
 _vp = ctypes.c_void_p
 _u32 = ctypes.c_uint32
 _SIGS = {
@@ -60,6 +75,8 @@ _SIGS = {
     "llmr_batch_matmul": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32]),
     "llmr_batch_matmul_pc": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp,
                                             ctypes.POINTER(BatchMatMulParams)]),
+    "llmr_batch_matmul_multi": (ctypes.c_int, [_vp, _u32, _u32, _u32, _u32, ctypes.POINTER(MatmulJob), _u32,
+                                               ctypes.POINTER(MatmulEpilogue)]),
     "llmr_batch_matmul_swiglu": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32]),
     "llmr_batch_matmul_swiglu_pc": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp,
                                                    ctypes.POINTER(BatchMatMulParams)]),
@@ -166,6 +183,12 @@ class Context:
                      out_dim: int, in_dim: int, seq_len: int, row_offset: int = 0) -> None:
         check(lib().llmr_batch_matmul(self._h, w_ptr, wtype, x_ptr, xtype, y_ptr, out_dim, in_dim,
                                       seq_len, row_offset))
+
+    def batch_matmul_multi(self, wtype: int, xtype: int, out_dim: int, in_dim: int, jobs, epilogue=None) -> None:
+        """jobs: sequence of MatmulJob; epilogue: MatmulEpilogue or None (plain store)."""
+        arr = (MatmulJob * len(jobs))(*jobs)
+        check(lib().llmr_batch_matmul_multi(self._h, wtype, xtype, out_dim, in_dim, arr, len(jobs),
+                                            ctypes.byref(epilogue) if epilogue is not None else None))
 
     def batch_matmul_swiglu(self, wg_ptr: int, wu_ptr: int, wtype: int, x_ptr: int, xtype: int,
                             y_ptr: int, out_dim: int, in_dim: int, seq_len: int) -> None:

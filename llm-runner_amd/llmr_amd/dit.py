@@ -31,13 +31,12 @@ from __future__ import annotations
 import dataclasses
 import math
 
-import numpy as np
 import torch
 
 from . import capi, glue, workloads
 from .gguf import GGML_Q4_K, GGML_Q8_0
-from .ops import FlashAttentionPC, RenderGraph, Tensor, default_graph, dispatch_batch_matmul, \
-    dispatch_batch_matmul_swiglu, dispatch_flash_attention
+from .ops import FlashAttentionPC, MatmulJob, RenderGraph, Tensor, default_graph, dispatch_batch_matmul, \
+    dispatch_batch_matmul_multi, dispatch_batch_matmul_swiglu, dispatch_flash_attention
 
 HEAD_DIM = 128
 
@@ -288,21 +287,17 @@ class FluxDiT:
         S, d, m, nt = c.seq, c.dim, c.mlp, c.n_txt
         self.rope = flux_rope(cfg, device)
         self.hidden = torch.empty(S, d, dtype=torch.float32, **e)   # joint residual stream, text rows first
-        self.xa = torch.empty(S, d, dtype=act_dtype, **e)
+        self.xa = torch.empty(S, d, dtype=act_dtype, **e)             # GEMM inputs of width dim
         self.patches = torch.empty(c.n_img, c.patch_dim, dtype=act_dtype, **e)
-        self.l1 = torch.empty(S, 3 * d + m, dtype=torch.float32, **e)  # linear1 out; its first 3d cols are QKV
+        self.qkv = torch.empty(S, 3 * d, dtype=torch.float32, **e)   # Q | K | V rows (both block types)
         self.q = torch.empty(c.n_heads, S, HEAD_DIM, dtype=torch.float16, **e)
         self.k = torch.empty_like(self.q)
         self.v = torch.empty_like(self.q)
         self.o = torch.empty(S, d, dtype=torch.float32, **e)
-        self.t = torch.empty(S, d, dtype=torch.float32, **e)
-        self.cat = torch.empty(S, d + m, dtype=act_dtype, **e)  # linear2 input [attention | MLP]
-        self.f = torch.empty(c.n_img, m, dtype=torch.float32, **e)  # double-block MLP up-projection
-        # dense views over the single block's buffers for the double block (GEMM
-        # outputs and inputs are dense [M, N]): QKV [S, 3d] and the MLP
-        # activations [n_img, mlp]; the two block types never overlap in time
-        self.qkv = self.l1.view(-1)[:S * 3 * d].view(S, 3 * d)
-        self.fa = self.cat.view(-1)[:c.n_img * m].view(c.n_img, m)
+        self.cat = torch.empty(S, d + m, dtype=act_dtype, **e)  # linear2 input [attention | gelu(MLP)]
+        # the double block's MLP activations [S, mlp] (dense: a GEMM input)
+        # share the single block's concat buffer; the block types never overlap
+        self.fa = self.cat.view(-1)[:S * m].view(S, m)
         self.t_emb = torch.empty(1, c.t_emb_dim, dtype=torch.float32, **e)
         self.vec0 = torch.empty(1, d, dtype=torch.float32, **e)
         self.vec = torch.empty(1, d, dtype=torch.float32, **e)
@@ -367,43 +362,59 @@ class FluxDiT:
 
     def _double(self, w: FluxDoubleWeights, mi: torch.Tensor, mt: torch.Tensor) -> None:
         """flux_dual_stream_block (flux_dit.c3:746-971). mi / mt: [6, dim]
-        (shift1, scale1, gate1, shift2, scale2, gate2) of the image / text stream."""
+        (shift1, scale1, gate1, shift2, scale2, gate2) of the image / text
+        stream. Each projection multiplies both streams in one launch
+        (text rows first, each with its own weight)."""
         c, g = self.cfg, self.g
         d, m, nt, H, S = c.dim, c.mlp, c.n_txt, c.n_heads, c.seq
-        streams = ((slice(nt, S), mi, w.img_qkv, w.img_proj, w.img_mlp0, w.img_mlp2, w.img_q_norm, w.img_k_norm),
-                   (slice(0, nt), mt, w.txt_qkv, w.txt_proj, w.txt_mlp0, w.txt_mlp2, w.txt_q_norm, w.txt_k_norm))
-        # LayerNorm + modulation, QKV, head norm + RoPE into the joint Q/K/V   (flux_dit.c3:761-863)
-        for sl, mod, wqkv, _, _, _, qn, kn in streams:
+        ts, im = slice(0, nt), slice(nt, S)
+        ni = S - nt
+
+        def jobs(wt, wi, K, x, out, gates=(None, None), out2=None):
+            """[text job, image job]: rows ts / im of x, out (and out2)."""
+            rows = wt.numel() // (K // 256 * 144)
+            return [MatmulJob(_qt(wt, GGML_Q4_K, rows, K), _t(x[ts]), out[ts], nt, 0, gates[0],
+                              None if out2 is None else out2[ts]),
+                    MatmulJob(_qt(wi, GGML_Q4_K, rows, K), _t(x[im]), out[im], ni, 0, gates[1],
+                              None if out2 is None else out2[im])]
+
+        # LayerNorm + modulation of each stream                      (flux_dit.c3:761-779)
+        for sl, mod in ((ts, mt), (im, mi)):
             glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0],
                                  g=g)
-            self._mm(wqkv, GGML_Q4_K, 3 * d, d, self.xa[sl], self.qkv[sl])
-            glue.qkv_heads(self.qkv[sl], H, self.q, self.k, self.v, sl.start, qn, kn, self.HN_EPS, self.rope, g=g)
+        # Q | K | V of both streams; head norm + RoPE into the joint Q/K/V (flux_dit.c3:786-863)
+        dispatch_batch_matmul_multi(g, jobs(w.txt_qkv, w.img_qkv, d, self.xa, self.qkv), 3 * d, d)
+        glue.qkv_heads(self.qkv[ts], H, self.q, self.k, self.v, 0, w.txt_q_norm, w.txt_k_norm, self.HN_EPS,
+                       self.rope, g=g)
+        glue.qkv_heads(self.qkv[im], H, self.q, self.k, self.v, nt, w.img_q_norm, w.img_k_norm, self.HN_EPS,
+                       self.rope, g=g)
         self._attention(S)
-        # per-stream output projection, gated residual                       (flux_dit.c3:875-898)
+        # output projections, hidden += gate1 * proj                  (flux_dit.c3:875-898)
         glue.activation(self.o, self.xa, capi.ACT_COPY, g=g)
-        for sl, mod, _, wproj, _, _, _, _ in streams:
-            self._mm(wproj, GGML_Q4_K, d, d, self.xa[sl], self.t[sl])
-            glue.gated_residual(self.hidden[sl], self.t[sl], mod[2], capi.GATE_LINEAR, g=g)
-        # per-stream MLP: LayerNorm + modulation, up, GELU, down, gated residual (flux_dit.c3:902-967)
-        for sl, mod, _, _, wm0, wm2, _, _ in streams:
-            n = sl.stop - sl.start
+        dispatch_batch_matmul_multi(g, jobs(w.txt_proj, w.img_proj, d, self.xa, self.hidden, (mt[2], mi[2])), d, d,
+                                    capi.EPI_GATED_RESIDUAL)
+        # MLP: LayerNorm + modulation, up + gelu, down, hidden += gate2 * down (flux_dit.c3:902-967)
+        for sl, mod in ((ts, mt), (im, mi)):
             glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[4], mod_shift=mod[3],
                                  g=g)
-            self._mm(wm0, GGML_Q4_K, m, d, self.xa[sl], self.f[:n])
-            glue.activation(self.f[:n], self.fa[:n], capi.ACT_GELU_TANH, g=g)
-            self._mm(wm2, GGML_Q4_K, d, m, self.fa[:n], self.t[sl])
-            glue.gated_residual(self.hidden[sl], self.t[sl], mod[5], capi.GATE_LINEAR, g=g)
+        dispatch_batch_matmul_multi(g, jobs(w.txt_mlp0, w.img_mlp0, d, self.xa, self.o, out2=self.fa), m, d,
+                                    capi.EPI_SPLIT_GELU, split=0)
+        dispatch_batch_matmul_multi(g, jobs(w.txt_mlp2, w.img_mlp2, m, self.fa, self.hidden, (mt[5], mi[5])), d, m,
+                                    capi.EPI_GATED_RESIDUAL)
 
     def _single(self, w: FluxSingleWeights, mod: torch.Tensor) -> None:
         """flux_single_stream_block (flux_dit.c3:975-1071). mod: [3, dim] (shift, scale, gate)."""
         c, g = self.cfg, self.g
         d, m, H, S = c.dim, c.mlp, c.n_heads, c.seq
         glue.batch_layernorm(self.hidden, self.xa, self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0], g=g)
-        self._mm(w.linear1, GGML_Q4_K, 3 * d + m, d, self.xa, self.l1)
-        glue.qkv_heads(self.l1, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, self.HN_EPS, self.rope, g=g)
+        # linear1: Q | K | V (f32) and gelu(MLP half) straight into linear2's input (flux_dit.c3:1005-1058)
+        dispatch_batch_matmul_multi(g, [MatmulJob(_qt(w.linear1, GGML_Q4_K, 3 * d + m, d), _t(self.xa), self.qkv,
+                                                  S, 0, None, self.cat[:, d:])],
+                                    3 * d + m, d, capi.EPI_SPLIT_GELU, split=3 * d)
+        glue.qkv_heads(self.qkv, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, self.HN_EPS, self.rope, g=g)
         self._attention(S)
-        # linear2 input = [attention out | gelu(MLP half)]          (flux_dit.c3:1049-1057)
         glue.activation(self.o, self.cat[:, :d], capi.ACT_COPY, g=g)
-        glue.activation(self.l1[:, 3 * d:], self.cat[:, d:], capi.ACT_GELU_TANH, g=g)
-        self._mm(w.linear2, GGML_Q4_K, d, d + m, self.cat, self.t)
-        glue.gated_residual(self.hidden, self.t, mod[2], capi.GATE_LINEAR, g=g)
+        # linear2, hidden += gate * linear2                           (flux_dit.c3:1060-1068)
+        dispatch_batch_matmul_multi(g, [MatmulJob(_qt(w.linear2, GGML_Q4_K, d, d + m), _t(self.cat), self.hidden,
+                                                  S, 0, mod[2])],
+                                    d, d + m, capi.EPI_GATED_RESIDUAL)

@@ -109,6 +109,73 @@ def dispatch_batch_matmul(g: RenderGraph, weight: Tensor, input: Tensor, output:
                        out_dim, in_dim, seq_len, row_offset)
 
 
+@dataclasses.dataclass
+class MatmulJob:
+    """One GEMM of dispatch_batch_matmul_multi: input [seq_len, in_dim] times weight
+    rows [row_offset, row_offset + out_dim). `output` / `output2` are 2-D device views
+    whose row strides become the epilogue's ldy / ldy2 (all jobs of a call must
+    share them); `gate` is the GATED_RESIDUAL per-feature gate."""
+    weight: Tensor
+    input: Tensor
+    output: torch.Tensor
+    seq_len: int
+    row_offset: int = 0
+    gate: torch.Tensor | None = None
+    output2: torch.Tensor | None = None
+
+
+def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim: int,
+                                epilogue: int = capi.EPI_STORE, split: int = 0) -> None:
+    """The jobs' GEMMs with a shared epilogue (llmr_batch_matmul_multi): a plain
+    store, `output += gate * result` (gated_residual_linear), or a column split
+    whose features >= split are GELU'd into output2 (linear1's MLP half feeding
+    linear2, flux_dit.c3:1049-1058). Pairs of jobs run as one launch."""
+    if not jobs:
+        return
+    wtype, xtype = jobs[0].weight.dtype, jobs[0].input.dtype
+
+    def stride(t):
+        if t.dim() != 2 or t.stride(1) != 1:
+            raise ValueError("outputs must be 2-D views with contiguous rows")
+        return t.stride(0) if t.shape[0] > 1 else (t.shape[1] + 3) // 4 * 4
+
+    ldy = stride(jobs[0].output)
+    ldy2 = stride(jobs[0].output2) if jobs[0].output2 is not None else 0
+    o2type = _TORCH_GGML.get(jobs[0].output2.dtype, 0) if jobs[0].output2 is not None else 0
+    cj = []
+    for j in jobs:
+        if j.weight.dtype != wtype or j.input.dtype != xtype:
+            raise ValueError("all jobs share the weight and input types")
+        _dev(j.weight, "weight")
+        _dev(j.input, "input")
+        if j.weight.shape[1] != in_dim or j.row_offset + out_dim > j.weight.shape[0]:
+            raise ValueError("weight shape does not cover [row_offset, row_offset+out_dim) x in_dim")
+        if j.input.data.numel() < j.seq_len * in_dim:
+            raise ValueError("input smaller than [seq_len, in_dim]")
+        if not j.output.is_cuda or j.output.dtype != torch.float32 or stride(j.output) != ldy:
+            raise ValueError("outputs must be f32 device views sharing one row stride")
+        width = split if epilogue == capi.EPI_SPLIT_GELU else out_dim
+        if j.output.shape[0] < j.seq_len or j.output.shape[1] < width:
+            raise ValueError("output view smaller than [seq_len, out_dim]")
+        o2 = 0
+        if j.output2 is not None:
+            if stride(j.output2) != ldy2 or _TORCH_GGML.get(j.output2.dtype) != o2type:
+                raise ValueError("output2 views must share row stride and dtype")
+            if j.output2.shape[0] < j.seq_len or j.output2.shape[1] < out_dim - split:
+                raise ValueError("output2 view smaller than [seq_len, out_dim - split]")
+            o2 = j.output2.data_ptr()
+        gp = 0
+        if j.gate is not None:
+            if j.gate.dtype != torch.float32 or not j.gate.is_contiguous() or j.gate.numel() < out_dim:
+                raise ValueError("gate must be a contiguous f32 vector of out_dim elements")
+            gp = j.gate.data_ptr()
+        cj.append(capi.MatmulJob(j.weight.ptr(), j.input.ptr(), j.output.data_ptr(), gp or None, o2 or None,
+                                 j.seq_len, j.row_offset))
+    epi = capi.MatmulEpilogue(epilogue, ldy, split, ldy2, o2type)
+    g.bind_stream()
+    g.ctx.batch_matmul_multi(wtype, xtype, out_dim, in_dim, cj, epi)
+
+
 def dispatch_batch_matmul_swiglu(g: RenderGraph, weight_gate: Tensor, weight_up: Tensor,
                                  input: Tensor, output: Tensor, out_dim: int, in_dim: int,
                                  seq_len: int) -> None:

@@ -46,8 +46,26 @@ CASES = [
     (12, 77, 130, 512, 0, 0),        # Q4_K f32
     (12, 129, 256, 1024, 30, 256),   # Q4_K bf16 with row_offset
     (12, 513, 1032, 768, 1, 0),      # Q4_K f16, ragged
-    (12, 1, 17, 256, 30, 1),         # one token, odd N
+    (12, 1, 17, 256, 30, 1),         # one token, odd N (small-M Q4_K kernel)
+    (12, 3, 1000, 768, 1, 4),        # small-M Q4_K kernel, f16, row_offset
+    (12, 8, 130, 512, 30, 0),        # small-M Q4_K kernel at its largest M
+    (12, 9, 72, 512, 30, 0),         # one token more: the tiled kernel again
 ]
+
+
+@pytest.mark.parametrize("M,N,K,row_offset", [(1, 18432, 3072, 0), (1, 3072, 256, 0), (5, 264, 4096, 16)])
+def test_small_m_q4k_f32_matches_reference_arithmetic(orc, dev, M, N, K, row_offset):
+    """M <= 8 Q4_K launches keep the activations in f32 and dequantize in
+    f32 like batch_matmul_q4k, so only the summation order differs from the
+    oracle: far inside the GEMM bar (the modulation-projection shape first)."""
+    from llmr_amd import gguf, synth
+    blk = gguf.quantize(synth.normal(21, 2, (N + row_offset) * K, 0.02), 12)
+    x = synth.normal(21, 1, M * K).reshape(M, K)
+    y, xr = _run(dev, blk, 12, x, 0, N, row_offset)
+    ref = orc.batch_matmul(blk, 12, xr, N, K, M, row_offset)
+    err = rel_l2(y, ref)
+    print(f"small-M Q4_K M={M} N={N} K={K}: rel_l2={err:.3e}")
+    assert err <= 1e-5
 
 
 @pytest.mark.parametrize("wtype,M,N,K,xtype,row_offset", CASES)
@@ -280,3 +298,118 @@ def test_bf16_activations_beyond_fp16_range(orc, dev, M, N, K):
     assert np.all(np.isfinite(y))
     assert np.abs(xr).max() > 65504.0
     assert rel_l2(y[rows.astype(np.int64)], ref) <= TOL
+
+
+# ---- llmr_batch_matmul_multi: grouped jobs and fused epilogues ----------------
+
+def _multi_setup(dev, wtype, Ms, N, K, xtype, seed):
+    import torch
+    from llmr_amd import gguf, ops, synth
+    blks, xs, wts = [], [], []
+    for i, M in enumerate(Ms):
+        blk = gguf.quantize(synth.normal(seed, 10 + i, (N + 8) * K, 0.02), wtype)
+        x = synth.normal(seed, 20 + i, M * K).reshape(M, K)
+        xt = _torch_x(x, xtype, dev)
+        blks.append(blk)
+        xs.append(xt)
+        wts.append(ops.Tensor.quantized(torch.from_numpy(blk).to(dev), wtype, N + 8, K))
+    return blks, xs, wts
+
+
+def _sample_rows(M):
+    return np.unique(np.array([0, 1, 63, 255, 256, M // 2, M - 2, M - 1], np.int64).clip(0, M - 1))
+
+
+@pytest.mark.parametrize("wtype,xtype", [(12, 30), (8, 30), (12, 1)])
+def test_multi_grouped_store_and_residual(orc, dev, wtype, xtype):
+    """Two jobs (512 and 3584 tokens, own weights) in one persistent launch:
+    a strided store, then a gated residual accumulate (one job without gate)."""
+    import torch
+    from llmr_amd import capi, ops
+    Ms, N, K = (512, 3584), 2304, 512
+    blks, xs, wts = _multi_setup(dev, wtype, Ms, N, K, xtype, 31)
+    g = ops.default_graph()
+    out = torch.full((sum(Ms), N + 64), 5.0, dtype=torch.float32, device=dev)
+    views = (out[:Ms[0], :N], out[Ms[0]:, :N])
+    jobs = [ops.MatmulJob(wts[i], ops.Tensor.from_torch(xs[i]), views[i], Ms[i], 4 * i) for i in range(2)]
+    ops.dispatch_batch_matmul_multi(g, jobs, N, K)
+    h0 = torch.randn(sum(Ms), N, device=dev)
+    h = h0.clone()
+    gate = torch.randn(N, device=dev)
+    jobs = [ops.MatmulJob(wts[i], ops.Tensor.from_torch(xs[i]), (h[:Ms[0]], h[Ms[0]:])[i], Ms[i], 4 * i,
+                          gate if i == 0 else None) for i in range(2)]
+    ops.dispatch_batch_matmul_multi(g, jobs, N, K, capi.EPI_GATED_RESIDUAL)
+    torch.cuda.synchronize()
+    assert (out[:, N:] == 5.0).all()  # columns past N untouched
+    for i, M in enumerate(Ms):
+        rows = _sample_rows(M)
+        ref = orc.batch_matmul(blks[i], wtype, _x_as_f32(xs[i]), N, K, M, 4 * i, rows=rows)
+        got = views[i][torch.from_numpy(rows).to(dev)].cpu().numpy()
+        assert rel_l2(got, ref) <= TOL, (i, rel_l2(got, ref))
+        hv = (h[:Ms[0]], h[Ms[0]:])[i][torch.from_numpy(rows).to(dev)].cpu().numpy()
+        hb = (h0[:Ms[0]], h0[Ms[0]:])[i][torch.from_numpy(rows).to(dev)].cpu().numpy()
+        gv = gate.cpu().numpy() if i == 0 else 1.0
+        assert rel_l2(hv - hb, gv * ref) <= TOL, (i, rel_l2(hv - hb, gv * ref))
+
+
+@pytest.mark.parametrize("M,xtype", [(4096, 30), (300, 30), (700, 0)])
+def test_multi_split_gelu(orc, dev, M, xtype):
+    """Features [0, split) to a strided f32 output, the rest gelu'd into a
+    bf16 column slice: the persistent epilogue (4096 tokens) and the
+    workspace path (few tiles; f32 input)."""
+    import torch
+    from llmr_amd import capi, ops
+    N, K, split = 2304, 512, 1000
+    blks, xs, wts = _multi_setup(dev, 12, (M,), N, K, xtype, 32)
+    q = torch.zeros(M, split + 24, dtype=torch.float32, device=dev)
+    cat = torch.zeros(M, 64 + N - split, dtype=torch.bfloat16, device=dev)
+    job = ops.MatmulJob(wts[0], ops.Tensor.from_torch(xs[0]), q[:, :split], M, 0, None, cat[:, 64:])
+    ops.dispatch_batch_matmul_multi(ops.default_graph(), [job], N, K, capi.EPI_SPLIT_GELU, split=split)
+    torch.cuda.synchronize()
+    rows = _sample_rows(M)
+    ref = orc.batch_matmul(blks[0], 12, _x_as_f32(xs[0]), N, K, M, 0, rows=rows)
+    ri = torch.from_numpy(rows).to(dev)
+    assert rel_l2(q[ri, :split].cpu().numpy(), ref[:, :split]) <= TOL
+    gel = orc.gelu(ref[:, split:])
+    assert rel_l2(cat[ri, 64:].float().cpu().numpy(), gel) <= TOL
+    assert (q[:, split:] == 0).all() and (cat[:, :64].float() == 0).all()
+
+
+def test_multi_fused_equals_unfused_at_flux_shapes(dev):
+    """Full Flux double-block shapes (512 text + 4096 image tokens, dim 3072):
+    the grouped launch with gated-residual and gelu epilogues equals plain
+    GEMM calls followed by the glue kernels (the same products; the fused gelu
+    differs from the glue's in the last f32 bits, so the bf16 outputs agree to
+    one bf16 ulp)."""
+    import torch
+    from llmr_amd import capi, glue, ops
+    d, m, nt, ni = 3072, 12288, 512, 4096
+    S = nt + ni
+    g = ops.default_graph()
+    wq = [glue.synth_q4k(m, d, 900 + i, device=dev) for i in range(2)]
+    wd = [glue.synth_q4k(d, m, 910 + i, device=dev) for i in range(2)]
+    x = torch.randn(S, d, device=dev).to(torch.bfloat16)
+    gates = [torch.randn(d, device=dev) for _ in range(2)]
+    sl = (slice(0, nt), slice(nt, S))
+    fa = torch.empty(S, m, dtype=torch.bfloat16, device=dev)
+    dummy = torch.empty(S, 16, device=dev)
+    jobs = [ops.MatmulJob(ops.Tensor.quantized(wq[i], 12, m, d), ops.Tensor.from_torch(x[sl[i]]), dummy[sl[i]],
+                          S - nt if i else nt, 0, None, fa[sl[i]]) for i in range(2)]
+    ops.dispatch_batch_matmul_multi(g, jobs, m, d, capi.EPI_SPLIT_GELU, split=0)
+    h = torch.randn(S, d, device=dev)
+    h_ref = h.clone()
+    jobs = [ops.MatmulJob(ops.Tensor.quantized(wd[i], 12, d, m), ops.Tensor.from_torch(fa[sl[i]]), h[sl[i]],
+                          S - nt if i else nt, 0, gates[i]) for i in range(2)]
+    ops.dispatch_batch_matmul_multi(g, jobs, d, m, capi.EPI_GATED_RESIDUAL)
+    # unfused: plain GEMMs + glue
+    for i in range(2):
+        f = ops.batch_matmul(wq[i], 12, x[sl[i]].contiguous(), m)
+        fa_u = torch.empty_like(fa[sl[i]])
+        glue.activation(f, fa_u, capi.ACT_GELU_TANH)
+        diff = (fa_u.float() - fa[sl[i]].float()).abs()
+        assert (diff <= 2.0 ** -7 * fa_u.float().abs() + 1e-6).all(), float(diff.max())
+        t = ops.batch_matmul(wd[i], 12, fa[sl[i]].contiguous(), d)
+        glue.gated_residual(h_ref[sl[i]], t, gates[i], capi.GATE_LINEAR)
+    torch.cuda.synchronize()
+    err = float((h - h_ref).abs().max() / h_ref.abs().max())
+    assert err < 1e-5, err
