@@ -1,12 +1,13 @@
-// gemv_q.hip - Q4_K dequant-GEMM for a handful of tokens (M <= 8): the
+// gemv_q.hip - Q4_K dequant-GEMM for a handful of tokens (M <= 4): the
 // modulation and timestep projections of a DiT step (M = 1) stream a whole
 // weight matrix for a few dot products, so they are bound by HBM reads of the
 // packed weight, not by the matrix cores. Here every weight byte is read
 // once, coalesced, dequantized in registers in f32 and used for all M tokens.
 //
-// Sixteen lanes per weight row: lane t of a row walks superblocks t, t+16, ...
-// (144 contiguous bytes each), a wave covers 4 rows and a workgroup 16; the
-// 16 partial sums of a row are reduced with lane shuffles. Arithmetic is the
+// A wave covers 16 weight rows: lane t (of 16) walks superblocks t, t+16,
+// ..., and each lane serves 4 of the rows with one register copy of the
+// activations it needs (a 64-element slice per token at a time); the 16
+// partial sums of a row are reduced with lane shuffles. Arithmetic is the
 // reference's f32 path (batch_matmul_q4k, llm.slang:2264-2365): weight
 // (d*sc)*q - dmin*mn with one rounding (the FMA below; both products are
 // exact), activations in f32, f32 accumulation (in a different order).
@@ -41,49 +42,73 @@ template <uint32_t XT, int MM>
 __global__ void __launch_bounds__(256) gemv_q4k_kernel(const uint8_t* __restrict__ W, const void* __restrict__ X,
                                                         float* __restrict__ Y, uint32_t N, uint32_t K, uint32_t M,
                                                         uint32_t row_offset) {
+    // lane t = l % 16 walks superblocks t, t+16, ...; lane group r = l / 16
+    // owns rows r, r+4, r+8, r+12 of the wave's 16: one 64-element slice of
+    // the activations (per token) is loaded once and used for all four rows
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t t = lane & 15u;
-    const uint32_t n = blockIdx.x * 16u + wave * 4u + (lane >> 4);
+    const uint32_t t = lane & 15u, r = lane >> 4;
+    const uint32_t n0 = blockIdx.x * 64u + wave * 16u + r;  // rows n0 + 4i, i < 4
     const uint32_t nsb = K / 256u;
-    float acc[MM];
+    const uint64_t rb = (uint64_t)nsb * 144u;
+    float acc[4][MM];
 #pragma unroll
-    for (int m = 0; m < MM; ++m) acc[m] = 0.0f;
-    if (n < N) {
-        const uint8_t* wr = W + (uint64_t)(row_offset + n) * nsb * 144u;
-        for (uint32_t sb = t; sb < nsb; sb += 16u) {
-            const uint32_t* b = (const uint32_t*)(wr + (uint64_t)sb * 144u);  // dword-aligned
-            const u32x4 hdr = *(const u32x4_a4*)b;
-            u32x4 qs[8];
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) qs[i] = *(const u32x4_a4*)(b + 4 + 4 * i);
-            const float d = f16_bits_to_f32(hdr.x & 0xffffu), dmin = f16_bits_to_f32(hdr.x >> 16);
-            const uint64_t xb = (uint64_t)sb * 256u;
+        for (int m = 0; m < MM; ++m) acc[i][m] = 0.0f;
+    for (uint32_t sb = t; sb < nsb; sb += 16u) {
+        const uint64_t xb = (uint64_t)sb * 256u;
+        u32x4 hdr[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t n = n0 + 4u * i;
+            hdr[i] = n < N ? *(const u32x4_a4*)(W + (uint64_t)(row_offset + n) * rb + (uint64_t)sb * 144u)
+                           : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            // activations of elements 64j .. 64j+63 of this superblock, per token
+            f32x4 xl[MM][8], xh[MM][8];
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                if (m < (int)M) {
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        const uint64_t e = (uint64_t)m * K + xb + 64u * j + 4u * c;
+                        xl[m][c] = load_x4<XT>(X, e);
+                        xh[m][c] = load_x4<XT>(X, e + 32u);
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t n = n0 + 4u * i;
+                if (n >= N) continue;
+                const uint32_t* b = (const uint32_t*)(W + (uint64_t)(row_offset + n) * rb + (uint64_t)sb * 144u);
+                const u32x4 q0 = *(const u32x4_a4*)(b + 4 + 8 * j), q1 = *(const u32x4_a4*)(b + 8 + 8 * j);
+                const float d = f16_bits_to_f32(hdr[i].x & 0xffffu), dmin = f16_bits_to_f32(hdr[i].x >> 16);
                 uint32_t sc0, mn0, sc1, mn1;
-                q4k_scale_min(2u * j, hdr.y, hdr.z, hdr.w, sc0, mn0);
-                q4k_scale_min(2u * j + 1u, hdr.y, hdr.z, hdr.w, sc1, mn1);
+                q4k_scale_min(2u * j, hdr[i].y, hdr[i].z, hdr[i].w, sc0, mn0);
+                q4k_scale_min(2u * j + 1u, hdr[i].y, hdr[i].z, hdr[i].w, sc1, mn1);
                 const float d0 = d * (float)sc0, m0 = dmin * (float)mn0;
                 const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
 #pragma unroll
                 for (int c = 0; c < 8; ++c) {
                     // bytes 4c .. 4c+3 of the pair's 32 quant bytes: elements
-                    // 64j + 4c + i (low nibble) and 64j + 32 + 4c + i (high)
-                    const uint32_t word = qs[2 * j + c / 4][c % 4];
+                    // 64j + 4c + k (low nibble) and 64j + 32 + 4c + k (high)
+                    const uint32_t word = c < 4 ? q0[c] : q1[c - 4];
                     f32x4 wl, wh;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const uint32_t q = (word >> (8 * i)) & 0xffu;
-                        wl[i] = __builtin_fmaf((float)(q & 15u), d0, -m0);
-                        wh[i] = __builtin_fmaf((float)(q >> 4), d1, -m1);
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t q = (word >> (8 * k)) & 0xffu;
+                        wl[k] = __builtin_fmaf((float)(q & 15u), d0, -m0);
+                        wh[k] = __builtin_fmaf((float)(q >> 4), d1, -m1);
                     }
 #pragma unroll
                     for (int m = 0; m < MM; ++m) {
                         if (m < (int)M) {
-                            const uint64_t e = (uint64_t)m * K + xb + 64u * j + 4u * c;
-                            const f32x4 xl = load_x4<XT>(X, e), xh = load_x4<XT>(X, e + 32u);
-                            acc[m] += (wl.x * xl.x + wl.y * xl.y) + (wl.z * xl.z + wl.w * xl.w) +
-                                      ((wh.x * xh.x + wh.y * xh.y) + (wh.z * xh.z + wh.w * xh.w));
+                            const f32x4 a = xl[m][c], h = xh[m][c];
+                            acc[i][m] += (wl.x * a.x + wl.y * a.y) + (wl.z * a.z + wl.w * a.w) +
+                                         ((wh.x * h.x + wh.y * h.y) + (wh.z * h.z + wh.w * h.w));
                         }
                     }
                 }
@@ -91,26 +116,33 @@ __global__ void __launch_bounds__(256) gemv_q4k_kernel(const uint8_t* __restrict
         }
     }
 #pragma unroll
-    for (int m = 0; m < MM; ++m) {
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1) acc[m] += __shfl_xor(acc[m], o, 64);
-    }
-    if (t == 0 && n < N) {
+        for (int m = 0; m < MM; ++m) {
 #pragma unroll
-        for (int m = 0; m < MM; ++m)
-            if (m < (int)M) Y[(uint64_t)m * N + n] = acc[m];
+            for (int o = 8; o > 0; o >>= 1) acc[i][m] += __shfl_xor(acc[i][m], o, 64);
+        }
+    if (t == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t n = n0 + 4u * i;
+            if (n < N) {
+#pragma unroll
+                for (int m = 0; m < MM; ++m)
+                    if (m < (int)M) Y[(uint64_t)m * N + n] = acc[i][m];
+            }
+        }
     }
 }
 
 template <uint32_t XT>
 hipError_t launch_t(const void* w, const void* x, float* y, uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset,
                     hipStream_t st) {
-    const dim3 grid((N + 15u) / 16u), block(256);
+    const dim3 grid((N + 63u) / 64u), block(256);
     const uint8_t* W = (const uint8_t*)w;
     if (M <= 1) hipLaunchKernelGGL((gemv_q4k_kernel<XT, 1>), grid, block, 0, st, W, x, y, N, K, M, row_offset);
     else if (M <= 2) hipLaunchKernelGGL((gemv_q4k_kernel<XT, 2>), grid, block, 0, st, W, x, y, N, K, M, row_offset);
-    else if (M <= 4) hipLaunchKernelGGL((gemv_q4k_kernel<XT, 4>), grid, block, 0, st, W, x, y, N, K, M, row_offset);
-    else hipLaunchKernelGGL((gemv_q4k_kernel<XT, 8>), grid, block, 0, st, W, x, y, N, K, M, row_offset);
+    else hipLaunchKernelGGL((gemv_q4k_kernel<XT, 4>), grid, block, 0, st, W, x, y, N, K, M, row_offset);
     return hipGetLastError();
 }
 

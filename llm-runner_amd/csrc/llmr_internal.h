@@ -44,7 +44,7 @@ hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N,
 
 // Q4_K weights times at most kGemvMaxTokens tokens (gemv_q.hip): an
 // HBM-bound weight stream, taken by launch_batch_matmul for such M.
-constexpr uint32_t kGemvMaxTokens = 8;
+constexpr uint32_t kGemvMaxTokens = 4;
 hipError_t launch_gemv_q4k(const void* w, uint32_t xtype, const void* x, float* y, uint32_t N, uint32_t K,
                            uint32_t M, uint32_t row_offset, hipStream_t st);
 
