@@ -77,6 +77,32 @@ def setup_attention(dev):
     return step, a.flops, a.bytes, cfg, "f16"
 
 
+def setup_lora(dev):
+    """The two-hop LoRA correction (rank 32, scale 1) on the Flux single-block
+    linear1 output: 4608 tokens, 3072 -> 21504, bf16 input, f32 output."""
+    import torch
+    from llmr_amd import ops
+    seq, in_dim, out_dim, rank = 4608, 3072, 21504, 32
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    a = (0.02 * torch.randn(rank, in_dim, generator=gen)).to(dev)
+    b = (0.02 * torch.randn(out_dim, rank, generator=gen)).to(dev)
+    lora = ops.LoraTensor(a, b, rank, 1.0)
+    x = torch.randn(seq, in_dim, generator=gen).bfloat16().to(dev)
+    y = torch.zeros(seq, out_dim, device=dev)
+    scratch = torch.empty(seq * rank, device=dev)
+    g = ops.default_graph()
+    xt, yt = ops.Tensor.from_torch(x), ops.Tensor.from_torch(y)
+
+    def step():
+        ops.dispatch_lora_correction(g, lora, scratch, xt, yt, in_dim, out_dim, seq)
+
+    flops = 2.0 * seq * rank * (in_dim + out_dim)
+    nbytes = seq * in_dim * 2 + rank * in_dim * 4 + out_dim * rank * 4 + 2 * seq * rank * 4 + 2 * seq * out_dim * 4
+    cfg = {"workload": "lora_flux_linear1", "seq_len": seq, "in_dim": in_dim, "out_dim": out_dim, "rank": rank,
+           "input": "bf16", "output": "f32 (accumulated)"}
+    return step, flops, nbytes, cfg, "f32"
+
+
 def setup_gemm(dev, name):
     import torch
     from llmr_amd import gguf, ops, workloads
@@ -170,14 +196,15 @@ MODEL_SETUPS = {"zimage_block": setup_zimage_block, "flux_step": setup_flux_step
 def gemm_kernel_name(name: str, num_cus: int) -> str:
     """The kernel the library's dispatch picks for a GEMM workload: the
     persistent 256x256 kernel for 16-bit activations with at least half the
-    CUs' worth of tiles (and N % 4 == 0), else the 4-wave tiled kernel."""
+    CUs' worth of tiles (and N % 4 == 0; on 8 waves for Q8_0), else the
+    4-wave tiled kernel."""
     from llmr_amd import gguf, workloads
     g = workloads.GEMMS[name]
     tiles = ((g.M + 255) // 256) * ((g.N + 255) // 256)
     if g.wtype == gguf.GGML_Q8_0 and g.K % 64:
         return "gemm_q_generic"
     if g.xtype != gguf.GGML_F32 and g.N % 4 == 0 and 2 * tiles >= num_cus:
-        return "gemm_q_persist"
+        return "gemm_q_persist8" if g.wtype == gguf.GGML_Q8_0 else "gemm_q_persist"
     return "gemm_q_mfma"
 
 
@@ -189,6 +216,8 @@ def measure(dev, name, steps, warmup):
         step, flops, nbytes, cfg, dtype = MODEL_SETUPS[name](dev)
     elif name in workloads.SWIGLUS:
         step, flops, nbytes, cfg, dtype = setup_swiglu(dev, name)
+    elif name == "lora_flux_linear1":
+        step, flops, nbytes, cfg, dtype = setup_lora(dev)
     else:
         step, flops, nbytes, cfg, dtype = setup_gemm(dev, name)
     total_ms, per = _time_steps(step, steps, warmup)
@@ -259,7 +288,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="flux_attention")
     ap.add_argument("--components",
-                    default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu,zimage_block,flux_step")
+                    default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu,lora_flux_linear1,zimage_block,flux_step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--hbm-copy-calibration", action="store_true",
                     help="time a plain 1 GiB device copy (reference for the FETCH_SIZE/WRITE_SIZE counters)")
@@ -296,7 +325,12 @@ def main():
         print(f"# {c}: {json.dumps(comps[c])}", file=sys.stderr, flush=True)
 
     ach = main_r["tflops"]
-    if args.workload in MODEL_SETUPS:  # a composed block / step: many kernels, no single roofline
+    if args.workload == "lora_flux_linear1":  # bandwidth-bound: priced against HBM
+        gbs = main_r["bytes"] / (main_r["ms"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": _traffic(args.workload),
+                "kernel": "lora_down_kernel + lora_up_kernel", "algorithmic_bytes": main_r["bytes"]}
+    elif args.workload in MODEL_SETUPS:  # a composed block / step: many kernels, no single roofline
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(ach / PEAK_TFLOPS, 4), "traffic": None,
                 "kernel": "composite (GEMM + attention + glue; GEMM and attention flops counted)"}
@@ -325,7 +359,7 @@ def main():
         "roofline": roof,
         "components": comps,
     }
-    if not args.no_cpu_baseline and args.workload not in MODEL_SETUPS:
+    if not args.no_cpu_baseline and args.workload not in MODEL_SETUPS and args.workload != "lora_flux_linear1":
         line["cpu_baseline"] = cpu_baseline(args.workload)
     print(json.dumps(line), flush=True)
     return 0

@@ -240,6 +240,63 @@ LLMR_API int llmr_batch_matmul_swiglu_pc(llmr_context* ctx, const void* weight_g
                                          uint32_t weight_type, const void* input, uint32_t input_type,
                                          float* output, const llmr_batch_matmul_params* pc);
 
+/* ---- LoRA ------------------------------------------------------------------ */
+
+/* A LoRA adapter of one linear (LoraTensor, lib/model/lora.c3:22-28): a
+ * [rank, in_dim] and b [out_rows, rank], f32 device pointers; the correction
+ * is scale * (b . a). */
+typedef struct llmr_lora {
+    const float* a;
+    const float* b;
+    uint32_t rank;
+    float scale;
+} llmr_lora;
+
+/* The two-hop LoRA correction appended to a base llmr_batch_matmul output
+ * (dispatch_lora_correction, dependencies/zimage.c3l/dit.c3:1319-1364):
+ *   hop 1: scratch[s, r] = sum_k a[r, k] * input[s, k]
+ *          (batch_matmul_simple, llm.slang:1146-1180; the sum in the order of
+ *          a 256-thread workgroup: strided partials, then the tree)
+ *   hop 2: output[s * out_dim + row_offset + o] += lora.scale *
+ *          sum_r b[weight_row_offset + o, r] * scratch[s, r]   for o < b_rows
+ *          (batch_matmul_add_scaled, llm.slang:1262-1294; the sum in r order)
+ * input [seq_len, in_dim] of input_type F32, F16 or BF16 (widened exactly);
+ * output f32 with row stride out_dim, accumulated. b_rows 0 means out_dim.
+ * scratch: seq_len * rank floats on the device, caller-owned (the
+ * reference's lora_scratch). Bit-identical to the CPU restatement. lora
+ * NULL or rank 0 or rank > 256: nothing is done and
+ * LLMR_OK is returned, as the reference skips those. The dot products are
+ * fused multiply-adds (the reference leaves contraction to its shader
+ * compiler). */
+LLMR_API int llmr_lora_correction(llmr_context* ctx, const llmr_lora* lora, float* scratch, const void* input,
+                                  uint32_t input_type, float* output, uint32_t in_dim, uint32_t out_dim,
+                                  uint32_t seq_len, uint32_t b_rows, uint32_t row_offset,
+                                  uint32_t weight_row_offset);
+
+/* llmr_batch_matmul followed by llmr_lora_correction, the reference's
+ * dispatch_batch_matmul with a LoRA (dit.c3:1198-1213: lora, lora_scratch,
+ * lora_b_rows, lora_row_offset, lora_weight_row_offset). lora NULL: the
+ * plain GEMM. */
+LLMR_API int llmr_batch_matmul_lora(llmr_context* ctx, const void* weight, uint32_t weight_type,
+                                    const void* input, uint32_t input_type, float* output, uint32_t out_dim,
+                                    uint32_t in_dim, uint32_t seq_len, uint32_t row_offset, const llmr_lora* lora,
+                                    float* lora_scratch, uint32_t lora_b_rows, uint32_t lora_row_offset,
+                                    uint32_t lora_weight_row_offset);
+
+/* Folds scale * (b . a) into rows [dst_row_offset, dst_row_offset + b_rows)
+ * of a Q8_0 weight [*, in_dim] in place and requantizes each 32-element
+ * block (q8_lora_merge, dependencies/llm_text.c3l/shaders/llm.slang:1337-1420;
+ * host merge_one_site, dependencies/flux.c3l/lora_merge.c3:36-73):
+ *   u = d * q + scale * sum_r b[j, r] * a[r, k]   (fused sum in r order)
+ *   d' = max(absmax(u over the block) / 127, 1e-8); q' = clamp(round(u / d'),
+ *   -127, 127) with halves away from zero (trunc(u/d' +- 0.5) in f32);
+ *   d' stored as f16, round to nearest even.
+ * b is [b_rows, rank]. in_dim % 256 == 0 and 1 <= rank <= 256
+ * (LLMR_ERR_UNSUPPORTED otherwise: the reference skips such merges and keeps
+ * the runtime correction). Bit-identical to the CPU restatement. */
+LLMR_API int llmr_q8_lora_merge(llmr_context* ctx, void* weight, const float* a, const float* b, uint32_t in_dim,
+                                uint32_t b_rows, uint32_t dst_row_offset, uint32_t rank, float scale);
+
 /* Non-causal attention, no mask:
  *   out[s, h*D + d] = sum_j softmax_j(scale * <q[h,s,:], k[h,j,:]>) * v[h,j,d]
  * q, k, v [n_heads, seq_len, head_dim] of qkv_type F32, F16 or BF16 (values are

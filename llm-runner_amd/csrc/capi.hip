@@ -221,6 +221,57 @@ int llmr_batch_matmul_pc(llmr_context* ctx, const void* weight, uint32_t wtype, 
                              pc->seq_len, pc->row_offset);
 }
 
+int llmr_lora_correction(llmr_context* ctx, const llmr_lora* lora, float* scratch, const void* input,
+                         uint32_t xtype, float* output, uint32_t in_dim, uint32_t out_dim, uint32_t seq_len,
+                         uint32_t b_rows, uint32_t row_offset, uint32_t weight_row_offset) {
+    if (int r = check_ctx(ctx)) return r;
+    // dit.c3:1333-1334: no adapter, or a rank beyond the scratch the
+    // reference sizes, leaves the base output as it is
+    if (!lora || lora->rank == 0 || lora->rank > llmr::kMaxLoraRank) return ok();
+    if (!is_act_type(xtype))
+        return fail(LLMR_ERR_UNSUPPORTED, "input type %u not supported (F32=0, F16=1, BF16=30)", xtype);
+    if (seq_len == 0) return ok();
+    if (!lora->a || !lora->b || !scratch || !input || !output)
+        return fail(LLMR_ERR_INVALID_ARG, "null LoRA, scratch, input or output pointer");
+    if (in_dim == 0) return fail(LLMR_ERR_INVALID_ARG, "in_dim must be positive");
+    if (b_rows == 0) b_rows = out_dim;
+    if ((uint64_t)row_offset + b_rows > out_dim)
+        return fail(LLMR_ERR_INVALID_ARG, "row_offset + b_rows (%u + %u) exceeds out_dim %u", row_offset, b_rows,
+                    out_dim);
+    hipError_t e = llmr::launch_lora_correction(lora->a, lora->b, lora->rank, lora->scale, scratch, input, xtype,
+                                                output, in_dim, out_dim, seq_len, b_rows, row_offset,
+                                                weight_row_offset, ctx->cur);
+    if (e != hipSuccess) return fail(LLMR_ERR_HIP, "lora_correction launch: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int llmr_batch_matmul_lora(llmr_context* ctx, const void* weight, uint32_t wtype, const void* input, uint32_t xtype,
+                           float* output, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len, uint32_t row_offset,
+                           const llmr_lora* lora, float* lora_scratch, uint32_t lora_b_rows,
+                           uint32_t lora_row_offset, uint32_t lora_weight_row_offset) {
+    if (int r = llmr_batch_matmul(ctx, weight, wtype, input, xtype, output, out_dim, in_dim, seq_len, row_offset))
+        return r;
+    return llmr_lora_correction(ctx, lora, lora_scratch, input, xtype, output, in_dim, out_dim, seq_len,
+                                lora_b_rows, lora_row_offset, lora_weight_row_offset);
+}
+
+int llmr_q8_lora_merge(llmr_context* ctx, void* weight, const float* a, const float* b, uint32_t in_dim,
+                       uint32_t b_rows, uint32_t dst_row_offset, uint32_t rank, float scale) {
+    if (int r = check_ctx(ctx)) return r;
+    // lora_merge.c3:55-62: the merge takes in_dim % 256 == 0 and rank <= 256
+    if (in_dim == 0 || in_dim % 256 != 0)
+        return fail(LLMR_ERR_UNSUPPORTED, "LoRA merge needs in_dim %% 256 == 0 (got %u)", in_dim);
+    if (rank == 0 || rank > llmr::kMaxLoraRank)
+        return fail(LLMR_ERR_UNSUPPORTED, "LoRA merge needs 1 <= rank <= %u (got %u)", llmr::kMaxLoraRank, rank);
+    if (b_rows == 0) return ok();
+    if (!weight || !a || !b) return fail(LLMR_ERR_INVALID_ARG, "null weight, a or b pointer");
+    if ((uint64_t)dst_row_offset + b_rows > 0xffffffffull)
+        return fail(LLMR_ERR_INVALID_ARG, "dst_row_offset + b_rows overflows");
+    hipError_t e = llmr::launch_q8_lora_merge(weight, a, b, in_dim, b_rows, dst_row_offset, rank, scale, ctx->cur);
+    if (e != hipSuccess) return fail(LLMR_ERR_HIP, "q8_lora_merge launch: %s", hipGetErrorString(e));
+    return ok();
+}
+
 // Grows the context workspace to `need` bytes (hipFree waits for every
 // launch that may still use the old one).
 static int grow_workspace(llmr_context* ctx, size_t need) {

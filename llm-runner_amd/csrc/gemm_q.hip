@@ -1012,6 +1012,404 @@ __global__ void __launch_bounds__(256, 1) gemm_q_persist(const PersistArgs args)
     LLMR_WAIT_VMCNT(0);  // no DMA may still be writing this workgroup's LDS when it exits
 }
 
+// ---------------------------------------------------------------------------
+// gemm_q_persist8: the persistent kernel on 8 waves (two per SIMD). A wave's
+// VALU and LDS instructions issue between its own MFMAs only at a cost
+// (about 2 cycles per VALU instruction on top of the MFMA's 32), but they
+// are free while the other wave of the SIMD keeps the matrix core busy; and
+// one wave alone reads LDS at ~32 B/clk, eight waves at ~220 B/clk. The
+// tile stays 256 x 256 with the same LDS rings, stage order and barriers;
+// wave w owns tokens 128 (w & 1) .. +127 x features 64 ((w >> 1) & 3) .. +63
+// (2 x 4 accumulators of 32 x 32), and two threads share each weight row.
+// ---------------------------------------------------------------------------
+
+// Half a weight row's stage for the 8-wave kernel: half h (uniform in a
+// wave) dequantizes the LDS chunks 2h, 2h+1, 4+2h, 4+2h+1 of the row (Q4_K:
+// qs bytes 16h .. 16h+15 of the stage's 32, low and high nibbles) or chunks
+// 4h .. 4h+3 (Q8_0: block h of the stage's two). Part p of 4 writes one chunk.
+template <uint32_t WT, uint32_t OT>
+struct WHalf;
+
+template <uint32_t OT>
+struct WHalf<kGgmlQ4K, OT> {
+    static constexpr int kLoads = 2;
+    u32x4 hdr, q;
+    template <int L>
+    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t s, uint32_t h) {
+        const uint32_t sh = (s >> 2) * 144u;
+        if constexpr (L == 0) hdr = bload16(r, voff, sh);
+        if constexpr (L == 1) q = bload16(r, voff, sh + 16u + 32u * (s & 3u) + 16u * h);
+    }
+    struct Scale {
+        float s0, b0, s1, b1;
+    };
+    // the same operand RN(d*sc*q - dmin*mn) as WRow<kGgmlQ4K>
+    __device__ __forceinline__ Scale scale(uint32_t s, uint32_t) const {
+        const uint32_t j = s & 3u;
+        const float d = f16_bits_to_f32(hdr.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(hdr.x >> 16);
+        uint32_t sc0, mn0, sc1, mn1;
+        q4k_scale_min(2 * j, hdr.y, hdr.z, hdr.w, sc0, mn0);
+        q4k_scale_min(2 * j + 1, hdr.y, hdr.z, hdr.w, sc1, mn1);
+        return Scale{d * (float)sc0 * 16777216.0f, -(dmin * (float)mn0), d * (float)sc1 * 1048576.0f,
+                     -(dmin * (float)mn1)};
+    }
+    template <int P>
+    __device__ __forceinline__ void store(uint8_t* lds, const Scale& c, uint32_t base, uint32_t h) const {
+        constexpr bool HI = (P & 1) != 0;
+        const uint32_t w0 = P < 2 ? q.x : q.z, w1 = P < 2 ? q.y : q.w;
+        const uint32_t mask = HI ? 0xf0f0f0f0u : 0x0f0f0f0fu;
+        const uint32_t m0 = w0 & mask, m1 = w1 & mask;
+        const float s = HI ? c.s1 : c.s0, b = HI ? c.b1 : c.b0;
+        const u32x4 v = {fma_pair<OT>(sub16x2(m0, kSelLo), s, b), fma_pair<OT>(sub16x2(m0, kSelHi), s, b),
+                         fma_pair<OT>(sub16x2(m1, kSelLo), s, b), fma_pair<OT>(sub16x2(m1, kSelHi), s, b)};
+        const uint32_t ch = (HI ? 4u : 0u) + 2u * h + (uint32_t)(P >> 1);
+        *(u32x4*)(lds + (base ^ (ch << 4))) = v;
+    }
+};
+
+template <uint32_t OT>
+struct WHalf<kGgmlQ8_0, OT> {
+    static constexpr int kLoads = 3;
+    u32x4 a, b;
+    uint32_t e;
+    // bytes [68 s + 32 h, +36): block h's scale is the half at byte 34 h - 32 h
+    // (h = 0: low half of dword 0; h = 1: high half), its 32 quants start at
+    // byte 2 (h = 0, unaligned) or 4 (h = 1)
+    template <int L>
+    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t s, uint32_t h) {
+        const uint32_t so = 68u * s + 32u * h;
+        if constexpr (L == 0) a = bload16(r, voff, so);
+        if constexpr (L == 1) b = bload16(r, voff + 16u, so);
+        if constexpr (L == 2) e = bload4(r, voff + 32u, so);
+    }
+    struct Scale {
+        float s, b;  // bf16: (2^24 d, -128 d); f16: (d, -)
+    };
+    __device__ __forceinline__ Scale scale(uint32_t, uint32_t h) const {
+        const float d = f16_bits_to_f32(h ? a.x >> 16 : a.x & 0xffffu);
+        if constexpr (OT == kGgmlBF16)
+            return Scale{d * 16777216.0f, -128.0f * d};
+        else
+            return Scale{d, 0.0f};
+    }
+    __device__ __forceinline__ uint32_t word(int i) const {
+        return i < 4 ? a[i] : i < 8 ? b[i - 4] : e;
+    }
+    template <int P>
+    __device__ __forceinline__ void store(uint8_t* lds, const Scale& k, uint32_t base, uint32_t h) const {
+        // quant dwords 2P, 2P+1 of the block
+        const uint32_t q0 = h ? word(2 * P + 1) : __builtin_amdgcn_alignbyte(word(2 * P + 1), word(2 * P), 2);
+        const uint32_t q1 = h ? word(2 * P + 2) : __builtin_amdgcn_alignbyte(word(2 * P + 2), word(2 * P + 1), 2);
+        u32x4 v;
+        if constexpr (OT == kGgmlBF16) {
+            const uint32_t u0 = q0 ^ 0x80808080u, u1 = q1 ^ 0x80808080u;
+            v = u32x4{fma_pair<OT>(sub16x2(u0, kSelLo), k.s, k.b), fma_pair<OT>(sub16x2(u0, kSelHi), k.s, k.b),
+                      fma_pair<OT>(sub16x2(u1, kSelLo), k.s, k.b), fma_pair<OT>(sub16x2(u1, kSelHi), k.s, k.b)};
+        } else {
+            const _Float16 d = (_Float16)k.s;
+            v = q8x8_f16(q0, q1, f16x2{d, d});
+        }
+        const uint32_t ch = 4u * h + (uint32_t)P;
+        *(u32x4*)(lds + (base ^ (ch << 4))) = v;
+    }
+};
+
+// One 16-wide k step of the 8-wave kernel: 8 MFMAs, the next step's six
+// fragment reads after the first six, the dequantization's VALU, its LDS
+// write and the step's loads in between.
+#define LLMR8_SLOT_R LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x002, 2)
+#define LLMR8_STEP_SCHEDULE                                                                 \
+    LLMR8_SLOT_R; LLMR8_SLOT_R; LLMR8_SLOT_R; LLMR8_SLOT_R; LLMR8_SLOT_R; LLMR8_SLOT_R;     \
+    LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 4); LLMR_SGB(0x200, 1);                             \
+    LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 4); LLMR_SGB(0x020, 2)
+
+struct Frags8 {
+    f16x8 x[4], w[2];
+};
+
+template <uint32_t WT, uint32_t XT, uint32_t EPI = kEpiStore, bool GROUPED = false>
+__global__ void __launch_bounds__(512, 1) gemm_q_persist8(const PersistArgs args) {
+    // every argument the kernel uses as a scalar local (see gemm_q_persist)
+    const uint32_t N = args.N, K = args.K, tiles_m = args.tiles_m, tiles_n = args.tiles_n;
+    const uint32_t ldy = args.ldy, ldy2 = args.ldy2, split = args.split, y2_bf16 = args.y2_bf16;
+    const uint8_t* const Wp0 = args.p[0].W;
+    const uint8_t* const Wp1 = GROUPED ? args.p[1].W : nullptr;
+    const void* const Xp0 = args.p[0].X;
+    const void* const Xp1 = GROUPED ? args.p[1].X : nullptr;
+    float* const Yp0 = args.p[0].Y;
+    float* const Yp1 = GROUPED ? args.p[1].Y : nullptr;
+    const float* const Gp0 = args.p[0].gate;
+    const float* const Gp1 = GROUPED ? args.p[1].gate : nullptr;
+    void* const Y2p0 = args.p[0].Y2;
+    void* const Y2p1 = GROUPED ? args.p[1].Y2 : nullptr;
+    const uint32_t Mp0 = args.p[0].M, Mp1 = GROUPED ? args.p[1].M : 0u;
+    const uint32_t Rp0 = args.p[0].row_offset, Rp1 = GROUPED ? args.p[1].row_offset : 0u;
+    const uint32_t Tp0 = args.p[0].tiles_m;
+    static_assert(XT == kGgmlF16 || XT == kGgmlBF16, "16-bit activations only");
+    constexpr uint32_t TILE = 256u * 128u;  // bytes of one 256-row x 64-wide 16-bit tile
+    constexpr int X_DMAS = 4;               // 1 KiB activation DMAs per wave per stage
+    constexpr int W_LOADS = WHalf<WT, XT>::kLoads;
+    constexpr int IN_FLIGHT = X_DMAS + W_LOADS;  // one stage's loads
+    __shared__ __attribute__((aligned(16))) uint8_t X0[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t X1[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t X2[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t W0[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t W1[TILE];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t l32 = lane & 31u, kh = lane >> 5;
+    const uint32_t wm = wave & 1u, wn = (wave >> 1) & 3u;
+    const uint32_t wh = wave >> 2;  // the weight-row half this wave dequantizes
+
+    const uint32_t G = gridDim.x, total = tiles_m * tiles_n;
+    const uint32_t n_tiles = (total - blockIdx.x + G - 1) / G;  // >= 1: grid <= total
+    const uint32_t S = K / kBK;
+    const uint32_t SP = (S + 5u) / 6u * 6u;
+    const uint32_t rb = (WT == kGgmlQ8_0) ? (K / 32u) * 34u : (K / 256u) * 144u;
+    const uint32_t xrow = K * 2u;
+
+    // activation DMA i of wave w: rows 32w + 8i + lane/8, physical chunk
+    // lane%8, logical chunk (lane%8) ^ ((row >> 1) & 7)
+    uint32_t xvoff[X_DMAS];
+#pragma unroll
+    for (int i = 0; i < X_DMAS; i++) {
+        const uint32_t row = 32u * wave + 8u * i + (lane >> 3);
+        const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
+        xvoff[i] = row * xrow + c * 16u;
+    }
+    // thread tid dequantizes half wh of weight row tid % 256 of the tile
+    const uint32_t wrow = tid & 255u;
+    const uint32_t wvoff = wrow * rb;
+    const uint32_t wbase = wrow * 128u + (((wrow >> 1) & 7u) << 4);  // its LDS chunk 0
+    uint32_t xoff[4], woff[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t ch = 4u * (t >> 1) + 2u * kh + (t & 1);
+        xoff[t] = lds_off(wm * 128u + l32, ch);
+        woff[t] = lds_off(wn * 64u + l32, ch);
+    }
+
+    struct Cursor {
+        uint32_t s;
+        const uint8_t* base;
+        uint32_t size;
+    };
+    auto tile_origin = [&](uint32_t k, uint32_t& p, uint32_t& m0, uint32_t& n0) {
+        uint32_t tm, tn;
+        map_tile_persist(blockIdx.x + k * G, G, tiles_m, tiles_n, tm, tn);
+        p = GROUPED && tm >= Tp0 ? 1u : 0u;
+        m0 = (tm - (p ? Tp0 : 0u)) * 256u;
+        n0 = tn * 256u;
+    };
+    auto x_tile = [&](Cursor& c, uint32_t k) {
+        uint32_t p, m0, n0;
+        tile_origin(k, p, m0, n0);
+        c.s = 0;
+        c.base = (const uint8_t*)pick(p, Xp0, Xp1) + (uint64_t)m0 * xrow;
+        c.size = k < n_tiles ? (pick(p, Mp0, Mp1) - m0) * xrow : 0u;
+    };
+    auto w_tile = [&](Cursor& c, uint32_t k) {
+        uint32_t p, m0, n0;
+        tile_origin(k, p, m0, n0);
+        c.s = 0;
+        c.base = pick(p, Wp0, Wp1) + (uint64_t)(pick(p, Rp0, Rp1) + n0) * rb;
+        c.size = k < n_tiles ? (N - n0) * rb : 0u;
+    };
+    Cursor cx{0, nullptr, 0}, cw{0, nullptr, 0};
+    Cursor nx{0, nullptr, 0}, nw{0, nullptr, 0};
+    auto advance = [&](Cursor& c, const Cursor& next) {
+        if (++c.s == SP) c = next;
+    };
+    auto dma = [&](rsrc_t xr, uint8_t* Xs, int i, uint32_t so) {
+        uint8_t* dst = Xs + wave * (32u * 128u) + 1024u * i;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)dst, 16, xvoff[i], so, 0, 0);
+    };
+    WHalf<WT, XT> R0, R1, R2;
+    auto issue_w_all = [&](WHalf<WT, XT>& U) {
+        const rsrc_t wr = make_rsrc(cw.base, cw.s < S ? cw.size : 0u);
+        static_for<0, W_LOADS>([&](auto L) { U.template load<decltype(L)::value>(wr, wvoff, cw.s, wh); });
+        advance(cw, nw);
+    };
+    auto issue_x_all = [&](uint8_t* Xs) {
+        const rsrc_t xr = make_rsrc(cx.base, cx.s < S ? cx.size : 0u);
+#pragma unroll
+        for (int i = 0; i < X_DMAS; i++) dma(xr, Xs, i, cx.s * 128u);
+        advance(cx, nx);
+    };
+    constexpr int N_OPS = W_LOADS + X_DMAS;
+    auto issue_part = [&](auto PART, rsrc_t wr, uint32_t ws, rsrc_t xr, uint32_t xso, uint8_t* Xs,
+                          WHalf<WT, XT>& U) {
+        constexpr int p = decltype(PART)::value;
+        static_for<p * N_OPS / 4, (p + 1) * N_OPS / 4>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            if constexpr (i < W_LOADS)
+                U.template load<i>(wr, wvoff, ws, wh);
+            else
+                dma(xr, Xs, i - W_LOADS, xso);
+        });
+    };
+
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = f32x16{};
+
+    auto read_frags = [&](Frags8& f, const uint8_t* Xs, const uint8_t* Ws, int t) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) f.x[b] = *(const f16x8*)(Xs + b * 32 * 128 + xoff[t]);
+#pragma unroll
+        for (int a = 0; a < 2; a++) f.w[a] = *(const f16x8*)(Ws + a * 32 * 128 + woff[t]);
+    };
+    auto mfma_step = [&](const Frags8& f) {
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) acc[a][b] = mfma16<XT>(f.w[a], f.x[b], acc[a][b]);
+    };
+    // Store the accumulators as tile k's results and clear them (N % 4 == 0,
+    // host-checked). nw = n - 4 kh is uniform in the wave; with split % 8 ==
+    // 0 (host-checked) nw < split is a uniform branch.
+    auto store_tile = [&](uint32_t k) {
+        uint32_t p, m0, n0;
+        tile_origin(k, p, m0, n0);
+        const uint32_t M = pick(p, Mp0, Mp1);
+        float* const Y = pick(p, Yp0, Yp1);
+        auto each = [&](auto&& f) __attribute__((always_inline)) {
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const uint32_t m = m0 + wm * 128u + b * 32u + l32;
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const uint32_t nw = n0 + wn * 64u + a * 32u + 8u * g;
+                        const uint32_t n = nw + 4u * kh;
+                        if (m < M && n < N)
+                            f(m, n, nw, f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2],
+                                              acc[a][b][4 * g + 3]});
+                    }
+                    acc[a][b] = f32x16{};
+                }
+        };
+        if constexpr (EPI == kEpiResidual) {
+            const float* const gate = pick(p, Gp0, Gp1);
+            each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
+                f32x4* const h = (f32x4*)(Y + (uint64_t)m * ldy + n);
+                const f32x4 gv = gate ? *(const f32x4*)(gate + n) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+                *h = *h + gv * v;
+            });
+        } else if constexpr (EPI == kEpiSplitGelu) {
+            uint16_t* const Y2 = (uint16_t*)pick(p, Y2p0, Y2p1);
+            const uint32_t bf = y2_bf16;
+            each([&](uint32_t m, uint32_t n, uint32_t nw, f32x4 v) __attribute__((always_inline)) {
+                if (nw < split) {
+                    *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
+                } else {
+                    const f32x4 gl{gelu_tanh(v.x), gelu_tanh(v.y), gelu_tanh(v.z), gelu_tanh(v.w)};
+                    u32x2 o;
+                    if (bf) {
+                        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+                        o.x = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.x, (__bf16)gl.y});
+                        o.y = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.z, (__bf16)gl.w});
+                    } else {
+                        o = u32x2{pack_f16x2(gl.x, gl.y), pack_f16x2(gl.z, gl.w)};
+                    }
+                    *(u32x2*)(Y2 + (uint64_t)m * ldy2 + (n - split)) = o;
+                }
+            });
+        } else {
+            each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
+                *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
+            });
+        }
+    };
+
+    // prologue, as gemm_q_persist's: W0 | W1 X0 | W2 X1, then stage 0's
+    // weights are dequantized and its activations have landed
+    x_tile(cx, 0);
+    w_tile(cw, 0);
+    x_tile(nx, 1);
+    w_tile(nw, 1);
+    issue_w_all(R0);
+    issue_w_all(R1);
+    issue_x_all(X0);
+    issue_w_all(R2);
+    issue_x_all(X1);
+    LLMR_WAIT_VMCNT(2 * W_LOADS + 2 * X_DMAS);
+    {
+        const auto sc0 = R0.scale(0, wh);
+        R0.template store<0>(W0, sc0, wbase, wh);
+        R0.template store<1>(W0, sc0, wbase, wh);
+        R0.template store<2>(W0, sc0, wbase, wh);
+        R0.template store<3>(W0, sc0, wbase, wh);
+    }
+    LLMR_STAGE_BARRIER(IN_FLIGHT);
+
+    Frags8 F0, F1;
+    // the stage of gemm_q_persist with this kernel's fragments and schedule
+#define LLMR_PERSIST8_STAGE(XC, WC, XD, WNX, RN, RL, NEXT)                                   \
+    {                                                                                       \
+        const rsrc_t wr_ = make_rsrc(cw.base, cw.s < S ? cw.size : 0u);                      \
+        const rsrc_t xr_ = make_rsrc(cx.base, cx.s < S ? cx.size : 0u);                      \
+        const uint32_t ws_ = cw.s, xso_ = cx.s * 128u;                                      \
+        LLMR_WAIT_VMCNT(X_DMAS + IN_FLIGHT);                                                \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        const auto sc_ = RN.scale(NEXT, wh);                                                \
+        issue_part(std::integral_constant<int, 0>{}, wr_, ws_, xr_, xso_, XD, RL);          \
+        read_frags(F0, XC, WC, 0);                                                          \
+        mfma_step(F1);                                                                      \
+        RN.template store<0>(WNX, sc_, wbase, wh);                                          \
+        LLMR8_STEP_SCHEDULE;                                                                \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(std::integral_constant<int, 1>{}, wr_, ws_, xr_, xso_, XD, RL);          \
+        read_frags(F1, XC, WC, 1);                                                          \
+        mfma_step(F0);                                                                      \
+        RN.template store<1>(WNX, sc_, wbase, wh);                                          \
+        LLMR8_STEP_SCHEDULE;                                                                \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(std::integral_constant<int, 2>{}, wr_, ws_, xr_, xso_, XD, RL);          \
+        read_frags(F0, XC, WC, 2);                                                          \
+        mfma_step(F1);                                                                      \
+        RN.template store<2>(WNX, sc_, wbase, wh);                                          \
+        LLMR8_STEP_SCHEDULE;                                                                \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(std::integral_constant<int, 3>{}, wr_, ws_, xr_, xso_, XD, RL);          \
+        read_frags(F1, XC, WC, 3);                                                          \
+        mfma_step(F0);                                                                      \
+        RN.template store<3>(WNX, sc_, wbase, wh);                                          \
+        LLMR8_STEP_SCHEDULE;                                                                \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        advance(cw, nw);                                                                    \
+        advance(cx, nx);                                                                    \
+        LLMR_STAGE_BARRIER(IN_FLIGHT);                                                      \
+    }
+    for (uint32_t k = 0; k < n_tiles; k++) {
+        if (k > 0) {
+            x_tile(nx, k + 1);
+            w_tile(nw, k + 1);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) F1.x[i] = f16x8{};
+#pragma unroll
+        for (int i = 0; i < 2; i++) F1.w[i] = f16x8{};
+        for (uint32_t s0 = 0; s0 < SP; s0 += 6) {
+            LLMR_PERSIST8_STAGE(X0, W0, X2, W1, R1, R0, s0 + 1)
+            LLMR_PERSIST8_STAGE(X1, W1, X0, W0, R2, R1, s0 + 2)
+            LLMR_PERSIST8_STAGE(X2, W0, X1, W1, R0, R2, s0 + 3)
+            LLMR_PERSIST8_STAGE(X0, W1, X2, W0, R1, R0, s0 + 4)
+            LLMR_PERSIST8_STAGE(X1, W0, X0, W1, R2, R1, s0 + 5)
+            LLMR_PERSIST8_STAGE(X2, W1, X1, W0, R0, R2, s0 + 6 == SP ? 0u : s0 + 6)
+        }
+        mfma_step(F1);
+        store_tile(k);
+    }
+#undef LLMR_PERSIST8_STAGE
+    LLMR_WAIT_VMCNT(0);  // no DMA may still be writing this workgroup's LDS when it exits
+}
+
 // Generic path for shapes the tiled kernel does not take (Q8_0 with
 // K % 64 == 32): one thread per output, operands as the MFMA paths (bf16
 // activations and weight operands for bf16 inputs, fp16 otherwise; f32
@@ -1110,7 +1508,12 @@ hipError_t dispatch_x(const void* w, const void* x, float* y, uint32_t N, uint32
             a.tiles_n = tiles_n;
             a.epi = kEpiStore;
             a.ldy = N;
-            hipLaunchKernelGGL((gemm_q_persist<WT, XT, false>), dim3(grid), dim3(256), 0, st, a);
+            // Q8_0 on the 8-wave kernel (its half-row dequantization is lighter
+            // than Q4_K's and it measures faster); Q4_K on the 4-wave one
+            if constexpr (WT == kGgmlQ8_0)
+                hipLaunchKernelGGL((gemm_q_persist8<WT, XT>), dim3(grid), dim3(512), 0, st, a);
+            else
+                hipLaunchKernelGGL((gemm_q_persist<WT, XT, false>), dim3(grid), dim3(256), 0, st, a);
             return hipGetLastError();
         }
     }
@@ -1267,10 +1670,17 @@ hipError_t launch_persist_multi(uint32_t N, uint32_t K, const GemmJob* jobs, uin
     a.split = epi.kind == kEpiSplitGelu ? epi.split : N;
     a.y2_bf16 = epi.y2_type == kGgmlBF16 ? 1u : 0u;
     const uint32_t grid = (uint32_t)min((uint64_t)tiles_m * tiles_n, (uint64_t)num_cus);
-    auto kern = epi.kind == kEpiResidual    ? gemm_q_persist<WT, XT, false, kEpiResidual, true>
-                : epi.kind == kEpiSplitGelu ? gemm_q_persist<WT, XT, false, kEpiSplitGelu, true>
-                                            : gemm_q_persist<WT, XT, false, kEpiStore, true>;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, st, a);
+    if constexpr (WT == kGgmlQ8_0) {
+        auto kern = epi.kind == kEpiResidual    ? gemm_q_persist8<WT, XT, kEpiResidual, true>
+                    : epi.kind == kEpiSplitGelu ? gemm_q_persist8<WT, XT, kEpiSplitGelu, true>
+                                                : gemm_q_persist8<WT, XT, kEpiStore, true>;
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(512), 0, st, a);
+    } else {
+        auto kern = epi.kind == kEpiResidual    ? gemm_q_persist<WT, XT, false, kEpiResidual, true>
+                    : epi.kind == kEpiSplitGelu ? gemm_q_persist<WT, XT, false, kEpiSplitGelu, true>
+                                                : gemm_q_persist<WT, XT, false, kEpiStore, true>;
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 

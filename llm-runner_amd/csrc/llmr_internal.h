@@ -42,6 +42,17 @@ hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N,
                                      uint32_t n_jobs, const GemmEpilogue& epi, int num_cus, void* ws,
                                      hipStream_t st);
 
+// LoRA (lora.hip): the two-hop correction appended to a base GEMM output and
+// the load-time Q8_0 merge. Ranks above kMaxLoraRank are not taken (the
+// reference sizes its scratch for 256).
+constexpr uint32_t kMaxLoraRank = 256;
+hipError_t launch_lora_correction(const float* A, const float* B, uint32_t rank, float scale, float* scratch,
+                                  const void* x, uint32_t xtype, float* out, uint32_t in_dim, uint32_t out_dim,
+                                  uint32_t seq_len, uint32_t b_rows, uint32_t row_offset, uint32_t weight_row_offset,
+                                  hipStream_t st);
+hipError_t launch_q8_lora_merge(void* base, const float* A, const float* B, uint32_t in_dim, uint32_t b_rows,
+                                uint32_t dst_row_offset, uint32_t rank, float scale, hipStream_t st);
+
 // Q4_K weights times at most kGemvMaxTokens tokens (gemv_q.hip): an
 // HBM-bound weight stream, taken by launch_batch_matmul for such M.
 constexpr uint32_t kGemvMaxTokens = 4;

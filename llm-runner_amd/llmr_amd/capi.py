@@ -56,6 +56,12 @@ class MatmulEpilogue(ctypes.Structure):
 
 EPI_STORE, EPI_GATED_RESIDUAL, EPI_SPLIT_GELU = 0, 1, 2
 
+
+class Lora(ctypes.Structure):
+    """llmr_lora: a [rank, in_dim] and b [rows, rank] f32 device pointers, rank, scale."""
+    _fields_ = [("a", ctypes.c_void_p), ("b", ctypes.c_void_p), ("rank", ctypes.c_uint32),
+                ("scale", ctypes.c_float)]
+
 _vp = ctypes.c_void_p
 _u32 = ctypes.c_uint32
 _SIGS = {
@@ -98,6 +104,10 @@ _SIGS = {
     "llmr_unpatchify": (ctypes.c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u32]),
     "llmr_synth_q4k": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, _u32, ctypes.c_uint64, ctypes.c_uint64,
                                       ctypes.c_double]),
+    "llmr_lora_correction": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
+    "llmr_batch_matmul_lora": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _vp, _vp,
+                                              _u32, _u32, _u32]),
+    "llmr_q8_lora_merge": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, ctypes.c_float]),
 }
 
 # Activation and gate selectors of llmr_activation / llmr_gated_residual.
@@ -234,3 +244,22 @@ class Context:
 
     def synth_q4k(self, out, n_rows, in_dim, seed, stream, std):
         check(lib().llmr_synth_q4k(self._h, out, n_rows, in_dim, seed, stream, float(std)))
+
+    def lora_correction(self, lora: "Lora | None", scratch: int, x_ptr: int, xtype: int, y_ptr: int,
+                        in_dim: int, out_dim: int, seq_len: int, b_rows: int = 0, row_offset: int = 0,
+                        weight_row_offset: int = 0) -> None:
+        check(lib().llmr_lora_correction(self._h, ctypes.byref(lora) if lora is not None else None, scratch,
+                                         x_ptr, xtype, y_ptr, in_dim, out_dim, seq_len, b_rows, row_offset,
+                                         weight_row_offset))
+
+    def batch_matmul_lora(self, w_ptr: int, wtype: int, x_ptr: int, xtype: int, y_ptr: int, out_dim: int,
+                          in_dim: int, seq_len: int, row_offset: int, lora: "Lora | None", scratch: int,
+                          b_rows: int = 0, lora_row_offset: int = 0, lora_weight_row_offset: int = 0) -> None:
+        check(lib().llmr_batch_matmul_lora(self._h, w_ptr, wtype, x_ptr, xtype, y_ptr, out_dim, in_dim, seq_len,
+                                           row_offset, ctypes.byref(lora) if lora is not None else None, scratch,
+                                           b_rows, lora_row_offset, lora_weight_row_offset))
+
+    def q8_lora_merge(self, w_ptr: int, a_ptr: int, b_ptr: int, in_dim: int, b_rows: int, dst_row_offset: int,
+                      rank: int, scale: float) -> None:
+        check(lib().llmr_q8_lora_merge(self._h, w_ptr, a_ptr, b_ptr, in_dim, b_rows, dst_row_offset, rank,
+                                       float(scale)))

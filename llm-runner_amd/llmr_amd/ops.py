@@ -23,6 +23,10 @@ import torch
 from . import capi
 from .gguf import GGML_BF16, GGML_F16, GGML_F32, GGML_Q4_K, GGML_Q8_0, row_bytes
 
+# Largest LoRA rank the backend takes (the reference sizes its scratch for 256:
+# DIT_MAX_LORA_RANK, dit.c3:42).
+MAX_LORA_RANK = 256
+
 _TORCH_GGML = {torch.float32: GGML_F32, torch.float16: GGML_F16, torch.bfloat16: GGML_BF16}
 
 
@@ -84,16 +88,65 @@ def _dev(t: Tensor, what: str) -> None:
         raise ValueError(f"{what} must be contiguous")
 
 
+@dataclasses.dataclass
+class LoraTensor:
+    """One linear's LoRA adapter (LoraTensor, lib/model/lora.c3:22-28): a [rank,
+    in_dim] and b [out_rows, rank] f32 device tensors; the correction is
+    scale * (b . a). `present` goes False once merged into the base weight."""
+    a: torch.Tensor
+    b: torch.Tensor
+    rank: int
+    scale: float
+    present: bool = True
+
+    def c_struct(self) -> capi.Lora:
+        for t, n in ((self.a, "lora.a"), (self.b, "lora.b")):
+            if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous():
+                raise ValueError(f"{n} must be a contiguous f32 device tensor")
+        if self.a.shape[0] != self.rank or self.b.shape[-1] != self.rank:
+            raise ValueError("lora.a must be [rank, in_dim] and lora.b [rows, rank]")
+        return capi.Lora(self.a.data_ptr(), self.b.data_ptr(), self.rank, float(self.scale))
+
+
+def dispatch_lora_correction(g: RenderGraph, lora: LoraTensor | None, lora_scratch: torch.Tensor | None,
+                             input: Tensor, output: Tensor, in_dim: int, out_dim: int, seq_len: int,
+                             b_rows: int = 0, row_offset: int = 0, weight_row_offset: int = 0) -> None:
+    """The two-hop LoRA correction on a base output (dispatch_lora_correction,
+    dit.c3:1319-1364): output[s, row_offset + o] += scale * (b . (a . input[s]))[
+    weight_row_offset + o] for o < b_rows (0: out_dim). No-op without a present
+    adapter or with rank > 256, as in the reference. lora_scratch: >= seq_len *
+    rank f32 on the device."""
+    if lora is None or not lora.present or lora.rank == 0 or lora.rank > MAX_LORA_RANK:
+        return
+    if lora_scratch is None or lora_scratch.dtype != torch.float32 or not lora_scratch.is_cuda:
+        raise ValueError("lora_scratch must be an f32 device tensor")
+    if lora_scratch.numel() < seq_len * lora.rank:
+        raise ValueError("lora_scratch smaller than seq_len * rank")
+    if lora.a.shape[1] != in_dim:
+        raise ValueError("lora.a must be [rank, in_dim]")
+    rows = b_rows or out_dim
+    if weight_row_offset + rows > lora.b.shape[0]:
+        raise ValueError("lora.b has fewer rows than weight_row_offset + b_rows")
+    for t, n in ((input, "input"), (output, "output")):
+        _dev(t, n)
+    if output.dtype != GGML_F32:
+        raise ValueError("output must be f32")
+    if input.data.numel() < seq_len * in_dim or output.data.numel() < seq_len * out_dim:
+        raise ValueError("input/output smaller than [seq_len, in_dim] / [seq_len, out_dim]")
+    g.bind_stream()
+    g.ctx.lora_correction(lora.c_struct(), lora_scratch.data_ptr(), input.ptr(), input.dtype, output.ptr(),
+                          in_dim, out_dim, seq_len, b_rows, row_offset, weight_row_offset)
+
+
 def dispatch_batch_matmul(g: RenderGraph, weight: Tensor, input: Tensor, output: Tensor,
                           out_dim: int, in_dim: int, seq_len: int, row_offset: int,
-                          lora=None) -> None:
-    """output[m, n] = sum_k input[m, k] * weight[row_offset + n, k] (f32, overwritten).
+                          lora: LoraTensor | None = None, lora_scratch: torch.Tensor | None = None,
+                          lora_b_rows: int = 0, lora_row_offset: int = 0, lora_weight_row_offset: int = 0) -> None:
+    """output[m, n] = sum_k input[m, k] * weight[row_offset + n, k] (f32, overwritten),
+    then the LoRA correction when an adapter is present.
 
-    Mirrors zimage::dispatch_batch_matmul for Q8_0 / Q4_K weights. A present
-    LoRA is a caller-side second hop in the reference (dit.c3:1305-1364) and
-    is not part of this backend."""
-    if lora is not None and getattr(lora, "present", True):
-        raise NotImplementedError("runtime LoRA correction stays on the caller side")
+    Mirrors zimage::dispatch_batch_matmul (dit.c3:1198-1301) for Q8_0 / Q4_K
+    weights, including its trailing dispatch_lora_correction."""
     if weight.dtype not in (GGML_Q8_0, GGML_Q4_K):
         raise capi.LlmrError(capi.LLMR_ERR_UNSUPPORTED, f"weight type {weight.dtype}")
     for t, n in ((weight, "weight"), (input, "input"), (output, "output")):
@@ -107,6 +160,30 @@ def dispatch_batch_matmul(g: RenderGraph, weight: Tensor, input: Tensor, output:
     g.bind_stream()
     g.ctx.batch_matmul(weight.ptr(), weight.dtype, input.ptr(), input.dtype, output.ptr(),
                        out_dim, in_dim, seq_len, row_offset)
+    dispatch_lora_correction(g, lora, lora_scratch, input, output, in_dim, out_dim, seq_len, lora_b_rows,
+                             lora_row_offset, lora_weight_row_offset)
+
+
+def merge_one_site(g: RenderGraph, base: Tensor, lora: LoraTensor, dst_row_offset: int = 0) -> bool:
+    """Folds a present adapter into a Q8_0 base weight in place (merge_one_site,
+    lora_merge.c3:36-73) and marks it merged. Returns False, leaving the adapter
+    for the runtime correction, where the reference skips the merge: a non-Q8_0
+    base, in_dim % 256 != 0 or rank > 256."""
+    if not lora.present:
+        return False
+    in_dim = base.shape[1]
+    if base.dtype != GGML_Q8_0 or in_dim % 256 != 0 or lora.rank > MAX_LORA_RANK:
+        return False
+    b_rows = lora.b.shape[0]
+    if dst_row_offset + b_rows > base.shape[0] or lora.a.shape[1] != in_dim:
+        raise ValueError("adapter does not fit the base weight")
+    _dev(base, "base")
+    lora.c_struct()
+    g.bind_stream()
+    g.ctx.q8_lora_merge(base.ptr(), lora.a.data_ptr(), lora.b.data_ptr(), in_dim, b_rows, dst_row_offset,
+                        lora.rank, lora.scale)
+    lora.present = False
+    return True
 
 
 @dataclasses.dataclass

@@ -42,6 +42,14 @@
  *                            invariance.
  *   orc_rope_tables/apply    closed form (cos/sin of pos*theta^(-2k/axis)) and
  *                            norm preservation of each rotated pair.
+ *   orc_lora_down/up         integer operands (every sum exact) == int64
+ *                            products with offsets; float data within f32
+ *                            rounding of a float64 product.
+ *   orc_q8_lora_merge        zero update == identity on reference-quantized
+ *                            blocks; requantization error <= half a step plus
+ *                            the f16 scale rounding; stored scale == f16 of
+ *                            absmax/127; halves away from zero and saturation
+ *                            on a hand-computed block; untouched rows.
  */
 #include "oracle.h"
 
@@ -820,5 +828,87 @@ void orc_unpatchify(const float* in, float* out, uint32_t C, uint32_t H, uint32_
         uint32_t p = (h / ps) * (W / ps) + w / ps;
         uint32_t e = (h % ps) * ps * C + (w % ps) * C + c;
         out[t] = in[(size_t)p * C * ps * ps + e];
+    }
+}
+
+/* ---- LoRA (dispatch_lora_correction, dit.c3:1319-1364; q8_lora_merge) ----
+ * The reference's `partial += a * b` dot products leave contraction to the
+ * Vulkan driver (its SPIR-V carries no NoContraction); here they are fused
+ * multiply-adds (fmaf), the matrix math's one contraction. Every other
+ * expression rounds each operation. */
+
+/* Hop 1: batch_matmul_simple (llm.slang:1146-1180) with the LoRA A [rank,
+ * in_dim] as its weight: scratch[s, r] = sum_k A[r, k] * x[s, k], each sum
+ * formed as one 256-thread workgroup forms it: fused partials, then
+ * wg_tree_sum. */
+void orc_lora_down(const float* A, const float* X, float* scratch, uint32_t rank, uint32_t in_dim,
+                   uint32_t seq_len) {
+#pragma omp parallel for schedule(static)
+    for (int64_t sr = 0; sr < (int64_t)seq_len * rank; sr++) {
+        const uint32_t s = (uint32_t)(sr / rank), r = (uint32_t)(sr % rank);
+        float part[256];
+        for (uint32_t gi = 0; gi < 256; gi++) {
+            float p = 0.0f;
+            for (uint32_t k = gi; k < in_dim; k += 256) p = fmaf(A[(size_t)r * in_dim + k], X[(size_t)s * in_dim + k], p);
+            part[gi] = p;
+        }
+        scratch[sr] = wg_tree_sum(part);
+    }
+}
+
+/* Hop 2: batch_matmul_add_scaled (llm.slang:1262-1294): for o < b_rows,
+ * out[s * out_dim + row_offset + o] += scale * (fused sum over r in order of
+ * B[(weight_row_offset + o) * rank + r] * scratch[s * rank + r]). */
+void orc_lora_up(const float* B, const float* scratch, float* out, uint32_t rank, uint32_t out_dim,
+                 uint32_t seq_len, float scale, uint32_t row_offset, uint32_t weight_row_offset, uint32_t b_rows) {
+#pragma omp parallel for schedule(static)
+    for (int64_t s = 0; s < (int64_t)seq_len; s++)
+        for (uint32_t o = 0; o < b_rows; o++) {
+            const float* b = B + (size_t)(weight_row_offset + o) * rank;
+            float p = 0.0f;
+            for (uint32_t r = 0; r < rank; r++) p = fmaf(b[r], scratch[(size_t)s * rank + r], p);
+            float* y = out + (size_t)s * out_dim + row_offset + o;
+            *y = *y + scale * p;
+        }
+}
+
+/* q8_lora_merge (llm.slang:1337-1420), in place on rows [dst_row_offset,
+ * dst_row_offset + b_rows) of a Q8_0 weight (in_dim % 256 == 0): element k
+ * of LoRA row j becomes d * q + scale * (fused sum over r in order of B[j, r] *
+ * A[r, k]); each 32-element block is requantized with d' = max(absmax / 127,
+ * 1e-8) (f32), q' = clamp(trunc(u / d' +- 0.5), -127, 127) (the half added
+ * in f32), and d' stored as f16 (round to nearest even). */
+void orc_q8_lora_merge(uint8_t* base, const float* A, const float* B, uint32_t in_dim, uint32_t b_rows,
+                       uint32_t dst_row_offset, uint32_t rank, float scale) {
+    const size_t row_bytes = (size_t)(in_dim / 32) * 34;
+#pragma omp parallel for schedule(static)
+    for (int64_t j = 0; j < (int64_t)b_rows; j++) {
+        uint8_t* row = base + (size_t)(dst_row_offset + (uint32_t)j) * row_bytes;
+        for (uint32_t blk = 0; blk < in_dim / 32; blk++) {
+            uint8_t* b = row + (size_t)blk * 34;
+            const float d = orc_f16_to_f32(rd_u16(b));
+            float u[32], amax = 0.0f;
+            for (uint32_t i = 0; i < 32; i++) {
+                const uint32_t k = blk * 32 + i;
+                const float base_val = d * (float)(int8_t)b[2 + i];
+                float delta = 0.0f;
+                for (uint32_t r = 0; r < rank; r++) delta = fmaf(B[(size_t)j * rank + r], A[(size_t)r * in_dim + k], delta);
+                delta *= scale;
+                u[i] = base_val + delta;
+                const float a = fabsf(u[i]);
+                if (a > amax) amax = a;
+            }
+            float dn = amax / 127.0f;
+            if (dn < 1e-8f) dn = 1e-8f;
+            for (uint32_t i = 0; i < 32; i++) {
+                const float qf = u[i] / dn;
+                int q = qf >= 0.0f ? (int)(qf + 0.5f) : (int)(qf - 0.5f);
+                q = q < -127 ? -127 : (q > 127 ? 127 : q);
+                b[2 + i] = (uint8_t)(int8_t)q;
+            }
+            const uint16_t h = orc_f32_to_f16(dn);
+            b[0] = (uint8_t)(h & 0xffu);
+            b[1] = (uint8_t)(h >> 8);
+        }
     }
 }

@@ -113,6 +113,15 @@ void orc_timestep_embed(float* out, uint32_t dim, float t);
 void orc_patchify(const float* in, float* out, uint32_t C, uint32_t H, uint32_t W, uint32_t ps);
 void orc_unpatchify(const float* in, float* out, uint32_t C, uint32_t H, uint32_t W, uint32_t ps);
 
+/* LoRA: the two-hop correction (hop 1 down-projection, hop 2 scaled
+ * accumulate) and the load-time Q8_0 merge with requantization. */
+void orc_lora_down(const float* A, const float* X, float* scratch, uint32_t rank, uint32_t in_dim,
+                   uint32_t seq_len);
+void orc_lora_up(const float* B, const float* scratch, float* out, uint32_t rank, uint32_t out_dim,
+                 uint32_t seq_len, float scale, uint32_t row_offset, uint32_t weight_row_offset, uint32_t b_rows);
+void orc_q8_lora_merge(uint8_t* base, const float* A, const float* B, uint32_t in_dim, uint32_t b_rows,
+                       uint32_t dst_row_offset, uint32_t rank, float scale);
+
 /* Number of OpenMP threads the oracle uses. */
 int orc_num_threads(void);
 

@@ -58,6 +58,9 @@ def lib():
             "orc_flash_attention": (None, [_f32p, _f32p, _f32p, _f32p, _u32, _u32, _u32, ctypes.c_float,
                                            _u32, _u32, _u32, _u32]),
             "orc_rope_tables": (None, [_u32p, _u32, _u32p, _u32, ctypes.c_float, _f32p, _f32p]),
+            "orc_lora_down": (None, [_f32p, _f32p, _f32p, _u32, _u32, _u32]),
+            "orc_lora_up": (None, [_f32p, _f32p, _f32p, _u32, _u32, _u32, ctypes.c_float, _u32, _u32, _u32]),
+            "orc_q8_lora_merge": (None, [_u8p, _f32p, _f32p, _u32, _u32, _u32, _u32, ctypes.c_float]),
             "orc_rope_apply": (None, [_f32p, _u32, _u32, _f32p, _f32p]),
             "orc_num_threads": (ctypes.c_int, []),
             "orc_batch_rmsnorm": (None, [_f32p, _f32p, _f32p, _u32, _u32, ctypes.c_float]),
@@ -333,4 +336,38 @@ def unpatchify(patches: np.ndarray, C: int, H: int, W: int, ps: int) -> np.ndarr
     x = _f32c(patches)
     out = np.empty((C, H, W), np.float32)
     lib().orc_unpatchify(_p(x, _f32p), _p(out, _f32p), C, H, W, ps)
+    return out
+
+
+def lora_down(A: np.ndarray, X: np.ndarray) -> np.ndarray:
+    """LoRA hop 1: scratch [seq, rank] = X [seq, in_dim] . A [rank, in_dim]^T."""
+    A = _f32c(A)
+    X = _f32c(X)
+    rank, in_dim = A.shape
+    out = np.empty((X.shape[0], rank), np.float32)
+    lib().orc_lora_down(_p(A, _f32p), _p(X, _f32p), _p(out, _f32p), rank, in_dim, X.shape[0])
+    return out
+
+
+def lora_up(B: np.ndarray, scratch: np.ndarray, out: np.ndarray, scale: float, row_offset: int = 0,
+            weight_row_offset: int = 0, b_rows: int | None = None) -> np.ndarray:
+    """LoRA hop 2 on a copy of `out` [seq, out_dim]; returns the updated copy."""
+    B = _f32c(B)
+    s = _f32c(scratch)
+    y = np.array(out, dtype=np.float32, copy=True, order="C")
+    rank = s.shape[1]
+    b_rows = B.shape[0] - weight_row_offset if b_rows is None else b_rows
+    lib().orc_lora_up(_p(B, _f32p), _p(s, _f32p), _p(y, _f32p), rank, y.shape[1], y.shape[0], float(scale),
+                      row_offset, weight_row_offset, b_rows)
+    return y
+
+
+def q8_lora_merge(base: np.ndarray, A: np.ndarray, B: np.ndarray, in_dim: int, scale: float,
+                  dst_row_offset: int = 0) -> np.ndarray:
+    """Merged copy of Q8_0 blocks `base` (uint8, rows of in_dim/32 blocks)."""
+    out = np.array(base, dtype=np.uint8, copy=True, order="C").reshape(-1)
+    A = _f32c(A)
+    B = _f32c(B)
+    lib().orc_q8_lora_merge(_p(out, _u8p), _p(A, _f32p), _p(B, _f32p), in_dim, B.shape[0], dst_row_offset,
+                            A.shape[0], float(scale))
     return out
