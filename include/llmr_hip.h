@@ -240,6 +240,63 @@ LLMR_API int llmr_batch_matmul_swiglu_pc(llmr_context* ctx, const void* weight_g
                                          uint32_t weight_type, const void* input, uint32_t input_type,
                                          float* output, const llmr_batch_matmul_params* pc);
 
+/* ---- GGUF checkpoints (host side) -------------------------------------------- */
+
+/* An open GGUF file: gguf_parse (lib/gguf/parser.c3:164-208) over a
+ * read-only memory map. Versions 2 and 3; tensor data aligned to 32 bytes
+ * after the tensor infos (the reference's hard-coded alignment,
+ * lib/gguf/types.c3:8). Every read is bounds-checked: a truncated or corrupt
+ * file gives LLMR_ERR_INVALID_ARG. Strings and data pointers returned below
+ * point into the handle and stay valid until llmr_gguf_close. */
+typedef struct llmr_gguf llmr_gguf;
+
+/* GGUFTensorInfo (parser.c3:135-160): ne[] fastest-varying first (a row-major
+ * [out, in] weight has ne = {in, out}), unused dims 1; offset relative to the
+ * data section; data_size = ceil(elements / block_size) * type_size
+ * (GGMLType tables, types.c3:50-98; 0 for an unknown type); data = the
+ * tensor's bytes in the mapping. */
+typedef struct llmr_gguf_tensor_info {
+    const char* name;
+    uint32_t type;
+    uint32_t n_dims;
+    uint64_t ne[4];
+    uint64_t offset;
+    uint64_t data_size;
+    const void* data;
+} llmr_gguf_tensor_info;
+
+/* GGUFMetaKV (parser.c3:94-133): type is the GGUFType (0 UINT8 ... 7 BOOL,
+ * 8 STRING, 9 ARRAY, 10 UINT64, 11 INT64, 12 FLOAT64); data points at the
+ * value (a scalar's bytes; a string's bytes, data_len long, not
+ * NUL-terminated; an array's elements, array_len of array_type, strings
+ * each prefixed by their u64 length). */
+typedef struct llmr_gguf_kv_info {
+    const char* key;
+    uint32_t type;
+    uint32_t array_type;
+    uint64_t array_len;
+    const void* data;
+    uint64_t data_len;
+} llmr_gguf_kv_info;
+
+LLMR_API int llmr_gguf_open(const char* path, llmr_gguf** out);
+LLMR_API int llmr_gguf_close(llmr_gguf* gguf);
+LLMR_API int llmr_gguf_info(const llmr_gguf* gguf, uint32_t* version, uint64_t* n_tensors, uint64_t* n_kv);
+LLMR_API int llmr_gguf_tensor(const llmr_gguf* gguf, uint64_t index, llmr_gguf_tensor_info* out);
+/* GGUFFile.find_tensor (parser-side lookup used by load_dit_tensor, flux_dit.c3:191-207) */
+LLMR_API int llmr_gguf_find_tensor(const llmr_gguf* gguf, const char* name, uint64_t* index);
+LLMR_API int llmr_gguf_kv(const llmr_gguf* gguf, uint64_t index, llmr_gguf_kv_info* out);
+LLMR_API int llmr_gguf_find_kv(const llmr_gguf* gguf, const char* key, uint64_t* index);
+
+/* upload_weight (lib/model/tensor.c3:48-66): the tensor's bytes, unchanged
+ * (quantized blocks in their GGUF layout), into a device buffer of at least
+ * data_size bytes; complete on return. llmr_gguf_load_tensor allocates that
+ * buffer (llmr_alloc; release it with llmr_free) as upload_weight does.
+ * LLMR_ERR_UNSUPPORTED for a type of unknown size. */
+LLMR_API int llmr_gguf_upload_tensor(llmr_context* ctx, const llmr_gguf* gguf, uint64_t index, void* dst_dev,
+                                     size_t dst_bytes);
+LLMR_API int llmr_gguf_load_tensor(llmr_context* ctx, const llmr_gguf* gguf, uint64_t index, void** out_dev_ptr);
+
 /* ---- LoRA ------------------------------------------------------------------ */
 
 /* A LoRA adapter of one linear (LoraTensor, lib/model/lora.c3:22-28): a

@@ -70,6 +70,12 @@ int check_weight(const void* w, uint32_t wtype, uint32_t in_dim) {
 
 }  // namespace
 
+namespace llmr {
+// The error record for the host-only sources (gguf_file.cpp): sets
+// llmr_last_error's message ("" on success) and returns code.
+int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace llmr
+
 extern "C" {
 
 const char* llmr_last_error(void) { return g_err; }

@@ -57,6 +57,19 @@ class MatmulEpilogue(ctypes.Structure):
 EPI_STORE, EPI_GATED_RESIDUAL, EPI_SPLIT_GELU = 0, 1, 2
 
 
+class GgufTensorInfo(ctypes.Structure):
+    """llmr_gguf_tensor_info."""
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_uint32), ("n_dims", ctypes.c_uint32),
+                ("ne", ctypes.c_uint64 * 4), ("offset", ctypes.c_uint64), ("data_size", ctypes.c_uint64),
+                ("data", ctypes.c_void_p)]
+
+
+class GgufKvInfo(ctypes.Structure):
+    """llmr_gguf_kv_info."""
+    _fields_ = [("key", ctypes.c_char_p), ("type", ctypes.c_uint32), ("array_type", ctypes.c_uint32),
+                ("array_len", ctypes.c_uint64), ("data", ctypes.c_void_p), ("data_len", ctypes.c_uint64)]
+
+
 class Lora(ctypes.Structure):
     """llmr_lora: a [rank, in_dim] and b [rows, rank] f32 device pointers, rank, scale."""
     _fields_ = [("a", ctypes.c_void_p), ("b", ctypes.c_void_p), ("rank", ctypes.c_uint32),
@@ -108,6 +121,16 @@ _SIGS = {
     "llmr_batch_matmul_lora": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _vp, _vp,
                                               _u32, _u32, _u32]),
     "llmr_q8_lora_merge": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, ctypes.c_float]),
+    "llmr_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "llmr_gguf_close": (ctypes.c_int, [_vp]),
+    "llmr_gguf_info": (ctypes.c_int, [_vp, ctypes.POINTER(_u32), ctypes.POINTER(ctypes.c_uint64),
+                                      ctypes.POINTER(ctypes.c_uint64)]),
+    "llmr_gguf_tensor": (ctypes.c_int, [_vp, ctypes.c_uint64, _vp]),
+    "llmr_gguf_find_tensor": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "llmr_gguf_kv": (ctypes.c_int, [_vp, ctypes.c_uint64, _vp]),
+    "llmr_gguf_find_kv": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "llmr_gguf_upload_tensor": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, _vp, ctypes.c_size_t]),
+    "llmr_gguf_load_tensor": (ctypes.c_int, [_vp, _vp, ctypes.c_uint64, ctypes.POINTER(_vp)]),
 }
 
 # Activation and gate selectors of llmr_activation / llmr_gated_residual.

@@ -264,6 +264,97 @@ def flux_weights(cfg: FluxConfig, device="cuda", seed: int = workloads.SEED, g: 
     return glob, doubles, singles
 
 
+# Checkpoint tensor names (the BFL Flux names the reference loads,
+# flux_dit.c3:680-735; modulation per block as in Flux.1-dev).
+_FLUX_GLOBAL = {"img_in": "img_in.weight", "txt_in": "txt_in.weight", "time_in0": "time_in.in_layer.weight",
+                "time_in1": "time_in.out_layer.weight", "final_mod": "final_layer.adaLN_modulation.1.weight",
+                "final_linear": "final_layer.linear.weight"}
+_FLUX_DOUBLE = {"img_mod": "img_mod.lin.weight", "txt_mod": "txt_mod.lin.weight",
+                "img_qkv": "img_attn.qkv.weight", "txt_qkv": "txt_attn.qkv.weight",
+                "img_proj": "img_attn.proj.weight", "txt_proj": "txt_attn.proj.weight",
+                "img_mlp0": "img_mlp.0.weight", "txt_mlp0": "txt_mlp.0.weight",
+                "img_mlp2": "img_mlp.2.weight", "txt_mlp2": "txt_mlp.2.weight",
+                "img_q_norm": "img_attn.norm.query_norm.scale", "img_k_norm": "img_attn.norm.key_norm.scale",
+                "txt_q_norm": "txt_attn.norm.query_norm.scale", "txt_k_norm": "txt_attn.norm.key_norm.scale"}
+_FLUX_SINGLE = {"mod": "modulation.lin.weight", "linear1": "linear1.weight", "linear2": "linear2.weight",
+                "q_norm": "norm.query_norm.scale", "k_norm": "norm.key_norm.scale"}
+
+
+def _flux_shapes(cfg: FluxConfig):
+    d, m = cfg.dim, cfg.mlp
+    glob = {"img_in": (d, cfg.patch_dim), "txt_in": (d, cfg.text_dim), "time_in0": (d, cfg.t_emb_dim),
+            "time_in1": (d, d), "final_mod": (2 * d, d), "final_linear": (cfg.patch_dim, d)}
+    dbl = {"img_mod": (6 * d, d), "txt_mod": (6 * d, d), "img_qkv": (3 * d, d), "txt_qkv": (3 * d, d),
+           "img_proj": (d, d), "txt_proj": (d, d), "img_mlp0": (m, d), "txt_mlp0": (m, d),
+           "img_mlp2": (d, m), "txt_mlp2": (d, m)}
+    sgl = {"mod": (3 * d, d), "linear1": (3 * d + m, d), "linear2": (d, d + m)}
+    return glob, dbl, sgl
+
+
+def save_flux_gguf(path: str, cfg: FluxConfig, glob: FluxGlobalWeights, doubles, singles) -> int:
+    """Writes Flux weights (device tensors) as a GGUF checkpoint with the
+    BFL tensor names: matrices in their quantized blocks (img_in Q8_0, the
+    rest Q4_K), norm scales F32. Returns the file size."""
+    from . import gguf_file
+    gs, ds, ss = _flux_shapes(cfg)
+    ents = []
+
+    def add(name, t, shape, gtype):
+        data = t.detach().cpu().numpy()
+        ents.append(gguf_file.TensorEntry(name, gtype, shape, data.tobytes()))
+
+    for k, name in _FLUX_GLOBAL.items():
+        add(name, getattr(glob, k), gs[k], GGML_Q8_0 if k == "img_in" else GGML_Q4_K)
+    for i, w in enumerate(doubles):
+        for k, name in _FLUX_DOUBLE.items():
+            t = getattr(w, k)
+            if k in ds:
+                add(f"double_blocks.{i}.{name}", t, ds[k], GGML_Q4_K)
+            else:
+                add(f"double_blocks.{i}.{name}", t.float(), (HEAD_DIM,), 0)
+    for i, w in enumerate(singles):
+        for k, name in _FLUX_SINGLE.items():
+            t = getattr(w, k)
+            if k in ss:
+                add(f"single_blocks.{i}.{name}", t, ss[k], GGML_Q4_K)
+            else:
+                add(f"single_blocks.{i}.{name}", t.float(), (HEAD_DIM,), 0)
+    meta = {"general.architecture": "flux", "flux.dim": cfg.dim, "flux.heads": cfg.n_heads, "flux.mlp": cfg.mlp,
+            "flux.double_blocks": cfg.n_double, "flux.single_blocks": cfg.n_single}
+    return gguf_file.write_gguf(path, ents, meta)
+
+
+def flux_weights_from_gguf(path: str, cfg: FluxConfig, device="cuda"):
+    """Flux weights loaded from a GGUF checkpoint (load_flux_dit,
+    flux_dit.c3:664-744): every matrix uploaded unchanged through the native
+    parser (upload_weight), norm scales widened to f32. Shapes and types are
+    checked against cfg (the GEMMs take Q4_K and Q8_0)."""
+    from . import gguf_file
+    gs, ds, ss = _flux_shapes(cfg)
+    with gguf_file.GGUFFile(path) as f:
+        def mat(name, shape):
+            t = f.by_name.get(name)
+            if t is None:
+                raise KeyError(f"{path}: no tensor {name}")
+            if t.shape != tuple(shape) or t.ggml_type not in (GGML_Q8_0, GGML_Q4_K):
+                raise ValueError(f"{name}: {t.shape} of type {t.ggml_type}, expected {shape} in Q8_0/Q4_K")
+            return f.upload(name, device)
+
+        def norm(name):
+            if name not in f.by_name:
+                raise KeyError(f"{path}: no tensor {name}")
+            return f.upload_f32(name, device).reshape(-1)
+
+        glob = FluxGlobalWeights(**{k: mat(n, gs[k]) for k, n in _FLUX_GLOBAL.items()})
+        doubles = [FluxDoubleWeights(**{k: (mat(f"double_blocks.{i}.{n}", ds[k]) if k in ds
+                                            else norm(f"double_blocks.{i}.{n}"))
+                                        for k, n in _FLUX_DOUBLE.items()}) for i in range(cfg.n_double)]
+        singles = [FluxSingleWeights(**{k: (mat(f"single_blocks.{i}.{n}", ss[k]) if k in ss
+                                            else norm(f"single_blocks.{i}.{n}"))
+                                        for k, n in _FLUX_SINGLE.items()}) for i in range(cfg.n_single)]
+    return glob, doubles, singles
+
+
 def flux_rope(cfg: FluxConfig, device="cuda"):
     """cos/sin [seq, 64] for text ids (0,0,0) then image ids (0, row, col)
     (precompute_flux_mrope, flux_dit.c3:396-529), computed on the host."""
