@@ -7,7 +7,9 @@
 // A wave covers 16 weight rows: lane t (of 16) walks superblocks t, t+16,
 // ..., and each lane serves 4 of the rows with one register copy of the
 // activations it needs (a 64-element slice per token at a time); the 16
-// partial sums of a row are reduced with lane shuffles. Arithmetic is the
+// partial sums of a row are reduced with lane shuffles. When the
+// activations fit in 48 KiB of LDS the variant below is used (activations
+// staged in LDS, 64-element units spread over all 16 lanes). Arithmetic is the
 // reference's f32 path (batch_matmul_q4k, llm.slang:2264-2365): weight
 // (d*sc)*q - dmin*mn with one rounding (the FMA below; both products are
 // exact), activations in f32, f32 accumulation (in a different order).
@@ -135,9 +137,133 @@ __global__ void __launch_bounds__(256) gemv_q4k_kernel(const uint8_t* __restrict
     }
 }
 
+// The same products with the activations staged in LDS (f32, once per
+// workgroup) and the work of a row split into 64-element units (quarter s
+// of superblock sb: its header and 32 quant bytes): lane t of 16 takes units
+// t, t+16, ..., so all lanes work whatever K / 256 is, and the next unit's
+// weight loads (header and quants of the lane's 4 rows) are issued before
+// the current unit is multiplied, keeping two units of loads in flight.
+constexpr uint32_t kGemvLdsBytes = 48u * 1024u;
+
+// 4 rows per lane (64 per workgroup): measured against 2 and 1, 4 is as fast
+// or faster at every Flux / Z-Image modulation shape.
+constexpr int kGemvRowsPerLane = 4;
+struct UnitW {
+    u32x4 hdr[4], qa[4], qb[4];  // the rows' header and 32 quant bytes of one unit
+};
+
+template <uint32_t XT, int MM, int RPL = kGemvRowsPerLane>
+__global__ void __launch_bounds__(256) gemv_q4k_lds_kernel(const uint8_t* __restrict__ W, const void* __restrict__ X,
+                                                            float* __restrict__ Y, uint32_t N, uint32_t K, uint32_t M,
+                                                            uint32_t row_offset) {
+    extern __shared__ f32x4 xs[];  // [M][K / 4]
+    const uint32_t K4 = K / 4u;
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+        if (m < (int)M)
+            for (uint32_t i = threadIdx.x; i < K4; i += 256u) xs[m * K4 + i] = load_x4<XT>(X, (uint64_t)m * K + 4u * i);
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t t = lane & 15u, r = lane >> 4;
+    const uint32_t n0 = blockIdx.x * (16u * RPL) + wave * (4u * RPL) + r;  // rows n0 + 4i, i < RPL
+    const uint32_t U = (K / 256u) * 4u;
+    const uint64_t rb = (uint64_t)(K / 256u) * 144u;
+    // rows past N read row N - 1 (in bounds, branch-free) and are not stored
+    auto load_unit = [&](uint32_t u) __attribute__((always_inline)) {
+        const uint32_t sb = u >> 2, j = u & 3u;
+        UnitW w;
+#pragma unroll
+        for (int i = 0; i < RPL; ++i) {
+            const uint32_t n = min(n0 + 4u * i, N - 1u);
+            const uint8_t* b = W + (uint64_t)(row_offset + n) * rb + (uint64_t)sb * 144u;
+            w.hdr[i] = *(const u32x4_a4*)b;
+            w.qa[i] = *(const u32x4_a4*)(b + 16u + 32u * j);
+            w.qb[i] = *(const u32x4_a4*)(b + 32u + 32u * j);
+        }
+        return w;
+    };
+    float acc[4][MM];
+#pragma unroll
+    for (int i = 0; i < RPL; i++)
+#pragma unroll
+        for (int m = 0; m < MM; m++) acc[i][m] = 0.0f;
+    // (U >= 4 > t is not guaranteed for K = 256: lanes t >= U have no unit)
+    UnitW cur = load_unit(min(t, U - 1u));
+    for (uint32_t u = t; u < U; u += 16u) {
+        const UnitW nxt = load_unit(min(u + 16u, U - 1u));
+        const uint32_t sb = u >> 2, j = u & 3u;
+#pragma unroll
+        for (int m = 0; m < MM; ++m) {
+            if (m >= (int)M) continue;
+            // activations of elements 64j .. 64j+63 of superblock sb
+            const f32x4* xr = xs + m * K4 + sb * 64u + 16u * j;
+            f32x4 xl[8], xh[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                xl[c] = xr[c];
+                xh[c] = xr[c + 8];
+            }
+#pragma unroll
+            for (int i = 0; i < RPL; ++i) {
+                const float d = f16_bits_to_f32(cur.hdr[i].x & 0xffffu), dmin = f16_bits_to_f32(cur.hdr[i].x >> 16);
+                uint32_t sc0, mn0, sc1, mn1;
+                q4k_scale_min(2u * j, cur.hdr[i].y, cur.hdr[i].z, cur.hdr[i].w, sc0, mn0);
+                q4k_scale_min(2u * j + 1u, cur.hdr[i].y, cur.hdr[i].z, cur.hdr[i].w, sc1, mn1);
+                const float d0 = d * (float)sc0, m0 = dmin * (float)mn0;
+                const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const uint32_t word = c < 4 ? cur.qa[i][c] : cur.qb[i][c - 4];
+                    f32x4 wl, wh;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const uint32_t q = (word >> (8 * k)) & 0xffu;
+                        wl[k] = __builtin_fmaf((float)(q & 15u), d0, -m0);
+                        wh[k] = __builtin_fmaf((float)(q >> 4), d1, -m1);
+                    }
+                    const f32x4 a = xl[c], h = xh[c];
+                    acc[i][m] += (wl.x * a.x + wl.y * a.y) + (wl.z * a.z + wl.w * a.w) +
+                                 ((wh.x * h.x + wh.y * h.y) + (wh.z * h.z + wh.w * h.w));
+                }
+            }
+        }
+        cur = nxt;
+    }
+#pragma unroll
+    for (int i = 0; i < RPL; i++)
+#pragma unroll
+        for (int m = 0; m < MM; m++) {
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) acc[i][m] += __shfl_xor(acc[i][m], o, 64);
+        }
+    if (t == 0) {
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            const uint32_t n = n0 + 4u * i;
+            if (n < N) {
+#pragma unroll
+                for (int m = 0; m < MM; m++)
+                    if (m < (int)M) Y[(uint64_t)m * N + n] = acc[i][m];
+            }
+        }
+    }
+}
+
 template <uint32_t XT>
 hipError_t launch_t(const void* w, const void* x, float* y, uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset,
                     hipStream_t st) {
+    const dim3 grid_l((N + 16u * kGemvRowsPerLane - 1u) / (16u * kGemvRowsPerLane)), block_l(256);
+    const uint8_t* Wl = (const uint8_t*)w;
+    const uint32_t lds = M * K * 4u;
+    if (lds <= kGemvLdsBytes) {
+        if (M <= 1)
+            hipLaunchKernelGGL((gemv_q4k_lds_kernel<XT, 1>), grid_l, block_l, lds, st, Wl, x, y, N, K, M, row_offset);
+        else if (M <= 2)
+            hipLaunchKernelGGL((gemv_q4k_lds_kernel<XT, 2>), grid_l, block_l, lds, st, Wl, x, y, N, K, M, row_offset);
+        else
+            hipLaunchKernelGGL((gemv_q4k_lds_kernel<XT, 4>), grid_l, block_l, lds, st, Wl, x, y, N, K, M, row_offset);
+        return hipGetLastError();
+    }
     const dim3 grid((N + 63u) / 64u), block(256);
     const uint8_t* W = (const uint8_t*)w;
     if (M <= 1) hipLaunchKernelGGL((gemv_q4k_kernel<XT, 1>), grid, block, 0, st, W, x, y, N, K, M, row_offset);
