@@ -195,6 +195,7 @@ int llmr_gguf_open(const char* path, llmr_gguf** out) {
         if (k.type == 9) {
             k.array_type = r.get<uint32_t>();
             k.array_len = r.get<uint64_t>();
+            if (!r.ok) break;
             k.data_off = r.pos;
             // re-read the array body by skipping it as a whole value
             r.pos -= 12;
@@ -228,7 +229,10 @@ int llmr_gguf_open(const char* path, llmr_gguf** out) {
         t.offset = r.get<uint64_t>();
         uint64_t bs, ts;
         ggml_block(t.type, bs, ts);
-        t.data_size = (n + bs - 1) / bs * ts;  // parser.c3:149-158
+        // ceil(n / bs) * ts (parser.c3:149-158), without wrapping
+        const uint64_t blocks = n / bs + (n % bs != 0);
+        if (ts && blocks > UINT64_MAX / ts) return bad("tensor byte size overflows");
+        t.data_size = blocks * ts;
         f->tensors.push_back(std::move(t));
     }
     if (!r.ok) return bad("truncated tensor infos");

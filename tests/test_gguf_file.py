@@ -119,6 +119,14 @@ def test_corruptions_are_errors(lib, tmp_path):
     # the tensor info: name "w" then n_dims
     kv_end = 24 + 8 + 1 + 4 + 4
     bad(lambda b: b.__setitem__(slice(kv_end + 9, kv_end + 13), struct.pack("<I", 5)))  # 5 dims
+    # 2^64 - 5 elements of Q4_K: ceil(n / 256) * 144 must not wrap to a size
+    # that fits the file
+    ne_pos = kv_end + 8 + 1 + 4
+
+    def huge_q4k(b):
+        b[ne_pos:ne_pos + 8] = struct.pack("<Q", 2 ** 64 - 5)
+        b[ne_pos + 8:ne_pos + 12] = struct.pack("<I", gguf.GGML_Q4_K)
+    bad(huge_q4k)
     # tensor offset past the file
     off_pos = kv_end + 8 + 1 + 4 + 8 + 4
     bad(lambda b: b.__setitem__(slice(off_pos, off_pos + 8), struct.pack("<Q", 1 << 20)))
