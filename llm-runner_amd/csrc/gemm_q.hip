@@ -1727,6 +1727,12 @@ size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32
 hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs,
                                      uint32_t n_jobs, const GemmEpilogue& epi, int num_cus, void* ws,
                                      hipStream_t st) {
+    // a group of Q4_K projections of a few tokens (the per-block
+    // modulation vectors) as one GEMV launch
+    if (wtype == kGgmlQ4K && epi.kind == kEpiStore && n_jobs > 1) {
+        const hipError_t e = launch_gemv_q4k_multi(xtype, jobs, n_jobs, N, K, epi.ldy, st);
+        if (e != hipErrorNotSupported) return e;
+    }
     for (uint32_t i = 0; i < n_jobs; i += 2) {
         const uint32_t n = min(2u, n_jobs - i);
         hipError_t e = hipSuccess;

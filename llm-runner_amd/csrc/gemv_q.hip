@@ -152,10 +152,27 @@ struct UnitW {
     u32x4 hdr[4], qa[4], qb[4];  // the rows' header and 32 quant bytes of one unit
 };
 
-template <uint32_t XT, int MM, int RPL = kGemvRowsPerLane>
-__global__ void __launch_bounds__(256) gemv_q4k_lds_kernel(const uint8_t* __restrict__ W, const void* __restrict__ X,
-                                                            float* __restrict__ Y, uint32_t N, uint32_t K, uint32_t M,
-                                                            uint32_t row_offset) {
+// Up to CAP projections of one shape [N, K] (each its own weight, input
+// and output rows, ldy apart): workgroup b serves rows 64 (b % bpj) .. of
+// job b / bpj. CAP = 1 for one projection, kGemvMaxJobs for a group.
+constexpr uint32_t kGemvMaxJobs = 64;
+template <uint32_t CAP>
+struct GemvJobs {
+    const uint8_t* w[CAP];
+    const void* x[CAP];
+    float* y[CAP];
+    uint32_t m[CAP], row_offset[CAP];
+};
+
+template <uint32_t XT, int MM, uint32_t CAP, int RPL = kGemvRowsPerLane>
+__global__ void __launch_bounds__(256) gemv_q4k_lds_kernel(const GemvJobs<CAP> jobs, uint32_t N, uint32_t K,
+                                                            uint32_t ldy, uint32_t bpj) {
+    const uint32_t job = CAP == 1u ? 0u : blockIdx.x / bpj;
+    const uint32_t blk = CAP == 1u ? blockIdx.x : blockIdx.x - job * bpj;
+    const uint8_t* __restrict__ W = jobs.w[job];
+    const void* __restrict__ X = jobs.x[job];
+    float* __restrict__ Y = jobs.y[job];
+    const uint32_t M = jobs.m[job], row_offset = jobs.row_offset[job];
     extern __shared__ f32x4 xs[];  // [M][K / 4]
     const uint32_t K4 = K / 4u;
 #pragma unroll
@@ -165,7 +182,7 @@ __global__ void __launch_bounds__(256) gemv_q4k_lds_kernel(const uint8_t* __rest
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t t = lane & 15u, r = lane >> 4;
-    const uint32_t n0 = blockIdx.x * (16u * RPL) + wave * (4u * RPL) + r;  // rows n0 + 4i, i < RPL
+    const uint32_t n0 = blk * (16u * RPL) + wave * (4u * RPL) + r;  // rows n0 + 4i, i < RPL
     const uint32_t U = (K / 256u) * 4u;
     const uint64_t rb = (uint64_t)(K / 256u) * 144u;
     // rows past N read row N - 1 (in bounds, branch-free) and are not stored
@@ -243,25 +260,32 @@ __global__ void __launch_bounds__(256) gemv_q4k_lds_kernel(const uint8_t* __rest
             if (n < N) {
 #pragma unroll
                 for (int m = 0; m < MM; m++)
-                    if (m < (int)M) Y[(uint64_t)m * N + n] = acc[i][m];
+                    if (m < (int)M) Y[(uint64_t)m * ldy + n] = acc[i][m];
             }
         }
     }
 }
 
+template <uint32_t XT, uint32_t CAP>
+void launch_lds(const GemvJobs<CAP>& jobs, uint32_t n_jobs, uint32_t N, uint32_t K, uint32_t ldy, uint32_t max_m,
+                hipStream_t st) {
+    const uint32_t bpj = (N + 16u * kGemvRowsPerLane - 1u) / (16u * kGemvRowsPerLane);
+    const dim3 grid(bpj * n_jobs), block(256);
+    const uint32_t lds = max_m * K * 4u;
+    if (max_m <= 1)
+        hipLaunchKernelGGL((gemv_q4k_lds_kernel<XT, 1, CAP>), grid, block, lds, st, jobs, N, K, ldy, bpj);
+    else if (max_m <= 2)
+        hipLaunchKernelGGL((gemv_q4k_lds_kernel<XT, 2, CAP>), grid, block, lds, st, jobs, N, K, ldy, bpj);
+    else
+        hipLaunchKernelGGL((gemv_q4k_lds_kernel<XT, 4, CAP>), grid, block, lds, st, jobs, N, K, ldy, bpj);
+}
+
 template <uint32_t XT>
 hipError_t launch_t(const void* w, const void* x, float* y, uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset,
                     hipStream_t st) {
-    const dim3 grid_l((N + 16u * kGemvRowsPerLane - 1u) / (16u * kGemvRowsPerLane)), block_l(256);
-    const uint8_t* Wl = (const uint8_t*)w;
-    const uint32_t lds = M * K * 4u;
-    if (lds <= kGemvLdsBytes) {
-        if (M <= 1)
-            hipLaunchKernelGGL((gemv_q4k_lds_kernel<XT, 1>), grid_l, block_l, lds, st, Wl, x, y, N, K, M, row_offset);
-        else if (M <= 2)
-            hipLaunchKernelGGL((gemv_q4k_lds_kernel<XT, 2>), grid_l, block_l, lds, st, Wl, x, y, N, K, M, row_offset);
-        else
-            hipLaunchKernelGGL((gemv_q4k_lds_kernel<XT, 4>), grid_l, block_l, lds, st, Wl, x, y, N, K, M, row_offset);
+    if ((uint64_t)M * K * 4u <= kGemvLdsBytes) {
+        const GemvJobs<1> one{{(const uint8_t*)w}, {x}, {y}, {M}, {row_offset}};
+        launch_lds<XT>(one, 1u, N, K, N, M, st);
         return hipGetLastError();
     }
     const dim3 grid((N + 63u) / 64u), block(256);
@@ -273,6 +297,30 @@ hipError_t launch_t(const void* w, const void* x, float* y, uint32_t N, uint32_t
 }
 
 }  // namespace
+
+hipError_t launch_gemv_q4k_multi(uint32_t xtype, const GemmJob* jobs, uint32_t n_jobs, uint32_t N, uint32_t K,
+                                 uint32_t ldy, hipStream_t st) {
+    if (n_jobs == 0 || N == 0) return hipSuccess;
+    if (n_jobs > kGemvMaxJobs) return hipErrorNotSupported;
+    GemvJobs<kGemvMaxJobs> t{};
+    uint32_t max_m = 0;
+    for (uint32_t q = 0; q < n_jobs; q++) {
+        if (jobs[q].M > kGemvMaxTokens || (uint64_t)jobs[q].M * K * 4u > kGemvLdsBytes) return hipErrorNotSupported;
+        t.w[q] = (const uint8_t*)jobs[q].w;
+        t.x[q] = jobs[q].x;
+        t.y[q] = jobs[q].y;
+        t.m[q] = jobs[q].M;
+        t.row_offset[q] = jobs[q].row_offset;
+        max_m = max(max_m, jobs[q].M);
+    }
+    if (max_m == 0) return hipSuccess;
+    switch (xtype) {
+        case kGgmlF32: launch_lds<kGgmlF32>(t, n_jobs, N, K, ldy, max_m, st); break;
+        case kGgmlF16: launch_lds<kGgmlF16>(t, n_jobs, N, K, ldy, max_m, st); break;
+        default: launch_lds<kGgmlBF16>(t, n_jobs, N, K, ldy, max_m, st); break;
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_gemv_q4k(const void* w, uint32_t xtype, const void* x, float* y, uint32_t N, uint32_t K,
                            uint32_t M, uint32_t row_offset, hipStream_t st) {

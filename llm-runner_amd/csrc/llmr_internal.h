@@ -38,6 +38,11 @@ struct GemmEpilogue {
 size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K,
                                           const GemmJob* jobs, uint32_t n_jobs, const GemmEpilogue& epi,
                                           int num_cus);
+// Q4_K projections of at most kGemvMaxTokens tokens, one launch for up to
+// 64 jobs of one shape [N, K] with plain stores (rows ldy apart);
+// hipErrorNotSupported when a job does not fit the LDS-staged kernel.
+hipError_t launch_gemv_q4k_multi(uint32_t xtype, const GemmJob* jobs, uint32_t n_jobs, uint32_t N, uint32_t K,
+                                 uint32_t ldy, hipStream_t st);
 hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs,
                                      uint32_t n_jobs, const GemmEpilogue& epi, int num_cus, void* ws,
                                      hipStream_t st);

@@ -422,15 +422,22 @@ class FluxDiT:
         glue.activation(self.vec0, self.vec0, capi.ACT_SILU, g=g)
         self._mm(self.glob.time_in1, GGML_Q4_K, d, d, self.vec0, self.vec)
         glue.activation(self.vec, self.vec, capi.ACT_SILU, g=g)
-        # 5: modulation vectors of every block from silu(vec) (flux_dit.c3:1131-1140)
-        mi = 0
-        for w in self.doubles:
-            self._mm(w.img_mod, GGML_Q4_K, 6 * d, d, self.vec, self.mods[:, mi * d:(mi + 6) * d])
-            self._mm(w.txt_mod, GGML_Q4_K, 6 * d, d, self.vec, self.mods[:, (mi + 6) * d:(mi + 12) * d])
-            mi += 12
+        # 5: modulation vectors of every block from silu(vec) (flux_dit.c3:1131-1140),
+        # each group of same-shape projections as one launch (at most 64 jobs)
+        vec = _t(self.vec)
+        dbl = []
+        for i, w in enumerate(self.doubles):
+            mi = 12 * i
+            dbl.append(MatmulJob(_qt(w.img_mod, GGML_Q4_K, 6 * d, d), vec, self.mods[:, mi * d:(mi + 6) * d], 1))
+            dbl.append(MatmulJob(_qt(w.txt_mod, GGML_Q4_K, 6 * d, d), vec, self.mods[:, (mi + 6) * d:(mi + 12) * d], 1))
+        mi = 12 * len(self.doubles)
+        sgl = []
         for w in self.singles:
-            self._mm(w.mod, GGML_Q4_K, 3 * d, d, self.vec, self.mods[:, mi * d:(mi + 3) * d])
+            sgl.append(MatmulJob(_qt(w.mod, GGML_Q4_K, 3 * d, d), vec, self.mods[:, mi * d:(mi + 3) * d], 1))
             mi += 3
+        for jobs, n in ((dbl, 6 * d), (sgl, 3 * d)):
+            for k in range(0, len(jobs), 64):
+                dispatch_batch_matmul_multi(g, jobs[k:k + 64], n, d)
         self._mm(self.glob.final_mod, GGML_Q4_K, 2 * d, d, self.vec, self.mods[:, mi * d:(mi + 2) * d])
         # 6-8: blocks (flux_dit.c3:1146-1162)
         mi = 0

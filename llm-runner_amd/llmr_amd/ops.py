@@ -206,7 +206,9 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
     """The jobs' GEMMs with a shared epilogue (llmr_batch_matmul_multi): a plain
     store, `output += gate * result` (gated_residual_linear), or a column split
     whose features >= split are GELU'd into output2 (linear1's MLP half feeding
-    linear2, flux_dit.c3:1049-1058). Pairs of jobs run as one launch."""
+    linear2, flux_dit.c3:1049-1058). Pairs of jobs run as one launch; a
+    group of Q4_K jobs of at most 4 tokens with a plain store (the per-block
+    modulation projections) runs as one GEMV launch."""
     if not jobs:
         return
     wtype, xtype = jobs[0].weight.dtype, jobs[0].input.dtype

@@ -407,6 +407,36 @@ def test_multi_grouped_store_and_residual(orc, dev, wtype, xtype):
         assert rel_l2(hv - hb, gv * ref) <= TOL, (i, rel_l2(hv - hb, gv * ref))
 
 
+@pytest.mark.parametrize("xtype", [0, 30])
+def test_multi_gemv_group(orc, dev, xtype):
+    """Q4_K jobs of 1-4 tokens grouped in one call (the per-block modulation
+    projections) run as one GEMV launch: every job equals its own
+    single-job launch bit for bit and the oracle within the small-M bar
+    (N = 300: a ragged last workgroup); rows past each job's M stay
+    untouched."""
+    import torch
+    from llmr_amd import gguf, ops, synth
+    N, K, Ms = 300, 512, (1, 3, 1, 4, 2, 1, 1)
+    g = ops.default_graph()
+    blks, xs, jobs = [], [], []
+    out = torch.full((len(Ms), 4, N), 7.0, dtype=torch.float32, device=dev)
+    for i, M in enumerate(Ms):
+        blk = gguf.quantize(synth.normal(40 + i, 2, (N + 7 * i) * K, 0.02), 12)
+        blks.append(blk)
+        xs.append(_torch_x(synth.normal(40 + i, 1, M * K).reshape(M, K), xtype, dev))
+        w = ops.Tensor.quantized(torch.from_numpy(blk).to(dev), 12, N + 7 * i, K)
+        jobs.append(ops.MatmulJob(w, ops.Tensor.from_torch(xs[i]), out[i, :M], M, 7 * i))
+    ops.dispatch_batch_matmul_multi(g, jobs, N, K)
+    torch.cuda.synchronize()
+    for i, M in enumerate(Ms):
+        single, xr = _run(dev, blks[i], 12, _x_as_f32(xs[i]), xtype, N, 7 * i)
+        got = out[i, :M].cpu().numpy()
+        assert np.array_equal(got, single), i
+        ref = orc.batch_matmul(blks[i], 12, xr, N, K, M, 7 * i)
+        assert rel_l2(got, ref) <= 1e-5, (i, rel_l2(got, ref))
+        assert (out[i, M:] == 7.0).all(), i
+
+
 @pytest.mark.parametrize("M,xtype", [(4096, 30), (300, 30), (700, 0)])
 def test_multi_split_gelu(orc, dev, M, xtype):
     """Features [0, split) to a strided f32 output, the rest gelu'd into a
