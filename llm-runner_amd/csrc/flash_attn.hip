@@ -365,7 +365,6 @@ __device__ __forceinline__ void fa64_body(const _Float16* __restrict__ Q, const 
     const uint8_t* Qh = (const uint8_t*)Q + head * head_bytes;
     const uint8_t* Kh = (const uint8_t*)K + head * head_bytes;
     const uint8_t* Vh = (const uint8_t*)V + head * head_bytes;
-    constexpr uint32_t W = 8u / NB;       // waves per workgroup
     constexpr uint32_t DI = 2u * NB;      // DMA instructions per tile per wave (64 / W keys)
     const uint32_t q0 = qb * kBQ64 + wave * 32u * NB;  // first query of this wave
 

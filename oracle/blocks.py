@@ -36,14 +36,6 @@ def _mm(W, wtype, X, N, row_offset=0):
     return orc.batch_matmul(W, wtype, X, N, X.shape[1], X.shape[0], row_offset)
 
 
-def _attention_from_rows(q_rows, k_rows, v_rows, n_heads, cos_t, sin_t):
-    """transpose_heads x3, mrope on Q and K, flash_attention_v2 -> O [S, H*128]."""
-    q = orc.rope_apply(orc.transpose_heads(q_rows, n_heads), cos_t, sin_t)
-    k = orc.rope_apply(orc.transpose_heads(k_rows, n_heads), cos_t, sin_t)
-    v = orc.transpose_heads(v_rows, n_heads)
-    return orc.flash_attention(q, k, v, 1.0 / math.sqrt(128.0))
-
-
 def zimage_layer(w: dict, hidden: np.ndarray, n_heads: int, cos_t, sin_t, eps: float = 1e-5) -> np.ndarray:
     """w: numpy copies of llmr_amd.dit.ZImageLayerWeights fields (raw Q8_0
     blocks, f32 vectors). Returns the updated hidden (f32 [S, dim])."""
@@ -57,7 +49,7 @@ def zimage_layer(w: dict, hidden: np.ndarray, n_heads: int, cos_t, sin_t, eps: f
     v = _mm(w["wqkv"], GGML_Q8_0, a, dim, 2 * dim)
     q = orc.batch_head_norm(q, w["q_norm"], n_heads, eps)
     k = orc.batch_head_norm(k, w["k_norm"], n_heads, eps)
-    o = _attention_from_rows(q, k, v, n_heads, cos_t, sin_t)
+    o = _attention_rows(q, k, v, n_heads, cos_t, sin_t, None)
     t = _mm(w["wo"], GGML_Q8_0, o, dim)
     h = orc.gated_residual(h, gate_msa, orc.batch_rmsnorm(t, w["attn_norm2"], eps), True)
     a = orc.modulate(orc.batch_rmsnorm(h, w["ffn_norm1"], eps), scale_mlp)
@@ -70,12 +62,133 @@ def _ln_mod(x, shift, scale, eps=1e-6):
     return orc.modulate(orc.batch_layernorm(x, eps), scale, shift)
 
 
+def _row_ranges(rows, S):
+    """Sorted query rows -> the 16-aligned [lo, hi) ranges covering them (the
+    oracle attention computes whole 16-query blocks)."""
+    if rows is None:
+        return [(0, S)]
+    out = []
+    for b in sorted({int(r) // 16 for r in rows}):
+        lo, hi = 16 * b, min(16 * b + 16, S)
+        if out and out[-1][1] == lo:
+            out[-1] = (out[-1][0], hi)
+        else:
+            out.append((lo, hi))
+    return out
+
+
+def _attention_rows(q_rows, k_rows, v_rows, n_heads, cos_t, sin_t, rows):
+    """transpose_heads x3, mrope on Q and K, flash_attention_v2: the attention
+    output [len(rows), H*128] of the query rows `rows` (all rows, [S, H*128],
+    when None); q_rows [S, H*128] holds Q for at least those rows, K/V all."""
+    S = k_rows.shape[0]
+    q = orc.rope_apply(orc.transpose_heads(q_rows, n_heads), cos_t, sin_t)
+    k = orc.rope_apply(orc.transpose_heads(k_rows, n_heads), cos_t, sin_t)
+    v = orc.transpose_heads(v_rows, n_heads)
+    scale = 1.0 / math.sqrt(128.0)
+    if rows is None:
+        return orc.flash_attention(q, k, v, scale)
+    o = np.full((S, q_rows.shape[1]), np.nan, np.float32)
+    for lo, hi in _row_ranges(rows, S):
+        o[lo:hi] = orc.flash_attention(q, k, v, scale, qrange=(lo, hi))[lo:hi]
+    return o[np.asarray(rows)]
+
+
+def _mm_rows(W, wtype, X, N, row_offset, rows):
+    """GEMM of the rows `rows` of X (all rows when None)."""
+    X = np.ascontiguousarray(X, np.float32)
+    if rows is None:
+        return orc.batch_matmul(W, wtype, X, N, X.shape[1], X.shape[0], row_offset)
+    return orc.batch_matmul(W, wtype, X, N, X.shape[1], X.shape[0], row_offset, rows=np.asarray(rows))
+
+
+def flux_double_block(w: dict, txt_h: np.ndarray, img: np.ndarray, mt: np.ndarray, mi: np.ndarray, n_heads: int,
+                      cos_t, sin_t, rows=None):
+    """flux_dual_stream_block (flux_dit.c3:746-971) with the Flux.1-dev GELU
+    MLP. txt_h [n_txt, d] / img [n_img, d]: the two residual streams; mt / mi
+    [6, d]: (shift1, scale1, gate1, shift2, scale2, gate2) of each stream.
+    Returns the updated (txt_h, img); with `rows` (joint row indices, text
+    rows first) only those rows' updates are computed and returned as one
+    [len(rows), d] array in joint order."""
+    d = txt_h.shape[1]
+    nt, ni = txt_h.shape[0], img.shape[0]
+    m = w["img_mlp0"].size // (d // 256 * 144)
+    eps_hn = 1e-6
+    a_i = _ln_mod(img, mi[0], mi[1])
+    a_t = _ln_mod(txt_h, mt[0], mt[1])
+    # K, V of every joint row; Q of the rows asked for
+    ki, vi = (_mm(w["img_qkv"], GGML_Q4_K, a_i, d, r * d) for r in (1, 2))
+    kt, vt = (_mm(w["txt_qkv"], GGML_Q4_K, a_t, d, r * d) for r in (1, 2))
+    if rows is None:
+        qt, qi = _mm(w["txt_qkv"], GGML_Q4_K, a_t, d, 0), _mm(w["img_qkv"], GGML_Q4_K, a_i, d, 0)
+        q = np.concatenate([qt, qi])
+    else:
+        rows = np.asarray(rows)
+        q = np.zeros((nt + ni, d), np.float32)
+        rt, ri = rows[rows < nt], rows[rows >= nt] - nt
+        if rt.size:
+            q[rt] = _mm_rows(w["txt_qkv"], GGML_Q4_K, a_t, d, 0, rt)
+        if ri.size:
+            q[ri + nt] = _mm_rows(w["img_qkv"], GGML_Q4_K, a_i, d, 0, ri)
+    q = np.concatenate([orc.batch_head_norm(q[:nt], w["txt_q_norm"], n_heads, eps_hn),
+                        orc.batch_head_norm(q[nt:], w["img_q_norm"], n_heads, eps_hn)])
+    k = np.concatenate([orc.batch_head_norm(kt, w["txt_k_norm"], n_heads, eps_hn),
+                        orc.batch_head_norm(ki, w["img_k_norm"], n_heads, eps_hn)])
+    v = np.concatenate([vt, vi])
+    o = _attention_rows(q, k, v, n_heads, cos_t, sin_t, rows)
+
+    def stream(h, mod, wp, w0, w2, o_s):
+        """Attention projection + gated residual, then the MLP half."""
+        h = orc.gated_residual(h, mod[2], _mm(wp, GGML_Q4_K, o_s, d), False)
+        a = _ln_mod(h, mod[3], mod[4])
+        return orc.gated_residual(h, mod[5], _mm(w2, GGML_Q4_K, orc.gelu(_mm(w0, GGML_Q4_K, a, m)), d), False)
+
+    if rows is None:
+        txt_h = stream(txt_h, mt, w["txt_proj"], w["txt_mlp0"], w["txt_mlp2"], o[:nt])
+        img = stream(img, mi, w["img_proj"], w["img_mlp0"], w["img_mlp2"], o[nt:])
+        return txt_h, img
+    out = np.empty((rows.size, d), np.float32)
+    sel_t, sel_i = rows < nt, rows >= nt
+    if sel_t.any():
+        out[sel_t] = stream(txt_h[rows[sel_t]], mt, w["txt_proj"], w["txt_mlp0"], w["txt_mlp2"], o[sel_t])
+    if sel_i.any():
+        out[sel_i] = stream(img[rows[sel_i] - nt], mi, w["img_proj"], w["img_mlp0"], w["img_mlp2"], o[sel_i])
+    return out
+
+
+def flux_single_block(w: dict, h: np.ndarray, ms: np.ndarray, n_heads: int, cos_t, sin_t, rows=None):
+    """flux_single_stream_block (flux_dit.c3:975-1071) with the Flux.1-dev
+    GELU MLP half of linear1. h [S, d] joint stream (text rows first); ms [3, d]
+    (shift, scale, gate). Returns the updated h, or with `rows` the updated
+    rows [len(rows), d]."""
+    S, d = h.shape
+    m = w["linear1"].size // (d // 256 * 144) - 3 * d
+    eps_hn = 1e-6
+    a = _ln_mod(h, ms[0], ms[1])
+    k, v = (_mm(w["linear1"], GGML_Q4_K, a, d, r * d) for r in (1, 2))
+    if rows is None:
+        q = _mm(w["linear1"], GGML_Q4_K, a, d, 0)
+        mlp = orc.gelu(_mm(w["linear1"], GGML_Q4_K, a, m, 3 * d))
+        h_r = h
+    else:
+        rows = np.asarray(rows)
+        q = np.zeros((S, d), np.float32)
+        q[rows] = _mm_rows(w["linear1"], GGML_Q4_K, a, d, 0, rows)
+        mlp = orc.gelu(_mm_rows(w["linear1"], GGML_Q4_K, a, m, 3 * d, rows))
+        h_r = h[rows]
+    q = orc.batch_head_norm(q, w["q_norm"], n_heads, eps_hn)
+    k = orc.batch_head_norm(k, w["k_norm"], n_heads, eps_hn)
+    o = _attention_rows(q, k, v, n_heads, cos_t, sin_t, rows)
+    cat = np.concatenate([o, mlp], axis=1)
+    return orc.gated_residual(h_r, ms[2], _mm(w["linear2"], GGML_Q4_K, cat, d), False)
+
+
 def flux_forward(cfg, glob: dict, doubles: list, singles: list, latent: np.ndarray, txt: np.ndarray,
                  sigma: float, cos_t, sin_t) -> np.ndarray:
     """cfg: llmr_amd.dit.FluxConfig; weights: dicts of numpy copies of the
     FluxGlobalWeights / FluxDoubleWeights / FluxSingleWeights fields. Returns
     the velocity f32 [C, H, W]."""
-    d, m, H, nt = cfg.dim, cfg.mlp, cfg.n_heads, cfg.n_txt
+    d, H, nt = cfg.dim, cfg.n_heads, cfg.n_txt
     patches = orc.patchify(latent, cfg.patch)
     img = _mm(glob["img_in"], GGML_Q8_0, patches, d)
     txt_h = _mm(glob["txt_in"], GGML_Q4_K, txt, d)
@@ -83,40 +196,11 @@ def flux_forward(cfg, glob: dict, doubles: list, singles: list, latent: np.ndarr
     vec = _mm(glob["time_in1"], GGML_Q4_K, orc.silu(_mm(glob["time_in0"], GGML_Q4_K, temb, d)), d)
     vec = orc.silu(vec)
     mod = lambda W, n: _mm(W, GGML_Q4_K, vec, n * d).reshape(n, d)  # noqa: E731
-    eps_hn = 1e-6
     for w in doubles:
-        mi, mt = mod(w["img_mod"], 6), mod(w["txt_mod"], 6)
-        a_i = _ln_mod(img, mi[0], mi[1])
-        a_t = _ln_mod(txt_h, mt[0], mt[1])
-        qi, ki, vi = (_mm(w["img_qkv"], GGML_Q4_K, a_i, d, r * d) for r in range(3))
-        qt, kt, vt = (_mm(w["txt_qkv"], GGML_Q4_K, a_t, d, r * d) for r in range(3))
-        q = np.concatenate([orc.batch_head_norm(qt, w["txt_q_norm"], H, eps_hn),
-                            orc.batch_head_norm(qi, w["img_q_norm"], H, eps_hn)])
-        k = np.concatenate([orc.batch_head_norm(kt, w["txt_k_norm"], H, eps_hn),
-                            orc.batch_head_norm(ki, w["img_k_norm"], H, eps_hn)])
-        v = np.concatenate([vt, vi])
-        o = _attention_from_rows(q, k, v, H, cos_t, sin_t)
-        txt_o = _mm(w["txt_proj"], GGML_Q4_K, o[:nt], d)
-        img_o = _mm(w["img_proj"], GGML_Q4_K, o[nt:], d)
-        img = orc.gated_residual(img, mi[2], img_o, False)
-        txt_h = orc.gated_residual(txt_h, mt[2], txt_o, False)
-        a_i = _ln_mod(img, mi[3], mi[4])
-        img = orc.gated_residual(img, mi[5], _mm(w["img_mlp2"], GGML_Q4_K,
-                                                 orc.gelu(_mm(w["img_mlp0"], GGML_Q4_K, a_i, m)), d), False)
-        a_t = _ln_mod(txt_h, mt[3], mt[4])
-        txt_h = orc.gated_residual(txt_h, mt[5], _mm(w["txt_mlp2"], GGML_Q4_K,
-                                                     orc.gelu(_mm(w["txt_mlp0"], GGML_Q4_K, a_t, m)), d), False)
+        txt_h, img = flux_double_block(w, txt_h, img, mod(w["txt_mod"], 6), mod(w["img_mod"], 6), H, cos_t, sin_t)
     h = np.concatenate([txt_h, img])
     for w in singles:
-        ms = mod(w["mod"], 3)
-        a = _ln_mod(h, ms[0], ms[1])
-        q, k, v = (_mm(w["linear1"], GGML_Q4_K, a, d, r * d) for r in range(3))
-        mlp = orc.gelu(_mm(w["linear1"], GGML_Q4_K, a, m, 3 * d))
-        q = orc.batch_head_norm(q, w["q_norm"], H, eps_hn)
-        k = orc.batch_head_norm(k, w["k_norm"], H, eps_hn)
-        o = _attention_from_rows(q, k, v, H, cos_t, sin_t)
-        cat = np.concatenate([o, mlp], axis=1)
-        h = orc.gated_residual(h, ms[2], _mm(w["linear2"], GGML_Q4_K, cat, d), False)
+        h = flux_single_block(w, h, mod(w["mod"], 3), H, cos_t, sin_t)
     fm = mod(glob["final_mod"], 2)
     a = _ln_mod(h[nt:], fm[0], fm[1])
     vel = _mm(glob["final_linear"], GGML_Q4_K, a, cfg.patch_dim)

@@ -50,3 +50,30 @@ def test_create_context_without_device_fails_cleanly():
     rc = capi.lib().llmr_create_context(0, ctypes.byref(h))
     assert rc == capi.LLMR_ERR_NO_DEVICE and not h
     assert capi.lib().llmr_create_context(0, None) == capi.LLMR_ERR_INVALID_ARG
+
+
+def _c_harness(name: str) -> str:
+    """tests/c/_build/<name>, built with gcc from tests/c when it is missing."""
+    import os
+    import subprocess
+    cdir = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c")
+    exe = os.path.join(cdir, "_build", name)
+    if not os.path.exists(exe):
+        subprocess.run(["make", "-C", cdir, f"_build/{name}"], check=True, capture_output=True)
+    return exe
+
+
+def test_header_compiles_as_c11_and_every_entry_point_links():
+    """tests/c/abi_symbols.c includes the header under gcc -std=c11 -pedantic
+    -Werror and references every declared entry point; it links against the
+    library and runs (loading it, touching no device)."""
+    import os
+    import re
+    import subprocess
+    exe = _c_harness("abi_symbols")
+    src = open(os.path.join(os.path.dirname(exe), "..", "abi_symbols.c")).read()
+    listed = re.findall(r'\{"(llmr_\w+)", ', src)
+    assert sorted(listed) == sorted(capi.header_symbols()), "abi_symbols.c out of sync with the header"
+    out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
+    n = len(listed)
+    assert out.strip() == f"{n} of {n} entry points resolved"

@@ -66,7 +66,7 @@ def test_flux_forward_vs_oracle(dev, act):
     err = rel_l2(got, ref)
     print(f"flux forward act={act}: velocity rel L2 {err:.2e}")
     assert np.isfinite(got).all()
-    assert err < (5e-3 if act == torch.float16 else 2e-2)
+    assert err < (5e-3 if act == torch.float16 else 1e-2)  # measured 2.9e-4 / 3.3e-3
 
 
 def test_flux_forward_is_deterministic(dev):
