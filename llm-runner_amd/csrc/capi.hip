@@ -16,8 +16,15 @@ struct llmr_context {
     int num_cus;
     hipStream_t own;
     hipStream_t cur;
-    void* ws;         // library workspace (the SwiGLU's f32-input and fallback paths), grow-only
+    // Library workspace, grow-only: f32 activations rounded to 16 bits, the
+    // 16-bit weight images of the two-pass GEMM, the fallback paths' f32
+    // intermediates. Calls on different streams are ordered through ws_done,
+    // recorded after every use on the stream that used it (ws_stream).
+    void* ws;
     size_t ws_bytes;
+    hipEvent_t ws_done;
+    hipStream_t ws_stream;
+    bool ws_used;
 };
 
 namespace {
@@ -101,6 +108,14 @@ int llmr_create_context(int device_index, llmr_context** out_ctx) {
     c->cur = c->own;
     c->ws = nullptr;
     c->ws_bytes = 0;
+    c->ws_stream = nullptr;
+    c->ws_used = false;
+    e = hipEventCreateWithFlags(&c->ws_done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(c->own);
+        delete c;
+        return fail(LLMR_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(e));
+    }
     *out_ctx = c;
     return ok();
 }
@@ -112,6 +127,7 @@ int llmr_destroy_context(llmr_context* ctx) {
     (void)hipStreamSynchronize(ctx->own);
     (void)hipStreamDestroy(ctx->own);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    (void)hipEventDestroy(ctx->ws_done);
     delete ctx;
     return ok();
 }
@@ -201,6 +217,32 @@ int llmr_dequant_operand_f16(llmr_context* ctx, const void* w, uint32_t wtype, u
     return dequant_common(ctx, w, wtype, n_rows, in_dim, row_offset, out, true);
 }
 
+// Makes the context workspace hold `need` bytes for a call about to be issued
+// on the current stream: orders it after the last call that used the
+// workspace on another stream, then grows it if needed (hipFree waits for
+// every launch that may still use the old one).
+static int acquire_workspace(llmr_context* ctx, size_t need) {
+    if (need == 0) return LLMR_OK;
+    if (ctx->ws_used && ctx->ws_stream != ctx->cur) LLMR_HIP_CHECK(hipStreamWaitEvent(ctx->cur, ctx->ws_done, 0));
+    if (need > ctx->ws_bytes) {
+        if (ctx->ws) LLMR_HIP_CHECK(hipFree(ctx->ws));
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+        LLMR_HIP_CHECK(hipMalloc(&ctx->ws, need));
+        ctx->ws_bytes = need;
+    }
+    return LLMR_OK;
+}
+
+// Marks the workspace as used by the work just issued on the current stream.
+static int release_workspace(llmr_context* ctx, size_t need) {
+    if (need == 0) return LLMR_OK;
+    LLMR_HIP_CHECK(hipEventRecord(ctx->ws_done, ctx->cur));
+    ctx->ws_stream = ctx->cur;
+    ctx->ws_used = true;
+    return LLMR_OK;
+}
+
 int llmr_batch_matmul(llmr_context* ctx, const void* weight, uint32_t wtype, const void* input,
                       uint32_t xtype, float* output, uint32_t out_dim, uint32_t in_dim,
                       uint32_t seq_len, uint32_t row_offset) {
@@ -214,9 +256,12 @@ int llmr_batch_matmul(llmr_context* ctx, const void* weight, uint32_t wtype, con
         return fail(LLMR_ERR_INVALID_ARG, "input/output pointers must be 16-byte aligned");
     if ((uint64_t)row_offset + out_dim > 0xffffffffull)
         return fail(LLMR_ERR_INVALID_ARG, "row_offset + out_dim overflows");
+    const size_t need = llmr::batch_matmul_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len, ctx->num_cus);
+    if (int r = acquire_workspace(ctx, need)) return r;
     hipError_t e = llmr::launch_batch_matmul(weight, wtype, input, xtype, output, out_dim, in_dim, seq_len,
-                                             row_offset, ctx->num_cus, ctx->cur);
+                                             row_offset, ctx->num_cus, ctx->ws, ctx->cur);
     if (e != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul launch: %s", hipGetErrorString(e));
+    if (int r = release_workspace(ctx, need)) return r;
     return ok();
 }
 
@@ -278,18 +323,6 @@ int llmr_q8_lora_merge(llmr_context* ctx, void* weight, const float* a, const fl
     return ok();
 }
 
-// Grows the context workspace to `need` bytes (hipFree waits for every
-// launch that may still use the old one).
-static int grow_workspace(llmr_context* ctx, size_t need) {
-    if (need <= ctx->ws_bytes) return LLMR_OK;
-    if (ctx->ws) LLMR_HIP_CHECK(hipFree(ctx->ws));
-    ctx->ws = nullptr;
-    ctx->ws_bytes = 0;
-    LLMR_HIP_CHECK(hipMalloc(&ctx->ws, need));
-    ctx->ws_bytes = need;
-    return LLMR_OK;
-}
-
 int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
                             const llmr_matmul_job* jobs, uint32_t n_jobs, const llmr_matmul_epilogue* epilogue) {
     if (int r = check_ctx(ctx)) return r;
@@ -340,10 +373,11 @@ int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t wtype, uint32_t xtype, u
     const llmr::GemmEpilogue ge{e.kind, e.ldy, e.ldy2, e.split, has2 ? e.output2_type : (uint32_t)LLMR_GGML_BF16};
     const size_t need = llmr::batch_matmul_multi_workspace_bytes(wtype, xtype, out_dim, in_dim, gj, n_jobs, ge,
                                                                  ctx->num_cus);
-    if (int r = grow_workspace(ctx, need)) return r;
+    if (int r = acquire_workspace(ctx, need)) return r;
     hipError_t err = llmr::launch_batch_matmul_multi(wtype, xtype, out_dim, in_dim, gj, n_jobs, ge, ctx->num_cus,
                                                      ctx->ws, ctx->cur);
     if (err != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul_multi launch: %s", hipGetErrorString(err));
+    if (int r = release_workspace(ctx, need)) return r;
     return ok();
 }
 
@@ -362,10 +396,12 @@ int llmr_batch_matmul_swiglu(llmr_context* ctx, const void* weight_gate, const v
     if (!input || !output) return fail(LLMR_ERR_INVALID_ARG, "null input/output pointer");
     if (!aligned(input, 16) || !aligned(output, 16))
         return fail(LLMR_ERR_INVALID_ARG, "input/output pointers must be 16-byte aligned");
-    if (int r = grow_workspace(ctx, llmr::swiglu_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len))) return r;
+    const size_t need = llmr::swiglu_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len, ctx->num_cus);
+    if (int r = acquire_workspace(ctx, need)) return r;
     hipError_t e = llmr::launch_batch_matmul_swiglu(weight_gate, weight_up, wtype, input, xtype, output, out_dim,
                                                     in_dim, seq_len, ctx->num_cus, ctx->ws, ctx->cur);
     if (e != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul_swiglu launch: %s", hipGetErrorString(e));
+    if (int r = release_workspace(ctx, need)) return r;
     return ok();
 }
 

@@ -28,35 +28,13 @@
 //    weight and activation rows in that XCD's L2.
 #include <type_traits>
 
+#include "gemm_q_common.h"
 #include "llmr_device.h"
 #include "llmr_internal.h"
 
 namespace llmr {
 
 namespace {
-
-constexpr int kBK = 64;  // K per stage
-
-// 16-byte chunk c (0..7) of LDS row r (128-byte rows). gfx950's LDS has 64
-// four-byte banks, so two rows share a 256-byte bank line; XOR-ing the chunk
-// with (r >> 1) & 7 makes the 16 rows of a 16-lane fragment read land on 16
-// distinct bank quads.
-__device__ __forceinline__ uint32_t lds_off(uint32_t r, uint32_t c) {
-    return r * 128u + ((c ^ ((r >> 1) & 7u)) << 4);
-}
-
-// 32x32x16 MFMA on 16-bit operand bits: bf16 operands for bf16 activations
-// (fp16 cannot hold bf16's range), fp16 otherwise.
-template <uint32_t XT>
-__device__ __forceinline__ f32x16 mfma16(f16x8 a, f16x8 b, f32x16 c) {
-    if constexpr (XT == kGgmlBF16) {
-        typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-    } else {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-    }
-}
 
 template <uint32_t XT>
 struct XLoad;
@@ -388,23 +366,6 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
 }
 
 // ---------------------------------------------------------------------------
-// Buffer-resource helpers for the persistent kernel below.
-// ---------------------------------------------------------------------------
-
-__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-}
-__device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
-}
-// Eight Q8_0 quants (two dwords) -> one 16-byte chunk of fp16 operands RN16(d*q).
-__device__ __forceinline__ u32x4 q8x8_f16(uint32_t q0, uint32_t q1, f16x2 d2) {
-    const f16x4 lo = q8x4_to_f16(q0, d2), hi = q8x4_to_f16(q1, d2);
-    return __builtin_bit_cast(u32x4, f16x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
-}
-
-
-// ---------------------------------------------------------------------------
 // Persistent 256 x 256 tile kernel for 16-bit activations (gfx950).
 //
 // One workgroup per CU (grid = min(tiles, CUs)), 256 threads = one wave64
@@ -428,234 +389,6 @@ __device__ __forceinline__ u32x4 q8x8_f16(uint32_t q0, uint32_t q1, f16x2 d2) {
 // to a multiple of 6 so the six ring-slot combinations are compile-time) and
 // tiles past the workgroup's last read through a zero-size descriptor.
 // ---------------------------------------------------------------------------
-
-// Tile order: in every full round of G = gridDim.x tiles the 32 workgroups
-// one XCD runs (dispatch is round-robin over the 8 XCDs) get 32 consecutive
-// indices, which the group-of-4-tile-rows order turns into a 4 x 8 block of
-// tiles (4 x 256 activation rows and 8 x 256 weight rows shared in the XCD's L2).
-__device__ __forceinline__ void map_tile_persist(uint32_t T, uint32_t G, uint32_t tiles_m, uint32_t tiles_n,
-                                                 uint32_t& tm, uint32_t& tn) {
-    constexpr uint32_t kXcd = 8, kGroupM = 4;
-    const uint32_t total = tiles_m * tiles_n;
-    uint32_t L = T;
-    if (G % kXcd == 0 && T / G < total / G) {
-        const uint32_t b = T % G;
-        L = (T - b) + (b % kXcd) * (G / kXcd) + b / kXcd;
-    }
-    const uint32_t per_group = kGroupM * tiles_n;
-    const uint32_t g = L / per_group;
-    const uint32_t first_m = g * kGroupM;
-    const uint32_t gsize = min(tiles_m - first_m, kGroupM);
-    const uint32_t in = L % per_group;
-    tm = first_m + in % gsize;
-    tn = in / gsize;
-}
-
-// Bytes 0,1 (SEL_LO) or 2,3 (SEL_HI) of `w` as two fp16 subnormals b * 2^-24
-// (exact: the byte is the mantissa of a zero-exponent half), so one mixed
-// FMA with a scale pre-multiplied by 2^24 forms scale * b + bias exactly
-// before its single rounding - no bias subtraction of the 1024+b encoding.
-constexpr uint32_t kSelLo = 0x0c010c00u, kSelHi = 0x0c030c02u;
-__device__ __forceinline__ f16x2 sub16x2(uint32_t w, uint32_t sel) {
-    return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, w, sel));
-}
-// Two operands RN(s * h + b) of type OT from the two halves of h, packed.
-template <uint32_t OT>
-__device__ __forceinline__ uint32_t fma_pair(f16x2 h, float s, float b) {
-    if constexpr (OT == kGgmlBF16) {
-        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-        bf16x2_t r;
-        r.x = (__bf16)__builtin_fmaf((float)h.x, s, b);
-        r.y = (__bf16)__builtin_fmaf((float)h.y, s, b);
-        return __builtin_bit_cast(uint32_t, r);
-    } else {
-        f16x2 r;
-        r.x = (_Float16)__builtin_fmaf((float)h.x, s, b);
-        r.y = (_Float16)__builtin_fmaf((float)h.y, s, b);
-        return __builtin_bit_cast(uint32_t, r);
-    }
-}
-
-template <uint32_t WT, uint32_t OT>
-struct WRow;
-
-// Q4_K row stage s: quarter s % 4 of superblock s / 4 = the 16-byte header
-// and qs bytes [32 (s%4), +32): low nibbles are k 0..31 of the stage
-// (sub-block 2j), high nibbles k 32..63 (sub-block 2j+1).
-// The dequantization is split in four parts (one per 16-wide k step of the
-// stage it overlaps): part p writes LDS chunks p and 4+p of the row.
-template <uint32_t OT>
-struct WRow<kGgmlQ4K, OT> {
-    static constexpr int kLoads = 3;
-    u32x4 hdr, qa, qb;
-    template <int L>
-    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t s) {
-        const uint32_t sh = (s >> 2) * 144u;
-        const uint32_t sq = sh + 16u + 32u * (s & 3u);
-        if constexpr (L == 0) hdr = bload16(r, voff, sh);
-        if constexpr (L == 1) qa = bload16(r, voff, sq);
-        if constexpr (L == 2) qb = bload16(r, voff + 16u, sq);
-    }
-    // Operand = RN(d*sc*q - dmin*mn) (products exact, one rounding): low
-    // nibbles are read as q * 2^-24, high nibbles (masked in place) as
-    // 16 q * 2^-24, so their scales carry 2^24 and 2^20.
-    struct Scale {
-        float s0, b0, s1, b1;
-    };
-    __device__ __forceinline__ Scale scale(uint32_t s) const {
-        const uint32_t j = s & 3u;
-        const float d = f16_bits_to_f32(hdr.x & 0xffffu);
-        const float dmin = f16_bits_to_f32(hdr.x >> 16);
-        uint32_t sc0, mn0, sc1, mn1;
-        q4k_scale_min(2 * j, hdr.y, hdr.z, hdr.w, sc0, mn0);
-        q4k_scale_min(2 * j + 1, hdr.y, hdr.z, hdr.w, sc1, mn1);
-        return Scale{d * (float)sc0 * 16777216.0f, -(dmin * (float)mn0), d * (float)sc1 * 1048576.0f,
-                     -(dmin * (float)mn1)};
-    }
-    // `base` = LDS offset of chunk 0 of the row; chunk c is at base ^ (c << 4)
-    template <int P>
-    __device__ __forceinline__ void store(uint8_t* lds, const Scale& c, uint32_t base) const {
-        const uint32_t w0 = P < 2 ? qa[2 * P] : qb[2 * P - 4];
-        const uint32_t w1 = P < 2 ? qa[2 * P + 1] : qb[2 * P - 3];
-        const uint32_t l0 = w0 & 0x0f0f0f0fu, l1 = w1 & 0x0f0f0f0fu;
-        const uint32_t h0 = w0 & 0xf0f0f0f0u, h1 = w1 & 0xf0f0f0f0u;
-        const u32x4 lo = {fma_pair<OT>(sub16x2(l0, kSelLo), c.s0, c.b0), fma_pair<OT>(sub16x2(l0, kSelHi), c.s0, c.b0),
-                          fma_pair<OT>(sub16x2(l1, kSelLo), c.s0, c.b0), fma_pair<OT>(sub16x2(l1, kSelHi), c.s0, c.b0)};
-        const u32x4 hi = {fma_pair<OT>(sub16x2(h0, kSelLo), c.s1, c.b1), fma_pair<OT>(sub16x2(h0, kSelHi), c.s1, c.b1),
-                          fma_pair<OT>(sub16x2(h1, kSelLo), c.s1, c.b1), fma_pair<OT>(sub16x2(h1, kSelHi), c.s1, c.b1)};
-        *(u32x4*)(lds + (base ^ ((uint32_t)P << 4))) = lo;
-        *(u32x4*)(lds + (base ^ ((uint32_t)(4 + P) << 4))) = hi;
-    }
-};
-
-// Q8_0 row stage s: blocks 2s and 2s+1 = bytes [68 s, 68 s + 68) of the row
-// (dword-aligned: K % 64 == 0). Block 0: scale in the low half of dword 0,
-// quants from byte 2 (chunks 0..3); block 1: scale in the high half of dword
-// 8, quants in dwords 9..16 (chunks 4..7). Part p writes chunks p and 4+p.
-template <uint32_t OT>
-struct WRow<kGgmlQ8_0, OT> {
-    static constexpr int kLoads = 5;
-    u32x4 a, b, c, d;
-    uint32_t e;
-    template <int L>
-    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t s) {
-        const uint32_t so = 68u * s;
-        if constexpr (L == 0) a = bload16(r, voff, so);
-        if constexpr (L == 1) b = bload16(r, voff + 16u, so);
-        if constexpr (L == 2) c = bload16(r, voff + 32u, so);
-        if constexpr (L == 3) d = bload16(r, voff + 48u, so);
-        if constexpr (L == 4) e = bload4(r, voff + 64u, so);
-    }
-    struct Scale {
-        float s0, b0, s1, b1;  // bf16: (2^24 d, -128 d) per block; f16: (d, -) per block
-    };
-    __device__ __forceinline__ Scale scale(uint32_t s) const {
-        (void)s;
-        const float d0 = f16_bits_to_f32(a.x & 0xffffu);
-        const float d1 = f16_bits_to_f32(c.x >> 16);
-        if constexpr (OT == kGgmlBF16)
-            return Scale{d0 * 16777216.0f, -128.0f * d0, d1 * 16777216.0f, -128.0f * d1};
-        else
-            return Scale{d0, 0.0f, d1, 0.0f};
-    }
-    __device__ __forceinline__ uint32_t word(int i) const {
-        return i < 4 ? a[i] : i < 8 ? b[i - 4] : i < 12 ? c[i - 8] : i < 16 ? d[i - 12] : e;
-    }
-    // chunk ch of the stage from its two quant dwords q0, q1
-    __device__ __forceinline__ u32x4 chunk(uint32_t q0, uint32_t q1, float sc, float bi) const {
-        if constexpr (OT == kGgmlBF16) {
-            // RN_bf16(d*q): q + 128 read as a subnormal half, d*q = (2^24 d) h - 128 d
-            // exactly in f32, then one rounding to bf16
-            const uint32_t u0 = q0 ^ 0x80808080u, u1 = q1 ^ 0x80808080u;
-            return u32x4{fma_pair<OT>(sub16x2(u0, kSelLo), sc, bi), fma_pair<OT>(sub16x2(u0, kSelHi), sc, bi),
-                         fma_pair<OT>(sub16x2(u1, kSelLo), sc, bi), fma_pair<OT>(sub16x2(u1, kSelHi), sc, bi)};
-        } else {
-            const _Float16 h = (_Float16)sc;
-            return q8x8_f16(q0, q1, f16x2{h, h});
-        }
-    }
-    template <int P>
-    __device__ __forceinline__ void store(uint8_t* lds, const Scale& k, uint32_t base) const {
-        const uint32_t q0 = __builtin_amdgcn_alignbyte(word(2 * P + 1), word(2 * P), 2);
-        const uint32_t q1 = __builtin_amdgcn_alignbyte(word(2 * P + 2), word(2 * P + 1), 2);
-        *(u32x4*)(lds + (base ^ ((uint32_t)P << 4))) = chunk(q0, q1, k.s0, k.b0);
-        *(u32x4*)(lds + (base ^ ((uint32_t)(4 + P) << 4))) = chunk(word(9 + 2 * P), word(10 + 2 * P), k.s1, k.b1);
-    }
-};
-
-
-// Schedule of one 16-wide k step inside a stage: its 16 MFMAs each followed
-// by a share of the stage's other work, so that work issues while the
-// matrix core is busy (on gfx950 a wave's VALU, LDS and buffer instructions
-// co-issue with its own MFMAs): the next step's fragment reads after the
-// first eight MFMAs, three VALU (the weight dequantization) after every one,
-// the two LDS writes of the dequantized weight chunks and the step's share
-// of the buffer loads spread in between.
-#define LLMR_SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
-#define LLMR_SLOT_R LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x002, 3)
-#define LLMR_SLOT_V LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 3)
-#define LLMR_SLOT_L LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 3); LLMR_SGB(0x020, 1)
-#define LLMR_SLOT_W LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 3); LLMR_SGB(0x200, 1)
-#define LLMR_SLOT_RA LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x002, 5)
-#define LLMR_SLOT_VA LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 5)
-#define LLMR_SLOT_LA LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 5); LLMR_SGB(0x020, 1)
-#define LLMR_SLOT_WA LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 5); LLMR_SGB(0x200, 1)
-// the first step of a stage also computes the dequantization scales
-#define LLMR_STEP_SCHEDULE_A                                                                \
-    LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA;       \
-    LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_LA; LLMR_SLOT_VA; LLMR_SLOT_WA; LLMR_SLOT_LA;       \
-    LLMR_SLOT_VA; LLMR_SLOT_WA; LLMR_SLOT_LA; LLMR_SLOT_LA
-#define LLMR_STEP_SCHEDULE                                                                  \
-    LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R;             \
-    LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_L; LLMR_SLOT_V; LLMR_SLOT_W; LLMR_SLOT_L;             \
-    LLMR_SLOT_V; LLMR_SLOT_W; LLMR_SLOT_L; LLMR_SLOT_L
-
-struct Frags {
-    f16x8 x[4], w[4];
-};
-
-// silu(g) = g / (1 + e^-g) (llm.slang:1903), e^-g as 2^(-g log2 e)
-__device__ __forceinline__ float silu(float g) {
-    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
-}
-
-// gelu (tanh form, lib/shaders/diffusion.slang:1103-1107) as
-// 0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)), u = 0.7978845608 (x + 0.044715 x^3)
-__device__ __forceinline__ float gelu_tanh(float x) {
-    const float u = 0.7978845608f * (x + 0.044715f * x * x * x);
-    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u));
-}
-
-// Output of the persistent kernel's tile accumulators (host-selected):
-//   kEpiStore      Y[m, n] = acc
-//   kEpiResidual   Y[m, n] += gate[n] * acc  (gate 1 when null)
-//   kEpiSplitGelu  n < split: Y[m, n] = acc; n >= split: Y2[m, n - split] =
-//                  16-bit gelu(acc)   (split % 8 == 0)
-// with row strides ldy (Y) and ldy2 (Y2).
-constexpr uint32_t kEpiStore = 0, kEpiResidual = 1, kEpiSplitGelu = 2;
-
-// One GEMM of a persistent launch. A launch multiplies up to two problems
-// that share N and K (e.g. the text and image rows of a block with their own
-// weights); their 256-row tiles are stacked along M, problem 0 first.
-struct PersistProblem {
-    const uint8_t* W;   // weight blocks; row row_offset is output feature 0
-    const void* X;      // [M, K] 16-bit activations
-    float* Y;           // f32 output (kEpiResidual: read and updated)
-    const float* gate;  // kEpiResidual: [N] or null
-    void* Y2;           // kEpiSplitGelu: 16-bit output
-    uint32_t M, row_offset, tiles_m;
-};
-struct PersistArgs {
-    PersistProblem p[2];
-    const uint8_t* W2;  // SwiGLU: the up weight (p[0].W is the gate)
-    uint32_t N, K, tiles_m, tiles_n;  // tiles_m of both problems
-    uint32_t epi, ldy, ldy2, split, y2_bf16;
-};
-
-template <typename T>
-__device__ __forceinline__ T pick(uint32_t p, T a, T b) {
-    return p ? b : a;
-}
 
 // SW (SwiGLU, batch_matmul_swiglu_q8, llm.slang:1769-1911): W holds the gate
 // rows and W2 the up rows (N each, row_offset unused); a tile covers 128
@@ -711,12 +444,12 @@ __global__ void __launch_bounds__(256, 1) gemm_q_persist(const PersistArgs args)
 
     // per-lane offsets (tile independent)
     // activation DMA i of wave w: rows 64w + 8i + lane/8, physical chunk lane%8,
-    // logical chunk (lane%8) ^ ((row >> 1) & 7) = (lane%8) ^ (lane/16) ^ 4(i&1)
+    // logical chunk (lane%8) ^ lds_swz(row)
     uint32_t xvoff[X_DMAS];
 #pragma unroll
     for (int i = 0; i < X_DMAS; i++) {
         const uint32_t row = 64u * wave + 8u * i + (lane >> 3);
-        const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
+        const uint32_t c = (lane & 7u) ^ lds_swz(row);
         xvoff[i] = row * xrow + c * 16u;
     }
     // Thread tid loads one weight row of the tile. SW: waves 0-1 the gate rows
@@ -725,7 +458,7 @@ __global__ void __launch_bounds__(256, 1) gemm_q_persist(const PersistArgs args)
     // 64-127 | up 64-127 (waves 1 and 2 swap places).
     const uint32_t wvoff = (SW ? (tid & 127u) : tid) * rb;
     const uint32_t wrow = SW ? (wave == 1u ? tid + 64u : wave == 2u ? tid - 64u : tid) : tid;
-    const uint32_t wbase = wrow * 128u + ((((wrow >> 1) & 7u)) << 4);  // its LDS chunk 0
+    const uint32_t wbase = wrow * 128u + (lds_swz(wrow) << 4);  // its LDS chunk 0
     // fragment offsets per 16-wide k step t: chunk 4(t>>1) + 2kh + (t&1) of
     // rows (block) + l32; the swizzle term depends only on l32
     uint32_t xoff[4], woff[4];
@@ -837,80 +570,8 @@ __global__ void __launch_bounds__(256, 1) gemm_q_persist(const PersistArgs args)
     auto store_tile = [&](uint32_t k) {
         uint32_t p, m0, n0;
         tile_origin(k, p, m0, n0);
-        const uint32_t M = pick(p, Mp0, Mp1);
-        float* const Y = pick(p, Yp0, Yp1);
-        if constexpr (SW) {
-            // acc[a] (gate) and acc[a + 2] (up) hold the same features
-#pragma unroll
-            for (int a = 0; a < 2; a++)
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const uint32_t m = m0 + wm * 128u + b * 32u + l32;
-#pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const uint32_t n = n0 + wn * 64u + a * 32u + 8u * g + 4u * kh;
-                        f32x4 v;
-#pragma unroll
-                        for (int e = 0; e < 4; e++) v[e] = silu(acc[a][b][4 * g + e]) * acc[a + 2][b][4 * g + e];
-                        if (m < M && n < N) *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
-                    }
-                    acc[a][b] = f32x16{};
-                    acc[a + 2][b] = f32x16{};
-                }
-            return;
-        }
-        // the lane's four consecutive features n .. n+3 of row m (N % 4 == 0,
-        // host-checked: all four in range or none). nw = n - 4 kh is the same
-        // for the whole wave; with split % 8 == 0 (host-checked) nw < split
-        // decides the side of split for both kh, as a uniform branch.
-        auto each = [&](auto&& f) __attribute__((always_inline)) {
-#pragma unroll
-            for (int a = 0; a < 4; a++)
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const uint32_t m = m0 + wm * 128u + b * 32u + l32;
-#pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const uint32_t nw = n0 + wn * 128u + a * 32u + 8u * g;
-                        const uint32_t n = nw + 4u * kh;
-                        if (m < M && n < N)
-                            f(m, n, nw, f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2],
-                                              acc[a][b][4 * g + 3]});
-                    }
-                    acc[a][b] = f32x16{};
-                }
-        };
-        if constexpr (EPI == kEpiResidual) {
-            const float* const gate = pick(p, Gp0, Gp1);
-            each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
-                f32x4* const h = (f32x4*)(Y + (uint64_t)m * ldy + n);
-                const f32x4 gv = gate ? *(const f32x4*)(gate + n) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
-                *h = *h + gv * v;
-            });
-        } else if constexpr (EPI == kEpiSplitGelu) {
-            uint16_t* const Y2 = (uint16_t*)pick(p, Y2p0, Y2p1);
-            const uint32_t bf = y2_bf16;
-            each([&](uint32_t m, uint32_t n, uint32_t nw, f32x4 v) __attribute__((always_inline)) {
-                if (nw < split) {
-                    *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
-                } else {
-                    const f32x4 gl{gelu_tanh(v.x), gelu_tanh(v.y), gelu_tanh(v.z), gelu_tanh(v.w)};
-                    u32x2 o;
-                    if (bf) {
-                        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-                        o.x = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.x, (__bf16)gl.y});
-                        o.y = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.z, (__bf16)gl.w});
-                    } else {
-                        o = u32x2{pack_f16x2(gl.x, gl.y), pack_f16x2(gl.z, gl.w)};
-                    }
-                    *(u32x2*)(Y2 + (uint64_t)m * ldy2 + (n - split)) = o;
-                }
-            });
-        } else {
-            each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
-                *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
-            });
-        }
+        store_tile_256<SW, EPI>(acc, pick(p, Yp0, Yp1), pick(p, Gp0, Gp1), pick(p, Y2p0, Y2p1), pick(p, Mp0, Mp1), N,
+                                m0, n0, wm, wn, l32, kh, ldy, ldy2, split, y2_bf16);
     };
 
     // prologue, issued in the steady state's order (a stage issues the
@@ -1171,18 +832,18 @@ __global__ void __launch_bounds__(512, 1) gemm_q_persist8(const PersistArgs args
     const uint32_t xrow = K * 2u;
 
     // activation DMA i of wave w: rows 32w + 8i + lane/8, physical chunk
-    // lane%8, logical chunk (lane%8) ^ ((row >> 1) & 7)
+    // lane%8, logical chunk (lane%8) ^ lds_swz(row)
     uint32_t xvoff[X_DMAS];
 #pragma unroll
     for (int i = 0; i < X_DMAS; i++) {
         const uint32_t row = 32u * wave + 8u * i + (lane >> 3);
-        const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
+        const uint32_t c = (lane & 7u) ^ lds_swz(row);
         xvoff[i] = row * xrow + c * 16u;
     }
     // thread tid dequantizes half wh of weight row tid % 256 of the tile
     const uint32_t wrow = tid & 255u;
     const uint32_t wvoff = wrow * rb;
-    const uint32_t wbase = wrow * 128u + (((wrow >> 1) & 7u) << 4);  // its LDS chunk 0
+    const uint32_t wbase = wrow * 128u + (lds_swz(wrow) << 4);  // its LDS chunk 0
     uint32_t xoff[4], woff[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
@@ -1489,36 +1150,8 @@ hipError_t dispatch_x(const void* w, const void* x, float* y, uint32_t N, uint32
     auto wgs = [&](uint32_t bm, uint32_t bn) {
         return (uint64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     };
-    // 16-bit activations with at least half the CUs' worth of 256 x 256
-    // tiles: the persistent kernel. It addresses activations and weight rows
-    // through 32-bit buffer offsets (X and the used weight rows must span
-    // less than 2 GiB) and stores four features per lane (N % 4 == 0).
-    if constexpr (XT != kGgmlF32) {
-        const uint64_t rb = (WT == kGgmlQ8_0) ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * 144;
-        const bool fits31 = (uint64_t)M * K * 2u < (1ull << 31) && (uint64_t)N * rb < (1ull << 31);
-        const uint64_t tiles = wgs(256, 256);
-        if (fits31 && N % 4 == 0 && 2 * tiles >= (uint64_t)num_cus) {
-            const uint32_t tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
-            const uint32_t grid = (uint32_t)min(tiles, (uint64_t)num_cus);
-            PersistArgs a{};
-            a.p[0] = PersistProblem{(const uint8_t*)w, x, y, nullptr, nullptr, M, row_offset, tiles_m};
-            a.N = N;
-            a.K = K;
-            a.tiles_m = tiles_m;
-            a.tiles_n = tiles_n;
-            a.epi = kEpiStore;
-            a.ldy = N;
-            // Q8_0 on the 8-wave kernel (its half-row dequantization is lighter
-            // than Q4_K's and it measures faster); Q4_K on the 4-wave one
-            if constexpr (WT == kGgmlQ8_0)
-                hipLaunchKernelGGL((gemm_q_persist8<WT, XT>), dim3(grid), dim3(512), 0, st, a);
-            else
-                hipLaunchKernelGGL((gemm_q_persist<WT, XT, false>), dim3(grid), dim3(256), 0, st, a);
-            return hipGetLastError();
-        }
-    }
-    // Otherwise the largest 4-wave tile that still gives every CU at least
-    // ~1.5 workgroups.
+    // the largest 4-wave tile that still gives every CU at least ~1.5
+    // workgroups
     const uint64_t want = (uint64_t)num_cus * 3 / 2;
     if (wgs(256, 256) >= want) return launch_tiled<WT, XT, 256, 256>(w, x, y, N, K, M, row_offset, st);
     if (wgs(128, 128) >= want) return launch_tiled<WT, XT, 128, 128>(w, x, y, N, K, M, row_offset, st);
@@ -1548,6 +1181,30 @@ __global__ void __launch_bounds__(256) f32_to_bf16_kernel(const float* __restric
     *(u32x2*)(y + 2 * i) = u32x2{rn(v.x) | (rn(v.y) << 16), rn(v.z) | (rn(v.w) << 16)};
 }
 
+// f32 -> fp16 with round to nearest even, the reference's float16_t(x) of
+// the GEMM activations (llm.slang:1673); 8 values per thread
+__global__ void __launch_bounds__(256) f32_to_f16_kernel(const float* __restrict__ x, u32x4* __restrict__ y,
+                                                         size_t n8) {
+    const size_t i = (size_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= n8) return;
+    const f32x4 a = *(const f32x4*)(x + 8 * i), b = *(const f32x4*)(x + 8 * i + 4);
+    y[i] = u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y), pack_f16x2(b.z, b.w)};
+}
+
+hipError_t convert_activations(const void* x, uint32_t xtype, void* out, uint32_t otype, size_t n, hipStream_t st) {
+    (void)xtype;  // f32
+    if (otype == kGgmlBF16) {
+        const size_t n4 = n / 4;
+        hipLaunchKernelGGL(f32_to_bf16_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, st,
+                           (const float*)x, (uint32_t*)out, n4);
+    } else {
+        const size_t n8 = n / 8;
+        hipLaunchKernelGGL(f32_to_f16_kernel, dim3((uint32_t)((n8 + 255) / 256)), dim3(256), 0, st,
+                           (const float*)x, (u32x4*)out, n8);
+    }
+    return hipGetLastError();
+}
+
 // y = silu(g) * u elementwise (the SwiGLU of two separately computed GEMMs)
 __global__ void __launch_bounds__(256) swiglu_combine_kernel(const float* __restrict__ g,
                                                              const float* __restrict__ u, float* __restrict__ y,
@@ -1556,21 +1213,66 @@ __global__ void __launch_bounds__(256) swiglu_combine_kernel(const float* __rest
     if (i < n) y[i] = silu(g[i]) * u[i];
 }
 
+size_t align256(size_t b) { return (b + 255u) / 256u * 256u; }
+
+uint64_t row_bytes_of(uint32_t wtype, uint32_t K) {
+    return (wtype == kGgmlQ8_0) ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * 144;
+}
+
+// How one GEMM runs. The persistent 256 x 256 kernels take launches with at
+// least half the CUs' worth of tiles, whole 64-wide K stages, N % 4 == 0
+// (four features per lane store) and 32-bit buffer offsets over the 16-bit
+// activations and the used weight rows. F32 activations then go through
+// the workspace as fp16 (the reference's rounding of x, llm.slang:1673).
+// From kW16MinTokens tokens the weight is dequantized once into a 16-bit
+// image (gemm_w16.hip) instead of once per 256-token tile.
+constexpr uint32_t kW16MinTokens = 2048;
+struct GemmPlan {
+    bool persistent, two_pass, convert_x;
+    uint32_t xt;                  // activation type the kernel reads
+    size_t x16_off, img_off, ws;  // workspace layout: [x16 | image]
+};
+GemmPlan plan_gemm(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M, int num_cus) {
+    GemmPlan p{};
+    const uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
+    p.persistent = (K % kBK) == 0 && N % 4 == 0 && 2 * tiles >= (uint64_t)num_cus &&
+                   (uint64_t)M * K * 2u < (1ull << 31) && (uint64_t)N * row_bytes_of(wtype, K) < (1ull << 31);
+    p.xt = xtype;
+    if (!p.persistent) return p;
+    p.convert_x = xtype == kGgmlF32;
+    if (p.convert_x) p.xt = kGgmlF16;
+    p.two_pass = M >= kW16MinTokens;
+    p.x16_off = 0;
+    p.img_off = p.convert_x ? align256((size_t)M * K * 2u) : 0u;
+    p.ws = p.img_off + (p.two_pass ? w16_image_bytes(N, K, false) : 0u);
+    return p;
+}
+
 // Whether the fused SwiGLU kernel takes this launch: four features per
 // lane store (N % 4 == 0) and 32-bit buffer offsets for the 16-bit
 // activations and each weight.
 bool swiglu_fused(uint32_t wtype, uint32_t N, uint32_t K, uint32_t M) {
-    const uint64_t rb = (wtype == kGgmlQ8_0) ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * 144;
+    const uint64_t rb = row_bytes_of(wtype, K);
     return N % 4 == 0 && (K % kBK) == 0 && (uint64_t)M * K * 2u < (1ull << 31) && (uint64_t)N * rb < (1ull << 31);
 }
 
 }  // namespace
 
+size_t batch_matmul_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M,
+                                    int num_cus) {
+    if (M == 0 || N == 0 || (wtype == kGgmlQ4K && M <= kGemvMaxTokens)) return 0;
+    return plan_gemm(wtype, xtype, N, K, M, num_cus).ws;
+}
+
 size_t swiglu_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
-                              uint32_t seq_len) {
-    if (!swiglu_fused(wtype, out_dim, in_dim, seq_len))
-        return 2 * (((size_t)seq_len * out_dim + 63) / 64 * 64) * sizeof(float);
-    return xtype == kGgmlF32 ? (size_t)seq_len * in_dim * 2u : 0u;
+                              uint32_t seq_len, int num_cus) {
+    const uint32_t N = out_dim, K = in_dim, M = seq_len;
+    if (!swiglu_fused(wtype, N, K, M)) {
+        const size_t gu = 2 * align256((size_t)M * N * sizeof(float));
+        return gu + batch_matmul_workspace_bytes(wtype, xtype, N, K, M, num_cus);
+    }
+    const size_t x16 = xtype == kGgmlF32 ? align256((size_t)M * K * 2u) : 0u;
+    return x16 + (M >= kW16MinTokens ? w16_image_bytes(N, K, true) : 0u);
 }
 
 hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t wtype, const void* x,
@@ -1578,12 +1280,14 @@ hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t w
                                       uint32_t seq_len, int num_cus, void* ws, hipStream_t st) {
     if (seq_len == 0 || out_dim == 0) return hipSuccess;
     const uint32_t N = out_dim, K = in_dim, M = seq_len;
+    if (wtype != kGgmlQ8_0) return hipErrorInvalidValue;
     if (!swiglu_fused(wtype, N, K, M)) {
         // two GEMMs into the workspace, then the elementwise SwiGLU
         float* g = (float*)ws;
-        float* u = g + ((size_t)M * N + 63) / 64 * 64;  // 256-byte aligned
-        hipError_t e = launch_batch_matmul(wg, wtype, x, xtype, g, N, K, M, 0, num_cus, st);
-        if (e == hipSuccess) e = launch_batch_matmul(wu, wtype, x, xtype, u, N, K, M, 0, num_cus, st);
+        float* u = (float*)((uint8_t*)ws + align256((size_t)M * N * sizeof(float)));
+        void* gemm_ws = (uint8_t*)ws + 2 * align256((size_t)M * N * sizeof(float));
+        hipError_t e = launch_batch_matmul(wg, wtype, x, xtype, g, N, K, M, 0, num_cus, gemm_ws, st);
+        if (e == hipSuccess) e = launch_batch_matmul(wu, wtype, x, xtype, u, N, K, M, 0, num_cus, gemm_ws, st);
         if (e != hipSuccess) return e;
         const size_t n = (size_t)M * N;
         hipLaunchKernelGGL(swiglu_combine_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, st, g, u, y, n);
@@ -1591,18 +1295,16 @@ hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t w
     }
     const void* x16 = x;
     uint32_t xt = xtype;
+    size_t off = 0;
     if (xtype == kGgmlF32) {  // activations rounded to bf16 once (range of f32 kept)
-        const size_t n4 = (size_t)M * K / 4;
-        hipLaunchKernelGGL(f32_to_bf16_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, st,
-                           (const float*)x, (uint32_t*)ws, n4);
-        hipError_t e = hipGetLastError();
+        hipError_t e = convert_activations(x, xtype, ws, kGgmlBF16, (size_t)M * K, st);
         if (e != hipSuccess) return e;
         x16 = ws;
         xt = kGgmlBF16;
+        off = align256((size_t)M * K * 2u);
     }
     const uint32_t tiles_m = (M + 255) / 256, tiles_n = (N + 127) / 128;
     const uint32_t grid = (uint32_t)min((uint64_t)tiles_m * tiles_n, (uint64_t)num_cus);
-    if (wtype != kGgmlQ8_0) return hipErrorInvalidValue;
     PersistArgs a{};
     a.p[0] = PersistProblem{(const uint8_t*)wg, x16, y, nullptr, nullptr, M, 0u, tiles_m};
     a.W2 = (const uint8_t*)wu;
@@ -1612,6 +1314,14 @@ hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t w
     a.tiles_n = tiles_n;
     a.epi = kEpiStore;
     a.ldy = N;
+    if (M >= kW16MinTokens) {
+        void* img = (uint8_t*)ws + off;
+        hipError_t e = launch_w16_image(wg, wu, wtype, xt, img, N, K, 0u, st);
+        if (e != hipSuccess) return e;
+        a.p[0].W = (const uint8_t*)img;
+        a.W2 = nullptr;
+        return launch_w16_gemm(a, xt, true, false, num_cus, st);
+    }
     if (xt == kGgmlF16)
         hipLaunchKernelGGL((gemm_q_persist<kGgmlQ8_0, kGgmlF16, true>), dim3(grid), dim3(256), 0, st, a);
     else
@@ -1621,13 +1331,53 @@ hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t w
 
 hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uint32_t xtype,
                                float* y, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,
-                               uint32_t row_offset, int num_cus, hipStream_t st) {
+                               uint32_t row_offset, int num_cus, void* ws, hipStream_t st) {
     if (seq_len == 0 || out_dim == 0) return hipSuccess;
-    if (wtype == kGgmlQ4K && seq_len <= kGemvMaxTokens)
-        return launch_gemv_q4k(w, xtype, x, y, out_dim, in_dim, seq_len, row_offset, st);
-    if (wtype == kGgmlQ8_0)
-        return dispatch_w<kGgmlQ8_0>(w, xtype, x, y, out_dim, in_dim, seq_len, row_offset, num_cus, st);
-    return dispatch_w<kGgmlQ4K>(w, xtype, x, y, out_dim, in_dim, seq_len, row_offset, num_cus, st);
+    const uint32_t N = out_dim, K = in_dim, M = seq_len;
+    if (wtype == kGgmlQ4K && M <= kGemvMaxTokens)
+        return launch_gemv_q4k(w, xtype, x, y, N, K, M, row_offset, st);
+    const GemmPlan pl = plan_gemm(wtype, xtype, N, K, M, num_cus);
+    if (!pl.persistent) {
+        if (wtype == kGgmlQ8_0) return dispatch_w<kGgmlQ8_0>(w, xtype, x, y, N, K, M, row_offset, num_cus, st);
+        return dispatch_w<kGgmlQ4K>(w, xtype, x, y, N, K, M, row_offset, num_cus, st);
+    }
+    const void* x16 = x;
+    if (pl.convert_x) {
+        x16 = (uint8_t*)ws + pl.x16_off;
+        hipError_t e = convert_activations(x, xtype, (void*)x16, pl.xt, (size_t)M * K, st);
+        if (e != hipSuccess) return e;
+    }
+    const uint32_t tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+    const uint32_t grid = (uint32_t)min((uint64_t)tiles_m * tiles_n, (uint64_t)num_cus);
+    PersistArgs a{};
+    a.p[0] = PersistProblem{(const uint8_t*)w, x16, y, nullptr, nullptr, M, row_offset, tiles_m};
+    a.N = N;
+    a.K = K;
+    a.tiles_m = tiles_m;
+    a.tiles_n = tiles_n;
+    a.epi = kEpiStore;
+    a.ldy = N;
+    if (pl.two_pass) {
+        void* img = (uint8_t*)ws + pl.img_off;
+        hipError_t e = launch_w16_image(w, nullptr, wtype, pl.xt, img, N, K, row_offset, st);
+        if (e != hipSuccess) return e;
+        a.p[0].W = (const uint8_t*)img;
+        return launch_w16_gemm(a, pl.xt, false, false, num_cus, st);
+    }
+    // Q8_0 on the 8-wave kernel (its half-row dequantization is lighter than
+    // Q4_K's and it measures faster); Q4_K on the 4-wave one
+    if (wtype == kGgmlQ8_0) {
+        if (pl.xt == kGgmlF16)
+            hipLaunchKernelGGL((gemm_q_persist8<kGgmlQ8_0, kGgmlF16>), dim3(grid), dim3(512), 0, st, a);
+        else
+            hipLaunchKernelGGL((gemm_q_persist8<kGgmlQ8_0, kGgmlBF16>), dim3(grid), dim3(512), 0, st, a);
+    } else {
+        if (pl.xt == kGgmlF16)
+            hipLaunchKernelGGL((gemm_q_persist<kGgmlQ4K, kGgmlF16, false>), dim3(grid), dim3(256), 0, st, a);
+        else
+            hipLaunchKernelGGL((gemm_q_persist<kGgmlQ4K, kGgmlBF16, false>), dim3(grid), dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
 }
 
 namespace {
@@ -1639,7 +1389,7 @@ namespace {
 bool multi_persistent(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n,
                       int num_cus) {
     if (xtype == kGgmlF32 || N % 4 || K % kBK) return false;
-    const uint64_t rb = (wtype == kGgmlQ8_0) ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * 144;
+    const uint64_t rb = row_bytes_of(wtype, K);
     uint64_t tiles = 0;
     for (uint32_t i = 0; i < n; i++) {
         if ((uint64_t)jobs[i].M * K * 2u >= (1ull << 31) || (uint64_t)N * rb >= (1ull << 31)) return false;
@@ -1648,9 +1398,15 @@ bool multi_persistent(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, co
     return 2 * tiles >= (uint64_t)num_cus;
 }
 
-template <uint32_t WT, uint32_t XT>
-hipError_t launch_persist_multi(uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n, const GemmEpilogue& epi,
-                                int num_cus, hipStream_t st) {
+// Whether a persistent job group runs two-pass (weight images): as a single
+// GEMM, by its total tokens.
+bool multi_two_pass(const GemmJob* jobs, uint32_t n) {
+    uint64_t m = 0;
+    for (uint32_t i = 0; i < n; i++) m += jobs[i].M;
+    return m >= kW16MinTokens;
+}
+
+PersistArgs multi_args(uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n, const GemmEpilogue& epi) {
     PersistArgs a{};
     const uint32_t tiles_n = (N + 255) / 256;
     uint32_t tiles_m = 0;
@@ -1669,16 +1425,21 @@ hipError_t launch_persist_multi(uint32_t N, uint32_t K, const GemmJob* jobs, uin
     a.ldy2 = epi.ldy2;
     a.split = epi.kind == kEpiSplitGelu ? epi.split : N;
     a.y2_bf16 = epi.y2_type == kGgmlBF16 ? 1u : 0u;
-    const uint32_t grid = (uint32_t)min((uint64_t)tiles_m * tiles_n, (uint64_t)num_cus);
+    return a;
+}
+
+template <uint32_t WT, uint32_t XT>
+hipError_t launch_persist_multi(const PersistArgs& a, int num_cus, hipStream_t st) {
+    const uint32_t grid = (uint32_t)min((uint64_t)a.tiles_m * a.tiles_n, (uint64_t)num_cus);
     if constexpr (WT == kGgmlQ8_0) {
-        auto kern = epi.kind == kEpiResidual    ? gemm_q_persist8<WT, XT, kEpiResidual, true>
-                    : epi.kind == kEpiSplitGelu ? gemm_q_persist8<WT, XT, kEpiSplitGelu, true>
-                                                : gemm_q_persist8<WT, XT, kEpiStore, true>;
+        auto kern = a.epi == kEpiResidual    ? gemm_q_persist8<WT, XT, kEpiResidual, true>
+                    : a.epi == kEpiSplitGelu ? gemm_q_persist8<WT, XT, kEpiSplitGelu, true>
+                                             : gemm_q_persist8<WT, XT, kEpiStore, true>;
         hipLaunchKernelGGL(kern, dim3(grid), dim3(512), 0, st, a);
     } else {
-        auto kern = epi.kind == kEpiResidual    ? gemm_q_persist<WT, XT, false, kEpiResidual, true>
-                    : epi.kind == kEpiSplitGelu ? gemm_q_persist<WT, XT, false, kEpiSplitGelu, true>
-                                                : gemm_q_persist<WT, XT, false, kEpiStore, true>;
+        auto kern = a.epi == kEpiResidual    ? gemm_q_persist<WT, XT, false, kEpiResidual, true>
+                    : a.epi == kEpiSplitGelu ? gemm_q_persist<WT, XT, false, kEpiSplitGelu, true>
+                                             : gemm_q_persist<WT, XT, false, kEpiStore, true>;
         hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, st, a);
     }
     return hipGetLastError();
@@ -1686,12 +1447,12 @@ hipError_t launch_persist_multi(uint32_t N, uint32_t K, const GemmJob* jobs, uin
 
 // One job the persistent kernel does not take: the plain GEMM into the
 // workspace `t` (directly into the output for an unstrided store), then
-// the epilogue as glue passes.
+// the epilogue as glue passes. `gemm_ws` is the GEMM's own workspace.
 hipError_t run_job_fallback(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob& j,
-                            const GemmEpilogue& epi, int num_cus, float* t, hipStream_t st) {
+                            const GemmEpilogue& epi, int num_cus, float* t, void* gemm_ws, hipStream_t st) {
     if (epi.kind == kEpiStore && epi.ldy == N)
-        return launch_batch_matmul(j.w, wtype, j.x, xtype, j.y, N, K, j.M, j.row_offset, num_cus, st);
-    hipError_t e = launch_batch_matmul(j.w, wtype, j.x, xtype, t, N, K, j.M, j.row_offset, num_cus, st);
+        return launch_batch_matmul(j.w, wtype, j.x, xtype, j.y, N, K, j.M, j.row_offset, num_cus, gemm_ws, st);
+    hipError_t e = launch_batch_matmul(j.w, wtype, j.x, xtype, t, N, K, j.M, j.row_offset, num_cus, gemm_ws, st);
     if (e != hipSuccess) return e;
     if (epi.kind == kEpiResidual) {
         const ResidualArgs r{j.y, t, nullptr, j.gate, epi.ldy, N, j.M, N, 0.0f};
@@ -1709,17 +1470,35 @@ hipError_t run_job_fallback(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t
     return e;
 }
 
+// Workspace of the fallback jobs: the largest job's f32 result (when the
+// epilogue is not a plain store), then the largest GEMM workspace.
+size_t fallback_t_bytes(uint32_t N, const GemmJob* jobs, uint32_t n_jobs, const GemmEpilogue& epi,
+                        uint32_t wtype, uint32_t xtype, uint32_t K, int num_cus) {
+    size_t t = 0;
+    for (uint32_t i = 0; i < n_jobs; i += 2) {
+        const uint32_t n = min(2u, n_jobs - i);
+        if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) continue;
+        if (epi.kind == kEpiStore && epi.ldy == N) continue;
+        for (uint32_t q = i; q < i + n; q++) t = max(t, align256((size_t)jobs[q].M * N * sizeof(float)));
+    }
+    return t;
+}
+
 }  // namespace
 
 size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K,
                                           const GemmJob* jobs, uint32_t n_jobs, const GemmEpilogue& epi,
                                           int num_cus) {
+    const size_t t = fallback_t_bytes(N, jobs, n_jobs, epi, wtype, xtype, K, num_cus);
     size_t need = 0;
     for (uint32_t i = 0; i < n_jobs; i += 2) {
         const uint32_t n = min(2u, n_jobs - i);
-        if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) continue;
-        if (epi.kind == kEpiStore && epi.ldy == N) continue;
-        for (uint32_t q = i; q < i + n; q++) need = max(need, (size_t)jobs[q].M * N * sizeof(float));
+        if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) {
+            if (multi_two_pass(jobs + i, n)) need = max(need, n * w16_image_bytes(N, K, false));
+            continue;
+        }
+        for (uint32_t q = i; q < i + n; q++)
+            need = max(need, t + batch_matmul_workspace_bytes(wtype, xtype, N, K, jobs[q].M, num_cus));
     }
     return need;
 }
@@ -1733,19 +1512,32 @@ hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N,
         const hipError_t e = launch_gemv_q4k_multi(xtype, jobs, n_jobs, N, K, epi.ldy, st);
         if (e != hipErrorNotSupported) return e;
     }
+    const size_t t_bytes = fallback_t_bytes(N, jobs, n_jobs, epi, wtype, xtype, K, num_cus);
     for (uint32_t i = 0; i < n_jobs; i += 2) {
         const uint32_t n = min(2u, n_jobs - i);
         hipError_t e = hipSuccess;
         if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) {
-            if (wtype == kGgmlQ8_0)
-                e = xtype == kGgmlF16 ? launch_persist_multi<kGgmlQ8_0, kGgmlF16>(N, K, jobs + i, n, epi, num_cus, st)
-                                      : launch_persist_multi<kGgmlQ8_0, kGgmlBF16>(N, K, jobs + i, n, epi, num_cus, st);
-            else
-                e = xtype == kGgmlF16 ? launch_persist_multi<kGgmlQ4K, kGgmlF16>(N, K, jobs + i, n, epi, num_cus, st)
-                                      : launch_persist_multi<kGgmlQ4K, kGgmlBF16>(N, K, jobs + i, n, epi, num_cus, st);
+            PersistArgs a = multi_args(N, K, jobs + i, n, epi);
+            if (multi_two_pass(jobs + i, n)) {
+                const size_t img_bytes = w16_image_bytes(N, K, false);
+                for (uint32_t q = 0; q < n && e == hipSuccess; q++) {
+                    void* img = (uint8_t*)ws + q * img_bytes;
+                    e = launch_w16_image(jobs[i + q].w, nullptr, wtype, xtype, img, N, K, jobs[i + q].row_offset,
+                                         st);
+                    a.p[q].W = (const uint8_t*)img;
+                }
+                if (e == hipSuccess) e = launch_w16_gemm(a, xtype, false, n == 2, num_cus, st);
+            } else if (wtype == kGgmlQ8_0) {
+                e = xtype == kGgmlF16 ? launch_persist_multi<kGgmlQ8_0, kGgmlF16>(a, num_cus, st)
+                                      : launch_persist_multi<kGgmlQ8_0, kGgmlBF16>(a, num_cus, st);
+            } else {
+                e = xtype == kGgmlF16 ? launch_persist_multi<kGgmlQ4K, kGgmlF16>(a, num_cus, st)
+                                      : launch_persist_multi<kGgmlQ4K, kGgmlBF16>(a, num_cus, st);
+            }
         } else {
             for (uint32_t q = i; q < i + n && e == hipSuccess; q++)
-                e = run_job_fallback(wtype, xtype, N, K, jobs[q], epi, num_cus, (float*)ws, st);
+                e = run_job_fallback(wtype, xtype, N, K, jobs[q], epi, num_cus, (float*)ws,
+                                     (uint8_t*)ws + t_bytes, st);
         }
         if (e != hipSuccess) return e;
     }

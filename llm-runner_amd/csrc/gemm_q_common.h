@@ -1,0 +1,372 @@
+// gemm_q_common.h - pieces shared by the persistent dequant-GEMM kernels
+// (gemm_q.hip) and the two-pass GEMM (gemm_w16.hip): the LDS tile layout,
+// the 32x32x16 MFMA on 16-bit operands, the per-row weight dequantization
+// of one 64-wide K stage, the tile order and the epilogue arguments.
+#pragma once
+
+#include <type_traits>
+
+#include "llmr_device.h"
+#include "llmr_internal.h"
+
+namespace llmr {
+
+// One GEMM of a persistent launch. A launch multiplies up to two problems
+// that share N and K (e.g. the text and image rows of a block with their own
+// weights); their 256-row tiles are stacked along M, problem 0 first.
+struct PersistProblem {
+    const uint8_t* W;   // weight blocks; row row_offset is output feature 0
+    const void* X;      // [M, K] 16-bit activations
+    float* Y;           // f32 output (kEpiResidual: read and updated)
+    const float* gate;  // kEpiResidual: [N] or null
+    void* Y2;           // kEpiSplitGelu: 16-bit output
+    uint32_t M, row_offset, tiles_m;
+};
+struct PersistArgs {
+    PersistProblem p[2];
+    const uint8_t* W2;  // SwiGLU: the up weight (p[0].W is the gate)
+    uint32_t N, K, tiles_m, tiles_n;  // tiles_m of both problems
+    uint32_t epi, ldy, ldy2, split, y2_bf16;
+};
+
+// The persistent all-DMA GEMM over weight images (gemm_w16.hip): p[i].W is
+// the image of problem i (launch_w16_image); swiglu: one 128-feature SwiGLU
+// image; grouped: two problems.
+hipError_t launch_w16_gemm(const PersistArgs& a, uint32_t xtype, bool swiglu, bool grouped, int num_cus,
+                           hipStream_t st);
+
+namespace {
+
+constexpr int kBK = 64;  // K per stage
+
+// Bank swizzle of 128-byte LDS rows (eight 16-byte chunks): chunk c of row r
+// sits at physical chunk c ^ lds_swz(r). A 16-byte fragment read touches one
+// chunk of consecutive rows; lds_swz gives any 8 consecutive rows (one
+// 128-byte bank line each) 8 distinct chunk positions, and the 8 even and the
+// 8 odd rows of any 16 consecutive ones (two rows per 256-byte line of the
+// 64 banks) 8 distinct positions each, so the read is conflict-free whether
+// the hardware serves 8 or 16 lanes of a 16-byte access per cycle.
+__device__ __forceinline__ uint32_t lds_swz(uint32_t r) { return (r & 7u) ^ ((r >> 3) & 1u); }
+__device__ __forceinline__ uint32_t lds_off(uint32_t r, uint32_t c) {
+    return r * 128u + ((c ^ lds_swz(r)) << 4);
+}
+
+// 32x32x16 MFMA on 16-bit operand bits: bf16 operands for bf16 activations
+// (fp16 cannot hold bf16's range), fp16 otherwise.
+template <uint32_t XT>
+__device__ __forceinline__ f32x16 mfma16(f16x8 a, f16x8 b, f32x16 c) {
+    if constexpr (XT == kGgmlBF16) {
+        typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+}
+
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t bload4(rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+// Eight Q8_0 quants (two dwords) -> one 16-byte chunk of fp16 operands RN16(d*q).
+__device__ __forceinline__ u32x4 q8x8_f16(uint32_t q0, uint32_t q1, f16x2 d2) {
+    const f16x4 lo = q8x4_to_f16(q0, d2), hi = q8x4_to_f16(q1, d2);
+    return __builtin_bit_cast(u32x4, f16x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w});
+}
+
+// Tile order: in every full round of G = gridDim.x tiles the 32 workgroups
+// one XCD runs (dispatch is round-robin over the 8 XCDs) get 32 consecutive
+// indices, which the group-of-4-tile-rows order turns into a 4 x 8 block of
+// tiles (4 x 256 activation rows and 8 x 256 weight rows shared in the XCD's L2).
+__device__ __forceinline__ void map_tile_persist(uint32_t T, uint32_t G, uint32_t tiles_m, uint32_t tiles_n,
+                                                 uint32_t& tm, uint32_t& tn) {
+    constexpr uint32_t kXcd = 8, kGroupM = 4;
+    const uint32_t total = tiles_m * tiles_n;
+    uint32_t L = T;
+    if (G % kXcd == 0 && T / G < total / G) {
+        const uint32_t b = T % G;
+        L = (T - b) + (b % kXcd) * (G / kXcd) + b / kXcd;
+    }
+    const uint32_t per_group = kGroupM * tiles_n;
+    const uint32_t g = L / per_group;
+    const uint32_t first_m = g * kGroupM;
+    const uint32_t gsize = min(tiles_m - first_m, kGroupM);
+    const uint32_t in = L % per_group;
+    tm = first_m + in % gsize;
+    tn = in / gsize;
+}
+
+// Bytes 0,1 (SEL_LO) or 2,3 (SEL_HI) of `w` as two fp16 subnormals b * 2^-24
+// (exact: the byte is the mantissa of a zero-exponent half), so one mixed
+// FMA with a scale pre-multiplied by 2^24 forms scale * b + bias exactly
+// before its single rounding - no bias subtraction of the 1024+b encoding.
+constexpr uint32_t kSelLo = 0x0c010c00u, kSelHi = 0x0c030c02u;
+__device__ __forceinline__ f16x2 sub16x2(uint32_t w, uint32_t sel) {
+    return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0u, w, sel));
+}
+// Two operands RN(s * h + b) of type OT from the two halves of h, packed.
+template <uint32_t OT>
+__device__ __forceinline__ uint32_t fma_pair(f16x2 h, float s, float b) {
+    if constexpr (OT == kGgmlBF16) {
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+        bf16x2_t r;
+        r.x = (__bf16)__builtin_fmaf((float)h.x, s, b);
+        r.y = (__bf16)__builtin_fmaf((float)h.y, s, b);
+        return __builtin_bit_cast(uint32_t, r);
+    } else {
+        f16x2 r;
+        r.x = (_Float16)__builtin_fmaf((float)h.x, s, b);
+        r.y = (_Float16)__builtin_fmaf((float)h.y, s, b);
+        return __builtin_bit_cast(uint32_t, r);
+    }
+}
+
+template <uint32_t WT, uint32_t OT>
+struct WRow;
+
+// Q4_K row stage s: quarter s % 4 of superblock s / 4 = the 16-byte header
+// and qs bytes [32 (s%4), +32): low nibbles are k 0..31 of the stage
+// (sub-block 2j), high nibbles k 32..63 (sub-block 2j+1).
+// The dequantization is split in four parts (one per 16-wide k step of the
+// stage it overlaps): part p writes LDS chunks p and 4+p of the row.
+template <uint32_t OT>
+struct WRow<kGgmlQ4K, OT> {
+    static constexpr int kLoads = 3;
+    u32x4 hdr, qa, qb;
+    template <int L>
+    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t s) {
+        const uint32_t sh = (s >> 2) * 144u;
+        const uint32_t sq = sh + 16u + 32u * (s & 3u);
+        if constexpr (L == 0) hdr = bload16(r, voff, sh);
+        if constexpr (L == 1) qa = bload16(r, voff, sq);
+        if constexpr (L == 2) qb = bload16(r, voff + 16u, sq);
+    }
+    // Operand = RN(d*sc*q - dmin*mn) (products exact, one rounding): low
+    // nibbles are read as q * 2^-24, high nibbles (masked in place) as
+    // 16 q * 2^-24, so their scales carry 2^24 and 2^20.
+    struct Scale {
+        float s0, b0, s1, b1;
+    };
+    __device__ __forceinline__ Scale scale(uint32_t s) const {
+        const uint32_t j = s & 3u;
+        const float d = f16_bits_to_f32(hdr.x & 0xffffu);
+        const float dmin = f16_bits_to_f32(hdr.x >> 16);
+        uint32_t sc0, mn0, sc1, mn1;
+        q4k_scale_min(2 * j, hdr.y, hdr.z, hdr.w, sc0, mn0);
+        q4k_scale_min(2 * j + 1, hdr.y, hdr.z, hdr.w, sc1, mn1);
+        return Scale{d * (float)sc0 * 16777216.0f, -(dmin * (float)mn0), d * (float)sc1 * 1048576.0f,
+                     -(dmin * (float)mn1)};
+    }
+    // `base` = LDS offset of chunk 0 of the row; chunk c is at base ^ (c << 4)
+    template <int P>
+    __device__ __forceinline__ void store(uint8_t* lds, const Scale& c, uint32_t base) const {
+        const uint32_t w0 = P < 2 ? qa[2 * P] : qb[2 * P - 4];
+        const uint32_t w1 = P < 2 ? qa[2 * P + 1] : qb[2 * P - 3];
+        const uint32_t l0 = w0 & 0x0f0f0f0fu, l1 = w1 & 0x0f0f0f0fu;
+        const uint32_t h0 = w0 & 0xf0f0f0f0u, h1 = w1 & 0xf0f0f0f0u;
+        const u32x4 lo = {fma_pair<OT>(sub16x2(l0, kSelLo), c.s0, c.b0), fma_pair<OT>(sub16x2(l0, kSelHi), c.s0, c.b0),
+                          fma_pair<OT>(sub16x2(l1, kSelLo), c.s0, c.b0), fma_pair<OT>(sub16x2(l1, kSelHi), c.s0, c.b0)};
+        const u32x4 hi = {fma_pair<OT>(sub16x2(h0, kSelLo), c.s1, c.b1), fma_pair<OT>(sub16x2(h0, kSelHi), c.s1, c.b1),
+                          fma_pair<OT>(sub16x2(h1, kSelLo), c.s1, c.b1), fma_pair<OT>(sub16x2(h1, kSelHi), c.s1, c.b1)};
+        *(u32x4*)(lds + (base ^ ((uint32_t)P << 4))) = lo;
+        *(u32x4*)(lds + (base ^ ((uint32_t)(4 + P) << 4))) = hi;
+    }
+};
+
+// Q8_0 row stage s: blocks 2s and 2s+1 = bytes [68 s, 68 s + 68) of the row
+// (dword-aligned: K % 64 == 0). Block 0: scale in the low half of dword 0,
+// quants from byte 2 (chunks 0..3); block 1: scale in the high half of dword
+// 8, quants in dwords 9..16 (chunks 4..7). Part p writes chunks p and 4+p.
+template <uint32_t OT>
+struct WRow<kGgmlQ8_0, OT> {
+    static constexpr int kLoads = 5;
+    u32x4 a, b, c, d;
+    uint32_t e;
+    template <int L>
+    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t s) {
+        const uint32_t so = 68u * s;
+        if constexpr (L == 0) a = bload16(r, voff, so);
+        if constexpr (L == 1) b = bload16(r, voff + 16u, so);
+        if constexpr (L == 2) c = bload16(r, voff + 32u, so);
+        if constexpr (L == 3) d = bload16(r, voff + 48u, so);
+        if constexpr (L == 4) e = bload4(r, voff + 64u, so);
+    }
+    struct Scale {
+        float s0, b0, s1, b1;  // bf16: (2^24 d, -128 d) per block; f16: (d, -) per block
+    };
+    __device__ __forceinline__ Scale scale(uint32_t s) const {
+        (void)s;
+        const float d0 = f16_bits_to_f32(a.x & 0xffffu);
+        const float d1 = f16_bits_to_f32(c.x >> 16);
+        if constexpr (OT == kGgmlBF16)
+            return Scale{d0 * 16777216.0f, -128.0f * d0, d1 * 16777216.0f, -128.0f * d1};
+        else
+            return Scale{d0, 0.0f, d1, 0.0f};
+    }
+    __device__ __forceinline__ uint32_t word(int i) const {
+        return i < 4 ? a[i] : i < 8 ? b[i - 4] : i < 12 ? c[i - 8] : i < 16 ? d[i - 12] : e;
+    }
+    // chunk ch of the stage from its two quant dwords q0, q1
+    __device__ __forceinline__ u32x4 chunk(uint32_t q0, uint32_t q1, float sc, float bi) const {
+        if constexpr (OT == kGgmlBF16) {
+            // RN_bf16(d*q): q + 128 read as a subnormal half, d*q = (2^24 d) h - 128 d
+            // exactly in f32, then one rounding to bf16
+            const uint32_t u0 = q0 ^ 0x80808080u, u1 = q1 ^ 0x80808080u;
+            return u32x4{fma_pair<OT>(sub16x2(u0, kSelLo), sc, bi), fma_pair<OT>(sub16x2(u0, kSelHi), sc, bi),
+                         fma_pair<OT>(sub16x2(u1, kSelLo), sc, bi), fma_pair<OT>(sub16x2(u1, kSelHi), sc, bi)};
+        } else {
+            const _Float16 h = (_Float16)sc;
+            return q8x8_f16(q0, q1, f16x2{h, h});
+        }
+    }
+    template <int P>
+    __device__ __forceinline__ void store(uint8_t* lds, const Scale& k, uint32_t base) const {
+        const uint32_t q0 = __builtin_amdgcn_alignbyte(word(2 * P + 1), word(2 * P), 2);
+        const uint32_t q1 = __builtin_amdgcn_alignbyte(word(2 * P + 2), word(2 * P + 1), 2);
+        *(u32x4*)(lds + (base ^ ((uint32_t)P << 4))) = chunk(q0, q1, k.s0, k.b0);
+        *(u32x4*)(lds + (base ^ ((uint32_t)(4 + P) << 4))) = chunk(word(9 + 2 * P), word(10 + 2 * P), k.s1, k.b1);
+    }
+};
+
+
+// Schedule of one 16-wide k step inside a stage: its 16 MFMAs each followed
+// by a share of the stage's other work, so that work issues while the
+// matrix core is busy (on gfx950 a wave's VALU, LDS and buffer instructions
+// co-issue with its own MFMAs): the next step's fragment reads after the
+// first eight MFMAs, three VALU (the weight dequantization) after every one,
+// the two LDS writes of the dequantized weight chunks and the step's share
+// of the buffer loads spread in between.
+#define LLMR_SGB(mask, n) __builtin_amdgcn_sched_group_barrier(mask, n, 0)
+#define LLMR_SLOT_R LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x002, 3)
+#define LLMR_SLOT_V LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 3)
+#define LLMR_SLOT_L LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 3); LLMR_SGB(0x020, 1)
+#define LLMR_SLOT_W LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 3); LLMR_SGB(0x200, 1)
+#define LLMR_SLOT_RA LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x002, 5)
+#define LLMR_SLOT_VA LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 5)
+#define LLMR_SLOT_LA LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 5); LLMR_SGB(0x020, 1)
+#define LLMR_SLOT_WA LLMR_SGB(0x008, 1); LLMR_SGB(0x002, 5); LLMR_SGB(0x200, 1)
+// the first step of a stage also computes the dequantization scales
+#define LLMR_STEP_SCHEDULE_A                                                                \
+    LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_RA;       \
+    LLMR_SLOT_RA; LLMR_SLOT_RA; LLMR_SLOT_LA; LLMR_SLOT_VA; LLMR_SLOT_WA; LLMR_SLOT_LA;       \
+    LLMR_SLOT_VA; LLMR_SLOT_WA; LLMR_SLOT_LA; LLMR_SLOT_LA
+#define LLMR_STEP_SCHEDULE                                                                  \
+    LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_R;             \
+    LLMR_SLOT_R; LLMR_SLOT_R; LLMR_SLOT_L; LLMR_SLOT_V; LLMR_SLOT_W; LLMR_SLOT_L;             \
+    LLMR_SLOT_V; LLMR_SLOT_W; LLMR_SLOT_L; LLMR_SLOT_L
+
+struct Frags {
+    f16x8 x[4], w[4];
+};
+
+// silu(g) = g / (1 + e^-g) (llm.slang:1903), e^-g as 2^(-g log2 e)
+__device__ __forceinline__ float silu(float g) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
+
+// gelu (tanh form, lib/shaders/diffusion.slang:1103-1107) as
+// 0.5 x (1 + tanh(u)) = x / (1 + e^(-2u)), u = 0.7978845608 (x + 0.044715 x^3)
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float u = 0.7978845608f * (x + 0.044715f * x * x * x);
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * u));
+}
+
+// Output of the persistent kernel's tile accumulators (host-selected):
+//   kEpiStore      Y[m, n] = acc
+//   kEpiResidual   Y[m, n] += gate[n] * acc  (gate 1 when null)
+//   kEpiSplitGelu  n < split: Y[m, n] = acc; n >= split: Y2[m, n - split] =
+//                  16-bit gelu(acc)   (split % 8 == 0)
+// with row strides ldy (Y) and ldy2 (Y2).
+constexpr uint32_t kEpiStore = 0, kEpiResidual = 1, kEpiSplitGelu = 2;
+
+template <typename T>
+__device__ __forceinline__ T pick(uint32_t p, T a, T b) {
+    return p ? b : a;
+}
+
+
+// Stores (through the epilogue EPI) and clears the accumulators of one
+// 256 x 256 tile of the 4-wave persistent kernels: wave (wm, wn) holds
+// tokens m0 + 128 wm + 32 b + l32 and features n0 + 128 wn + 32 a + 8 g +
+// 4 kh + 0..3 in acc[a][b][4 g .. 4 g + 3]. SW: a 128-feature SwiGLU tile,
+// acc[a] (gate) and acc[a + 2] (up) of the same features, y = silu(g) * u.
+// N % 4 == 0 (host-checked): a lane's four consecutive features are all in
+// range or none. nw = n - 4 kh is the same for the whole wave; with split %
+// 8 == 0 (host-checked) nw < split decides the side of split for both kh, as
+// a uniform branch.
+template <bool SW, uint32_t EPI>
+__device__ __forceinline__ void store_tile_256(f32x16 (&acc)[4][4], float* Y, const float* gate, void* Y2v,
+                                               uint32_t M, uint32_t N, uint32_t m0, uint32_t n0, uint32_t wm,
+                                               uint32_t wn, uint32_t l32, uint32_t kh, uint32_t ldy, uint32_t ldy2,
+                                               uint32_t split, uint32_t y2_bf16) {
+    if constexpr (SW) {
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint32_t m = m0 + wm * 128u + b * 32u + l32;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const uint32_t n = n0 + wn * 64u + a * 32u + 8u * g + 4u * kh;
+                    f32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = silu(acc[a][b][4 * g + e]) * acc[a + 2][b][4 * g + e];
+                    if (m < M && n < N) *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
+                }
+                acc[a][b] = f32x16{};
+                acc[a + 2][b] = f32x16{};
+            }
+        return;
+    }
+    auto each = [&](auto&& f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint32_t m = m0 + wm * 128u + b * 32u + l32;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const uint32_t nw = n0 + wn * 128u + a * 32u + 8u * g;
+                    const uint32_t n = nw + 4u * kh;
+                    if (m < M && n < N)
+                        f(m, n, nw, f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2],
+                                          acc[a][b][4 * g + 3]});
+                }
+                acc[a][b] = f32x16{};
+            }
+    };
+    if constexpr (EPI == kEpiResidual) {
+        each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
+            f32x4* const h = (f32x4*)(Y + (uint64_t)m * ldy + n);
+            const f32x4 gv = gate ? *(const f32x4*)(gate + n) : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+            *h = *h + gv * v;
+        });
+    } else if constexpr (EPI == kEpiSplitGelu) {
+        uint16_t* const Y2 = (uint16_t*)Y2v;
+        each([&](uint32_t m, uint32_t n, uint32_t nw, f32x4 v) __attribute__((always_inline)) {
+            if (nw < split) {
+                *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
+            } else {
+                const f32x4 gl{gelu_tanh(v.x), gelu_tanh(v.y), gelu_tanh(v.z), gelu_tanh(v.w)};
+                u32x2 o;
+                if (y2_bf16) {
+                    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+                    o.x = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.x, (__bf16)gl.y});
+                    o.y = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.z, (__bf16)gl.w});
+                } else {
+                    o = u32x2{pack_f16x2(gl.x, gl.y), pack_f16x2(gl.z, gl.w)};
+                }
+                *(u32x2*)(Y2 + (uint64_t)m * ldy2 + (n - split)) = o;
+            }
+        });
+    } else {
+        each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
+            *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
+        });
+    }
+}
+
+}  // namespace
+}  // namespace llmr

@@ -1,0 +1,394 @@
+// gemm_w16.hip - the two-pass dequant-GEMM for many tokens.
+//
+//   Y[m, n] = sum_k X[m, k] * W[row_offset + n, k]     (f32 out)
+//
+// Same operands and the same MFMA order as the fused persistent kernel
+// (gemm_q_persist): the result is bit-identical. What differs is where the
+// dequantization happens. The fused kernel dequantizes a weight tile once per
+// 256-token tile it multiplies, inside its stage loop, where the VALU work
+// and the register staging of the packed bytes compete with the MFMAs of the
+// same wave. With thousands of tokens each weight row is dequantized M / 256
+// times (18 times at M = 4608). Here:
+//   pass 1 (w16_image_kernel) dequantizes every weight element once into a
+//          16-bit image of the weight, laid out exactly as the GEMM's LDS
+//          tiles: for each 256-row panel and each 64-wide K stage a
+//          contiguous 32 KiB block, row r at r * 128 bytes, 16-byte chunk c
+//          at (c ^ lds_swz(r)) * 16;
+//   pass 2 (gemm_w16_persist) is the persistent 256 x 256 kernel with both
+//          operands copied HBM -> LDS by buffer DMA (the weight block is one
+//          contiguous 32 KiB copy): a stage is 64 MFMAs, 32 fragment reads
+//          and 16 DMAs per wave, no dequantization and no register staging.
+// The image costs N * K * 2 bytes of workspace and one write + one read of
+// it; the dispatcher takes this path when M is large enough for that to pay.
+#include "gemm_q_common.h"
+#include "llmr_device.h"
+#include "llmr_internal.h"
+
+namespace llmr {
+
+namespace {
+
+constexpr uint32_t kBlk = 256u * 128u;  // bytes of one 256-row x 64-wide 16-bit block
+
+// Pass 1. Workgroup (panel p, stage group j), thread r: weight row r of the
+// panel for stages 4j .. 4j+3 (one Q4_K superblock, eight Q8_0 blocks: the
+// row's bytes of the group are read by this one thread, so no other
+// workgroup - on another XCD, with its own L2 - fetches them again),
+// dequantized with the fused kernel's own WRow code (operand type OT: bf16
+// for bf16 activations, fp16 otherwise) into a 32 KiB block in LDS, which
+// the workgroup then copies to image block (p, s) in 16-byte pieces of
+// consecutive addresses (each store instruction writes 1 KiB of whole
+// lines; written straight from the rows, every instruction would touch 64
+// lines). Two LDS blocks alternate, so one barrier per stage suffices. SW:
+// the panel is a 128-feature SwiGLU tile, rows gate 0-63 | up 0-63 | gate
+// 64-127 | up 64-127 (the fused SwiGLU kernel's LDS arrangement). Rows past
+// N read as zero through the descriptor and give zero operands.
+constexpr uint32_t kImgStages = 4;
+template <uint32_t WT, uint32_t OT, bool SW>
+__global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2,
+                                                         uint8_t* __restrict__ img, uint32_t N, uint32_t K,
+                                                         uint32_t row_offset) {
+    __shared__ __attribute__((aligned(16))) uint8_t lblk[2][kBlk];
+    const uint32_t S = K / kBK, groups = (S + kImgStages - 1) / kImgStages;
+    const uint32_t p = blockIdx.x / groups, s0 = (blockIdx.x % groups) * kImgStages, r = threadIdx.x;
+    const uint32_t rb = (WT == kGgmlQ8_0) ? (K / 32u) * 34u : (K / 256u) * 144u;
+    const uint8_t* src;
+    uint32_t n0, row;  // first feature of the panel, this thread's row within it
+    if constexpr (SW) {
+        n0 = 128u * p;
+        const uint32_t q = r >> 6;
+        src = (q & 1u) ? W2 : W;
+        row = (q >> 1) * 64u + (r & 63u);
+    } else {
+        n0 = 256u * p;
+        src = W + (uint64_t)row_offset * rb;
+        row = r;
+    }
+    const rsrc_t rs = make_rsrc(src + (uint64_t)n0 * rb, (uint64_t)(N - n0) * rb);
+    WRow<WT, OT> u[kImgStages];
+#pragma unroll
+    for (uint32_t i = 0; i < kImgStages; i++)
+        if (s0 + i < S)
+            static_for<0, WRow<WT, OT>::kLoads>(
+                [&](auto L) { u[i].template load<decltype(L)::value>(rs, row * rb, s0 + i); });
+    const uint32_t base = r * 128u + (lds_swz(r) << 4);
+#pragma unroll
+    for (uint32_t i = 0; i < kImgStages; i++) {
+        if (s0 + i >= S) break;
+        uint8_t* const lb = lblk[i & 1u];
+        const auto sc = u[i].scale(s0 + i);
+        u[i].template store<0>(lb, sc, base);
+        u[i].template store<1>(lb, sc, base);
+        u[i].template store<2>(lb, sc, base);
+        u[i].template store<3>(lb, sc, base);
+        __syncthreads();
+        u32x4* const dst = (u32x4*)(img + ((uint64_t)p * S + s0 + i) * kBlk);
+#pragma unroll
+        for (uint32_t c = 0; c < kBlk / 16u / 256u; c++) dst[r + 256u * c] = ((const u32x4*)lb)[r + 256u * c];
+    }
+}
+
+// One 16-wide k step of the all-DMA stage: 16 MFMAs, the next step's eight
+// fragment reads after the first eight, the step's four DMAs after the next
+// four.
+#define LLMR16_STEP_SCHEDULE                                                                   \
+    LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1);           \
+    LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1);           \
+    LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1);           \
+    LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1); LLMR_SGB(0x008, 1); LLMR_SGB(0x100, 1);           \
+    LLMR_SGB(0x008, 1); LLMR_SGB(0x020, 1); LLMR_SGB(0x008, 1); LLMR_SGB(0x020, 1);           \
+    LLMR_SGB(0x008, 1); LLMR_SGB(0x020, 1); LLMR_SGB(0x008, 1); LLMR_SGB(0x020, 1);           \
+    LLMR_SGB(0x008, 4)
+
+// Pass 2: the persistent 256 x 256 kernel (tile order, wave layout,
+// fragment reads, MFMA order and epilogues of gemm_q_persist) with the weight
+// operand DMA'd from the image. LDS: five 32 KiB slots, three for the
+// activations (fetched two stages ahead) and two for the weights (one stage
+// ahead: the image blocks are contiguous, and each is shared by the four
+// tile rows an XCD runs at once).
+//   args.p[i].W  the image of problem i (block (panel, stage) at
+//                (panel * K/64 + stage) * 32 KiB); row_offset is unused (the
+//                image starts at the problem's first feature).
+template <uint32_t XT, bool SW, uint32_t EPI = kEpiStore, bool GROUPED = false>
+__global__ void __launch_bounds__(256, 1) gemm_w16_persist(const PersistArgs args) {
+    static_assert(!(SW && GROUPED) && (!SW || EPI == kEpiStore), "SwiGLU launches are single, plain stores");
+    static_assert(XT == kGgmlF16 || XT == kGgmlBF16, "16-bit activations only");
+    const uint32_t N = args.N, K = args.K, tiles_m = args.tiles_m, tiles_n = args.tiles_n;
+    const uint32_t ldy = args.ldy, ldy2 = args.ldy2, split = args.split, y2_bf16 = args.y2_bf16;
+    const uint8_t* const Wp0 = args.p[0].W;
+    const uint8_t* const Wp1 = GROUPED ? args.p[1].W : nullptr;
+    const void* const Xp0 = args.p[0].X;
+    const void* const Xp1 = GROUPED ? args.p[1].X : nullptr;
+    float* const Yp0 = args.p[0].Y;
+    float* const Yp1 = GROUPED ? args.p[1].Y : nullptr;
+    const float* const Gp0 = args.p[0].gate;
+    const float* const Gp1 = GROUPED ? args.p[1].gate : nullptr;
+    void* const Y2p0 = args.p[0].Y2;
+    void* const Y2p1 = GROUPED ? args.p[1].Y2 : nullptr;
+    const uint32_t Mp0 = args.p[0].M, Mp1 = GROUPED ? args.p[1].M : 0u;
+    const uint32_t Tp0 = args.p[0].tiles_m;
+    constexpr uint32_t NT = SW ? 128u : 256u;  // output features per tile
+    constexpr int DMAS = 8;                    // 1 KiB DMAs per wave per operand per stage
+    __shared__ __attribute__((aligned(16))) uint8_t X0[kBlk];
+    __shared__ __attribute__((aligned(16))) uint8_t X1[kBlk];
+    __shared__ __attribute__((aligned(16))) uint8_t X2[kBlk];
+    __shared__ __attribute__((aligned(16))) uint8_t W0[kBlk];
+    __shared__ __attribute__((aligned(16))) uint8_t W1[kBlk];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t l32 = lane & 31u, kh = lane >> 5;
+    const uint32_t wm = wave & 1u, wn = wave >> 1;
+
+    const uint32_t G = gridDim.x, total = tiles_m * tiles_n;
+    const uint32_t n_tiles = (total - blockIdx.x + G - 1) / G;  // >= 1: grid <= total
+    const uint32_t S = K / kBK;
+    const uint32_t SP = (S + 5u) / 6u * 6u;
+    const uint32_t xrow = K * 2u;
+    const uint32_t panel = S * kBlk;  // image bytes of one 256-row panel
+
+    // activation DMA i of wave w: rows 64w + 8i + lane/8, physical chunk
+    // lane%8, logical chunk (lane%8) ^ lds_swz(row); weight DMA i of wave w:
+    // bytes 8192 w + 1024 i + 16 lane of the block, copied as they are
+    uint32_t xvoff[DMAS];
+#pragma unroll
+    for (int i = 0; i < DMAS; i++) {
+        const uint32_t row = 64u * wave + 8u * i + (lane >> 3);
+        const uint32_t c = (lane & 7u) ^ lds_swz(row);
+        xvoff[i] = row * xrow + c * 16u;
+    }
+    const uint32_t wvoff = wave * 8192u + lane * 16u;
+    uint32_t xoff[4], woff[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t ch = 4u * (t >> 1) + 2u * kh + (t & 1);
+        xoff[t] = lds_off(wm * 128u + l32, ch);
+        woff[t] = lds_off(wn * 128u + l32, ch);
+    }
+
+    struct Cursor {
+        uint32_t s;               // stage within the tile
+        const uint8_t* base;      // the tile's first activation row / its image panel
+        uint32_t size;            // bytes readable from base (0 past the last tile)
+    };
+    auto tile_origin = [&](uint32_t k, uint32_t& p, uint32_t& m0, uint32_t& n0) {
+        uint32_t tm, tn;
+        map_tile_persist(blockIdx.x + k * G, G, tiles_m, tiles_n, tm, tn);
+        p = GROUPED && tm >= Tp0 ? 1u : 0u;
+        m0 = (tm - (p ? Tp0 : 0u)) * 256u;
+        n0 = tn * NT;
+    };
+    auto x_tile = [&](Cursor& c, uint32_t k) {
+        uint32_t p, m0, n0;
+        tile_origin(k, p, m0, n0);
+        c.s = 0;
+        c.base = (const uint8_t*)pick(p, Xp0, Xp1) + (uint64_t)m0 * xrow;
+        c.size = k < n_tiles ? (pick(p, Mp0, Mp1) - m0) * xrow : 0u;
+    };
+    auto w_tile = [&](Cursor& c, uint32_t k) {
+        uint32_t p, m0, n0;
+        tile_origin(k, p, m0, n0);
+        c.s = 0;
+        c.base = pick(p, Wp0, Wp1) + (uint64_t)(n0 / NT) * panel;
+        c.size = k < n_tiles ? panel : 0u;
+    };
+    Cursor cx{0, nullptr, 0}, cw{0, nullptr, 0};
+    Cursor nx{0, nullptr, 0}, nw{0, nullptr, 0};
+    auto advance = [&](Cursor& c, const Cursor& next) {
+        if (++c.s == SP) c = next;
+    };
+    auto xdma = [&](rsrc_t xr, uint8_t* Xs, int i, uint32_t so) {
+        uint8_t* dst = Xs + wave * (64u * 128u) + 1024u * i;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)dst, 16, xvoff[i], so, 0, 0);
+    };
+    auto wdma = [&](rsrc_t wr, uint8_t* Ws, int i, uint32_t so) {
+        uint8_t* dst = Ws + wave * 8192u + 1024u * i;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)dst, 16, wvoff + 1024u * i, so, 0, 0);
+    };
+    auto x_rsrc = [&]() { return make_rsrc(cx.base, cx.s < S ? cx.size : 0u); };
+    auto w_rsrc = [&]() { return make_rsrc(cw.base, cw.s < S ? cw.size : 0u); };
+    // part p of a stage's loads: the weights of the next stage (parts 0-1),
+    // then the activations two stages ahead (parts 2-3)
+    auto issue_part = [&](auto PART, rsrc_t wr, uint32_t wso, uint8_t* Wd, rsrc_t xr, uint32_t xso, uint8_t* Xd) {
+        constexpr int p = decltype(PART)::value;
+        static_for<4 * p, 4 * p + 4>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            if constexpr (i < DMAS)
+                wdma(wr, Wd, i, wso);
+            else
+                xdma(xr, Xd, i - DMAS, xso);
+        });
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc[a][b] = f32x16{};
+
+    auto read_frags = [&](Frags& f, const uint8_t* Xs, const uint8_t* Ws, int t) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) f.x[b] = *(const f16x8*)(Xs + b * 32 * 128 + xoff[t]);
+#pragma unroll
+        for (int a = 0; a < 4; a++) f.w[a] = *(const f16x8*)(Ws + a * 32 * 128 + woff[t]);
+    };
+    auto mfma_step = [&](const Frags& f) {
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) acc[a][b] = mfma16<XT>(f.w[a], f.x[b], acc[a][b]);
+    };
+    auto store_tile = [&](uint32_t k) {
+        uint32_t p, m0, n0;
+        tile_origin(k, p, m0, n0);
+        store_tile_256<SW, EPI>(acc, pick(p, Yp0, Yp1), pick(p, Gp0, Gp1), pick(p, Y2p0, Y2p1), pick(p, Mp0, Mp1), N,
+                                m0, n0, wm, wn, l32, kh, ldy, ldy2, split, y2_bf16);
+    };
+
+    // prologue: W(0) -> W0, X(0) -> X0, X(1) -> X1 (in the steady state's
+    // order: a stage issues W(g+1), then X(g+2)); stage 0's operands have
+    // landed once at most X(1)'s DMAs are in flight
+    x_tile(cx, 0);
+    w_tile(cw, 0);
+    x_tile(nx, 1);
+    w_tile(nw, 1);
+    {
+        const rsrc_t wr = w_rsrc();
+#pragma unroll
+        for (int i = 0; i < DMAS; i++) wdma(wr, W0, i, cw.s * kBlk);
+        advance(cw, nw);
+        const rsrc_t xr = x_rsrc();
+#pragma unroll
+        for (int i = 0; i < DMAS; i++) xdma(xr, X0, i, cx.s * 128u);
+        advance(cx, nx);
+        const rsrc_t xr1 = x_rsrc();
+#pragma unroll
+        for (int i = 0; i < DMAS; i++) xdma(xr1, X1, i, cx.s * 128u);
+        advance(cx, nx);
+    }
+    LLMR_STAGE_BARRIER(DMAS);
+
+    Frags F0, F1;
+
+    // Global stage g reads X[g%3], W[g%2] and issues W(g+1) -> W[(g+1)%2] and
+    // X(g+2) -> X[(g+2)%3] (both slots were last read in stage g-1, before
+    // the previous barrier). The barrier at its end waits until at most
+    // X(g+2)'s DMAs are in flight: W(g+1) and X(g+1) have landed.
+#define LLMR16_STAGE(XC, WC, XD, WD)                                                          \
+    {                                                                                       \
+        const rsrc_t wr_ = w_rsrc();                                                        \
+        const rsrc_t xr_ = x_rsrc();                                                        \
+        const uint32_t wso_ = cw.s * kBlk, xso_ = cx.s * 128u;                              \
+        issue_part(std::integral_constant<int, 0>{}, wr_, wso_, WD, xr_, xso_, XD);          \
+        read_frags(F0, XC, WC, 0);                                                          \
+        mfma_step(F1);                                                                      \
+        LLMR16_STEP_SCHEDULE;                                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(std::integral_constant<int, 1>{}, wr_, wso_, WD, xr_, xso_, XD);          \
+        read_frags(F1, XC, WC, 1);                                                          \
+        mfma_step(F0);                                                                      \
+        LLMR16_STEP_SCHEDULE;                                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(std::integral_constant<int, 2>{}, wr_, wso_, WD, xr_, xso_, XD);          \
+        read_frags(F0, XC, WC, 2);                                                          \
+        mfma_step(F1);                                                                      \
+        LLMR16_STEP_SCHEDULE;                                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(std::integral_constant<int, 3>{}, wr_, wso_, WD, xr_, xso_, XD);          \
+        read_frags(F1, XC, WC, 3);                                                          \
+        mfma_step(F0);                                                                      \
+        LLMR16_STEP_SCHEDULE;                                                               \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        advance(cw, nw);                                                                    \
+        advance(cx, nx);                                                                    \
+        LLMR_STAGE_BARRIER(DMAS);                                                           \
+    }
+    for (uint32_t k = 0; k < n_tiles; k++) {
+        if (k > 0) {  // the load cursors have moved on to tile k: prepare tile k+1
+            x_tile(nx, k + 1);
+            w_tile(nw, k + 1);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            F1.x[i] = f16x8{};
+            F1.w[i] = f16x8{};
+        }
+        for (uint32_t s0 = 0; s0 < SP; s0 += 6) {
+            LLMR16_STAGE(X0, W0, X2, W1)
+            LLMR16_STAGE(X1, W1, X0, W0)
+            LLMR16_STAGE(X2, W0, X1, W1)
+            LLMR16_STAGE(X0, W1, X2, W0)
+            LLMR16_STAGE(X1, W0, X0, W1)
+            LLMR16_STAGE(X2, W1, X1, W0)
+        }
+        mfma_step(F1);
+        store_tile(k);
+    }
+#undef LLMR16_STAGE
+    LLMR_WAIT_VMCNT(0);  // no DMA may still be writing this workgroup's LDS when it exits
+}
+
+template <uint32_t WT, uint32_t OT, bool SW>
+hipError_t build_image(const void* w, const void* w2, void* img, uint32_t N, uint32_t K, uint32_t row_offset,
+                       hipStream_t st) {
+    const uint32_t panels = SW ? (N + 127u) / 128u : (N + 255u) / 256u;
+    const uint32_t blocks = panels * ((K / (uint32_t)kBK + kImgStages - 1) / kImgStages);
+    hipLaunchKernelGGL((w16_image_kernel<WT, OT, SW>), dim3(blocks), dim3(256), 0, st, (const uint8_t*)w,
+                       (const uint8_t*)w2, (uint8_t*)img, N, K, row_offset);
+    return hipGetLastError();
+}
+
+template <uint32_t XT, bool SW, uint32_t EPI, bool GROUPED>
+hipError_t launch_w16(const PersistArgs& a, int num_cus, hipStream_t st) {
+    const uint32_t grid = (uint32_t)min((uint64_t)a.tiles_m * a.tiles_n, (uint64_t)num_cus);
+    hipLaunchKernelGGL((gemm_w16_persist<XT, SW, EPI, GROUPED>), dim3(grid), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+template <uint32_t XT>
+hipError_t launch_w16_epi(const PersistArgs& a, bool grouped, int num_cus, hipStream_t st) {
+    switch (a.epi) {
+        case kEpiResidual:
+            return grouped ? launch_w16<XT, false, kEpiResidual, true>(a, num_cus, st)
+                           : launch_w16<XT, false, kEpiResidual, false>(a, num_cus, st);
+        case kEpiSplitGelu:
+            return grouped ? launch_w16<XT, false, kEpiSplitGelu, true>(a, num_cus, st)
+                           : launch_w16<XT, false, kEpiSplitGelu, false>(a, num_cus, st);
+        default:
+            return grouped ? launch_w16<XT, false, kEpiStore, true>(a, num_cus, st)
+                           : launch_w16<XT, false, kEpiStore, false>(a, num_cus, st);
+    }
+}
+
+}  // namespace
+
+size_t w16_image_bytes(uint32_t N, uint32_t K, bool swiglu) {
+    const uint64_t panels = swiglu ? (N + 127u) / 128u : (N + 255u) / 256u;
+    return (size_t)(panels * (K / (uint32_t)kBK) * kBlk);
+}
+
+hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
+                            uint32_t K, uint32_t row_offset, hipStream_t st) {
+    const bool sw = w2 != nullptr;
+    if (wtype == kGgmlQ8_0) {
+        if (otype == kGgmlBF16)
+            return sw ? build_image<kGgmlQ8_0, kGgmlBF16, true>(w, w2, img, N, K, row_offset, st)
+                      : build_image<kGgmlQ8_0, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st);
+        return sw ? build_image<kGgmlQ8_0, kGgmlF16, true>(w, w2, img, N, K, row_offset, st)
+                  : build_image<kGgmlQ8_0, kGgmlF16, false>(w, w2, img, N, K, row_offset, st);
+    }
+    if (sw) return hipErrorInvalidValue;  // the SwiGLU takes Q8_0 weights
+    if (otype == kGgmlBF16) return build_image<kGgmlQ4K, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st);
+    return build_image<kGgmlQ4K, kGgmlF16, false>(w, w2, img, N, K, row_offset, st);
+}
+
+hipError_t launch_w16_gemm(const PersistArgs& a, uint32_t xtype, bool swiglu, bool grouped, int num_cus,
+                           hipStream_t st) {
+    if (swiglu)
+        return xtype == kGgmlF16 ? launch_w16<kGgmlF16, true, kEpiStore, false>(a, num_cus, st)
+                                 : launch_w16<kGgmlBF16, true, kEpiStore, false>(a, num_cus, st);
+    return xtype == kGgmlF16 ? launch_w16_epi<kGgmlF16>(a, grouped, num_cus, st)
+                             : launch_w16_epi<kGgmlBF16>(a, grouped, num_cus, st);
+}
+
+}  // namespace llmr

@@ -15,9 +15,15 @@ hipError_t launch_dequant_operand_f16(const void* w, uint32_t wtype, uint32_t n_
                                       uint32_t in_dim, uint32_t row_offset, uint16_t* out,
                                       hipStream_t st);
 
+// One GEMM (dispatch_batch_matmul). `ws` must hold
+// batch_matmul_workspace_bytes(...) bytes (may be 0): f32 activations rounded
+// to fp16 and, from a few thousand tokens, the 16-bit weight image of the
+// two-pass path.
+size_t batch_matmul_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M,
+                                    int num_cus);
 hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uint32_t xtype,
                                float* y, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,
-                               uint32_t row_offset, int num_cus, hipStream_t st);
+                               uint32_t row_offset, int num_cus, void* ws, hipStream_t st);
 
 // Several GEMMs of one shape (N, K, weight and activation types) with a
 // shared epilogue (kind kEpi* of gemm_q.hip: 0 store, 1 gated residual
@@ -67,10 +73,18 @@ hipError_t launch_gemv_q4k(const void* w, uint32_t xtype, const void* x, float* 
 // SwiGLU of two Q8_0 GEMMs (batch_matmul_swiglu_q8). `ws` must hold
 // swiglu_workspace_bytes(...) bytes (may be 0).
 size_t swiglu_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
-                              uint32_t seq_len);
+                              uint32_t seq_len, int num_cus);
 hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t wtype, const void* x,
                                       uint32_t xtype, float* y, uint32_t out_dim, uint32_t in_dim,
                                       uint32_t seq_len, int num_cus, void* ws, hipStream_t st);
+
+// The two-pass GEMM (gemm_w16.hip): the 16-bit image of weight rows
+// [row_offset, row_offset + N) (w2 non-null: the SwiGLU arrangement of gate
+// w and up w2), operand type otype, into `img` (w16_image_bytes). The GEMM
+// launcher itself (launch_w16_gemm) is declared in gemm_q_common.h.
+size_t w16_image_bytes(uint32_t N, uint32_t K, bool swiglu);
+hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
+                            uint32_t K, uint32_t row_offset, hipStream_t st);
 
 hipError_t launch_flash_attention(const void* q, const void* k, const void* v, uint32_t xtype,
                                   float* o, uint32_t n_heads, uint32_t seq_len, float scale,

@@ -178,6 +178,8 @@ def batch_matmul(W: np.ndarray, wtype: int, X: np.ndarray, out_dim: int, in_dim:
         fn(_p(W, _u8p), _p(X, _f32p), _p(Y, _f32p), out_dim, in_dim, seq_len, row_offset)
         return Y
     r = np.ascontiguousarray(rows, dtype=np.uint32)
+    if r.size and int(r.max()) >= seq_len:
+        raise ValueError(f"sampled row {int(r.max())} >= seq_len {seq_len}")
     Y = np.empty((r.size, out_dim), np.float32)
     fn = L.orc_batch_matmul_q8_rows if wtype == 8 else L.orc_batch_matmul_q4k_rows
     fn(_p(W, _u8p), _p(X, _f32p), _p(Y, _f32p), out_dim, in_dim, seq_len, row_offset,
@@ -201,6 +203,8 @@ def batch_matmul_swiglu_q8(Wg: np.ndarray, Wu: np.ndarray, X: np.ndarray, out_di
                                      seq_len)
         return Y
     r = np.ascontiguousarray(rows, dtype=np.uint32)
+    if r.size and int(r.max()) >= seq_len:
+        raise ValueError(f"sampled row {int(r.max())} >= seq_len {seq_len}")
     Y = np.empty((r.size, out_dim), np.float32)
     L.orc_batch_matmul_swiglu_q8_rows(_p(Wg, _u8p), _p(Wu, _u8p), _p(X, _f32p), _p(Y, _f32p), out_dim, in_dim,
                                       seq_len, _p(r, _u32p), r.size)

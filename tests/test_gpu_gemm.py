@@ -145,6 +145,12 @@ PERSIST_CASES = [
     (12, 4608, 3072, 1024, 30, 0),
     (8, 4608, 3072, 640, 1, 0),      # Q8_0 f16, 10 of 12 stages real
     (12, 4608, 9216, 768, 30, 16),   # 648 tiles: 2 whole rounds + 136
+    # f32 activations rounded to fp16 in the workspace first: from 2048
+    # tokens the two-pass path, below it the fused kernel
+    (12, 4100, 4100, 768, 0, 0),
+    (8, 2560, 3332, 640, 0, 4),
+    (8, 1024, 8192, 512, 0, 0),
+    (12, 1500, 5376, 512, 0, 256),
 ]
 
 
@@ -158,8 +164,8 @@ def test_persistent_kernel_sampled_rows(orc, dev, wtype, M, N, K, xtype, row_off
     xt = _torch_x(x, xtype, dev)
     y = ops.batch_matmul(w, wtype, xt, N, row_offset=row_offset)
     torch.cuda.synchronize()
-    rows = np.array([0, 1, 31, 32, 255, 256, 511, 1024 + 7, M // 2, M - 257, M - 256, M - 2, M - 1],
-                    np.uint32)
+    rows = np.unique(np.array([0, 1, 31, 32, 255, 256, 511, 1024 + 7, M // 2, M - 257, M - 256, M - 2, M - 1],
+                              np.int64).clip(0, M - 1)).astype(np.uint32)  # every sampled row < M
     ref = orc.batch_matmul(blk, wtype, _x_as_f32(xt), N, K, M, row_offset, rows=rows)
     got = y[torch.from_numpy(rows.astype(np.int64)).to(dev)].cpu().numpy()
     err = rel_l2(got, ref)
@@ -498,3 +504,63 @@ def test_multi_fused_equals_unfused_at_flux_shapes(dev):
     torch.cuda.synchronize()
     err = float((h - h_ref).abs().max() / h_ref.abs().max())
     assert err < 1e-5, err
+
+
+@pytest.mark.parametrize("wtype,xtype", [(8, 1), (8, 30), (12, 1), (12, 30), (12, 0)])
+def test_two_pass_bit_identical_to_one_pass(dev, wtype, xtype):
+    """From 2048 tokens the weight is dequantized once into a 16-bit image and
+    multiplied by the all-DMA kernel; fewer tokens run the one-pass kernels.
+    Both multiply the same operands in the same MFMA order, so rows of a
+    4100-token launch (two-pass) equal the same rows of a 1000-token launch
+    (one-pass) bit for bit: ragged N, row_offset into a fused weight."""
+    import torch
+    from llmr_amd import ops
+    M, N, K, ro = 4100, 4100, 768, 16
+    w = _weights(dev, wtype, N + ro, K, 90 + wtype)
+    g = torch.Generator(device="cpu").manual_seed(wtype * 100 + xtype)
+    x = torch.randn(M, K, generator=g)
+    x = (x if xtype == 0 else x.to(torch.float16 if xtype == 1 else torch.bfloat16)).to(dev)
+    y = ops.batch_matmul(w, wtype, x, N, row_offset=ro)
+    part = ops.batch_matmul(w, wtype, x[1000:2000].contiguous(), N, row_offset=ro)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y).all())
+    assert torch.equal(y[1000:2000], part)
+
+
+@pytest.mark.parametrize("xtype", [1, 30, 0])
+def test_swiglu_two_pass_bit_identical_to_one_pass(dev, xtype):
+    """The SwiGLU from 2048 tokens (gate and up dequantized into one 16-bit
+    image in the fused kernel's row arrangement) equals the one-pass fused
+    SwiGLU on the same rows bit for bit."""
+    import torch
+    from llmr_amd import gguf, ops, synth
+    M, N, K = 2300, 1036, 640
+    wg = torch.from_numpy(gguf.quantize(synth.normal(95, 1, N * K, 0.02), 8)).to(dev)
+    wu = torch.from_numpy(gguf.quantize(synth.normal(95, 2, N * K, 0.02), 8)).to(dev)
+    g = torch.Generator(device="cpu").manual_seed(96 + xtype)
+    x = torch.randn(M, K, generator=g)
+    x = (x if xtype == 0 else x.to(torch.float16 if xtype == 1 else torch.bfloat16)).to(dev)
+    y = ops.batch_matmul_swiglu(wg, wu, x, N)
+    part = ops.batch_matmul_swiglu(wg, wu, x[700:1900].contiguous(), N)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y).all())
+    assert torch.equal(y[700:1900], part)
+
+
+def test_multi_two_pass_jobs_equal_single_launches(dev):
+    """A grouped pair of 300 + 2000 tokens (two-pass with one image per job)
+    equals each job's own single launch bit for bit, for a strided store."""
+    import torch
+    from llmr_amd import ops
+    Ms, N, K = (300, 2000), 4096, 512
+    blks, xs, wts = _multi_setup(dev, 12, Ms, N, K, 30, 41)
+    out = torch.zeros(sum(Ms), N + 32, dtype=torch.float32, device=dev)
+    views = (out[:Ms[0], :N], out[Ms[0]:, :N])
+    jobs = [ops.MatmulJob(wts[i], ops.Tensor.from_torch(xs[i]), views[i], Ms[i], 8 * i) for i in range(2)]
+    ops.dispatch_batch_matmul_multi(ops.default_graph(), jobs, N, K)
+    torch.cuda.synchronize()
+    for i in range(2):
+        single = ops.batch_matmul(torch.from_numpy(blks[i]).to(dev), 12, xs[i], N, row_offset=8 * i)
+        torch.cuda.synchronize()
+        assert torch.equal(views[i], single), i
+    assert (out[:, N:] == 0).all()
