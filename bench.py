@@ -59,22 +59,27 @@ def _traffic(name: str):
         return None
 
 
-def setup_attention(dev):
+def setup_attention(dev, f32: bool = False):
+    """The Flux attention; with f32, Q/K/V are handed over as f32 (the
+    reference's buffer type, rounded to fp16 by the backend)."""
     import torch
     from llmr_amd import ops, workloads
     a = workloads.FLUX_ATTENTION
     q, k, v = workloads.attention_inputs(a)
     qt, kt, vt = (torch.from_numpy(t).to(dev) for t in (q, k, v))
+    if f32:
+        qt, kt, vt = (t.float() for t in (qt, kt, vt))
     out = torch.empty((a.S, a.H * a.D), dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(a.D)
 
     def step():
         ops.flash_attention(qt, kt, vt, scale, out=out)
 
-    cfg = {"workload": "flux_attention", "heads": a.H, "seq_len": a.S, "head_dim": a.D,
-           "qkv_dtype": "f16", "rope": "3-axis 16/56/56 theta=1e4, applied beforehand",
-           "causal": False}
-    return step, a.flops, a.bytes, cfg, "f16"
+    cfg = {"workload": "flux_attention_f32" if f32 else "flux_attention", "heads": a.H, "seq_len": a.S,
+           "head_dim": a.D, "qkv_dtype": "f32" if f32 else "f16",
+           "rope": "3-axis 16/56/56 theta=1e4, applied beforehand", "causal": False}
+    nbytes = a.bytes + (3 * a.H * a.S * a.D * 2 if f32 else 0)  # f32 Q/K/V: twice the input bytes
+    return step, a.flops, nbytes, cfg, "f16"
 
 
 def setup_lora(dev):
@@ -210,8 +215,8 @@ def gemm_kernel_name(name: str, num_cus: int) -> str:
 
 def measure(dev, name, steps, warmup):
     from llmr_amd import workloads
-    if name == "flux_attention":
-        step, flops, nbytes, cfg, dtype = setup_attention(dev)
+    if name in ("flux_attention", "flux_attention_f32"):
+        step, flops, nbytes, cfg, dtype = setup_attention(dev, f32=name.endswith("_f32"))
     elif name in MODEL_SETUPS:
         step, flops, nbytes, cfg, dtype = MODEL_SETUPS[name](dev)
     elif name in workloads.SWIGLUS:
@@ -288,7 +293,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="flux_attention")
     ap.add_argument("--components",
-                    default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu,lora_flux_linear1,zimage_block,flux_step")
+                    default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu,flux_linear1_f32,"
+                            "flux_linear2_f32,flux_attention_f32,lora_flux_linear1,zimage_block,flux_step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--hbm-copy-calibration", action="store_true",
                     help="time a plain 1 GiB device copy (reference for the FETCH_SIZE/WRITE_SIZE counters)")

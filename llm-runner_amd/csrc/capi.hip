@@ -433,10 +433,13 @@ int llmr_flash_attention(llmr_context* ctx, const void* q, const void* k, const 
     if ((uint64_t)n_heads * ((seq_len + 127) / 128) > 0x7fffffffull)
         return fail(LLMR_ERR_INVALID_ARG, "grid too large");
     // one head's [S, 128] slab is addressed with 32-bit byte offsets
-    if ((uint64_t)seq_len * 128u * (xtype == 0 ? 4u : 2u) > 0xffffffffull)
+    if ((uint64_t)seq_len * 128u * (xtype == LLMR_GGML_F32 ? 4u : 2u) > 0xffffffffull)
         return fail(LLMR_ERR_INVALID_ARG, "seq_len %u too large: one head must span < 4 GiB", seq_len);
-    hipError_t e = llmr::launch_flash_attention(q, k, v, xtype, out, n_heads, seq_len, scale, ctx->cur);
+    const size_t need = llmr::flash_attention_workspace_bytes(xtype, n_heads, seq_len);
+    if (int r = acquire_workspace(ctx, need)) return r;
+    hipError_t e = llmr::launch_flash_attention(q, k, v, xtype, out, n_heads, seq_len, scale, ctx->ws, ctx->cur);
     if (e != hipSuccess) return fail(LLMR_ERR_HIP, "flash_attention launch: %s", hipGetErrorString(e));
+    if (int r = release_workspace(ctx, need)) return r;
     return ok();
 }
 

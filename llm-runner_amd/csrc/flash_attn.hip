@@ -3,29 +3,14 @@
 //   O[s, h*128 + d] = sum_j softmax_j(scale * <Q[h,s,:], K[h,j,:]>) V[h,j,d]
 //
 // Semantics of flash_attention_v2 (dependencies/zimage.c3l/shaders/flash_attn.slang:38-241):
-// Q/K/V [H,S,128] rounded to fp16 for the products, f32 scores and online
-// softmax state, output divided by the row sum, written as f32 [S, H*128]
-// (reverse head transpose fused).
-//
-// Design (one 256-thread workgroup = 4 wave64s per 128 queries of one head):
-//  * Each wave owns 32 queries. Scores are computed transposed, S^T = K Q^T,
-//    with v_mfma_f32_32x32x16_f16 (K rows as the A operand from LDS, the
-//    wave's Q as the B operand held in registers for the whole kernel), so a
-//    lane holds one query and 16 of every 32 keys: the row max and row sum
-//    are in-lane reductions plus one exchange between the two half-waves.
-//  * exp2 with the scale folded into log2(e)*scale; P is rounded to fp16 and
-//    used directly as the B operand of O^T += V^T P^T: the accumulator layout
-//    of the score MFMA is already the operand layout (no data movement), given
-//    that V^T is stored in LDS with the keys of each 16-key chunk permuted
-//    (swap of key-index bits 2 and 3) to match it.
-//  * K and V tiles of 64 keys are double buffered in LDS (K as [key][d],
-//    V transposed to [d][key] while staging), with XOR-swizzled 16-byte
-//    chunks, read from HBM through buffer descriptors that return zeros past
-//    the sequence end (no bounds branches), and software-pipelined so the
-//    score MFMAs of the next tile overlap the softmax of the current one
-//    (see flash_attn_fwd). One barrier per tile.
-//  * Workgroups are remapped so all query blocks of a head run on one XCD
-//    (its K/V stay in that XCD's L2).
+// Q/K/V [H,S,128] rounded to fp16 for the products (the reference rounds
+// them to fp16 in its LDS tiles), f32 scores and online softmax state,
+// output divided by the row sum, written as f32 [S, H*128] (reverse head
+// transpose fused). One kernel, flash_attn_fwd64_w8, on fp16 K/V; f32 and
+// bf16 K and V are rounded to fp16 (nearest even) by one conversion pass into
+// the context workspace first, and f32 / bf16 Q as the kernel loads it
+// (once per workgroup): the reference rounds Q/K/V to fp16 in its LDS
+// tiles, so the result is the same.
 #include <type_traits>
 
 #include "llmr_device.h"
@@ -36,266 +21,7 @@ namespace llmr {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kBQ = 128;  // queries per workgroup
-constexpr int kBKV = 64;  // keys per tile
-constexpr uint32_t kKBytes = kBKV * kD * 2;   // K tile [64][128] fp16
-constexpr uint32_t kVBytes = kD * kBKV * 2;   // V^T tile [128][64] fp16
 
-// K tile: 256-byte rows (16 chunks), swizzle by key & 15.
-__device__ __forceinline__ uint32_t k_off(uint32_t key, uint32_t c) {
-    return key * 256u + ((c ^ (key & 15u)) << 4);
-}
-// V^T tile: 128-byte rows (8 chunks). gfx950's LDS has 64 four-byte banks
-// (two 128-byte rows per bank line). The swizzle (d & 7) ^ ((d >> 3) & 7)
-// keeps both access patterns spread over the banks: fragment reads (16
-// consecutive d, one chunk) hit 16 distinct bank quads, and the transposing
-// staging writes (rows 8 apart) no longer all land on one quad.
-__device__ __forceinline__ uint32_t v_off(uint32_t d, uint32_t c) {
-    return d * 128u + ((c ^ ((d & 7u) ^ ((d >> 3) & 7u))) << 4);
-}
-
-// Position of key r (0..15) of a 16-key chunk inside the V^T row: bits 2 and 3
-// swapped, so lane half kh finds its 8 keys {4kh..4kh+3, 8+4kh..8+4kh+3} at
-// positions 8kh..8kh+7.
-__device__ __forceinline__ uint32_t vpos(uint32_t r) {
-    return (r & 3u) | (((r >> 3) & 1u) << 2) | (((r >> 2) & 1u) << 3);
-}
-
-
-// 8 consecutive elements of a row of one head, loaded through the head's
-// buffer descriptor (rows past the sequence end read as zero), as fp16.
-template <uint32_t XT>
-struct Row8B {
-    static constexpr int kN = (XT == kGgmlF32) ? 2 : 1;
-    u32x4 v[kN];
-    __device__ __forceinline__ void load(rsrc_t r, uint32_t voff, uint32_t soff) {
-        v[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
-        if constexpr (kN == 2)
-            v[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16u, soff, 0));
-    }
-    __device__ __forceinline__ u32x4 f16() const {
-        if constexpr (XT == kGgmlF32) {
-            const f32x4 a = __builtin_bit_cast(f32x4, v[0]), b = __builtin_bit_cast(f32x4, v[1]);
-            return u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y), pack_f16x2(b.z, b.w)};
-        } else if constexpr (XT == kGgmlBF16) {
-            return u32x4{bf16x2_to_f16x2(v[0].x), bf16x2_to_f16x2(v[0].y), bf16x2_to_f16x2(v[0].z),
-                         bf16x2_to_f16x2(v[0].w)};
-        } else {
-            return v[0];
-        }
-    }
-};
-
-// Software-pipelined tile loop. Per 64-key tile t a wave
-//   1. issues S(t+1) = K(t+1) Q^T on the matrix cores,
-//   2. runs the online softmax of S(t) on the vector ALU meanwhile,
-//   3. accumulates O^T += V(t)^T P(t)^T,
-//   4. stores the prefetched K(t+2) and V(t+1) into the free LDS buffers and
-//      issues the global loads of K(t+3) and V(t+2).
-// K and V have their own double buffers, phased one tile apart, so one
-// barrier per tile suffices. The running max used for the exponentials is
-// only raised when a new score exceeds it by more than 2^8 (log2 domain), so
-// most tiles skip rescaling O; p = exp2(s - m) then stays below 2^8, and the
-// final O / l is the same softmax.
-template <uint32_t XT>
-__global__ void __launch_bounds__(256, 2)
-flash_attn_fwd(const void* __restrict__ Q, const void* __restrict__ K, const void* __restrict__ V,
-               float* __restrict__ O, uint32_t S, uint32_t H, float scale_log2, uint32_t n_qb) {
-    __shared__ __attribute__((aligned(16))) uint8_t Kb0[kKBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t Kb1[kKBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t Vb0[kVBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t Vb1[kVBytes];
-    constexpr uint32_t XE = (XT == kGgmlF32) ? 4u : 2u;
-    constexpr uint32_t ROW = kD * XE;  // bytes per token row of one head
-
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t l32 = lane & 31u, kh = lane >> 5;
-
-    // workgroup -> (head, query block), all blocks of a head on one XCD
-    const uint32_t total = n_qb * H;
-    uint32_t L = blockIdx.x;
-    if (total % 8u == 0) L = (L % 8u) * (total / 8u) + L / 8u;
-    const uint32_t head = L / n_qb, qb = L % n_qb;
-
-    const uint64_t head_bytes = (uint64_t)S * ROW;
-    const rsrc_t qr = make_rsrc((const uint8_t*)Q + head * head_bytes, head_bytes);
-    const rsrc_t kr = make_rsrc((const uint8_t*)K + head * head_bytes, head_bytes);
-    const rsrc_t vr = make_rsrc((const uint8_t*)V + head * head_bytes, head_bytes);
-    const uint32_t q_idx = qb * kBQ + wave * 32u + l32;
-
-    // Q fragments (B operand of S^T = K Q^T): d = 32c + 16kh + 8st + 0..7
-    f16x8 qf[4][2];
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-            Row8B<XT> r;
-            r.load(qr, q_idx * ROW + (32u * c + 16u * kh + 8u * st) * XE, 0);
-            qf[c][st] = __builtin_bit_cast(f16x8, r.f16());
-        }
-
-    // staging: K thread -> (16-byte chunk tid&15, keys tid>>4 + 16i);
-    // V thread -> (dims 8*(tid&15).., keys 4*(tid>>4)..+3)
-    const uint32_t kc = tid & 15u, krow = tid >> 4;
-    const uint32_t vdg = tid & 15u, vkg = tid >> 4;
-    Row8B<XT> kreg[4], vreg[4];
-    auto load_k = [&](uint32_t t) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) kreg[i].load(kr, (krow + 16u * i) * ROW + kc * 8u * XE, t * kBKV * ROW);
-    };
-    auto load_v = [&](uint32_t t) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) vreg[i].load(vr, (4u * vkg + i) * ROW + vdg * 8u * XE, t * kBKV * ROW);
-    };
-    auto store_k = [&](uint8_t* Ks) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) *(u32x4*)(Ks + k_off(krow + 16u * i, kc)) = kreg[i].f16();
-    };
-    auto store_v = [&](uint8_t* Vs) {
-        u32x4 v[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = vreg[i].f16();
-        // keys 4*vkg..+3: 16-key chunk vkg/4, group vkg%4 -> positions 16*(vkg/4) + vpos(4*(vkg%4))..+3
-        const uint32_t pos = 16u * (vkg >> 2) + vpos(4u * (vkg & 3u));
-        const uint32_t chunk = pos >> 3, sub = (pos & 7u) * 2u;
-#pragma unroll
-        for (int dd = 0; dd < 8; dd++) {
-            const uint32_t w0 = v[0][dd >> 1], w1 = v[1][dd >> 1], w2 = v[2][dd >> 1], w3 = v[3][dd >> 1];
-            const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-            u32x2 pr;
-            pr.x = __builtin_amdgcn_perm(w1, w0, sel);
-            pr.y = __builtin_amdgcn_perm(w3, w2, sel);
-            *(u32x2*)(Vs + v_off(8u * vdg + dd, chunk) + sub) = pr;
-        }
-    };
-    // S^T[key][query] for the two 32-key halves of the tile in Ks
-    auto qk = [&](const uint8_t* Ks, f32x16 (&s)[2]) {
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-#pragma unroll
-            for (int j = 0; j < 16; j++) s[kb][j] = 0.0f;
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-#pragma unroll
-                for (int st = 0; st < 2; st++) {
-                    const f16x8 a = *(const f16x8*)(Ks + k_off(32u * kb + l32, 4u * c + 2u * kh + st));
-                    s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[c][st], s[kb], 0, 0, 0);
-                }
-        }
-    };
-
-    f32x16 o[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 16; j++) o[i][j] = 0.0f;
-    float m_ref = -1.0e30f;  // max used by the exponentials (log2 domain); reference starts at -1e30
-    float l_i = 0.0f;        // this lane's partial row sum
-
-    // softmax of S(t) and O^T += V(t)^T P(t)^T; keys >= S masked when kMask
-    auto softmax_pv = [&](f32x16 (&sc)[2], const uint8_t* Vs, uint32_t t, auto mask_tag) {
-        constexpr bool kMask = decltype(mask_tag)::value;
-        if constexpr (kMask) {
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const uint32_t key = t * kBKV + 32u * kb + 8u * (j >> 2) + 4u * kh + (j & 3);
-                    sc[kb][j] = key < S ? sc[kb][j] : -INFINITY;
-                }
-        }
-        float mx = sc[0][0];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int j = 0; j < 16; j++) mx = fmaxf(mx, sc[kb][j]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = mx * scale_log2;
-        if (__builtin_amdgcn_ballot_w64(m_new > m_ref + 8.0f) != 0) {
-            const float m2 = fmaxf(m_ref, m_new);
-            const float alpha = __builtin_amdgcn_exp2f(m_ref - m2);
-            m_ref = m2;
-            l_i *= alpha;
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[i] *= alpha;
-        }
-        float rs = 0.0f;
-        f16x8 pf[2][2];
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][j], scale_log2, -m_ref));
-                rs += p;
-                pf[kb][j >> 3][j & 7] = (_Float16)p;
-            }
-        l_i += rs;
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-                for (int c = 0; c < 2; c++) {
-                    const f16x8 a = *(const f16x8*)(Vs + v_off(32u * dt + l32, 2u * (2u * kb + c) + kh));
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[kb][c], o[dt], 0, 0, 0);
-                }
-    };
-
-    // one pipelined tile: reads K(t+1) from Kr and V(t) from Vr, writes K(t+2)
-    // into Kw and V(t+1) into Vw
-    f32x16 sc[2];
-    auto body = [&](uint32_t t, const uint8_t* Kr, const uint8_t* Vr, uint8_t* Kw, uint8_t* Vw) {
-        f32x16 sn[2];
-        qk(Kr, sn);
-        softmax_pv(sc, Vr, t, std::false_type{});
-        store_k(Kw);
-        store_v(Vw);
-        load_k(t + 3);
-        load_v(t + 2);
-        __syncthreads();
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++) sc[kb] = sn[kb];
-    };
-
-    const uint32_t n_tiles = (S + kBKV - 1) / kBKV;
-    load_k(0);
-    load_v(0);
-    store_k(Kb0);
-    store_v(Vb0);
-    load_k(1);
-    store_k(Kb1);
-    load_k(2);
-    load_v(1);
-    __syncthreads();
-    qk(Kb0, sc);
-    __syncthreads();  // every wave has read K(0) before the first body() overwrites Kb0
-
-    uint32_t t = 0;
-    const uint32_t n_main = n_tiles - 1;  // the last tile may be partial: done below with masking
-    for (; t + 2 <= n_main; t += 2) {
-        body(t, Kb1, Vb0, Kb0, Vb1);
-        body(t + 1, Kb0, Vb1, Kb1, Vb0);
-    }
-    if (t < n_main) {
-        body(t, Kb1, Vb0, Kb0, Vb1);
-        t++;
-    }
-    softmax_pv(sc, (t & 1u) ? Vb1 : Vb0, t, std::true_type{});
-
-    const float l_tot = l_i + __shfl_xor(l_i, 32);
-    const float inv_l = 1.0f / l_tot;
-    if (q_idx < S) {
-        float* orow = O + (uint64_t)q_idx * H * kD + (uint64_t)head * kD;
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const uint32_t d = 32u * dt + 8u * g + 4u * kh;
-                *(f32x4*)(orow + d) = f32x4{o[dt][4 * g] * inv_l, o[dt][4 * g + 1] * inv_l,
-                                             o[dt][4 * g + 2] * inv_l, o[dt][4 * g + 3] * inv_l};
-            }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // fp16 fast path: 256 queries per workgroup, DMA-fed LDS rings.
@@ -314,8 +40,9 @@ flash_attn_fwd(const void* __restrict__ Q, const void* __restrict__ K, const voi
 // tile t a wave: DMAs K(t+3) and V(t+2); computes S(t+1) on the matrix
 // cores while the vector ALU exponentiates S(t) into the fp16 P(t);
 // accumulates O^T += V(t)^T P(t)^T while taking the row max of S(t+1);
-// rescales O if a running max grew by more than 2^8 (lazily, as in
-// flash_attn_fwd); then one barrier. The main loop is unrolled by 3 (the
+// rescales O if a running max grew by more than 2^8 (lazily: O and the row
+// sum keep a stale max until then, exp2 of at most 2^8 cannot overflow);
+// then one barrier. The main loop is unrolled by 3 (the
 // halves) and walks the LDS rings with scalar slot offsets. It runs while
 // S(t+1) has no keys past the sequence end; one masked iteration follows
 // when the last tile is partial, then a final iteration that only
@@ -344,8 +71,10 @@ __device__ __forceinline__ float xhalf_sum(float x) {
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 
-template <int NB>  // query blocks of 32 per wave; 8 / NB waves per workgroup
-__device__ __forceinline__ void fa64_body(const _Float16* __restrict__ Q, const _Float16* __restrict__ K,
+// QT: type of Q (F16, or F32 / BF16 rounded to fp16 as the fragments are
+// loaded: Q is read once per workgroup, so it needs no conversion pass)
+template <int NB, uint32_t QT>  // query blocks of 32 per wave; 8 / NB waves per workgroup
+__device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Float16* __restrict__ K,
                                           const _Float16* __restrict__ V, float* __restrict__ O, uint32_t S,
                                           uint32_t H, float scale_log2, uint32_t n_qb) {
     // K ring in slots 0..2, V ring in slots 3..5
@@ -362,7 +91,8 @@ __device__ __forceinline__ void fa64_body(const _Float16* __restrict__ Q, const 
     if (total % 8u == 0) L = (L % 8u) * (total / 8u) + L / 8u;
     const uint32_t head = L / n_qb, qb = L % n_qb;
     const uint64_t head_bytes = (uint64_t)S * ROW;
-    const uint8_t* Qh = (const uint8_t*)Q + head * head_bytes;
+    constexpr uint32_t QB = QT == kGgmlF32 ? 4u : 2u;  // bytes per Q element
+    const uint8_t* Qh = (const uint8_t*)Q + head * (uint64_t)S * kD * QB;
     const uint8_t* Kh = (const uint8_t*)K + head * head_bytes;
     const uint8_t* Vh = (const uint8_t*)V + head * head_bytes;
     constexpr uint32_t DI = 2u * NB;      // DMA instructions per tile per wave (64 / W keys)
@@ -372,16 +102,27 @@ __device__ __forceinline__ void fa64_body(const _Float16* __restrict__ Q, const 
     // d = 32c + 16kh + 8st + 0..7 of query q0 + 32b + l32
     f16x8 qf[NB][4][2];
     {
-        const rsrc_t qr = make_rsrc(Qh, head_bytes);
+        const rsrc_t qr = make_rsrc(Qh, (uint64_t)S * kD * QB);
 #pragma unroll
         for (int b = 0; b < NB; b++)
 #pragma unroll
             for (int c = 0; c < 4; c++)
 #pragma unroll
-                for (int st = 0; st < 2; st++)
-                    qf[b][c][st] = __builtin_bit_cast(
-                        f16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                                   qr, (q0 + 32u * b + l32) * ROW + (32u * c + 16u * kh + 8u * st) * 2u, 0, 0));
+                for (int st = 0; st < 2; st++) {
+                    const uint32_t off = ((q0 + 32u * b + l32) * kD + 32u * c + 16u * kh + 8u * st) * QB;
+                    if constexpr (QT == kGgmlF32) {
+                        const f32x4 a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+                        const f32x4 e = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off + 16u, 0, 0));
+                        qf[b][c][st] = __builtin_bit_cast(f16x8, u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w),
+                                                                      pack_f16x2(e.x, e.y), pack_f16x2(e.z, e.w)});
+                    } else if constexpr (QT == kGgmlBF16) {
+                        const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+                        qf[b][c][st] = __builtin_bit_cast(f16x8, u32x4{bf16x2_to_f16x2(w.x), bf16x2_to_f16x2(w.y),
+                                                                      bf16x2_to_f16x2(w.z), bf16x2_to_f16x2(w.w)});
+                    } else {
+                        qf[b][c][st] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+                    }
+                }
     }
 
     // DMA lane offsets: instruction i of wave w fills keys 4(DI w + i) +
@@ -681,40 +422,67 @@ __device__ __forceinline__ void fa64_body(const _Float16* __restrict__ Q, const 
 // 8 waves of 32 queries: two waves per SIMD, so one wave's softmax runs
 // beside the other's MFMAs (measured 827 vs 737 TFLOP/s for 4 waves of 64
 // queries at H = 24, S = 4608, which also need 495 of the 512 registers)
+template <uint32_t QT>
 __global__ void __launch_bounds__(512, 1)
-flash_attn_fwd64_w8(const _Float16* __restrict__ Q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
+flash_attn_fwd64_w8(const void* __restrict__ Q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
                     float* __restrict__ O, uint32_t S, uint32_t H, float scale_log2, uint32_t n_qb) {
-    fa64_body<1>(Q, K, V, O, S, H, scale_log2, n_qb);
+    fa64_body<1, QT>(Q, K, V, O, S, H, scale_log2, n_qb);
 }
+
+// K and V (blockIdx.y = 0, 1) of f32 or bf16 type -> fp16, round to nearest
+// even; 8 elements per thread.
+template <uint32_t XT>
+__global__ void __launch_bounds__(256) kv_to_f16_kernel(const void* __restrict__ k, const void* __restrict__ v,
+                                                        u32x4* __restrict__ out, size_t n8) {
+    const size_t i = (size_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= n8) return;
+    const void* src = blockIdx.y == 0 ? k : v;
+    u32x4 r;
+    if constexpr (XT == kGgmlF32) {
+        const f32x4 a = ((const f32x4*)src)[2 * i], b = ((const f32x4*)src)[2 * i + 1];
+        r = u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y), pack_f16x2(b.z, b.w)};
+    } else {
+        const u32x4 w = ((const u32x4*)src)[i];
+        r = u32x4{bf16x2_to_f16x2(w.x), bf16x2_to_f16x2(w.y), bf16x2_to_f16x2(w.z), bf16x2_to_f16x2(w.w)};
+    }
+    out[(size_t)blockIdx.y * n8 + i] = r;
+}
+
 }  // namespace
 
+size_t flash_attention_workspace_bytes(uint32_t xtype, uint32_t n_heads, uint32_t seq_len) {
+    return xtype == kGgmlF16 ? 0u : 2u * (size_t)n_heads * seq_len * kD * 2u;
+}
+
 hipError_t launch_flash_attention(const void* q, const void* k, const void* v, uint32_t xtype,
-                                  float* o, uint32_t n_heads, uint32_t seq_len, float scale,
+                                  float* o, uint32_t n_heads, uint32_t seq_len, float scale, void* ws,
                                   hipStream_t st) {
     if (seq_len == 0 || n_heads == 0) return hipSuccess;
+    if (xtype != kGgmlF16) {  // K and V to fp16 in the workspace; Q is converted as it is loaded
+        const size_t n8 = (size_t)n_heads * seq_len * kD / 8u;
+        const dim3 grid((uint32_t)((n8 + 255) / 256), 2);
+        if (xtype == kGgmlF32)
+            hipLaunchKernelGGL(kv_to_f16_kernel<kGgmlF32>, grid, dim3(256), 0, st, k, v, (u32x4*)ws, n8);
+        else
+            hipLaunchKernelGGL(kv_to_f16_kernel<kGgmlBF16>, grid, dim3(256), 0, st, k, v, (u32x4*)ws, n8);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        k = ws;
+        v = (const u32x4*)ws + n8;
+    }
     const float scale_log2 = scale * 1.4426950408889634f;
-    if (xtype == kGgmlF16) {
-        const uint32_t n_qb64 = (seq_len + kBQ64 - 1) / kBQ64;
-        hipLaunchKernelGGL(flash_attn_fwd64_w8, dim3(n_qb64 * n_heads), dim3(512), 0, st, (const _Float16*)q,
-                           (const _Float16*)k, (const _Float16*)v, o, seq_len, n_heads, scale_log2, n_qb64);
-        return hipGetLastError();
-    }
-    const uint32_t n_qb = (seq_len + kBQ - 1) / kBQ;
-    const dim3 grid(n_qb * n_heads);
-    switch (xtype) {
-        case kGgmlF16:
-            hipLaunchKernelGGL(flash_attn_fwd<kGgmlF16>, grid, dim3(256), 0, st, q, k, v, o, seq_len, n_heads,
-                               scale_log2, n_qb);
-            break;
-        case kGgmlBF16:
-            hipLaunchKernelGGL(flash_attn_fwd<kGgmlBF16>, grid, dim3(256), 0, st, q, k, v, o, seq_len, n_heads,
-                               scale_log2, n_qb);
-            break;
-        default:
-            hipLaunchKernelGGL(flash_attn_fwd<kGgmlF32>, grid, dim3(256), 0, st, q, k, v, o, seq_len, n_heads,
-                               scale_log2, n_qb);
-            break;
-    }
+    const uint32_t n_qb64 = (seq_len + kBQ64 - 1) / kBQ64;
+    const dim3 grid(n_qb64 * n_heads), block(512);
+    const _Float16 *kh = (const _Float16*)k, *vh = (const _Float16*)v;
+    if (xtype == kGgmlF32)
+        hipLaunchKernelGGL(flash_attn_fwd64_w8<kGgmlF32>, grid, block, 0, st, q, kh, vh, o, seq_len, n_heads,
+                           scale_log2, n_qb64);
+    else if (xtype == kGgmlBF16)
+        hipLaunchKernelGGL(flash_attn_fwd64_w8<kGgmlBF16>, grid, block, 0, st, q, kh, vh, o, seq_len, n_heads,
+                           scale_log2, n_qb64);
+    else
+        hipLaunchKernelGGL(flash_attn_fwd64_w8<kGgmlF16>, grid, block, 0, st, q, kh, vh, o, seq_len, n_heads,
+                           scale_log2, n_qb64);
     return hipGetLastError();
 }
 

@@ -86,8 +86,11 @@ size_t w16_image_bytes(uint32_t N, uint32_t K, bool swiglu);
 hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
                             uint32_t K, uint32_t row_offset, hipStream_t st);
 
+// Attention (flash_attn.hip). F32 / BF16 Q, K, V are rounded to fp16 into
+// `ws` first (flash_attention_workspace_bytes; 0 for F16).
+size_t flash_attention_workspace_bytes(uint32_t xtype, uint32_t n_heads, uint32_t seq_len);
 hipError_t launch_flash_attention(const void* q, const void* k, const void* v, uint32_t xtype,
-                                  float* o, uint32_t n_heads, uint32_t seq_len, float scale,
+                                  float* o, uint32_t n_heads, uint32_t seq_len, float scale, void* ws,
                                   hipStream_t st);
 
 // --- block glue (glue.hip). Strides are in elements; the C-ABI layer checks

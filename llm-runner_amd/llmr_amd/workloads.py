@@ -7,6 +7,8 @@ Shapes are in GEMM form: M = tokens (seq_len), N = out_dim, K = in_dim.
                   applied beforehand
   flux_linear1    Flux single-stream fused QKV+MLP-in, Q4_K, bf16 [4608, 3072] -> 21504
   flux_linear2    Flux single-stream output projection, Q4_K, bf16 [4608, 15360] -> 3072
+  flux_linear1_f32, flux_linear2_f32
+                  the same with f32 activations (the reference's activation type)
   zimage_*        Z-Image block GEMMs (Q8_0, bf16 activations, S = 4096 + 256)
   zimage_swiglu   Z-Image FFN in-projection: silu(x Wg^T) * (x Wu^T), Q8_0 gate and
                   up [10240, 3840], bf16 [4352, 3840] (batch_matmul_swiglu_q8)
@@ -85,13 +87,16 @@ Q8_LINEAR = Gemm("q8_linear", 256, 3072, 3072, gguf.GGML_Q8_0, gguf.GGML_F32, 1,
 FLUX_ATTENTION = Attention("flux_attention", 24, 4608, 128, 512, 64, 64, (16, 56, 56), 10000.0)
 FLUX_LINEAR1 = Gemm("flux_linear1", 4608, 21504, 3072, gguf.GGML_Q4_K, gguf.GGML_BF16, 6, 7)
 FLUX_LINEAR2 = Gemm("flux_linear2", 4608, 3072, 15360, gguf.GGML_Q4_K, gguf.GGML_BF16, 8, 9)
+FLUX_LINEAR1_F32 = Gemm("flux_linear1_f32", 4608, 21504, 3072, gguf.GGML_Q4_K, gguf.GGML_F32, 6, 7)
+FLUX_LINEAR2_F32 = Gemm("flux_linear2_f32", 4608, 3072, 15360, gguf.GGML_Q4_K, gguf.GGML_F32, 8, 9)
 ZIMAGE_QKV = Gemm("zimage_qkv", 4352, 11520, 3840, gguf.GGML_Q8_0, gguf.GGML_BF16, 10, 11)
 ZIMAGE_O = Gemm("zimage_o", 4352, 3840, 3840, gguf.GGML_Q8_0, gguf.GGML_BF16, 12, 13)
 ZIMAGE_DOWN = Gemm("zimage_down", 4352, 3840, 10240, gguf.GGML_Q8_0, gguf.GGML_BF16, 14, 15)
 ZIMAGE_SWIGLU = SwiGLU("zimage_swiglu", 4352, 10240, 3840, gguf.GGML_Q8_0, gguf.GGML_BF16, 16, 17)
 ZIMAGE_ATTENTION = Attention("zimage_attention", 30, 4352, 128, 256, 64, 64, (32, 48, 48), 256.0)
 
-GEMMS = {g.name: g for g in (Q8_LINEAR, FLUX_LINEAR1, FLUX_LINEAR2, ZIMAGE_QKV, ZIMAGE_O, ZIMAGE_DOWN)}
+GEMMS = {g.name: g for g in (Q8_LINEAR, FLUX_LINEAR1, FLUX_LINEAR2, FLUX_LINEAR1_F32, FLUX_LINEAR2_F32, ZIMAGE_QKV,
+                              ZIMAGE_O, ZIMAGE_DOWN)}
 SWIGLUS = {g.name: g for g in (ZIMAGE_SWIGLU,)}
 
 
