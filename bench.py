@@ -5,8 +5,9 @@
 
 A step is one pass of the hot path over one batch of synthetic input already
 resident in HBM: for the default workload `flux_attention` one non-causal
-attention launch at the Flux shape (H=24, S=4608, D=128, f16, RoPE applied),
-for a GEMM workload one dequant-GEMM launch. Rank 0 prints one JSON line:
+attention call at the Flux shape (H=24, S=4608, D=128, f16, RoPE applied),
+for a GEMM workload one dequant-GEMM call, each through the C-ABI with device
+pointers (what a compiled caller issues per step). Rank 0 prints one JSON line:
 `value` is the workload's TFLOP/s (4*H*S^2*D or 2*M*N*K per step), timed
 with HIP events on the stream the kernels run on; `components` carries the
 same measurement for the other configurations (Q4_K Flux linears, the Q8_0
@@ -59,6 +60,17 @@ def _traffic(name: str):
         return None
 
 
+def _bound_ctx():
+    """The library context bound to the current stream. Kernel-level steps call
+    the C-ABI with device pointers resolved once, as a compiled caller (the
+    reference's C3 host) does; the Python checks of llmr_amd.ops run once in
+    set-up, not per step."""
+    from llmr_amd import ops
+    g = ops.default_graph()
+    g.bind_stream()
+    return g.ctx
+
+
 def setup_attention(dev, f32: bool = False):
     """The Flux attention; with f32, Q/K/V are handed over as f32 (the
     reference's buffer type, rounded to fp16 by the backend)."""
@@ -71,9 +83,12 @@ def setup_attention(dev, f32: bool = False):
         qt, kt, vt = (t.float() for t in (qt, kt, vt))
     out = torch.empty((a.S, a.H * a.D), dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(a.D)
+    ops.flash_attention(qt, kt, vt, scale, out=out)  # the checked host path once
+    ctx, xt = _bound_ctx(), ops.Tensor.from_torch(qt).dtype
+    ptrs = (qt.data_ptr(), kt.data_ptr(), vt.data_ptr(), xt, out.data_ptr(), a.D, a.H, a.S, scale)
 
     def step():
-        ops.flash_attention(qt, kt, vt, scale, out=out)
+        ctx.flash_attention(*ptrs)
 
     cfg = {"workload": "flux_attention_f32" if f32 else "flux_attention", "heads": a.H, "seq_len": a.S,
            "head_dim": a.D, "qkv_dtype": "f32" if f32 else "f16",
@@ -118,9 +133,12 @@ def setup_gemm(dev, name):
     xt = torch.from_numpy(x)
     xt = {gguf.GGML_F32: xt, gguf.GGML_F16: xt.half(), gguf.GGML_BF16: xt.bfloat16()}[g.xtype].to(dev)
     out = torch.empty((g.M, g.N), dtype=torch.float32, device=dev)
+    ops.batch_matmul(w, g.wtype, xt, g.N, out=out)  # the checked host path once
+    ctx = _bound_ctx()
+    ptrs = (w.data_ptr(), g.wtype, xt.data_ptr(), ops.Tensor.from_torch(xt).dtype, out.data_ptr(), g.N, g.K, g.M, 0)
 
     def step():
-        ops.batch_matmul(w, g.wtype, xt, g.N, out=out)
+        ctx.batch_matmul(*ptrs)
 
     cfg = {"workload": name, "M": g.M, "N": g.N, "K": g.K, "weight": gguf.TYPE_NAMES[g.wtype],
            "activations": gguf.TYPE_NAMES[g.xtype].lower(), "output": "f32"}
@@ -137,9 +155,13 @@ def setup_swiglu(dev, name):
     xt = torch.from_numpy(workloads.gemm_activations_f32(g))
     xt = {gguf.GGML_F32: xt, gguf.GGML_F16: xt.half(), gguf.GGML_BF16: xt.bfloat16()}[g.xtype].to(dev)
     out = torch.empty((g.M, g.N), dtype=torch.float32, device=dev)
+    ops.batch_matmul_swiglu(wg, wu, xt, g.N, out=out)  # the checked host path once
+    ctx = _bound_ctx()
+    ptrs = (wg.data_ptr(), wu.data_ptr(), g.wtype, xt.data_ptr(), ops.Tensor.from_torch(xt).dtype, out.data_ptr(),
+            g.N, g.K, g.M)
 
     def step():
-        ops.batch_matmul_swiglu(wg, wu, xt, g.N, out=out)
+        ctx.batch_matmul_swiglu(*ptrs)
 
     cfg = {"workload": name, "M": g.M, "N": g.N, "K": g.K, "weight": "Q8_0 gate + up",
            "activations": gguf.TYPE_NAMES[g.xtype].lower(), "output": "f32 silu(gate) * up"}

@@ -17,9 +17,10 @@ struct llmr_context {
     hipStream_t own;
     hipStream_t cur;
     // Library workspace, grow-only: f32 activations rounded to 16 bits, the
-    // 16-bit weight images of the two-pass GEMM, the fallback paths' f32
-    // intermediates. Calls on different streams are ordered through ws_done,
-    // recorded after every use on the stream that used it (ws_stream).
+    // 16-bit weight images of the two-pass GEMM, split-K partials, the
+    // fallback paths' f32 intermediates. A call on another stream than the
+    // last user (ws_stream) waits for it through ws_done, recorded when the
+    // context switched away from that stream.
     void* ws;
     size_t ws_bytes;
     hipEvent_t ws_done;
@@ -134,7 +135,14 @@ int llmr_destroy_context(llmr_context* ctx) {
 
 int llmr_set_stream(llmr_context* ctx, void* hip_stream) {
     if (!ctx) return fail(LLMR_ERR_INVALID_ARG, "null context");
-    ctx->cur = (hipStream_t)hip_stream;
+    const hipStream_t s = (hipStream_t)hip_stream;
+    // leaving the stream that last used the workspace: mark the end of its
+    // work for the next workspace user on another stream
+    if (s != ctx->cur && ctx->ws_used && ctx->ws_stream == ctx->cur) {
+        LLMR_HIP_CHECK(hipSetDevice(ctx->device));
+        LLMR_HIP_CHECK(hipEventRecord(ctx->ws_done, ctx->cur));
+    }
+    ctx->cur = s;
     return ok();
 }
 
@@ -218,9 +226,12 @@ int llmr_dequant_operand_f16(llmr_context* ctx, const void* w, uint32_t wtype, u
 }
 
 // Makes the context workspace hold `need` bytes for a call about to be issued
-// on the current stream: orders it after the last call that used the
-// workspace on another stream, then grows it if needed (hipFree waits for
-// every launch that may still use the old one).
+// on the current stream. When the workspace was last used on another stream,
+// the call first waits for ws_done, which llmr_set_stream recorded on that
+// stream when the context left it (after everything issued there, the last
+// use included); then the workspace grows if needed (hipFree waits for every
+// launch that may still use the old one). Calls that stay on one stream
+// record and wait for nothing.
 static int acquire_workspace(llmr_context* ctx, size_t need) {
     if (need == 0) return LLMR_OK;
     if (ctx->ws_used && ctx->ws_stream != ctx->cur) LLMR_HIP_CHECK(hipStreamWaitEvent(ctx->cur, ctx->ws_done, 0));
@@ -237,7 +248,6 @@ static int acquire_workspace(llmr_context* ctx, size_t need) {
 // Marks the workspace as used by the work just issued on the current stream.
 static int release_workspace(llmr_context* ctx, size_t need) {
     if (need == 0) return LLMR_OK;
-    LLMR_HIP_CHECK(hipEventRecord(ctx->ws_done, ctx->cur));
     ctx->ws_stream = ctx->cur;
     ctx->ws_used = true;
     return LLMR_OK;

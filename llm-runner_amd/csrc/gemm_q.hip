@@ -26,6 +26,7 @@
 //    operands, so every fragment is one 16-byte LDS read.
 //  * Workgroups are remapped so the tiles one XCD runs concurrently share
 //    weight and activation rows in that XCD's L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "gemm_q_common.h"
@@ -233,7 +234,7 @@ template <uint32_t WT, uint32_t XT, int BM, int BN>
 __global__ void __launch_bounds__(256, (BM * BN >= 256 * 256) ? 1 : 2)
 gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __restrict__ Y,
             uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset, uint32_t tiles_m,
-            uint32_t tiles_n) {
+            uint32_t tiles_n, uint32_t split_stages, uint64_t split_stride) {
     constexpr uint32_t OT = (XT == kGgmlBF16) ? kGgmlBF16 : kGgmlF16;  // MFMA operand type
     constexpr int WM = BM / 2, WN = BN / 2;  // per-wave tile (tokens x features)
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -253,12 +254,19 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
     const uint32_t m0 = tile_m * BM, n0 = tile_n * BN;
     const uint64_t row_bytes = (WT == kGgmlQ8_0) ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * 144;
     const uint8_t* Wt = W + (uint64_t)row_offset * row_bytes;
-    const uint32_t n_stages = K / kBK;
+    // split-K: workgroup row blockIdx.y takes stages [s_begin, s_end) and
+    // writes its partial tile split_stride floats further on (one split: the
+    // whole K, straight into Y)
+    const uint32_t s_begin = blockIdx.y * split_stages;
+    const uint32_t s_end = min(K / (uint32_t)kBK, s_begin + split_stages);
+    Y += blockIdx.y * split_stride;
 
-    XLoad<XT> xl[X_PER_T];
-    WLoad<WT> wl[W_PER_T];
+    // 64 x 64 tiles keep two register sets: the loads of stage s + 2 are in
+    // flight while stage s is multiplied and stage s + 1 (landed) goes to LDS
+    XLoad<XT> xa[X_PER_T], xb[X_PER_T];
+    WLoad<WT> wa[W_PER_T], wb[W_PER_T];
 
-    auto load_stage = [&](uint32_t s) {
+    auto load_stage = [&](XLoad<XT>(&xl)[X_PER_T], WLoad<WT>(&wl)[W_PER_T], uint32_t s) {
         const uint32_t k0 = s * kBK;
 #pragma unroll
         for (int i = 0; i < X_PER_T; i++) {
@@ -274,7 +282,8 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
             wl[i].load(Wt, row_bytes, n0 + r, unit, k0, ok);
         }
     };
-    auto store_stage = [&](uint32_t s, uint32_t buf) {
+    auto store_stage = [&](const XLoad<XT>(&xl)[X_PER_T], const WLoad<WT>(&wl)[W_PER_T], uint32_t s,
+                           uint32_t buf) {
         uint8_t* As = smem + buf * STAGE;
         uint8_t* Bs = As + A_BYTES;
 #pragma unroll
@@ -303,13 +312,7 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[a][b][i] = 0.0f;
 
-    load_stage(0);
-    store_stage(0, 0);
-    __syncthreads();
-
-    for (uint32_t s = 0; s < n_stages; s++) {
-        const uint32_t buf = s & 1u;
-        if (s + 1 < n_stages) load_stage(s + 1);
+    auto compute_stage = [&](uint32_t buf) {
         const uint8_t* As = smem + buf * STAGE;
         const uint8_t* Bs = As + A_BYTES;
 #pragma unroll
@@ -335,8 +338,38 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
                         acc[a][b] = mfma16<OT>(wf[a], xf[b], acc[a][b]);
             }
         }
-        if (s + 1 < n_stages) store_stage(s + 1, buf ^ 1u);
+    };
+
+    load_stage(xa, wa, s_begin);
+    store_stage(xa, wa, s_begin, 0);
+    if constexpr (BM * BN > 64 * 64) {
+        // larger tiles: one stage of loads in flight (a second register set
+        // would spill)
         __syncthreads();
+        for (uint32_t s = s_begin; s < s_end; s++) {
+            const uint32_t buf = (s - s_begin) & 1u;
+            if (s + 1 < s_end) load_stage(xa, wa, s + 1);
+            compute_stage(buf);
+            if (s + 1 < s_end) store_stage(xa, wa, s + 1, buf ^ 1u);
+            __syncthreads();
+        }
+    } else {
+    if (s_begin + 1 < s_end) load_stage(xa, wa, s_begin + 1);
+    __syncthreads();
+
+    for (uint32_t s = s_begin; s < s_end; s += 2) {
+        // stage s in LDS slot 0, stage s + 1 in registers xa / wa
+        if (s + 2 < s_end) load_stage(xb, wb, s + 2);
+        compute_stage(0);
+        if (s + 1 < s_end) store_stage(xa, wa, s + 1, 1);
+        __syncthreads();
+        if (s + 1 >= s_end) break;
+        // stage s + 1 in LDS slot 1, stage s + 2 in registers xb / wb
+        if (s + 3 < s_end) load_stage(xa, wa, s + 3);
+        compute_stage(1);
+        if (s + 2 < s_end) store_stage(xb, wb, s + 2, 0);
+        __syncthreads();
+    }
     }
 
     // Epilogue: lane holds token m = .. + l32 and features n = 8g + 4kh + 0..3.
@@ -1121,9 +1154,22 @@ __global__ void __launch_bounds__(256) gemm_q_generic(const uint8_t* __restrict_
     Y[(uint64_t)m * N + n] = acc;
 }
 
+// Y = sum over the split partials P[0 .. splits-1] (each `stride` floats),
+// added in split order; four floats per thread.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restrict__ P, float* __restrict__ Y,
+                                                            uint64_t n4, uint32_t splits, uint64_t stride) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (i >= n4) return;
+    f32x4 a = ((const f32x4*)P)[i];
+    for (uint32_t q = 1; q < splits; q++) a += ((const f32x4*)(P + q * stride))[i];
+    ((f32x4*)Y)[i] = a;
+}
+
+// splits > 1: the partials go to `part` (splits * M * N floats), then the
+// reduction writes Y.
 template <uint32_t WT, uint32_t XT, int BM, int BN>
 hipError_t launch_tiled(const void* w, const void* x, float* y, uint32_t N, uint32_t K, uint32_t M,
-                        uint32_t row_offset, hipStream_t st) {
+                        uint32_t row_offset, uint32_t splits, float* part, hipStream_t st) {
     constexpr uint32_t lds = 2u * (BM + BN) * kBK * 2;
     auto kern = gemm_q_mfma<WT, XT, BM, BN>;
     static bool attr_set = false;
@@ -1133,38 +1179,63 @@ hipError_t launch_tiled(const void* w, const void* x, float* y, uint32_t N, uint
         attr_set = true;
     }
     const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n), dim3(256), lds, st, (const uint8_t*)w, x, y, N,
-                       K, M, row_offset, tiles_m, tiles_n);
+    const uint32_t n_stages = K / kBK, per = (n_stages + splits - 1) / splits;
+    const uint64_t mn = (uint64_t)M * N;
+    hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n, splits), dim3(256), lds, st, (const uint8_t*)w, x,
+                       splits > 1 ? part : y, N, K, M, row_offset, tiles_m, tiles_n, per, splits > 1 ? mn : 0ull);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splits == 1) return e;
+    const uint64_t n4 = mn / 4;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, st, part, y, n4,
+                       splits, mn);
     return hipGetLastError();
+}
+
+// Tiles of the 4-wave kernel: the largest that still gives every CU ~1.5
+// workgroups. Launches with fewer workgroups than kSplitWgsPerCu per CU
+// split K (at least kSplitMinStages stages per split, M * N % 4 == 0 for
+// the reduction) so the CUs run several short K ranges side by side
+// instead of one long chain of dependent stages each.
+constexpr uint32_t kSplitWgsPerCu = 2, kSplitMinStages = 4;
+struct TilePlan {
+    uint32_t bm, splits;
+};
+TilePlan plan_tiles(uint32_t wtype, uint32_t N, uint32_t K, uint32_t M, int num_cus) {
+    auto wgs = [&](uint32_t bm) { return (uint64_t)((M + bm - 1) / bm) * ((N + bm - 1) / bm); };
+    const uint64_t want = (uint64_t)num_cus * 3 / 2;
+    TilePlan t{64, 1};
+    if (wgs(256) >= want) t.bm = 256;
+    else if (wgs(128) >= want) t.bm = 128;
+    if (wtype == kGgmlQ8_0 && K % kBK) return t;  // the generic kernel
+    const uint64_t w = wgs(t.bm), target = (uint64_t)num_cus * kSplitWgsPerCu;
+    const uint32_t n_stages = K / kBK;
+    if (w < target && n_stages >= 2 * kSplitMinStages && ((uint64_t)M * N) % 4 == 0)
+        t.splits = (uint32_t)std::min<uint64_t>((target + w - 1) / w, n_stages / kSplitMinStages);
+    return t;
 }
 
 template <uint32_t WT, uint32_t XT>
 hipError_t dispatch_x(const void* w, const void* x, float* y, uint32_t N, uint32_t K, uint32_t M,
-                      uint32_t row_offset, int num_cus, hipStream_t st) {
+                      uint32_t row_offset, int num_cus, float* part, hipStream_t st) {
     if (WT == kGgmlQ8_0 && (K % kBK) != 0) {
         const uint64_t threads = (uint64_t)M * N;
         hipLaunchKernelGGL((gemm_q_generic<WT, XT>), dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0,
                            st, (const uint8_t*)w, x, y, N, K, M, row_offset);
         return hipGetLastError();
     }
-    auto wgs = [&](uint32_t bm, uint32_t bn) {
-        return (uint64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    };
-    // the largest 4-wave tile that still gives every CU at least ~1.5
-    // workgroups
-    const uint64_t want = (uint64_t)num_cus * 3 / 2;
-    if (wgs(256, 256) >= want) return launch_tiled<WT, XT, 256, 256>(w, x, y, N, K, M, row_offset, st);
-    if (wgs(128, 128) >= want) return launch_tiled<WT, XT, 128, 128>(w, x, y, N, K, M, row_offset, st);
-    return launch_tiled<WT, XT, 64, 64>(w, x, y, N, K, M, row_offset, st);
+    const TilePlan t = plan_tiles(WT, N, K, M, num_cus);
+    if (t.bm == 256) return launch_tiled<WT, XT, 256, 256>(w, x, y, N, K, M, row_offset, t.splits, part, st);
+    if (t.bm == 128) return launch_tiled<WT, XT, 128, 128>(w, x, y, N, K, M, row_offset, t.splits, part, st);
+    return launch_tiled<WT, XT, 64, 64>(w, x, y, N, K, M, row_offset, t.splits, part, st);
 }
 
 template <uint32_t WT>
 hipError_t dispatch_w(const void* w, uint32_t xtype, const void* x, float* y, uint32_t N, uint32_t K,
-                      uint32_t M, uint32_t row_offset, int num_cus, hipStream_t st) {
+                      uint32_t M, uint32_t row_offset, int num_cus, float* part, hipStream_t st) {
     switch (xtype) {
-        case kGgmlF32: return dispatch_x<WT, kGgmlF32>(w, x, y, N, K, M, row_offset, num_cus, st);
-        case kGgmlF16: return dispatch_x<WT, kGgmlF16>(w, x, y, N, K, M, row_offset, num_cus, st);
-        default: return dispatch_x<WT, kGgmlBF16>(w, x, y, N, K, M, row_offset, num_cus, st);
+        case kGgmlF32: return dispatch_x<WT, kGgmlF32>(w, x, y, N, K, M, row_offset, num_cus, part, st);
+        case kGgmlF16: return dispatch_x<WT, kGgmlF16>(w, x, y, N, K, M, row_offset, num_cus, part, st);
+        default: return dispatch_x<WT, kGgmlBF16>(w, x, y, N, K, M, row_offset, num_cus, part, st);
     }
 }
 
@@ -1230,7 +1301,7 @@ constexpr uint32_t kW16MinTokens = 2048;
 struct GemmPlan {
     bool persistent, two_pass, convert_x;
     uint32_t xt;                  // activation type the kernel reads
-    size_t x16_off, img_off, ws;  // workspace layout: [x16 | image]
+    size_t x16_off, img_off, ws;  // workspace: [x16 | image] (persistent), split-K partials (tiled)
 };
 GemmPlan plan_gemm(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M, int num_cus) {
     GemmPlan p{};
@@ -1238,7 +1309,11 @@ GemmPlan plan_gemm(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint3
     p.persistent = (K % kBK) == 0 && N % 4 == 0 && 2 * tiles >= (uint64_t)num_cus &&
                    (uint64_t)M * K * 2u < (1ull << 31) && (uint64_t)N * row_bytes_of(wtype, K) < (1ull << 31);
     p.xt = xtype;
-    if (!p.persistent) return p;
+    if (!p.persistent) {
+        const TilePlan t = plan_tiles(wtype, N, K, M, num_cus);
+        p.ws = t.splits > 1 ? (size_t)t.splits * M * N * sizeof(float) : 0u;
+        return p;
+    }
     p.convert_x = xtype == kGgmlF32;
     if (p.convert_x) p.xt = kGgmlF16;
     p.two_pass = M >= kW16MinTokens;
@@ -1338,8 +1413,9 @@ hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uin
         return launch_gemv_q4k(w, xtype, x, y, N, K, M, row_offset, st);
     const GemmPlan pl = plan_gemm(wtype, xtype, N, K, M, num_cus);
     if (!pl.persistent) {
-        if (wtype == kGgmlQ8_0) return dispatch_w<kGgmlQ8_0>(w, xtype, x, y, N, K, M, row_offset, num_cus, st);
-        return dispatch_w<kGgmlQ4K>(w, xtype, x, y, N, K, M, row_offset, num_cus, st);
+        if (wtype == kGgmlQ8_0)
+            return dispatch_w<kGgmlQ8_0>(w, xtype, x, y, N, K, M, row_offset, num_cus, (float*)ws, st);
+        return dispatch_w<kGgmlQ4K>(w, xtype, x, y, N, K, M, row_offset, num_cus, (float*)ws, st);
     }
     const void* x16 = x;
     if (pl.convert_x) {
