@@ -169,6 +169,30 @@ LLMR_API int llmr_batch_matmul_pc(llmr_context* ctx, const void* weight, uint32_
                                   const void* input, uint32_t input_type, float* output,
                                   const llmr_batch_matmul_params* pc);
 
+/* Bytes of the fixed scratch array of llmr_batch_matmul_noalloc. */
+#define LLMR_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* llmr_batch_matmul that allocates nothing (no hipMalloc, hipFree or
+ * allocating library call), for callers that cannot allocate: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid it. No
+ * counterpart in the reference. Its scratch (f32 activations rounded to
+ * fp16 for the persistent kernels, split-K partials of launches with few
+ * tiles, the two-pass path's weight image) is a fixed
+ * LLMR_NOALLOC_SCRATCH_BYTES array of device memory that each GPU holds from
+ * the library's load to the end of the process. Where llmr_batch_matmul's
+ * plan needs more, the call takes the form that fits: the one-pass kernels
+ * instead of the weight image (the same bits), fewer K splits (the same
+ * result to f32 summation order). Only f32 activations of more than 16 Mi
+ * elements on a launch that converts them cannot shrink: such a call
+ * returns LLMR_ERR_INVALID_ARG and launches nothing. Every call on one GPU
+ * uses that GPU's one array, whose contents persist between calls: calls
+ * that may overlap on a GPU (other streams, other contexts, other threads)
+ * race. */
+LLMR_API int llmr_batch_matmul_noalloc(llmr_context* ctx, const void* weight, uint32_t weight_type,
+                                       const void* input, uint32_t input_type, float* output,
+                                       uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,
+                                       uint32_t row_offset);
+
 /* One GEMM of llmr_batch_matmul_multi: output = input · W[row_offset ..]^T as
  * llmr_batch_matmul, written through the call's epilogue. */
 typedef struct llmr_matmul_job {

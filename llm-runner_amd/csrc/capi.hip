@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "llmr_hip.h"
 #include "llmr_internal.h"
@@ -28,9 +29,38 @@ struct llmr_context {
     bool ws_used;
 };
 
+// The no-allocation GEMM's scratch (llmr_batch_matmul_noalloc): a fixed
+// device array each GPU holds from the library's load to the end of the
+// process. Host code never uses the array's name as an address (on the host
+// it is only a handle): the device address comes from hipGetSymbolAddress,
+// once per device, at the first context creation on that device.
+constexpr size_t kNoAllocScratchBytes = LLMR_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 namespace {
 
 thread_local char g_err[512] = "";
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device `dev` (resolved once).
+hipError_t resolve_scratch(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch[dev]) return hipSuccess;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) g_scratch[dev] = p;
+    return e;
+}
+
+void* scratch_ptr(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return g_scratch[dev];
+}
 
 int fail(int code, const char* fmt, ...) {
     va_list ap;
@@ -96,6 +126,7 @@ int llmr_create_context(int device_index, llmr_context** out_ctx) {
     if (device_index < 0 || device_index >= n)
         return fail(LLMR_ERR_NO_DEVICE, "device index %d out of range [0, %d)", device_index, n);
     LLMR_HIP_CHECK(hipSetDevice(device_index));
+    LLMR_HIP_CHECK(resolve_scratch(device_index));
     hipDeviceProp_t prop;
     LLMR_HIP_CHECK(hipGetDeviceProperties(&prop, device_index));
     llmr_context* c = new llmr_context;
@@ -253,19 +284,29 @@ static int release_workspace(llmr_context* ctx, size_t need) {
     return LLMR_OK;
 }
 
-int llmr_batch_matmul(llmr_context* ctx, const void* weight, uint32_t wtype, const void* input,
-                      uint32_t xtype, float* output, uint32_t out_dim, uint32_t in_dim,
-                      uint32_t seq_len, uint32_t row_offset) {
+// Argument checks of llmr_batch_matmul and its no-allocation variant.
+static int check_batch_matmul(llmr_context* ctx, const void* weight, uint32_t wtype, const void* input,
+                              uint32_t xtype, const float* output, uint32_t out_dim, uint32_t in_dim,
+                              uint32_t seq_len, uint32_t row_offset) {
     if (int r = check_ctx(ctx)) return r;
     if (int r = check_weight(weight, wtype, in_dim)) return r;
     if (!is_act_type(xtype))
         return fail(LLMR_ERR_UNSUPPORTED, "input type %u not supported (F32=0, F16=1, BF16=30)", xtype);
-    if (seq_len == 0 || out_dim == 0) return ok();
+    if (seq_len == 0 || out_dim == 0) return LLMR_OK;
     if (!input || !output) return fail(LLMR_ERR_INVALID_ARG, "null input/output pointer");
     if (!aligned(input, 16) || !aligned(output, 16))
         return fail(LLMR_ERR_INVALID_ARG, "input/output pointers must be 16-byte aligned");
     if ((uint64_t)row_offset + out_dim > 0xffffffffull)
         return fail(LLMR_ERR_INVALID_ARG, "row_offset + out_dim overflows");
+    return LLMR_OK;
+}
+
+int llmr_batch_matmul(llmr_context* ctx, const void* weight, uint32_t wtype, const void* input,
+                      uint32_t xtype, float* output, uint32_t out_dim, uint32_t in_dim,
+                      uint32_t seq_len, uint32_t row_offset) {
+    if (int r = check_batch_matmul(ctx, weight, wtype, input, xtype, output, out_dim, in_dim, seq_len, row_offset))
+        return r;
+    if (seq_len == 0 || out_dim == 0) return ok();
     const size_t need = llmr::batch_matmul_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len, ctx->num_cus);
     if (int r = acquire_workspace(ctx, need)) return r;
     hipError_t e = llmr::launch_batch_matmul(weight, wtype, input, xtype, output, out_dim, in_dim, seq_len,
@@ -280,6 +321,27 @@ int llmr_batch_matmul_pc(llmr_context* ctx, const void* weight, uint32_t wtype, 
     if (!pc) return fail(LLMR_ERR_INVALID_ARG, "null push constants");
     return llmr_batch_matmul(ctx, weight, wtype, input, xtype, output, pc->out_dim, pc->in_dim,
                              pc->seq_len, pc->row_offset);
+}
+
+int llmr_batch_matmul_noalloc(llmr_context* ctx, const void* weight, uint32_t wtype, const void* input,
+                              uint32_t xtype, float* output, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,
+                              uint32_t row_offset) {
+    if (int r = check_batch_matmul(ctx, weight, wtype, input, xtype, output, out_dim, in_dim, seq_len, row_offset))
+        return r;
+    if (seq_len == 0 || out_dim == 0) return ok();
+    const size_t need = llmr::batch_matmul_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len, ctx->num_cus,
+                                                           kNoAllocScratchBytes);
+    if (need > kNoAllocScratchBytes)
+        return fail(LLMR_ERR_INVALID_ARG,
+                    "this GEMM needs %zu bytes of scratch (its f32 activations as fp16), beyond the %zu the "
+                    "no-allocation entry point holds; pass 16-bit activations or call llmr_batch_matmul",
+                    need, kNoAllocScratchBytes);
+    void* const ptr = scratch_ptr(ctx->device);
+    if (need > 0 && !ptr) return fail(LLMR_ERR_HIP, "scratch of device %d not resolved", ctx->device);
+    hipError_t e = llmr::launch_batch_matmul(weight, wtype, input, xtype, output, out_dim, in_dim, seq_len, row_offset,
+                                             ctx->num_cus, ptr, ctx->cur, kNoAllocScratchBytes);
+    if (e != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul launch: %s", hipGetErrorString(e));
+    return ok();
 }
 
 int llmr_lora_correction(llmr_context* ctx, const llmr_lora* lora, float* scratch, const void* input,

@@ -1216,14 +1216,13 @@ TilePlan plan_tiles(uint32_t wtype, uint32_t N, uint32_t K, uint32_t M, int num_
 
 template <uint32_t WT, uint32_t XT>
 hipError_t dispatch_x(const void* w, const void* x, float* y, uint32_t N, uint32_t K, uint32_t M,
-                      uint32_t row_offset, int num_cus, float* part, hipStream_t st) {
+                      uint32_t row_offset, const TilePlan& t, float* part, hipStream_t st) {
     if (WT == kGgmlQ8_0 && (K % kBK) != 0) {
         const uint64_t threads = (uint64_t)M * N;
         hipLaunchKernelGGL((gemm_q_generic<WT, XT>), dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0,
                            st, (const uint8_t*)w, x, y, N, K, M, row_offset);
         return hipGetLastError();
     }
-    const TilePlan t = plan_tiles(WT, N, K, M, num_cus);
     if (t.bm == 256) return launch_tiled<WT, XT, 256, 256>(w, x, y, N, K, M, row_offset, t.splits, part, st);
     if (t.bm == 128) return launch_tiled<WT, XT, 128, 128>(w, x, y, N, K, M, row_offset, t.splits, part, st);
     return launch_tiled<WT, XT, 64, 64>(w, x, y, N, K, M, row_offset, t.splits, part, st);
@@ -1231,11 +1230,11 @@ hipError_t dispatch_x(const void* w, const void* x, float* y, uint32_t N, uint32
 
 template <uint32_t WT>
 hipError_t dispatch_w(const void* w, uint32_t xtype, const void* x, float* y, uint32_t N, uint32_t K,
-                      uint32_t M, uint32_t row_offset, int num_cus, float* part, hipStream_t st) {
+                      uint32_t M, uint32_t row_offset, const TilePlan& t, float* part, hipStream_t st) {
     switch (xtype) {
-        case kGgmlF32: return dispatch_x<WT, kGgmlF32>(w, x, y, N, K, M, row_offset, num_cus, part, st);
-        case kGgmlF16: return dispatch_x<WT, kGgmlF16>(w, x, y, N, K, M, row_offset, num_cus, part, st);
-        default: return dispatch_x<WT, kGgmlBF16>(w, x, y, N, K, M, row_offset, num_cus, part, st);
+        case kGgmlF32: return dispatch_x<WT, kGgmlF32>(w, x, y, N, K, M, row_offset, t, part, st);
+        case kGgmlF16: return dispatch_x<WT, kGgmlF16>(w, x, y, N, K, M, row_offset, t, part, st);
+        default: return dispatch_x<WT, kGgmlBF16>(w, x, y, N, K, M, row_offset, t, part, st);
     }
 }
 
@@ -1298,27 +1297,39 @@ uint64_t row_bytes_of(uint32_t wtype, uint32_t K) {
 // From kW16MinTokens tokens the weight is dequantized once into a 16-bit
 // image (gemm_w16.hip) instead of once per 256-token tile.
 constexpr uint32_t kW16MinTokens = 2048;
+// With a workspace limit (the no-allocation entry point's fixed array) the
+// plan keeps to it where it can: the two-pass path only when its image fits,
+// split-K with as many splits as fit (none if fewer than two). Only the fp16
+// copy of f32 activations for the persistent kernels has no smaller form,
+// so a plan may still exceed the limit there (the caller refuses it).
 struct GemmPlan {
     bool persistent, two_pass, convert_x;
     uint32_t xt;                  // activation type the kernel reads
+    TilePlan tiles;               // the tiled kernel's tile and splits (not persistent)
     size_t x16_off, img_off, ws;  // workspace: [x16 | image] (persistent), split-K partials (tiled)
 };
-GemmPlan plan_gemm(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M, int num_cus) {
+GemmPlan plan_gemm(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M, int num_cus,
+                   size_t ws_limit) {
     GemmPlan p{};
     const uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
     p.persistent = (K % kBK) == 0 && N % 4 == 0 && 2 * tiles >= (uint64_t)num_cus &&
                    (uint64_t)M * K * 2u < (1ull << 31) && (uint64_t)N * row_bytes_of(wtype, K) < (1ull << 31);
     p.xt = xtype;
     if (!p.persistent) {
-        const TilePlan t = plan_tiles(wtype, N, K, M, num_cus);
-        p.ws = t.splits > 1 ? (size_t)t.splits * M * N * sizeof(float) : 0u;
+        p.tiles = plan_tiles(wtype, N, K, M, num_cus);
+        const size_t part = (size_t)M * N * sizeof(float);
+        if (p.tiles.splits > 1 && (size_t)p.tiles.splits * part > ws_limit) {
+            const size_t fit = ws_limit / part;
+            p.tiles.splits = fit >= 2 ? (uint32_t)fit : 1u;
+        }
+        p.ws = p.tiles.splits > 1 ? (size_t)p.tiles.splits * part : 0u;
         return p;
     }
     p.convert_x = xtype == kGgmlF32;
     if (p.convert_x) p.xt = kGgmlF16;
-    p.two_pass = M >= kW16MinTokens;
     p.x16_off = 0;
     p.img_off = p.convert_x ? align256((size_t)M * K * 2u) : 0u;
+    p.two_pass = M >= kW16MinTokens && p.img_off + w16_image_bytes(N, K, false) <= ws_limit;
     p.ws = p.img_off + (p.two_pass ? w16_image_bytes(N, K, false) : 0u);
     return p;
 }
@@ -1334,9 +1345,9 @@ bool swiglu_fused(uint32_t wtype, uint32_t N, uint32_t K, uint32_t M) {
 }  // namespace
 
 size_t batch_matmul_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M,
-                                    int num_cus) {
+                                    int num_cus, size_t ws_limit) {
     if (M == 0 || N == 0 || (wtype == kGgmlQ4K && M <= kGemvMaxTokens)) return 0;
-    return plan_gemm(wtype, xtype, N, K, M, num_cus).ws;
+    return plan_gemm(wtype, xtype, N, K, M, num_cus, ws_limit).ws;
 }
 
 size_t swiglu_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
@@ -1406,16 +1417,16 @@ hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t w
 
 hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uint32_t xtype,
                                float* y, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,
-                               uint32_t row_offset, int num_cus, void* ws, hipStream_t st) {
+                               uint32_t row_offset, int num_cus, void* ws, hipStream_t st, size_t ws_limit) {
     if (seq_len == 0 || out_dim == 0) return hipSuccess;
     const uint32_t N = out_dim, K = in_dim, M = seq_len;
     if (wtype == kGgmlQ4K && M <= kGemvMaxTokens)
         return launch_gemv_q4k(w, xtype, x, y, N, K, M, row_offset, st);
-    const GemmPlan pl = plan_gemm(wtype, xtype, N, K, M, num_cus);
+    const GemmPlan pl = plan_gemm(wtype, xtype, N, K, M, num_cus, ws_limit);
     if (!pl.persistent) {
         if (wtype == kGgmlQ8_0)
-            return dispatch_w<kGgmlQ8_0>(w, xtype, x, y, N, K, M, row_offset, num_cus, (float*)ws, st);
-        return dispatch_w<kGgmlQ4K>(w, xtype, x, y, N, K, M, row_offset, num_cus, (float*)ws, st);
+            return dispatch_w<kGgmlQ8_0>(w, xtype, x, y, N, K, M, row_offset, pl.tiles, (float*)ws, st);
+        return dispatch_w<kGgmlQ4K>(w, xtype, x, y, N, K, M, row_offset, pl.tiles, (float*)ws, st);
     }
     const void* x16 = x;
     if (pl.convert_x) {

@@ -17,13 +17,18 @@ hipError_t launch_dequant_operand_f16(const void* w, uint32_t wtype, uint32_t n_
 
 // One GEMM (dispatch_batch_matmul). `ws` must hold
 // batch_matmul_workspace_bytes(...) bytes (may be 0): f32 activations rounded
-// to fp16 and, from a few thousand tokens, the 16-bit weight image of the
-// two-pass path.
+// to fp16, split-K partials of launches with few tiles and, from a few
+// thousand tokens, the 16-bit weight image of the two-pass path. With a
+// ws_limit the plan keeps within it where a smaller form exists (the
+// one-pass kernels instead of the image, fewer splits); pass the same limit
+// to both calls.
+constexpr size_t kNoWorkspaceLimit = ~(size_t)0;
 size_t batch_matmul_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M,
-                                    int num_cus);
+                                    int num_cus, size_t ws_limit = kNoWorkspaceLimit);
 hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uint32_t xtype,
                                float* y, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,
-                               uint32_t row_offset, int num_cus, void* ws, hipStream_t st);
+                               uint32_t row_offset, int num_cus, void* ws, hipStream_t st,
+                               size_t ws_limit = kNoWorkspaceLimit);
 
 // Several GEMMs of one shape (N, K, weight and activation types) with a
 // shared epilogue (kind kEpi* of gemm_q.hip: 0 store, 1 gated residual

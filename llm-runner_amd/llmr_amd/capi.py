@@ -94,6 +94,7 @@ _SIGS = {
     "llmr_batch_matmul": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32]),
     "llmr_batch_matmul_pc": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp,
                                             ctypes.POINTER(BatchMatMulParams)]),
+    "llmr_batch_matmul_noalloc": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32]),
     "llmr_batch_matmul_multi": (ctypes.c_int, [_vp, _u32, _u32, _u32, _u32, ctypes.POINTER(MatmulJob), _u32,
                                                ctypes.POINTER(MatmulEpilogue)]),
     "llmr_batch_matmul_swiglu": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32]),
@@ -216,6 +217,11 @@ class Context:
                      out_dim: int, in_dim: int, seq_len: int, row_offset: int = 0) -> None:
         check(lib().llmr_batch_matmul(self._h, w_ptr, wtype, x_ptr, xtype, y_ptr, out_dim, in_dim,
                                       seq_len, row_offset))
+
+    def batch_matmul_noalloc(self, w_ptr: int, wtype: int, x_ptr: int, xtype: int, y_ptr: int,
+                             out_dim: int, in_dim: int, seq_len: int, row_offset: int = 0) -> None:
+        check(lib().llmr_batch_matmul_noalloc(self._h, w_ptr, wtype, x_ptr, xtype, y_ptr, out_dim, in_dim,
+                                              seq_len, row_offset))
 
     def batch_matmul_multi(self, wtype: int, xtype: int, out_dim: int, in_dim: int, jobs, epilogue=None) -> None:
         """jobs: sequence of MatmulJob; epilogue: MatmulEpilogue or None (plain store)."""

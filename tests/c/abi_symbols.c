@@ -30,6 +30,7 @@ static const struct {
     {"llmr_dequant_operand_f16", (void (*)(void))(uintptr_t)llmr_dequant_operand_f16},
     {"llmr_batch_matmul", (void (*)(void))(uintptr_t)llmr_batch_matmul},
     {"llmr_batch_matmul_pc", (void (*)(void))(uintptr_t)llmr_batch_matmul_pc},
+    {"llmr_batch_matmul_noalloc", (void (*)(void))(uintptr_t)llmr_batch_matmul_noalloc},
     {"llmr_batch_matmul_multi", (void (*)(void))(uintptr_t)llmr_batch_matmul_multi},
     {"llmr_batch_matmul_swiglu", (void (*)(void))(uintptr_t)llmr_batch_matmul_swiglu},
     {"llmr_batch_matmul_swiglu_pc", (void (*)(void))(uintptr_t)llmr_batch_matmul_swiglu_pc},
