@@ -236,7 +236,8 @@ typedef struct llmr_matmul_epilogue {
  *   - the single block's linear1 slots plus silu/gelu and concat_rows_copy
  *     (flux_dit.c3:1005-1018, 1049-1058): Q | K | V to `output`, the
  *     activated MLP half straight into linear2's input;
- *   - the per-block modulation projections of one step (flux_dit.c3:1131-1140):
+ *   - the modulation projections of one step (the reference makes three
+ *     shared ones, flux_dit.c3:1131-1140; a Flux.1-dev model has one per block):
  *     Q4_K jobs of at most 4 tokens with LLMR_EPI_STORE run as one launch
  *     for the whole group.
  * A job pair that cannot run as one persistent launch (f32 input, too few

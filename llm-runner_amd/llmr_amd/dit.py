@@ -264,8 +264,13 @@ def flux_weights(cfg: FluxConfig, device="cuda", seed: int = workloads.SEED, g: 
     return glob, doubles, singles
 
 
-# Checkpoint tensor names (the BFL Flux names the reference loads,
-# flux_dit.c3:680-735; modulation per block as in Flux.1-dev).
+# Checkpoint tensor names: the BFL Flux.1-dev layout this model uses (per-block
+# img_mod / txt_mod / modulation weights, a GELU MLP with img_mlp.0 of
+# [mlp, dim], linear1 of [3 dim + mlp, dim]). The reference's loader
+# (load_flux_dit, flux_dit.c3:664-744) reads the Flux Klein layout instead:
+# shared double_stream_modulation_img/txt and single_stream_modulation
+# weights and SwiGLU halves (img_mlp.0 of [2 mlp, dim], linear1 of
+# [3 dim + 2 mlp, dim]), so its checkpoints do not load here unchanged.
 _FLUX_GLOBAL = {"img_in": "img_in.weight", "txt_in": "txt_in.weight", "time_in0": "time_in.in_layer.weight",
                 "time_in1": "time_in.out_layer.weight", "final_mod": "final_layer.adaLN_modulation.1.weight",
                 "final_linear": "final_layer.linear.weight"}
@@ -293,7 +298,8 @@ def _flux_shapes(cfg: FluxConfig):
 
 def save_flux_gguf(path: str, cfg: FluxConfig, glob: FluxGlobalWeights, doubles, singles) -> int:
     """Writes Flux weights (device tensors) as a GGUF checkpoint with the
-    BFL tensor names: matrices in their quantized blocks (img_in Q8_0, the
+    BFL Flux.1-dev tensor names and shapes (not the Klein layout the
+    reference loads): matrices in their quantized blocks (img_in Q8_0, the
     rest Q4_K), norm scales F32. Returns the file size."""
     from . import gguf_file
     gs, ds, ss = _flux_shapes(cfg)
@@ -325,8 +331,9 @@ def save_flux_gguf(path: str, cfg: FluxConfig, glob: FluxGlobalWeights, doubles,
 
 
 def flux_weights_from_gguf(path: str, cfg: FluxConfig, device="cuda"):
-    """Flux weights loaded from a GGUF checkpoint (load_flux_dit,
-    flux_dit.c3:664-744): every matrix uploaded unchanged through the native
+    """Flux.1-dev weights loaded from a GGUF checkpoint in the layout of
+    save_flux_gguf, the way load_flux_dit (flux_dit.c3:664-744) loads its
+    Klein checkpoints: every matrix uploaded unchanged through the native
     parser (upload_weight), norm scales widened to f32. Shapes and types are
     checked against cfg (the GEMMs take Q4_K and Q8_0)."""
     from . import gguf_file

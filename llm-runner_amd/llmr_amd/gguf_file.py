@@ -96,6 +96,8 @@ def encode_tensor(x: np.ndarray, ggml_type: int) -> bytes:
     if ggml_type == gguf.GGML_BF16:
         u = x.view(np.uint32).astype(np.uint64)
         r = ((u + 0x7fff + ((u >> 16) & 1)) >> 16).astype(np.uint16)  # round to nearest even
+        nan = (u & 0x7fffffff) > 0x7f800000  # NaN stays a (quiet) NaN, as the rounding would carry it to Inf or 0
+        r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
         return r.astype("<u2").tobytes()
     if ggml_type in (gguf.GGML_Q8_0, gguf.GGML_Q4_K):
         return gguf.quantize(x.reshape(-1, x.shape[-1]), ggml_type).tobytes()

@@ -214,13 +214,23 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
     wtype, xtype = jobs[0].weight.dtype, jobs[0].input.dtype
 
     def stride(t):
+        # a one-row view writes row 0 only, so it fits any common row stride
         if t.dim() != 2 or t.stride(1) != 1:
             raise ValueError("outputs must be 2-D views with contiguous rows")
-        return t.stride(0) if t.shape[0] > 1 else (t.shape[1] + 3) // 4 * 4
+        return t.stride(0) if t.shape[0] > 1 else None
 
-    ldy = stride(jobs[0].output)
-    ldy2 = stride(jobs[0].output2) if jobs[0].output2 is not None else 0
-    o2type = _TORCH_GGML.get(jobs[0].output2.dtype, 0) if jobs[0].output2 is not None else 0
+    def common_stride(views, what):
+        strides = {stride(t) for t in views} - {None}
+        if len(strides) > 1:
+            raise ValueError(f"{what} views must share one row stride")
+        return strides.pop() if strides else (views[0].shape[1] + 3) // 4 * 4
+
+    ldy = common_stride([j.output for j in jobs], "output")
+    has2 = [j.output2 is not None for j in jobs]
+    if any(has2) and not all(has2):
+        raise ValueError("either every job has output2 or none")
+    ldy2 = common_stride([j.output2 for j in jobs], "output2") if has2[0] else 0
+    o2type = _TORCH_GGML.get(jobs[0].output2.dtype, 0) if has2[0] else 0
     cj = []
     for j in jobs:
         if j.weight.dtype != wtype or j.input.dtype != xtype:
@@ -231,15 +241,15 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
             raise ValueError("weight shape does not cover [row_offset, row_offset+out_dim) x in_dim")
         if j.input.data.numel() < j.seq_len * in_dim:
             raise ValueError("input smaller than [seq_len, in_dim]")
-        if not j.output.is_cuda or j.output.dtype != torch.float32 or stride(j.output) != ldy:
-            raise ValueError("outputs must be f32 device views sharing one row stride")
+        if not j.output.is_cuda or j.output.dtype != torch.float32:
+            raise ValueError("outputs must be f32 device views")
         width = split if epilogue == capi.EPI_SPLIT_GELU else out_dim
         if j.output.shape[0] < j.seq_len or j.output.shape[1] < width:
             raise ValueError("output view smaller than [seq_len, out_dim]")
         o2 = 0
         if j.output2 is not None:
-            if stride(j.output2) != ldy2 or _TORCH_GGML.get(j.output2.dtype) != o2type:
-                raise ValueError("output2 views must share row stride and dtype")
+            if _TORCH_GGML.get(j.output2.dtype) != o2type:
+                raise ValueError("output2 views must share one dtype")
             if j.output2.shape[0] < j.seq_len or j.output2.shape[1] < out_dim - split:
                 raise ValueError("output2 view smaller than [seq_len, out_dim - split]")
             o2 = j.output2.data_ptr()

@@ -146,3 +146,20 @@ def test_find_and_unknown_type_sizes(lib, tmp_path):
         assert lib.llmr_gguf_find_tensor(f._h, b"nope", ctypes.byref(idx)) == capi.LLMR_ERR_INVALID_ARG
         capi.check(lib.llmr_gguf_find_kv(f._h, b"a.key", ctypes.byref(idx)))
         assert lib.llmr_gguf_find_kv(f._h, b"b", ctypes.byref(idx)) == capi.LLMR_ERR_INVALID_ARG
+
+
+def test_bf16_encoding_rounds_to_nearest_even_and_keeps_specials():
+    """BF16 is the high half of the f32 pattern, rounded to nearest even;
+    NaNs stay NaNs (a NaN whose payload sits in the low half would otherwise
+    round to Inf, or carry into the sign), infinities and signed zeros stay
+    as they are."""
+    bits = np.array([0x3f800000, 0x3f808000, 0x3f818000, 0x3f808001, 0x7f7fffff,
+                     0x7f800000, 0xff800000, 0x00000000, 0x80000000,
+                     0x7f800001, 0xffffffff, 0x7fc00000, 0xff800001], np.uint32)
+    out = np.frombuffer(gf.encode_tensor(bits.view(np.float32), gguf.GGML_BF16), "<u2")
+    want = [0x3f80, 0x3f80, 0x3f82, 0x3f81, 0x7f80, 0x7f80, 0xff80, 0x0000, 0x8000]
+    np.testing.assert_array_equal(out[:9], want)
+    back = (out.astype(np.uint32) << 16).view(np.float32)
+    assert np.isnan(back[9:]).all()
+    assert (out[9:] & 0x0040).all()                            # quiet bit set
+    np.testing.assert_array_equal(out[9:] >> 15, bits[9:] >> 31)  # sign kept

@@ -348,7 +348,7 @@ def test_swiglu_full_size_sampled(orc, dev):
 def test_bf16_activations_beyond_fp16_range(orc, dev, M, N, K):
     """bf16 activations of magnitude ~1e5 (past fp16's 65504) stay finite: every
     kernel uses bf16 operands for bf16 inputs (small launch: 4-wave tiles;
-    large: the persistent kernel). Q4_K keeps the reference's all-f32 operand."""
+    large: the persistent kernel), where Q4_K weights become bf16 operands too."""
     import torch
     from llmr_amd import gguf, ops, synth
     blk = gguf.quantize_q4k(synth.normal(24, 1, N * K, 0.02))
@@ -413,34 +413,63 @@ def test_multi_grouped_store_and_residual(orc, dev, wtype, xtype):
         assert rel_l2(hv - hb, gv * ref) <= TOL, (i, rel_l2(hv - hb, gv * ref))
 
 
-@pytest.mark.parametrize("xtype", [0, 30])
-def test_multi_gemv_group(orc, dev, xtype):
+@pytest.mark.parametrize("xtype,pad", [(0, 0), (30, 0), (1, 0), (30, 40), (1, 40)])
+def test_multi_gemv_group(orc, dev, xtype, pad):
     """Q4_K jobs of 1-4 tokens grouped in one call (the per-block modulation
     projections) run as one GEMV launch: every job equals its own
     single-job launch bit for bit and the oracle within the small-M bar
-    (N = 300: a ragged last workgroup); rows past each job's M stay
-    untouched."""
+    (N = 300: a ragged last workgroup); rows past each job's M, and the
+    columns between N and a row stride of N + pad, stay untouched."""
     import torch
     from llmr_amd import gguf, ops, synth
     N, K, Ms = 300, 512, (1, 3, 1, 4, 2, 1, 1)
     g = ops.default_graph()
     blks, xs, jobs = [], [], []
-    out = torch.full((len(Ms), 4, N), 7.0, dtype=torch.float32, device=dev)
+    out = torch.full((len(Ms), 4, N + pad), 7.0, dtype=torch.float32, device=dev)
     for i, M in enumerate(Ms):
         blk = gguf.quantize(synth.normal(40 + i, 2, (N + 7 * i) * K, 0.02), 12)
         blks.append(blk)
         xs.append(_torch_x(synth.normal(40 + i, 1, M * K).reshape(M, K), xtype, dev))
         w = ops.Tensor.quantized(torch.from_numpy(blk).to(dev), 12, N + 7 * i, K)
-        jobs.append(ops.MatmulJob(w, ops.Tensor.from_torch(xs[i]), out[i, :M], M, 7 * i))
+        jobs.append(ops.MatmulJob(w, ops.Tensor.from_torch(xs[i]), out[i, :M, :N], M, 7 * i))
     ops.dispatch_batch_matmul_multi(g, jobs, N, K)
     torch.cuda.synchronize()
     for i, M in enumerate(Ms):
         single, xr = _run(dev, blks[i], 12, _x_as_f32(xs[i]), xtype, N, 7 * i)
-        got = out[i, :M].cpu().numpy()
+        got = out[i, :M, :N].cpu().numpy()
         assert np.array_equal(got, single), i
         ref = orc.batch_matmul(blks[i], 12, xr, N, K, M, 7 * i)
         assert rel_l2(got, ref) <= 1e-5, (i, rel_l2(got, ref))
-        assert (out[i, M:] == 7.0).all(), i
+        assert (out[i, M:] == 7.0).all() and (out[i, :, N:] == 7.0).all(), i
+
+
+@pytest.mark.parametrize("N,xtype", [(18432, 30), (9216, 0)])
+def test_multi_gemv_group_flux_modulation(orc, dev, N, xtype):
+    """The Flux.1-dev modulation projections of one step at full size: 38
+    one-token jobs of K = 3072 (19 double blocks x image/text at N = 18432,
+    or 38 single blocks at N = 9216) in one grouped launch, stored with a
+    row stride past N. Three weights are shared round-robin so the host
+    quantizes only three; sampled jobs equal their single-job launch bit for
+    bit, job 0 the oracle."""
+    import torch
+    from llmr_amd import gguf, ops, synth
+    K, J = 3072, 38
+    g = ops.default_graph()
+    blks = [gguf.quantize(synth.normal(60 + i, 2, N * K, 0.02), 12) for i in range(3)]
+    wts = [ops.Tensor.quantized(torch.from_numpy(b).to(dev), 12, N, K) for b in blks]
+    xs = [_torch_x(synth.normal(70 + j, 1, K).reshape(1, K), xtype, dev) for j in range(J)]
+    out = torch.full((J, 1, N + 64), 7.0, dtype=torch.float32, device=dev)
+    jobs = [ops.MatmulJob(wts[j % 3], ops.Tensor.from_torch(xs[j]), out[j, :, :N], 1, 0) for j in range(J)]
+    ops.dispatch_batch_matmul_multi(g, jobs, N, K)
+    torch.cuda.synchronize()
+    assert (out[:, :, N:] == 7.0).all()
+    for j in (0, 1, 2, 17, 36, 37):
+        single, xr = _run(dev, blks[j % 3], 12, _x_as_f32(xs[j]), xtype, N, 0)
+        got = out[j, :, :N].cpu().numpy()
+        assert np.array_equal(got, single), j
+        if j == 0:
+            ref = orc.batch_matmul(blks[0], 12, xr, N, K, 1, 0)
+            assert rel_l2(got, ref) <= 1e-5, rel_l2(got, ref)
 
 
 @pytest.mark.parametrize("M,xtype", [(4096, 30), (300, 30), (700, 0)])
