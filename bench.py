@@ -146,6 +146,41 @@ def setup_gemm(dev, name):
     return step, g.flops, g.bytes, cfg, "bf16" if g.xtype == gguf.GGML_BF16 else "f16"
 
 
+def setup_gemm_lora(dev):
+    """flux_linear1 (Q4_K, 4608 x 21504 x 3072, bf16) with a rank-32 LoRA on
+    its whole output through llmr_batch_matmul_lora: the adapter is merged into
+    the two-pass GEMM's 16-bit weight image as the image is built. Its time
+    against flux_linear1's is the adapter's cost."""
+    import torch
+    from llmr_amd import capi, gguf, ops, workloads
+    g = workloads.GEMMS["flux_linear1"]
+    rank = 32
+    w = torch.from_numpy(workloads.gemm_weight_blocks(g)).to(dev)
+    xt = torch.from_numpy(workloads.gemm_activations_f32(g)).bfloat16().to(dev)
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    a = (0.02 * torch.randn(rank, g.K, generator=gen)).to(dev)
+    b = (0.02 * torch.randn(g.N, rank, generator=gen)).to(dev)
+    lora = ops.LoraTensor(a, b, rank, 1.0)
+    out = torch.empty((g.M, g.N), dtype=torch.float32, device=dev)
+    scratch = torch.empty(g.M * rank, device=dev)
+    gr = ops.default_graph()
+    wt = ops.Tensor.quantized(w, g.wtype, g.N, g.K)
+    ops.dispatch_batch_matmul(gr, wt, ops.Tensor.from_torch(xt), ops.Tensor.from_torch(out), g.N, g.K, g.M, 0,
+                              lora=lora, lora_scratch=scratch)  # the checked host path once
+    ctx = _bound_ctx()
+    lc = lora.c_struct()
+    args = (w.data_ptr(), g.wtype, xt.data_ptr(), gguf.GGML_BF16, out.data_ptr(), g.N, g.K, g.M, 0, lc,
+            scratch.data_ptr())
+
+    def step():
+        ctx.batch_matmul_lora(*args)
+
+    flops = g.flops + 2.0 * g.M * rank * (g.K + g.N)
+    cfg = {"workload": "flux_linear1_lora", "M": g.M, "N": g.N, "K": g.K, "weight": "Q4_K", "activations": "bf16",
+           "output": "f32", "lora_rank": rank}
+    return step, flops, g.bytes, cfg, "bf16"
+
+
 def setup_swiglu(dev, name):
     import torch
     from llmr_amd import gguf, ops, workloads
@@ -245,6 +280,8 @@ def measure(dev, name, steps, warmup):
         step, flops, nbytes, cfg, dtype = setup_swiglu(dev, name)
     elif name == "lora_flux_linear1":
         step, flops, nbytes, cfg, dtype = setup_lora(dev)
+    elif name == "flux_linear1_lora":
+        step, flops, nbytes, cfg, dtype = setup_gemm_lora(dev)
     else:
         step, flops, nbytes, cfg, dtype = setup_gemm(dev, name)
     total_ms, per = _time_steps(step, steps, warmup)
@@ -316,7 +353,7 @@ def main():
     ap.add_argument("--workload", default="flux_attention")
     ap.add_argument("--components",
                     default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu,flux_linear1_f32,"
-                            "flux_linear2_f32,flux_attention_f32,lora_flux_linear1,zimage_block,flux_step")
+                            "flux_linear2_f32,flux_attention_f32,lora_flux_linear1,flux_linear1_lora,zimage_block,flux_step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--hbm-copy-calibration", action="store_true",
                     help="time a plain 1 GiB device copy (reference for the FETCH_SIZE/WRITE_SIZE counters)")

@@ -358,10 +358,17 @@ LLMR_API int llmr_lora_correction(llmr_context* ctx, const llmr_lora* lora, floa
                                   uint32_t seq_len, uint32_t b_rows, uint32_t row_offset,
                                   uint32_t weight_row_offset);
 
-/* llmr_batch_matmul followed by llmr_lora_correction, the reference's
- * dispatch_batch_matmul with a LoRA (dit.c3:1198-1213: lora, lora_scratch,
- * lora_b_rows, lora_row_offset, lora_weight_row_offset). lora NULL: the
- * plain GEMM. */
+/* llmr_batch_matmul with its LoRA, the reference's dispatch_batch_matmul
+ * with a LoRA (dit.c3:1198-1213: lora, lora_scratch, lora_b_rows,
+ * lora_row_offset, lora_weight_row_offset). lora NULL: the plain GEMM. A GEMM
+ * on the two-pass kernel (seq_len >= 2048, at least half the CUs' worth of
+ * 256 x 256 tiles) with rank <= 64 merges the adapter into its 16-bit weight
+ * image: W' = RN16(W16 + scale * b a) on output features [lora_row_offset,
+ * lora_row_offset + b_rows), one more 16-bit rounding of those weights
+ * (within the GEMM's tolerance of the reference; the other features are
+ * bit-identical to llmr_batch_matmul), lora_scratch unused and lora->a
+ * 16-byte aligned. Every other call is llmr_batch_matmul followed by
+ * llmr_lora_correction. */
 LLMR_API int llmr_batch_matmul_lora(llmr_context* ctx, const void* weight, uint32_t weight_type,
                                     const void* input, uint32_t input_type, float* output, uint32_t out_dim,
                                     uint32_t in_dim, uint32_t seq_len, uint32_t row_offset, const llmr_lora* lora,

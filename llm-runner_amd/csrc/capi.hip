@@ -372,10 +372,34 @@ int llmr_batch_matmul_lora(llmr_context* ctx, const void* weight, uint32_t wtype
                            float* output, uint32_t out_dim, uint32_t in_dim, uint32_t seq_len, uint32_t row_offset,
                            const llmr_lora* lora, float* lora_scratch, uint32_t lora_b_rows,
                            uint32_t lora_row_offset, uint32_t lora_weight_row_offset) {
-    if (int r = llmr_batch_matmul(ctx, weight, wtype, input, xtype, output, out_dim, in_dim, seq_len, row_offset))
+    // a GEMM on the two-pass kernel merges the LoRA (rank <= 64) into its
+    // weight image; the rest runs the GEMM, then the exact correction
+    if (int r = check_batch_matmul(ctx, weight, wtype, input, xtype, output, out_dim, in_dim, seq_len, row_offset))
         return r;
-    return llmr_lora_correction(ctx, lora, lora_scratch, input, xtype, output, in_dim, out_dim, seq_len,
-                                lora_b_rows, lora_row_offset, lora_weight_row_offset);
+    const bool present = lora && lora->rank > 0 && lora->rank <= llmr::kMaxLoraRank && seq_len > 0 && out_dim > 0;
+    const size_t need = present ? llmr::batch_matmul_lora_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len,
+                                                                          lora->rank, ctx->num_cus)
+                                : 0u;
+    if (need == 0) {
+        if (int r = llmr_batch_matmul(ctx, weight, wtype, input, xtype, output, out_dim, in_dim, seq_len, row_offset))
+            return r;
+        return llmr_lora_correction(ctx, lora, lora_scratch, input, xtype, output, in_dim, out_dim, seq_len,
+                                    lora_b_rows, lora_row_offset, lora_weight_row_offset);
+    }
+    if (!lora->a || !lora->b) return fail(LLMR_ERR_INVALID_ARG, "null LoRA a or b pointer");
+    if (!aligned(lora->a, 16)) return fail(LLMR_ERR_INVALID_ARG, "LoRA a must be 16-byte aligned");
+    const uint32_t b_rows = lora_b_rows ? lora_b_rows : out_dim;
+    if ((uint64_t)lora_row_offset + b_rows > out_dim)
+        return fail(LLMR_ERR_INVALID_ARG, "row_offset + b_rows (%u + %u) exceeds out_dim %u", lora_row_offset,
+                    b_rows, out_dim);
+    const llmr::LoraGemm l{lora->a, lora->b, lora->rank, lora->scale, b_rows, lora_row_offset,
+                           lora_weight_row_offset};
+    if (int r = acquire_workspace(ctx, need)) return r;
+    hipError_t e = llmr::launch_batch_matmul_lora(weight, wtype, input, xtype, output, out_dim, in_dim, seq_len,
+                                                  row_offset, l, ctx->num_cus, ctx->ws, ctx->cur);
+    if (e != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul_lora launch: %s", hipGetErrorString(e));
+    if (int r = release_workspace(ctx, need)) return r;
+    return ok();
 }
 
 int llmr_q8_lora_merge(llmr_context* ctx, void* weight, const float* a, const float* b, uint32_t in_dim,

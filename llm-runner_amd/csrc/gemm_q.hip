@@ -1350,6 +1350,50 @@ size_t batch_matmul_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, 
     return plan_gemm(wtype, xtype, N, K, M, num_cus, ws_limit).ws;
 }
 
+namespace {
+
+// The LoRA GEMM's plan: the two-pass GEMM whose image carries the adapter.
+GemmPlan lora_plan(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M, uint32_t rank, int num_cus) {
+    GemmPlan p{};
+    if (rank == 0 || rank > kLoraImageMaxRank || M == 0 || N == 0) return p;
+    if (wtype == kGgmlQ4K && M <= kGemvMaxTokens) return p;
+    p = plan_gemm(wtype, xtype, N, K, M, num_cus, kNoWorkspaceLimit);
+    if (!p.two_pass) p = GemmPlan{};
+    return p;
+}
+
+}  // namespace
+
+size_t batch_matmul_lora_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M,
+                                         uint32_t rank, int num_cus) {
+    return lora_plan(wtype, xtype, N, K, M, rank, num_cus).ws;
+}
+
+hipError_t launch_batch_matmul_lora(const void* w, uint32_t wtype, const void* x, uint32_t xtype, float* y,
+                                    uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset, const LoraGemm& l,
+                                    int num_cus, void* ws, hipStream_t st) {
+    const GemmPlan pl = lora_plan(wtype, xtype, N, K, M, l.rank, num_cus);
+    if (!pl.two_pass) return hipErrorNotSupported;
+    const void* x16 = x;
+    hipError_t e = hipSuccess;
+    if (pl.convert_x) {
+        x16 = (uint8_t*)ws + pl.x16_off;
+        if ((e = convert_activations(x, xtype, (void*)x16, pl.xt, (size_t)M * K, st)) != hipSuccess) return e;
+    }
+    void* img = (uint8_t*)ws + pl.img_off;
+    if ((e = launch_w16_image_lora(w, wtype, pl.xt, img, N, K, row_offset, l, st)) != hipSuccess) return e;
+    const uint32_t tiles_m = (M + 255) / 256, tiles_n = (N + 255) / 256;
+    PersistArgs a{};
+    a.p[0] = PersistProblem{(const uint8_t*)img, x16, y, nullptr, nullptr, M, 0u, tiles_m};
+    a.N = N;
+    a.K = K;
+    a.tiles_m = tiles_m;
+    a.tiles_n = tiles_n;
+    a.epi = kEpiStore;
+    a.ldy = N;
+    return launch_w16_gemm(a, pl.xt, false, false, num_cus, st);
+}
+
 size_t swiglu_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
                               uint32_t seq_len, int num_cus) {
     const uint32_t N = out_dim, K = in_dim, M = seq_len;

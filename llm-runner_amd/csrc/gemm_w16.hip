@@ -43,12 +43,50 @@ constexpr uint32_t kBlk = 256u * 128u;  // bytes of one 256-row x 64-wide 16-bit
 // the panel is a 128-feature SwiGLU tile, rows gate 0-63 | up 0-63 | gate
 // 64-127 | up 64-127 (the fused SwiGLU kernel's LDS arrangement). Rows past
 // N read as zero through the descriptor and give zero operands.
+//
+// LORA: a LoRA adapter merged into the image (the reference applies it as a
+// correction after the GEMM, dispatch_lora_correction): feature n in
+// [lro, lro + b_rows) of the panel gets d[n, k] = sum_r (scale b[wro + n -
+// lro, r]) a[r, k] added to its dequantized weight in f32, then the 16-bit
+// rounding once more (features outside keep their image bit for bit). d is
+// a 256 x 64 x rank product per stage, computed on the matrix cores as d^T =
+// a^T (scale b)^T with 32x32x16 bf16 MFMAs: both factors split into bf16
+// hi + lo parts (x = hi + lo to 2^-17 relative) and summed as hi hi + hi lo
+// + lo hi, so d carries about 16 correct bits (the dropped lo lo term is
+// 2^-16 of it) - far below the 16-bit rounding that follows. Wave w holds the
+// (scale b)^T fragments of panel rows 64 w .. 64 w + 63 in registers for the
+// whole workgroup and loads each stage's a^T fragments (f32, from L2) one
+// stage ahead; a lane's accumulators are four consecutive k of one of its
+// wave's rows, one 8-byte read-modify-write of the LDS block.
 constexpr uint32_t kImgStages = 4;
-template <uint32_t WT, uint32_t OT, bool SW>
+constexpr uint32_t kLoraSteps = kLoraImageMaxRank / 16u;  // 16-wide rank steps
+struct ImageLora {
+    const float* a;  // [rank, K]
+    const float* b;  // [*, rank]
+    float scale;
+    uint32_t rank, lro, b_rows, wro;
+};
+// x -> (bf16 hi, bf16 lo) with x = hi + lo to 2^-17 relative, packed for
+// eight values into two 16-byte MFMA operands
+__device__ __forceinline__ void split_bf16x8(const float (&v)[8], u32x4& hi, u32x4& lo) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (uint32_t e = 0; e < 4; e++) {
+        const bf16x2_t h{(__bf16)v[2 * e], (__bf16)v[2 * e + 1]};
+        const bf16x2_t l{(__bf16)(v[2 * e] - (float)h[0]), (__bf16)(v[2 * e + 1] - (float)h[1])};
+        hi[e] = __builtin_bit_cast(uint32_t, h);
+        lo[e] = __builtin_bit_cast(uint32_t, l);
+    }
+}
+template <uint32_t WT, uint32_t OT, bool SW, uint32_t RS = 0>
 __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2,
                                                          uint8_t* __restrict__ img, uint32_t N, uint32_t K,
-                                                         uint32_t row_offset) {
+                                                         uint32_t row_offset, const ImageLora lo) {
+    constexpr bool LORA = RS > 0;         // RS: rank steps of 16 the kernel holds (rank <= 16 RS)
+    constexpr uint32_t RA = LORA ? RS : 1u;  // register array extent
     __shared__ __attribute__((aligned(16))) uint8_t lblk[2][kBlk];
+    // LORA: a^T fragments of the stage, [k tile 2][rank step RS][hi, lo][64 lanes] x 16 B
+    __shared__ __attribute__((aligned(16))) u32x4 afr[LORA ? 2u * RS * 2u * 64u : 1u];
     const uint32_t S = K / kBK, groups = (S + kImgStages - 1) / kImgStages;
     const uint32_t p = blockIdx.x / groups, s0 = (blockIdx.x % groups) * kImgStages, r = threadIdx.x;
     const uint32_t rb = (WT == kGgmlQ8_0) ? (K / 32u) * 34u : (K / 256u) * 144u;
@@ -64,6 +102,48 @@ __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restric
         src = W + (uint64_t)row_offset * rb;
         row = r;
     }
+    // LORA loads go first, ahead of the weight rows: they are L2 hits and
+    // return before the rows, so waiting for them (the memory counter is in
+    // order) costs nothing the rows do not.
+    //  bv: the wave's scale * b, rows 64 wave + 32 nt + l32 and ranks
+    //      16 j + 8 kh + 0..7 (its (scale b)^T MFMA fragments);
+    //  av: a for the thread's units q = r + 256 h of each stage (rank group
+    //      rg = q / 64, column k = q % 64, rows 8 rg .. 8 rg + 7).
+    // Rows outside the slot and ranks >= rank lie past the descriptors'
+    // ranges and read as zero, so every load is unconditional.
+    const uint32_t wave = r >> 6, lane = r & 63u;
+    const uint32_t w0 = n0 + 64u * wave;  // the wave's rows [w0, w0 + 64) of the weight
+    float bv[2][RA][8], av[kImgStages][LORA ? RS / 2u : 1u][8];
+    bool in_slot[2] = {false, false};
+    bool wave_any = false;
+    if constexpr (LORA) {
+        const rsrc_t rbv = make_rsrc(lo.b + (uint64_t)lo.wro * lo.rank, (uint64_t)lo.b_rows * lo.rank * 4u);
+        wave_any = w0 < N && w0 + 64u > lo.lro && w0 < lo.lro + lo.b_rows;
+#pragma unroll
+        for (uint32_t nt = 0; nt < 2; nt++) {
+            const uint32_t n = w0 + 32u * nt + (lane & 31u);
+            in_slot[nt] = n < N && n >= lo.lro && n - lo.lro < lo.b_rows;
+#pragma unroll
+            for (uint32_t j = 0; j < RS; j++)
+#pragma unroll
+                for (uint32_t e = 0; e < 8; e++) {
+                    const uint32_t rr = 16u * j + 8u * (lane >> 5) + e;
+                    const uint32_t off = (in_slot[nt] && rr < lo.rank) ? ((n - lo.lro) * lo.rank + rr) * 4u : ~0u;
+                    bv[nt][j][e] = __uint_as_float(bload4(rbv, off, 0u));
+                }
+        }
+        const rsrc_t rav = make_rsrc(lo.a, (uint64_t)lo.rank * K * 4u);
+#pragma unroll
+        for (uint32_t i = 0; i < kImgStages; i++)
+#pragma unroll
+            for (uint32_t h = 0; h < RS / 2u; h++) {
+                const uint32_t q = r + 256u * h, k = q & 63u, rg = q >> 6;
+                const uint32_t st = min(s0 + i, S - 1u);
+#pragma unroll
+                for (uint32_t e = 0; e < 8; e++)
+                    av[i][h][e] = __uint_as_float(bload4(rav, ((8u * rg + e) * K + 64u * st + k) * 4u, 0u));
+            }
+    }
     const rsrc_t rs = make_rsrc(src + (uint64_t)n0 * rb, (uint64_t)(N - n0) * rb);
     WRow<WT, OT> u[kImgStages];
 #pragma unroll
@@ -72,6 +152,17 @@ __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restric
             static_for<0, WRow<WT, OT>::kLoads>(
                 [&](auto L) { u[i].template load<decltype(L)::value>(rs, row * rb, s0 + i); });
     const uint32_t base = r * 128u + (lds_swz(r) << 4);
+    u32x4 bh[2][RA], bl[2][RA];
+    if constexpr (LORA) {
+#pragma unroll
+        for (uint32_t nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (uint32_t j = 0; j < RS; j++) {
+#pragma unroll
+                for (uint32_t e = 0; e < 8; e++) bv[nt][j][e] *= lo.scale;
+                split_bf16x8(bv[nt][j], bh[nt][j], bl[nt][j]);
+            }
+    }
 #pragma unroll
     for (uint32_t i = 0; i < kImgStages; i++) {
         if (s0 + i >= S) break;
@@ -81,6 +172,63 @@ __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restric
         u[i].template store<1>(lb, sc, base);
         u[i].template store<2>(lb, sc, base);
         u[i].template store<3>(lb, sc, base);
+        if constexpr (LORA) {
+            // the stage's a split into its MFMA fragments in afr
+#pragma unroll
+            for (uint32_t h = 0; h < RS / 2u; h++) {
+                const uint32_t q = r + 256u * h, k = q & 63u, rg = q >> 6;
+                const uint32_t slot = ((k >> 5) * RS + (rg >> 1)) * 128u + 32u * (rg & 1u) + (k & 31u);
+                split_bf16x8(av[i][h], afr[slot], afr[slot + 64u]);
+            }
+            __syncthreads();
+            if (wave_any) {
+#pragma unroll
+                for (uint32_t t = 0; t < 2; t++) {
+                    f32x16 acc[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+                    for (uint32_t j = 0; j < RS; j++) {
+                        const u32x4 ah = afr[(t * RS + j) * 128u + lane];
+                        const u32x4 alo = afr[(t * RS + j) * 128u + 64u + lane];
+#pragma unroll
+                        for (uint32_t nt = 0; nt < 2; nt++) {
+                            acc[nt] = mfma16<kGgmlBF16>(__builtin_bit_cast(f16x8, ah),
+                                                        __builtin_bit_cast(f16x8, bh[nt][j]), acc[nt]);
+                            acc[nt] = mfma16<kGgmlBF16>(__builtin_bit_cast(f16x8, ah),
+                                                        __builtin_bit_cast(f16x8, bl[nt][j]), acc[nt]);
+                            acc[nt] = mfma16<kGgmlBF16>(__builtin_bit_cast(f16x8, alo),
+                                                        __builtin_bit_cast(f16x8, bh[nt][j]), acc[nt]);
+                        }
+                    }
+                    // lane: row 64 w + 32 nt + l32, k = 32 t + 8 g + 4 kh + 0..3
+#pragma unroll
+                    for (uint32_t nt = 0; nt < 2; nt++) {
+                        if (!in_slot[nt]) continue;
+                        const uint32_t pr = 64u * wave + 32u * nt + (lane & 31u);
+#pragma unroll
+                        for (uint32_t g = 0; g < 4; g++) {
+                            u32x2* const cell =
+                                (u32x2*)(lb + pr * 128u + (((4u * t + g) ^ lds_swz(pr)) << 4) + 8u * (lane >> 5));
+                            u32x2 v = *cell;
+#pragma unroll
+                            for (uint32_t e = 0; e < 2; e++) {
+                                const float d0 = acc[nt][4 * g + 2 * e], d1 = acc[nt][4 * g + 2 * e + 1];
+                                if constexpr (OT == kGgmlBF16) {
+                                    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+                                    v[e] = __builtin_bit_cast(
+                                        uint32_t, bf16x2_t{(__bf16)(__uint_as_float(v[e] << 16) + d0),
+                                                           (__bf16)(__uint_as_float(v[e] & 0xffff0000u) + d1)});
+                                } else {
+                                    v[e] = pack_f16x2(
+                                        (float)__builtin_bit_cast(_Float16, (uint16_t)(v[e] & 0xffffu)) + d0,
+                                        (float)__builtin_bit_cast(_Float16, (uint16_t)(v[e] >> 16)) + d1);
+                                }
+                            }
+                            *cell = v;
+                        }
+                    }
+                }
+            }
+        }
         __syncthreads();
         u32x4* const dst = (u32x4*)(img + ((uint64_t)p * S + s0 + i) * kBlk);
 #pragma unroll
@@ -328,13 +476,13 @@ __global__ void __launch_bounds__(256, 1) gemm_w16_persist(const PersistArgs arg
     LLMR_WAIT_VMCNT(0);  // no DMA may still be writing this workgroup's LDS when it exits
 }
 
-template <uint32_t WT, uint32_t OT, bool SW>
+template <uint32_t WT, uint32_t OT, bool SW, uint32_t RS = 0>
 hipError_t build_image(const void* w, const void* w2, void* img, uint32_t N, uint32_t K, uint32_t row_offset,
-                       hipStream_t st) {
+                       hipStream_t st, const ImageLora& lo = ImageLora{}) {
     const uint32_t panels = SW ? (N + 127u) / 128u : (N + 255u) / 256u;
     const uint32_t blocks = panels * ((K / (uint32_t)kBK + kImgStages - 1) / kImgStages);
-    hipLaunchKernelGGL((w16_image_kernel<WT, OT, SW>), dim3(blocks), dim3(256), 0, st, (const uint8_t*)w,
-                       (const uint8_t*)w2, (uint8_t*)img, N, K, row_offset);
+    hipLaunchKernelGGL((w16_image_kernel<WT, OT, SW, RS>), dim3(blocks), dim3(256), 0, st, (const uint8_t*)w,
+                       (const uint8_t*)w2, (uint8_t*)img, N, K, row_offset, lo);
     return hipGetLastError();
 }
 
@@ -380,6 +528,23 @@ hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint3
     if (sw) return hipErrorInvalidValue;  // the SwiGLU takes Q8_0 weights
     if (otype == kGgmlBF16) return build_image<kGgmlQ4K, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st);
     return build_image<kGgmlQ4K, kGgmlF16, false>(w, w2, img, N, K, row_offset, st);
+}
+
+hipError_t launch_w16_image_lora(const void* w, uint32_t wtype, uint32_t otype, void* img, uint32_t N, uint32_t K,
+                                 uint32_t row_offset, const LoraGemm& l, hipStream_t st) {
+    if (l.rank == 0 || l.rank > kLoraImageMaxRank) return hipErrorInvalidValue;
+    const ImageLora lo{l.a, l.b, l.scale, l.rank, l.row_offset, l.b_rows, l.weight_row_offset};
+    auto go = [&](auto rs) {
+        constexpr uint32_t R = decltype(rs)::value;
+        if (wtype == kGgmlQ8_0)
+            return otype == kGgmlBF16
+                       ? build_image<kGgmlQ8_0, kGgmlBF16, false, R>(w, nullptr, img, N, K, row_offset, st, lo)
+                       : build_image<kGgmlQ8_0, kGgmlF16, false, R>(w, nullptr, img, N, K, row_offset, st, lo);
+        return otype == kGgmlBF16 ? build_image<kGgmlQ4K, kGgmlBF16, false, R>(w, nullptr, img, N, K, row_offset, st, lo)
+                                  : build_image<kGgmlQ4K, kGgmlF16, false, R>(w, nullptr, img, N, K, row_offset, st, lo);
+    };
+    // rank <= 32: two rank steps of 16 (fewer registers), else four
+    return l.rank <= 32u ? go(std::integral_constant<uint32_t, 2>{}) : go(std::integral_constant<uint32_t, kLoraSteps>{});
 }
 
 hipError_t launch_w16_gemm(const PersistArgs& a, uint32_t xtype, bool swiglu, bool grouped, int num_cus,

@@ -90,6 +90,29 @@ hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t w
 size_t w16_image_bytes(uint32_t N, uint32_t K, bool swiglu);
 hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
                             uint32_t K, uint32_t row_offset, hipStream_t st);
+// A LoRA on a single GEMM (the reference's dispatch_batch_matmul with a
+// LoRA): output columns [row_offset, row_offset + b_rows) get scale *
+// b[weight_row_offset + o] . (a x).
+struct LoraGemm {
+    const float* a;
+    const float* b;
+    uint32_t rank;
+    float scale;
+    uint32_t b_rows, row_offset, weight_row_offset;
+};
+// The GEMM with its LoRA merged into the two-pass kernel's weight image
+// (w + scale * b a, rounded to 16 bits once), when the GEMM runs two-pass
+// and rank <= kLoraImageMaxRank: then the workspace it needs, else 0.
+constexpr uint32_t kLoraImageMaxRank = 64;
+// The weight image of launch_w16_image (no SwiGLU) with the LoRA merged:
+// w + scale * b a on features [row_offset, row_offset + b_rows).
+hipError_t launch_w16_image_lora(const void* w, uint32_t wtype, uint32_t otype, void* img, uint32_t N, uint32_t K,
+                                 uint32_t row_offset, const LoraGemm& l, hipStream_t st);
+size_t batch_matmul_lora_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M,
+                                         uint32_t rank, int num_cus);
+hipError_t launch_batch_matmul_lora(const void* w, uint32_t wtype, const void* x, uint32_t xtype, float* y,
+                                    uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset, const LoraGemm& l,
+                                    int num_cus, void* ws, hipStream_t st);
 
 // Attention (flash_attn.hip). F32 / BF16 Q, K, V are rounded to fp16 into
 // `ws` first (flash_attention_workspace_bytes; 0 for F16).

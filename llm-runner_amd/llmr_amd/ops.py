@@ -146,7 +146,11 @@ def dispatch_batch_matmul(g: RenderGraph, weight: Tensor, input: Tensor, output:
     then the LoRA correction when an adapter is present.
 
     Mirrors zimage::dispatch_batch_matmul (dit.c3:1198-1301) for Q8_0 / Q4_K
-    weights, including its trailing dispatch_lora_correction."""
+    weights, including its trailing dispatch_lora_correction: a GEMM on the
+    two-pass kernel (>= 2048 tokens, enough tiles) merges a rank <= 64
+    adapter into its 16-bit weight image (W + scale * b a on the adapter's
+    output features, rounded once more to 16 bits); otherwise the exact
+    correction follows the GEMM."""
     if weight.dtype not in (GGML_Q8_0, GGML_Q4_K):
         raise capi.LlmrError(capi.LLMR_ERR_UNSUPPORTED, f"weight type {weight.dtype}")
     for t, n in ((weight, "weight"), (input, "input"), (output, "output")):
@@ -157,11 +161,24 @@ def dispatch_batch_matmul(g: RenderGraph, weight: Tensor, input: Tensor, output:
         raise ValueError("weight shape does not cover [row_offset, row_offset+out_dim) x in_dim")
     if input.data.numel() < seq_len * in_dim or output.data.numel() < seq_len * out_dim:
         raise ValueError("input/output smaller than [seq_len, in_dim] / [seq_len, out_dim]")
+    if lora is not None and lora.present and 0 < lora.rank <= MAX_LORA_RANK:
+        # llmr_batch_matmul_lora: on the two-pass GEMM the adapter is merged
+        # into the weight image; otherwise the GEMM, then the exact correction
+        if lora_scratch is None or lora_scratch.dtype != torch.float32 or not lora_scratch.is_cuda:
+            raise ValueError("lora_scratch must be an f32 device tensor")
+        if lora_scratch.numel() < seq_len * lora.rank:
+            raise ValueError("lora_scratch smaller than seq_len * rank")
+        rows = lora_b_rows or out_dim
+        if lora.a.shape[1] != in_dim or lora_weight_row_offset + rows > lora.b.shape[0]:
+            raise ValueError("lora.a must be [rank, in_dim] and lora.b cover weight_row_offset + b_rows rows")
+        g.bind_stream()
+        g.ctx.batch_matmul_lora(weight.ptr(), weight.dtype, input.ptr(), input.dtype, output.ptr(), out_dim, in_dim,
+                                seq_len, row_offset, lora.c_struct(), lora_scratch.data_ptr(), lora_b_rows,
+                                lora_row_offset, lora_weight_row_offset)
+        return
     g.bind_stream()
     g.ctx.batch_matmul(weight.ptr(), weight.dtype, input.ptr(), input.dtype, output.ptr(),
                        out_dim, in_dim, seq_len, row_offset)
-    dispatch_lora_correction(g, lora, lora_scratch, input, output, in_dim, out_dim, seq_len, lora_b_rows,
-                             lora_row_offset, lora_weight_row_offset)
 
 
 def merge_one_site(g: RenderGraph, base: Tensor, lora: LoraTensor, dst_row_offset: int = 0) -> bool:

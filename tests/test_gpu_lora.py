@@ -1,6 +1,8 @@
 """GPU LoRA (llmr_lora_correction, llmr_batch_matmul_lora, llmr_q8_lora_merge)
 vs the oracle: bit-identical (the kernels form every f32 sum in the
-reference's order, without contraction)."""
+reference's order, without contraction), except llmr_batch_matmul_lora on
+the two-pass GEMM, which merges the adapter into its 16-bit weight image and
+is held to the GEMM's tolerance."""
 import numpy as np
 import pytest
 
@@ -131,3 +133,91 @@ def test_lora_rejects_and_skips(dev):
     _, _, l3 = _lora(dev, r, 4, 256, 64, 1.0)
     with pytest.raises(capi.LlmrError):
         g.ctx.lora_correction(l3.c_struct(), scratch.data_ptr(), x.data_ptr(), 0, y.data_ptr(), 256, 64, 4, 40, 30)
+
+
+def _split_bf16(x):
+    from llmr_amd.workloads import round_bf16
+    hi = round_bf16(x)
+    return hi, round_bf16((x - hi).astype(np.float32))
+
+
+def _merged_rows(orc, blk, xs16, A, B, scale, rows_s, N, K, row_off, w_off, b_rows, ot):
+    """Sampled output rows of x . W'^T in f64, W' the 16-bit weight image
+    with the adapter merged: W16 + d on the slot's features, d = (scale B) A
+    with both factors split into bf16 hi + lo parts and summed as hi hi +
+    hi lo + lo hi (exactly here, rounded to f32 once), added to W16 in f32
+    and rounded to the operand type once more (nearest even)."""
+    from llmr_amd.workloads import round_bf16
+    if ot == 1:
+        w16 = orc.f16_to_f32(orc.dequant_q4k_operand(blk)).reshape(N, K)
+    else:
+        w16 = round_bf16(orc.dequant_q4k(blk)).reshape(N, K)
+    bs = np.float32(scale) * B[w_off:w_off + b_rows]  # [b_rows, rank], f32 products
+    bh, bl = (t.astype(np.float64) for t in _split_bf16(bs))
+    ah, al = (t.astype(np.float64) for t in _split_bf16(A))
+    dlt = (bh @ ah + bh @ al + bl @ ah).astype(np.float32)
+    merged = w16.copy()
+    s = w16[row_off:row_off + b_rows] + dlt
+    merged[row_off:row_off + b_rows] = (s.astype(np.float16).astype(np.float32) if ot == 1 else round_bf16(s))
+    return xs16[rows_s].astype(np.float64) @ merged.T.astype(np.float64)
+
+
+# GEMMs on the two-pass kernel (>= 2048 tokens, >= 128 tiles of 256 x 256)
+# with rank <= 64 merge the adapter into the 16-bit weight image as it is
+# built: W' = RN16(W16 + d) on the slot's features, d = (scale B) A on the
+# matrix cores from bf16 hi/lo splits of both factors. Features outside
+# the slot equal the plain GEMM bit for bit (their image is untouched); the
+# slot equals x . W'^T to f32 accumulation order (checked against an exact
+# host model of W'), GEMM + exact correction within the 16-bit rounding of
+# W', and the oracle (the reference's f32 correction after the GEMM) within
+# the GEMM bar.
+@pytest.mark.parametrize("M,N,K,rank,b_rows,row_off,w_off,xtype", [
+    (2304, 4096, 512, 16, 1024, 512, 64, 30),    # bf16, a slot of the output
+    (2400, 4100, 768, 48, 0, 0, 0, 1),           # f16, whole output, ragged M and N
+    (2048, 4096, 512, 64, 2000, 100, 7, 0),      # f32 input (converted to f16 first), the largest merged rank
+])
+def test_batch_matmul_lora_fused(orc, dev, M, N, K, rank, b_rows, row_off, w_off, xtype):
+    import torch
+    from llmr_amd import gguf, ops, synth
+    from conftest import rel_l2
+    r = np.random.default_rng(M + rank)
+    rows = b_rows or N
+    A, B, lora = _lora(dev, r, rank, K, w_off + rows + 5, 0.7)
+    blk = gguf.quantize(synth.normal(17, 2, N * K, 0.02), gguf.GGML_Q4_K)
+    wt = ops.Tensor.quantized(torch.from_numpy(blk).to(dev), gguf.GGML_Q4_K, N, K)
+    xt = _act(synth.normal(17, 1, M * K).reshape(M, K), xtype, dev)
+    g = ops.default_graph()
+    base = torch.empty(M, N, device=dev)
+    ops.dispatch_batch_matmul(g, wt, ops.Tensor.from_torch(xt), ops.Tensor.from_torch(base), N, K, M, 0)
+    fused = torch.empty(M, N, device=dev)
+    scratch = torch.empty(M * rank, device=dev)
+    ops.dispatch_batch_matmul(g, wt, ops.Tensor.from_torch(xt), ops.Tensor.from_torch(fused), N, K, M, 0,
+                              lora=lora, lora_scratch=scratch, lora_b_rows=b_rows, lora_row_offset=row_off,
+                              lora_weight_row_offset=w_off)
+    again = torch.empty(M, N, device=dev)
+    ops.dispatch_batch_matmul(g, wt, ops.Tensor.from_torch(xt), ops.Tensor.from_torch(again), N, K, M, 0,
+                              lora=lora, lora_scratch=scratch, lora_b_rows=b_rows, lora_row_offset=row_off,
+                              lora_weight_row_offset=w_off)
+    exact = base.clone()
+    ops.dispatch_lora_correction(g, lora, scratch, ops.Tensor.from_torch(xt), ops.Tensor.from_torch(exact), K, N,
+                                 M, b_rows, row_off, w_off)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, again)  # deterministic
+    f, e, b0 = fused.cpu().numpy(), exact.cpu().numpy(), base.cpu().numpy()
+    slot = slice(row_off, row_off + rows)
+    outside = np.ones(N, bool)
+    outside[slot] = False
+    assert np.array_equal(f[:, outside], b0[:, outside])
+    err = rel_l2(f[:, slot], e[:, slot])
+    rows_s = np.array([0, 1, M // 2, M - 1], np.int64)
+    xs = xt.float().cpu().numpy()
+    xs16 = xs.astype(np.float16).astype(np.float32) if xtype == 0 else xs
+    model = _merged_rows(orc, blk, xs16, A, B, 0.7, rows_s, N, K, row_off, w_off, rows, 30 if xtype == 30 else 1)
+    err_model = rel_l2(f[rows_s], model)
+    print(f"M={M} N={N} K={K} rank={rank}: vs merged-image model {err_model:.2e}, vs GEMM + correction {err:.2e}")
+    assert err_model <= 2e-5
+    assert err <= (5e-3 if xtype == 30 else 1e-3)
+    ref = orc.batch_matmul(blk, gguf.GGML_Q4_K, xs, N, K, M, 0, rows=rows_s.astype(np.uint32))
+    s_ref = orc.lora_down(A, xs[rows_s])
+    ref = orc.lora_up(B, s_ref, ref, 0.7, row_offset=row_off, weight_row_offset=w_off, b_rows=rows)
+    assert rel_l2(f[rows_s], ref) <= 1e-2
