@@ -84,9 +84,13 @@ __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restric
                                                          uint32_t row_offset, const ImageLora lo) {
     constexpr bool LORA = RS > 0;         // RS: rank steps of 16 the kernel holds (rank <= 16 RS)
     constexpr uint32_t RA = LORA ? RS : 1u;  // register array extent
-    __shared__ __attribute__((aligned(16))) uint8_t lblk[2][kBlk];
-    // LORA: a^T fragments of the stage, [k tile 2][rank step RS][hi, lo][64 lanes] x 16 B
-    __shared__ __attribute__((aligned(16))) u32x4 afr[LORA ? 2u * RS * 2u * 64u : 1u];
+    // one LDS object: two image blocks, then (LORA) the stage's a^T
+    // fragments, [k tile 2][rank step RS][hi, lo][64 lanes] x 16 B; before
+    // the first stage the panel's b rows are staged across all of it
+    constexpr uint32_t kAfr = LORA ? 2u * RS * 2u * 64u * 16u : 0u;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2u * kBlk + kAfr];
+    uint8_t(*const lblk)[kBlk] = (uint8_t(*)[kBlk])lds;
+    u32x4* const afr = (u32x4*)(lds + 2u * kBlk);
     const uint32_t S = K / kBK, groups = (S + kImgStages - 1) / kImgStages;
     const uint32_t p = blockIdx.x / groups, s0 = (blockIdx.x % groups) * kImgStages, r = threadIdx.x;
     const uint32_t rb = (WT == kGgmlQ8_0) ? (K / 32u) * 34u : (K / 256u) * 144u;
@@ -105,32 +109,23 @@ __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restric
     // LORA loads go first, ahead of the weight rows: they are L2 hits and
     // return before the rows, so waiting for them (the memory counter is in
     // order) costs nothing the rows do not.
-    //  bv: the wave's scale * b, rows 64 wave + 32 nt + l32 and ranks
-    //      16 j + 8 kh + 0..7 (its (scale b)^T MFMA fragments);
+    //  bv: the panel's b rows, element u = r + 256 i of [256 rows][16 RS]
+    //      (consecutive threads read consecutive floats of a row);
     //  av: a for the thread's units q = r + 256 h of each stage (rank group
     //      rg = q / 64, column k = q % 64, rows 8 rg .. 8 rg + 7).
     // Rows outside the slot and ranks >= rank lie past the descriptors'
     // ranges and read as zero, so every load is unconditional.
     const uint32_t wave = r >> 6, lane = r & 63u;
-    const uint32_t w0 = n0 + 64u * wave;  // the wave's rows [w0, w0 + 64) of the weight
-    float bv[2][RA][8], av[kImgStages][LORA ? RS / 2u : 1u][8];
+    float bv[LORA ? RS * 16u : 1u], av[kImgStages][LORA ? RS / 2u : 1u][8];
     bool in_slot[2] = {false, false};
     bool wave_any = false;
     if constexpr (LORA) {
         const rsrc_t rbv = make_rsrc(lo.b + (uint64_t)lo.wro * lo.rank, (uint64_t)lo.b_rows * lo.rank * 4u);
-        wave_any = w0 < N && w0 + 64u > lo.lro && w0 < lo.lro + lo.b_rows;
 #pragma unroll
-        for (uint32_t nt = 0; nt < 2; nt++) {
-            const uint32_t n = w0 + 32u * nt + (lane & 31u);
-            in_slot[nt] = n < N && n >= lo.lro && n - lo.lro < lo.b_rows;
-#pragma unroll
-            for (uint32_t j = 0; j < RS; j++)
-#pragma unroll
-                for (uint32_t e = 0; e < 8; e++) {
-                    const uint32_t rr = 16u * j + 8u * (lane >> 5) + e;
-                    const uint32_t off = (in_slot[nt] && rr < lo.rank) ? ((n - lo.lro) * lo.rank + rr) * 4u : ~0u;
-                    bv[nt][j][e] = __uint_as_float(bload4(rbv, off, 0u));
-                }
+        for (uint32_t i = 0; i < RS * 16u; i++) {
+            const uint32_t u = r + 256u * i, n = n0 + u / (16u * RS), c = u % (16u * RS);
+            const bool ok = n < N && n >= lo.lro && n - lo.lro < lo.b_rows && c < lo.rank;
+            bv[i] = __uint_as_float(bload4(rbv, ok ? ((n - lo.lro) * lo.rank + c) * 4u : ~0u, 0u));
         }
         const rsrc_t rav = make_rsrc(lo.a, (uint64_t)lo.rank * K * 4u);
 #pragma unroll
@@ -152,16 +147,35 @@ __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restric
             static_for<0, WRow<WT, OT>::kLoads>(
                 [&](auto L) { u[i].template load<decltype(L)::value>(rs, row * rb, s0 + i); });
     const uint32_t base = r * 128u + (lds_swz(r) << 4);
+    // LORA: the wave's (scale b)^T MFMA fragments, rows 64 wave + 32 nt +
+    // l32 and ranks 16 j + 8 kh + 0..7, through LDS (row stride 16 RS + 4
+    // floats: the 16-byte fragment reads of 32 rows fall in distinct banks)
     u32x4 bh[2][RA], bl[2][RA];
     if constexpr (LORA) {
+        constexpr uint32_t ld = 16u * RS + 4u;
+        float* const bs = (float*)lds;
 #pragma unroll
-        for (uint32_t nt = 0; nt < 2; nt++)
+        for (uint32_t i = 0; i < RS * 16u; i++) {
+            const uint32_t u = r + 256u * i;
+            bs[(u / (16u * RS)) * ld + u % (16u * RS)] = bv[i];
+        }
+        __syncthreads();
+        const uint32_t w0 = n0 + 64u * wave;  // the wave's rows [w0, w0 + 64) of the weight
+        wave_any = w0 < N && w0 + 64u > lo.lro && w0 < lo.lro + lo.b_rows;
+#pragma unroll
+        for (uint32_t nt = 0; nt < 2; nt++) {
+            const uint32_t pr = 64u * wave + 32u * nt + (lane & 31u), n = n0 + pr;
+            in_slot[nt] = n < N && n >= lo.lro && n - lo.lro < lo.b_rows;
 #pragma unroll
             for (uint32_t j = 0; j < RS; j++) {
-#pragma unroll
-                for (uint32_t e = 0; e < 8; e++) bv[nt][j][e] *= lo.scale;
-                split_bf16x8(bv[nt][j], bh[nt][j], bl[nt][j]);
+                const float* const src8 = bs + pr * ld + 16u * j + 8u * (lane >> 5);
+                const f32x4 x0 = *(const f32x4*)src8, x1 = *(const f32x4*)(src8 + 4);
+                const float v[8] = {lo.scale * x0[0], lo.scale * x0[1], lo.scale * x0[2], lo.scale * x0[3],
+                                    lo.scale * x1[0], lo.scale * x1[1], lo.scale * x1[2], lo.scale * x1[3]};
+                split_bf16x8(v, bh[nt][j], bl[nt][j]);
             }
+        }
+        __syncthreads();  // the staged b is read before the first stage's stores
     }
 #pragma unroll
     for (uint32_t i = 0; i < kImgStages; i++) {
