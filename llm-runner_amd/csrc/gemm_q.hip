@@ -1165,6 +1165,17 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restr
     ((f32x4*)Y)[i] = a;
 }
 
+}  // namespace
+
+hipError_t launch_splitk_reduce(const float* part, float* y, uint64_t mn, uint32_t splits, hipStream_t st) {
+    const uint64_t n4 = mn / 4;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, st, part, y, n4,
+                       splits, mn);
+    return hipGetLastError();
+}
+
+namespace {
+
 // splits > 1: the partials go to `part` (splits * M * N floats), then the
 // reduction writes Y.
 template <uint32_t WT, uint32_t XT, int BM, int BN>
@@ -1185,10 +1196,7 @@ hipError_t launch_tiled(const void* w, const void* x, float* y, uint32_t N, uint
                        splits > 1 ? part : y, N, K, M, row_offset, tiles_m, tiles_n, per, splits > 1 ? mn : 0ull);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || splits == 1) return e;
-    const uint64_t n4 = mn / 4;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((uint32_t)((n4 + 255) / 256)), dim3(256), 0, st, part, y, n4,
-                       splits, mn);
-    return hipGetLastError();
+    return launch_splitk_reduce(part, y, mn, splits, st);
 }
 
 // Tiles of the 4-wave kernel: the largest that still gives every CU ~1.5
@@ -1303,10 +1311,12 @@ constexpr uint32_t kW16MinTokens = 2048;
 // copy of f32 activations for the persistent kernels has no smaller form,
 // so a plan may still exceed the limit there (the caller refuses it).
 struct GemmPlan {
-    bool persistent, two_pass, convert_x;
+    bool persistent, two_pass, convert_x, skinny;
     uint32_t xt;                  // activation type the kernel reads
     TilePlan tiles;               // the tiled kernel's tile and splits (not persistent)
-    size_t x16_off, img_off, ws;  // workspace: [x16 | image] (persistent), split-K partials (tiled)
+    uint32_t splits;              // the skinny kernel's K splits
+    size_t x16_off, img_off, ws;  // workspace: [x16 | image] (persistent), [packed x | partials]
+                                  // (skinny), split-K partials (tiled)
 };
 GemmPlan plan_gemm(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M, int num_cus,
                    size_t ws_limit) {
@@ -1315,6 +1325,25 @@ GemmPlan plan_gemm(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint3
     p.persistent = (K % kBK) == 0 && N % 4 == 0 && 2 * tiles >= (uint64_t)num_cus &&
                    (uint64_t)M * K * 2u < (1ull << 31) && (uint64_t)N * row_bytes_of(wtype, K) < (1ull << 31);
     p.xt = xtype;
+    if (!p.persistent && M <= 256 && (K % kBK) == 0 && N % 4 == 0 && (uint64_t)M * K * 2u < (1ull << 31) &&
+        (uint64_t)N * row_bytes_of(wtype, K) < (1ull << 31)) {
+        // few tokens: the skinny kernel (one workgroup per CU: its LDS),
+        // K split so the launch fills the CUs in one round (at least
+        // kSplitMinStages stages per split), as far as the partials fit the
+        // workspace
+        const size_t x16 = skinny_x_bytes(xtype, M, K), part = (size_t)M * N * sizeof(float);
+        if (x16 <= ws_limit) {
+            const uint32_t S = K / kBK, tn = (N + 63) / 64;
+            uint32_t splits = std::max<uint32_t>(1u, std::min<uint32_t>((uint32_t)num_cus / tn, S / kSplitMinStages));
+            if (splits > 1 && x16 + splits * part > ws_limit)
+                splits = std::max<uint32_t>(1u, (uint32_t)((ws_limit - x16) / part));
+            const uint32_t per = (S + splits - 1) / splits;
+            p.skinny = true;
+            p.splits = (S + per - 1) / per;
+            p.ws = x16 + (p.splits > 1 ? p.splits * part : 0u);
+            return p;
+        }
+    }
     if (!p.persistent) {
         p.tiles = plan_tiles(wtype, N, K, M, num_cus);
         const size_t part = (size_t)M * N * sizeof(float);
@@ -1467,6 +1496,7 @@ hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uin
     if (wtype == kGgmlQ4K && M <= kGemvMaxTokens)
         return launch_gemv_q4k(w, xtype, x, y, N, K, M, row_offset, st);
     const GemmPlan pl = plan_gemm(wtype, xtype, N, K, M, num_cus, ws_limit);
+    if (pl.skinny) return launch_gemm_skinny(w, wtype, x, xtype, y, N, K, M, row_offset, pl.splits, ws, st);
     if (!pl.persistent) {
         if (wtype == kGgmlQ8_0)
             return dispatch_w<kGgmlQ8_0>(w, xtype, x, y, N, K, M, row_offset, pl.tiles, (float*)ws, st);

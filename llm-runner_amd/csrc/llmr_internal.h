@@ -88,6 +88,17 @@ hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t w
 // w and up w2), operand type otype, into `img` (w16_image_bytes). The GEMM
 // launcher itself (launch_w16_gemm) is declared in gemm_q_common.h.
 size_t w16_image_bytes(uint32_t N, uint32_t K, bool swiglu);
+// y = sum of the split partials part[0 .. splits) (each mn floats, mn % 4 ==
+// 0), added in split order.
+hipError_t launch_splitk_reduce(const float* part, float* y, uint64_t mn, uint32_t splits, hipStream_t st);
+// The few-token GEMM (M <= 256, K % 64 == 0, activations f32 / f16 /
+// bf16): all M tokens x 64 features per workgroup, K in `splits` non-empty
+// ranges. Workspace: f32 activations rounded to fp16 (skinny_x_bytes), then,
+// for splits > 1, the partials (splits * M * N floats) reduced into y.
+size_t skinny_x_bytes(uint32_t xtype, uint32_t M, uint32_t K);
+hipError_t launch_gemm_skinny(const void* w, uint32_t wtype, const void* x, uint32_t xtype, float* y, uint32_t N,
+                              uint32_t K, uint32_t M, uint32_t row_offset, uint32_t splits, void* ws,
+                              hipStream_t st);
 hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
                             uint32_t K, uint32_t row_offset, hipStream_t st);
 // A LoRA on a single GEMM (the reference's dispatch_batch_matmul with a

@@ -50,6 +50,13 @@ CASES = [
     (12, 3, 1000, 768, 1, 4),        # small-M Q4_K kernel, f16, row_offset
     (12, 4, 130, 512, 30, 0),        # small-M Q4_K kernel at its largest M
     (12, 5, 72, 512, 30, 0),         # one token more: the tiled kernel again
+    # few tokens, N % 4 == 0: the skinny kernel (all tokens x 64 features per
+    # workgroup, K split across workgroups)
+    (8, 200, 1000, 768, 30, 8),      # ragged M and N, bf16, row_offset
+    (8, 33, 64, 4096, 0, 0),         # one feature tile: 16 K splits, f32
+    (12, 250, 3072, 3072, 1, 0),     # Q4_K f16 at the single-linear size
+    (12, 256, 21504, 1024, 30, 0),   # 336 feature tiles: no split
+    (8, 17, 128, 192, 1, 0),         # three stages: one split, short pipeline
 ]
 
 
