@@ -256,17 +256,25 @@ MODEL_SETUPS = {"zimage_block": setup_zimage_block, "flux_step": setup_flux_step
 
 
 def gemm_kernel_name(name: str, num_cus: int) -> str:
-    """The kernel the library's dispatch picks for a GEMM workload: the
-    persistent 256x256 kernel for 16-bit activations with at least half the
-    CUs' worth of tiles (and N % 4 == 0; on 8 waves for Q8_0), else the
-    4-wave tiled kernel."""
+    """The kernels the library's dispatch runs for a GEMM workload (the one
+    that dominates first): the two-pass path (weight image, then the all-DMA
+    persistent GEMM) from 2048 tokens with at least half the CUs' worth of
+    256 x 256 tiles; the one-pass persistent kernels below 2048 tokens; the
+    few-token kernel up to 256 tokens; else the 4-wave tiled kernel."""
     from llmr_amd import gguf, workloads
     g = workloads.GEMMS[name]
     tiles = ((g.M + 255) // 256) * ((g.N + 255) // 256)
     if g.wtype == gguf.GGML_Q8_0 and g.K % 64:
         return "gemm_q_generic"
-    if g.xtype != gguf.GGML_F32 and g.N % 4 == 0 and 2 * tiles >= num_cus:
-        return "gemm_q_persist8" if g.wtype == gguf.GGML_Q8_0 else "gemm_q_persist"
+    if g.wtype == gguf.GGML_Q4_K and g.M <= 4:
+        return "gemv_q4k"
+    pre = "f32->f16 conversion + " if g.xtype == gguf.GGML_F32 else ""
+    if g.K % 64 == 0 and g.N % 4 == 0 and 2 * tiles >= num_cus:
+        if g.M >= 2048:
+            return "gemm_w16_persist + w16_image_kernel" + (" + f32->f16 conversion" if pre else "")
+        return pre + ("gemm_q_persist8" if g.wtype == gguf.GGML_Q8_0 else "gemm_q_persist")
+    if g.M <= 256 and g.K % 64 == 0 and g.N % 4 == 0:
+        return "gemm_q_skinny + splitk_reduce_kernel" + (" + skinny_pack_kernel" if pre else "")
     return "gemm_q_mfma"
 
 
