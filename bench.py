@@ -278,6 +278,20 @@ def gemm_kernel_name(name: str, num_cus: int) -> str:
     return "gemm_q_mfma"
 
 
+def kernel_name(name: str, num_cus: int) -> str:
+    """The kernels a kernel-level workload runs (the dominant one first)."""
+    from llmr_amd import workloads
+    if name == "flux_attention":
+        return "flash_attn_fwd64_w8"
+    if name == "flux_attention_f32":
+        return "flash_attn_fwd64_w8 + kv_to_f16_kernel"
+    if name == "flux_linear1_lora":
+        return "gemm_w16_persist + w16_image_kernel (LoRA merged)"
+    if name in workloads.SWIGLUS:
+        return "gemm_w16_persist (SwiGLU) + w16_image_kernel"
+    return gemm_kernel_name(name, num_cus)
+
+
 def measure(dev, name, steps, warmup):
     from llmr_amd import workloads
     if name in ("flux_attention", "flux_attention_f32"):
@@ -410,9 +424,7 @@ def main():
     else:
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(ach / PEAK_TFLOPS, 4), "traffic": _traffic(args.workload),
-                "kernel": ("flash_attn_fwd64_w8" if args.workload == "flux_attention" else
-                           gemm_kernel_name(args.workload,
-                                            torch.cuda.get_device_properties(dev).multi_processor_count)),
+                "kernel": kernel_name(args.workload, torch.cuda.get_device_properties(dev).multi_processor_count),
                 "algorithmic_bytes": main_r["bytes"],
                 "hbm_frac_algorithmic": round(main_r["bytes"] / (main_r["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
     line = {

@@ -366,9 +366,8 @@ LLMR_API int llmr_lora_correction(llmr_context* ctx, const llmr_lora* lora, floa
  * image: W' = RN16(W16 + scale * b a) on output features [lora_row_offset,
  * lora_row_offset + b_rows), one more 16-bit rounding of those weights
  * (within the GEMM's tolerance of the reference; the other features are
- * bit-identical to llmr_batch_matmul), lora_scratch unused and lora->a
- * 16-byte aligned. Every other call is llmr_batch_matmul followed by
- * llmr_lora_correction. */
+ * bit-identical to llmr_batch_matmul), lora_scratch unused. Every other
+ * call is llmr_batch_matmul followed by llmr_lora_correction. */
 LLMR_API int llmr_batch_matmul_lora(llmr_context* ctx, const void* weight, uint32_t weight_type,
                                     const void* input, uint32_t input_type, float* output, uint32_t out_dim,
                                     uint32_t in_dim, uint32_t seq_len, uint32_t row_offset, const llmr_lora* lora,

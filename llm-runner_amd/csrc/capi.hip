@@ -387,7 +387,6 @@ int llmr_batch_matmul_lora(llmr_context* ctx, const void* weight, uint32_t wtype
                                     lora_b_rows, lora_row_offset, lora_weight_row_offset);
     }
     if (!lora->a || !lora->b) return fail(LLMR_ERR_INVALID_ARG, "null LoRA a or b pointer");
-    if (!aligned(lora->a, 16)) return fail(LLMR_ERR_INVALID_ARG, "LoRA a must be 16-byte aligned");
     const uint32_t b_rows = lora_b_rows ? lora_b_rows : out_dim;
     if ((uint64_t)lora_row_offset + b_rows > out_dim)
         return fail(LLMR_ERR_INVALID_ARG, "row_offset + b_rows (%u + %u) exceeds out_dim %u", lora_row_offset,
