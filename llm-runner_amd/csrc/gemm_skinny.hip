@@ -260,7 +260,8 @@ size_t skinny_x_bytes(uint32_t xtype, uint32_t M, uint32_t K) {
 hipError_t launch_gemm_skinny(const void* w, uint32_t wtype, const void* x, uint32_t xtype, float* y, uint32_t N,
                               uint32_t K, uint32_t M, uint32_t row_offset, uint32_t splits, void* ws,
                               hipStream_t st) {
-    if (M == 0 || M > 256 || K % kBK || splits == 0) return hipErrorInvalidValue;
+    // splits > 1: the reduction takes four floats per thread (N % 4 == 0)
+    if (M == 0 || M > 256 || K % kBK || splits == 0 || (splits > 1 && N % 4u)) return hipErrorInvalidValue;
     const uint32_t S = K / kBK, per = (S + splits - 1) / splits;
     if ((S + per - 1) / per != splits) return hipErrorInvalidValue;  // every split non-empty
     // f32 activations: rounded to fp16, stage-major, at the start of the

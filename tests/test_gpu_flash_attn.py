@@ -68,6 +68,25 @@ def test_fa_large_scores(orc, dev, xtype):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("H,S,xtype", [(5, 700, 0), (24, 4608, 0), (2, 300, 30), (7, 129, 30)])
+def test_fa_wide_inputs_match_fp16_inputs(dev, H, S, xtype):
+    """f32 / bf16 Q, K, V are rounded to fp16 where the kernel reads them (K and
+    V by a conversion pass into the workspace, Q as it is loaded), so the
+    output equals, bit for bit, the fp16 launch on the fp16-rounded inputs:
+    a head read from the wrong workspace slot would differ."""
+    import torch
+    from llmr_amd import ops
+    g = torch.Generator(device="cpu").manual_seed(H * 1000 + S)
+    q, k, v = (torch.randn(H, S, 128, generator=g) * 2 for _ in range(3))
+    if xtype == 30:
+        q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    q, k, v = (t.to(dev) for t in (q, k, v))
+    o_wide = ops.flash_attention(q, k, v, 1.0 / math.sqrt(128))
+    o_16 = ops.flash_attention(q.half(), k.half(), v.half(), 1.0 / math.sqrt(128))
+    torch.cuda.synchronize()
+    assert torch.equal(o_wide, o_16)
+
+
 def test_fa_constant_values(dev):
     """V constant along the keys -> every output row equals that row of V."""
     from llmr_amd import synth

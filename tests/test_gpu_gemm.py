@@ -351,11 +351,12 @@ def test_swiglu_full_size_sampled(orc, dev):
     assert err <= TOL
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 128, 512), (2304, 2304, 512)])
+@pytest.mark.parametrize("M,N,K", [(64, 128, 512), (2304, 2304, 512), (2304, 4096, 512)])
 def test_bf16_activations_beyond_fp16_range(orc, dev, M, N, K):
     """bf16 activations of magnitude ~1e5 (past fp16's 65504) stay finite: every
-    kernel uses bf16 operands for bf16 inputs (small launch: 4-wave tiles;
-    large: the persistent kernel), where Q4_K weights become bf16 operands too."""
+    kernel uses bf16 operands for bf16 inputs (64 tokens: the few-token kernel;
+    2304 x 2304: the 4-wave tiled kernel; 2304 x 4096: the two-pass path), where
+    Q4_K weights become bf16 operands too."""
     import torch
     from llmr_amd import gguf, ops, synth
     blk = gguf.quantize_q4k(synth.normal(24, 1, N * K, 0.02))
