@@ -83,12 +83,19 @@ __global__ void __launch_bounds__(256) row_norm_kernel(RowNormArgs a) {
     const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
     if (row >= a.rows) return;
     const float* xr = a.x + (size_t)row * a.x_stride;
-    f32x4 v[NV];
+    f32x4 v[NV], sc[NV], sh[NV];
     float s = 0.0f;
+    // the row and, when given, the modulation vectors all requested up
+    // front (the vectors' latency hidden behind the row's reductions)
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const uint32_t c = 4u * lane + 256u * i;
         v[i] = c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        sc[i] = a.scale && c < a.dim ? ld4(a.scale + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        sh[i] = a.shift && c < a.dim ? ld4(a.shift + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
         if constexpr (LN) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
         else s += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
     }
@@ -118,8 +125,8 @@ __global__ void __launch_bounds__(256) row_norm_kernel(RowNormArgs a) {
         f32x4 y;
         if constexpr (LN) y = (v[i] - mean) * r;
         else y = (v[i] * r) * ld4(a.w + c);
-        if (a.scale) y = y * (1.0f + ld4(a.scale + c));
-        if (a.shift) y = y + ld4(a.shift + c);
+        if (a.scale) y = y * (1.0f + sc[i]);
+        if (a.shift) y = y + sh[i];
         store4<OT>(orow, c, y);
     }
 }
@@ -307,6 +314,7 @@ hipError_t launch_row_norm_t(const RowNormArgs& a, bool ln, hipStream_t st) {
     }
     LLMR_ROW_NORM(4)
     LLMR_ROW_NORM(8)
+    LLMR_ROW_NORM(12)
     LLMR_ROW_NORM(16)
     LLMR_ROW_NORM(32)
 #undef LLMR_ROW_NORM
