@@ -57,6 +57,7 @@ CASES = [
     (12, 250, 3072, 3072, 1, 0),     # Q4_K f16 at the single-linear size
     (12, 256, 21504, 1024, 30, 0),   # 336 feature tiles: no split
     (8, 17, 128, 192, 1, 0),         # three stages: one split, short pipeline
+    (12, 100, 256, 1024, 0, 256),    # Q4_K, f32 activations packed to fp16, row_offset
 ]
 
 
