@@ -266,6 +266,13 @@ __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restric
 // step 1% slower (its loads of the residual rows dominate), and the
 // split-gelu one's per-lane choice of side made the compiler treat the load
 // cursors as divergent: both keep the direct stores.
+// The stores are non-temporal (streamed through L2: a tile's 256 KiB of
+// results are not read again by this kernel, its operand panels are; the L2
+// hit rates were not counted): flux_linear1 0.583 -> 0.568 ms,
+// flux_linear2 0.440 -> 0.423 ms, the Flux step 79.1 -> 78.9 ms (three
+// runs each). The gated-residual and split-gelu
+// epilogues keep cached stores: streamed, their rows (read again by the
+// next block's glue) made the step 0.7% slower.
 __device__ __forceinline__ void store_tile_rows(f32x16 (&acc)[4][4], float* Y, uint32_t M, uint32_t N, uint32_t m0,
                                                 uint32_t n0, uint32_t wm, uint32_t wn, uint32_t lane, uint32_t ldy,
                                                 uint8_t* st) {
@@ -293,7 +300,7 @@ __device__ __forceinline__ void store_tile_rows(f32x16 (&acc)[4][4], float* Y, u
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const uint32_t m = m0 + wm * 128u + 32u * b + 4u * i + rq;
-                if (m < M && n < N) *(f32x4*)(Y + (uint64_t)m * ldy + n) = v[i];
+                if (m < M && n < N) __builtin_nontemporal_store(v[i], (f32x4*)(Y + (uint64_t)m * ldy + n));
             }
         }
     }
