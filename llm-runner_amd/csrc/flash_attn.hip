@@ -50,6 +50,9 @@ constexpr int kD = 128;
 // ---------------------------------------------------------------------------
 constexpr uint32_t kBQ64 = 256;            // queries per workgroup
 constexpr uint32_t kTile64 = 64u * 256u;   // one K or V tile: 64 keys x 128 fp16
+// LDS of a workgroup: the K and V rings (6 tiles), or the epilogue's
+// staging of the output rows (kBQ64 queries x 128 f32)
+constexpr uint32_t kFaLds = kBQ64 * 128u * 4u > 6u * kTile64 ? kBQ64 * 128u * 4u : 6u * kTile64;
 
 // LDS rows are 256 bytes (16 chunks of 8 fp16). K: chunk c of key r at
 // c ^ (r & 15) (a 16-lane fragment read touches 16 distinct bank quads).
@@ -78,7 +81,8 @@ __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Flo
                                           const _Float16* __restrict__ V, float* __restrict__ O, uint32_t S,
                                           uint32_t H, float scale_log2, uint32_t n_qb) {
     // K ring in slots 0..2, V ring in slots 3..5
-    __shared__ __attribute__((aligned(16))) uint8_t lds[6u * kTile64];
+    // (after the key loop the epilogue stages O in it: 16 KiB per 32 queries)
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kFaLds];
     constexpr uint32_t ROW = kD * 2u;  // bytes per token row of one head
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -401,21 +405,41 @@ __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Flo
     }
     LLMR_WAIT_VMCNT(0);  // no DMA may still be writing LDS when the wave exits
 
-    // O = O^T / l, rows of this wave's queries
+    // O = O^T / l through LDS: the lanes hold 16-byte pieces of 32 query
+    // rows (query l32, dims 32 dt + 8 g + 4 kh + 0..3); stored as they are,
+    // every store instruction would write 32-byte pieces of 32 rows 12 KiB
+    // apart. Each wave stages its rows in its own 16 KiB per query block
+    // (row r at r * 512 bytes, 16-byte chunk c at (c ^ (r % 32)) * 16) once
+    // every wave is done with the K/V rings, and stores two whole 512-byte
+    // rows per instruction (flux_attention 0.315 -> 0.309 ms, mean of three
+    // runs each on one box).
+    __syncthreads();
 #pragma unroll
     for (int b = 0; b < NB; b++) {
+        float* const ot = (float*)lds + (wave * NB + b) * (32u * kD);
         const float inv_l = 1.0f / xhalf_sum(l_i[b]);
-        const uint32_t q = q0 + 32u * b + l32;
-        if (q < S) {
-            float* orow = O + (uint64_t)q * H * kD + (uint64_t)head * kD;
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++)
+        for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const uint32_t d = 32u * dt + 8u * g + 4u * kh;
-                    *(f32x4*)(orow + d) = f32x4{o[dt][b][4 * g] * inv_l, o[dt][b][4 * g + 1] * inv_l,
-                                                 o[dt][b][4 * g + 2] * inv_l, o[dt][b][4 * g + 3] * inv_l};
-                }
+            for (int g = 0; g < 4; g++) {
+                const uint32_t c = 8u * dt + 2u * g + kh;
+                *(f32x4*)(ot + l32 * kD + ((c ^ l32) << 2)) =
+                    f32x4{o[dt][b][4 * g] * inv_l, o[dt][b][4 * g + 1] * inv_l, o[dt][b][4 * g + 2] * inv_l,
+                          o[dt][b][4 * g + 3] * inv_l};
+            }
+    }
+    // the wave reads back only what it wrote: its LDS operations run in order
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const float* const ot = (const float*)lds + (wave * NB + b) * (32u * kD);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t r = 2u * i + kh, q = q0 + 32u * b + r;
+            const f32x4 v = *(const f32x4*)(ot + r * kD + ((l32 ^ r) << 2));
+            if (q < S) *(f32x4*)(O + (uint64_t)q * H * kD + (uint64_t)head * kD + 4u * l32) = v;
         }
     }
 }
