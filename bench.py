@@ -15,6 +15,11 @@ linear, the Z-Image QKV and SwiGLU projections) and the composed ones: one
 full Z-Image block and one Flux-dev-shaped denoising step (ms/step), so the
 three-part headline metric is reported in one line. `roofline` describes the workload's kernel,
 `cpu_baseline` the oracle timed on a bounded sample on the host cores.
+Every measurement runs its step back to back for DEVICE_WARMUP_MS of GPU
+time before the W warmup and K timed steps (the GPU's clock settles only
+after some tens of milliseconds of load); `cold_ms_per_step` is the
+headline's K steps timed straight after set-up and W warmup steps, without
+that.
 """
 from __future__ import annotations
 
@@ -32,6 +37,36 @@ METRIC = "Q4_K/Q8_0 dequant-GEMM TFLOPS, flash-attn TFLOPS, Flux 1024² ms/step"
 PEAK_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA, published
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
+
+
+# Sustained load first runs the GPU below its steady clock: on MI355X the
+# flash-attention launch takes ~306 us over its first 20 steps, ~287 over the
+# next 20 and settles at ~261 after ~100 (~30 ms), with the shader clock read
+# between steps dipping to ~2.0 GHz and returning to ~2.4 GHz. Each
+# measurement therefore first runs its step back to back for this much GPU
+# time (at most DEVICE_WARMUP_MAX_STEPS steps: after ~11k back-to-back calls
+# of the 28 us few-token GEMM, each of three launches, its later steps ran
+# 2-4x slower, which 3.7k calls did not do), then the W warmup steps and the
+# K timed steps.
+DEVICE_WARMUP_MS = 100.0
+DEVICE_WARMUP_MAX_STEPS = 2000
+
+
+def _device_warmup(fn, min_ms: float = DEVICE_WARMUP_MS):
+    """Runs `fn` back to back for about `min_ms` of GPU time (untimed, at most
+    DEVICE_WARMUP_MAX_STEPS steps); returns the number of steps run."""
+    import torch
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    fn()
+    b.record(st)
+    torch.cuda.synchronize()
+    n = min(DEVICE_WARMUP_MAX_STEPS, max(1, math.ceil(min_ms / max(a.elapsed_time(b), 1e-3)))) - 1
+    for _ in range(n):
+        fn()
+    torch.cuda.synchronize()
+    return n + 1
 
 
 def _time_steps(fn, steps: int, warmup: int):
@@ -292,7 +327,7 @@ def kernel_name(name: str, num_cus: int) -> str:
     return gemm_kernel_name(name, num_cus)
 
 
-def measure(dev, name, steps, warmup):
+def measure(dev, name, steps, warmup, cold: bool = False):
     from llmr_amd import workloads
     if name in ("flux_attention", "flux_attention_f32"):
         step, flops, nbytes, cfg, dtype = setup_attention(dev, f32=name.endswith("_f32"))
@@ -306,13 +341,17 @@ def measure(dev, name, steps, warmup):
         step, flops, nbytes, cfg, dtype = setup_gemm_lora(dev)
     else:
         step, flops, nbytes, cfg, dtype = setup_gemm(dev, name)
+    cold_ms = None
+    if cold:  # W warmup + K timed steps straight after set-up, before the device warm-up
+        cold_ms = _time_steps(step, steps, warmup)[0] / steps
+    _device_warmup(step)
     total_ms, per = _time_steps(step, steps, warmup)
     ms = total_ms / steps
     per.sort()
     med = per[len(per) // 2]
     tflops = flops / (ms * 1e-3) / 1e12
     return {"name": name, "ms": ms, "median_ms": med, "tflops": tflops, "flops": flops,
-            "bytes": nbytes, "cfg": cfg, "dtype": dtype}
+            "bytes": nbytes, "cfg": cfg, "dtype": dtype, "cold_ms": cold_ms}
 
 
 def cpu_baseline(name: str, budget_s: float = 10.0):
@@ -395,7 +434,7 @@ def main():
     from llmr_amd import capi
     capi.lib()  # fail loudly if the HIP library is missing
 
-    main_r = measure(dev, args.workload, args.steps, args.warmup)
+    main_r = measure(dev, args.workload, args.steps, args.warmup, cold=True)
     comps = {}
     for c in [c for c in args.components.split(",") if c and c != args.workload]:
         if c in MODEL_SETUPS:  # whole blocks / steps: fewer, longer steps
@@ -435,6 +474,10 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(main_r["ms"], 5),
+        # untimed GPU time of back-to-back steps before the W warmup steps,
+        # and the K steps timed straight after set-up without it
+        "device_warmup_ms": DEVICE_WARMUP_MS,
+        "cold_ms_per_step": round(main_r["cold_ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
