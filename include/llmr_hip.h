@@ -247,6 +247,56 @@ LLMR_API int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t weight_type, ui
                                      uint32_t out_dim, uint32_t in_dim, const llmr_matmul_job* jobs,
                                      uint32_t n_jobs, const llmr_matmul_epilogue* epilogue);
 
+/* Weight images built ahead of the GEMM. From a few thousand tokens a GEMM
+ * runs in two passes: its weight rows are first dequantized into a 16-bit
+ * image (laid out as the GEMM's LDS tiles), which the matrix-core pass then
+ * streams. A caller that knows its next GEMM group (a whole denoising step)
+ * can have each call build the next group's images: the current GEMM's
+ * workgroups that have no tile in its last round build part of them, the
+ * rest runs right after it. No reference counterpart (the reference
+ * dequantizes inside every matmul dispatch, llm.slang:1677-1705, 2321-2328);
+ * the results are bit-identical to llmr_batch_matmul_multi.
+ *
+ * llmr_weight_image_bytes: bytes of the image of out_dim rows of in_dim
+ * (0 when in_dim % 64 != 0).
+ * llmr_build_weight_image: rows [row_offset, row_offset + out_dim) of a
+ * Q8_0 / Q4_K weight into `image` (256-byte aligned, image_bytes >= the size
+ * above), as operands for input_type F16 or BF16, on the context's current
+ * stream. */
+LLMR_API size_t llmr_weight_image_bytes(uint32_t out_dim, uint32_t in_dim);
+LLMR_API int llmr_build_weight_image(llmr_context* ctx, const void* weight, uint32_t weight_type,
+                                     uint32_t input_type, uint32_t out_dim, uint32_t in_dim, uint32_t row_offset,
+                                     void* image, size_t image_bytes);
+
+/* The weight images of the GEMM group a caller issues next: `count` (1 or 2)
+ * weights of weight_type with out_dim rows from row_offset[i] and in_dim
+ * columns, for the same input_type as the call that builds them. */
+typedef struct llmr_next_weight_images {
+    uint32_t weight_type;
+    uint32_t out_dim;
+    uint32_t in_dim;  /* % 64 == 0 */
+    uint32_t count;
+    const void* weight[2];
+    uint32_t row_offset[2];
+    void* image[2];   /* 256-byte aligned, image_bytes each */
+    size_t image_bytes;
+} llmr_next_weight_images;
+
+/* llmr_batch_matmul_multi, plus:
+ *   images (NULL, or one per job): images[i] = the image of job i's weight,
+ *     built by llmr_build_weight_image or by the `next` of an earlier call
+ *     with the job's weight, weight_type, input_type, out_dim, in_dim and
+ *     row_offset (the weight unchanged since; the call cannot check the
+ *     contents). Job groups that run two-pass use them instead of building
+ *     their own; other groups ignore them.
+ *   next (NULL or the next group's images): built before the call returns
+ *     its work to the stream, partly by this call's idle workgroups.
+ * Either needs input_type F16 or BF16. */
+LLMR_API int llmr_batch_matmul_multi_images(llmr_context* ctx, uint32_t weight_type, uint32_t input_type,
+                                            uint32_t out_dim, uint32_t in_dim, const llmr_matmul_job* jobs,
+                                            uint32_t n_jobs, const llmr_matmul_epilogue* epilogue,
+                                            const void* const* images, const llmr_next_weight_images* next);
+
 /* SwiGLU feed-forward in-projection, both matmuls and the activation in one op:
  *   g = input · weight_gate^T,  u = input · weight_up^T,
  *   output[s, o] = silu(g[s, o]) * u[s, o],  silu(g) = g / (1 + e^-g)

@@ -418,15 +418,49 @@ int llmr_q8_lora_merge(llmr_context* ctx, void* weight, const float* a, const fl
     return ok();
 }
 
-int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
-                            const llmr_matmul_job* jobs, uint32_t n_jobs, const llmr_matmul_epilogue* epilogue) {
+static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t xtype, uint32_t out_dim,
+                                   uint32_t in_dim, const llmr_matmul_job* jobs, uint32_t n_jobs,
+                                   const llmr_matmul_epilogue* epilogue, const void* const* images,
+                                   const llmr_next_weight_images* next) {
     if (int r = check_ctx(ctx)) return r;
+    llmr::NextImageSet nx{};
+    if (next) {
+        if (xtype != LLMR_GGML_F16 && xtype != LLMR_GGML_BF16)
+            return fail(LLMR_ERR_INVALID_ARG, "next weight images need F16 or BF16 input");
+        if (next->count == 0 || next->count > 2) return fail(LLMR_ERR_INVALID_ARG, "next: count must be 1 or 2");
+        if (next->in_dim % 64 || next->out_dim == 0)
+            return fail(LLMR_ERR_INVALID_ARG, "next: in_dim %% 64 == 0 and out_dim > 0 needed");
+        const size_t need = llmr::w16_image_bytes(next->out_dim, next->in_dim, false);
+        if (next->image_bytes < need)
+            return fail(LLMR_ERR_INVALID_ARG, "next: images hold %zu bytes, need %zu", next->image_bytes, need);
+        for (uint32_t i = 0; i < next->count; i++) {
+            if (int r = check_weight(next->weight[i], next->weight_type, next->in_dim)) return r;
+            if ((uint64_t)next->row_offset[i] + next->out_dim > 0xffffffffull)
+                return fail(LLMR_ERR_INVALID_ARG, "next: row_offset + out_dim overflows");
+            if (!next->image[i] || !aligned(next->image[i], 256))
+                return fail(LLMR_ERR_INVALID_ARG, "next: image %u must be non-null and 256-byte aligned", i);
+            if (images)
+                for (uint32_t j = 0; j < n_jobs; j++)
+                    if (images[j] == next->image[i])
+                        return fail(LLMR_ERR_INVALID_ARG, "next: image %u is also an image of this call", i);
+            nx.w[i] = next->weight[i];
+            nx.img[i] = next->image[i];
+            nx.row_offset[i] = next->row_offset[i];
+        }
+        nx.count = next->count;
+        nx.wtype = next->weight_type;
+        nx.N = next->out_dim;
+        nx.K = next->in_dim;
+    }
     if (!is_act_type(xtype))
         return fail(LLMR_ERR_UNSUPPORTED, "input type %u not supported (F32=0, F16=1, BF16=30)", xtype);
-    if (n_jobs == 0) return ok();
+    if (n_jobs == 0 || out_dim == 0) {  // no GEMM: the next group's images alone
+        if (!next) return ok();
+        const hipError_t e = llmr::finish_next_images(nx, xtype, 0u, ctx->cur);
+        return e == hipSuccess ? ok() : fail(LLMR_ERR_HIP, "weight image launch: %s", hipGetErrorString(e));
+    }
     if (!jobs) return fail(LLMR_ERR_INVALID_ARG, "null jobs");
     if (n_jobs > 64) return fail(LLMR_ERR_INVALID_ARG, "at most 64 jobs per call (got %u)", n_jobs);
-    if (out_dim == 0) return ok();
     llmr_matmul_epilogue e = epilogue ? *epilogue : llmr_matmul_epilogue{LLMR_EPI_STORE, 0, 0, 0, 0};
     if (e.kind > LLMR_EPI_SPLIT_GELU) return fail(LLMR_ERR_INVALID_ARG, "unknown epilogue kind %u", e.kind);
     const bool split = e.kind == LLMR_EPI_SPLIT_GELU;
@@ -462,17 +496,57 @@ int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t wtype, uint32_t xtype, u
             return fail(LLMR_ERR_INVALID_ARG, "job %u: gate must be 16-byte aligned", i);
         if (has2 && j.seq_len && (!j.output2 || !aligned(j.output2, 16)))
             return fail(LLMR_ERR_INVALID_ARG, "job %u: output2 must be non-null and 16-byte aligned", i);
+        if (images && (!images[i] || !aligned(images[i], 256)))
+            return fail(LLMR_ERR_INVALID_ARG, "job %u: weight image must be non-null and 256-byte aligned", i);
         gj[i] = llmr::GemmJob{j.weight, j.input, j.output, e.kind == LLMR_EPI_GATED_RESIDUAL ? j.gate : nullptr,
                               has2 ? j.output2 : nullptr, j.seq_len, j.row_offset};
     }
+    if (images && (xtype == LLMR_GGML_F32 || in_dim % 64))
+        return fail(LLMR_ERR_INVALID_ARG, "weight images need F16/BF16 input and in_dim %% 64 == 0");
     const llmr::GemmEpilogue ge{e.kind, e.ldy, e.ldy2, e.split, has2 ? e.output2_type : (uint32_t)LLMR_GGML_BF16};
     const size_t need = llmr::batch_matmul_multi_workspace_bytes(wtype, xtype, out_dim, in_dim, gj, n_jobs, ge,
-                                                                 ctx->num_cus);
+                                                                 ctx->num_cus, images != nullptr);
     if (int r = acquire_workspace(ctx, need)) return r;
     hipError_t err = llmr::launch_batch_matmul_multi(wtype, xtype, out_dim, in_dim, gj, n_jobs, ge, ctx->num_cus,
-                                                     ctx->ws, ctx->cur);
+                                                     ctx->ws, ctx->cur, images, next ? &nx : nullptr);
     if (err != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul_multi launch: %s", hipGetErrorString(err));
     if (int r = release_workspace(ctx, need)) return r;
+    return ok();
+}
+
+int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t wtype, uint32_t xtype, uint32_t out_dim, uint32_t in_dim,
+                            const llmr_matmul_job* jobs, uint32_t n_jobs, const llmr_matmul_epilogue* epilogue) {
+    return batch_matmul_multi_impl(ctx, wtype, xtype, out_dim, in_dim, jobs, n_jobs, epilogue, nullptr, nullptr);
+}
+
+int llmr_batch_matmul_multi_images(llmr_context* ctx, uint32_t wtype, uint32_t xtype, uint32_t out_dim,
+                                   uint32_t in_dim, const llmr_matmul_job* jobs, uint32_t n_jobs,
+                                   const llmr_matmul_epilogue* epilogue, const void* const* images,
+                                   const llmr_next_weight_images* next) {
+    return batch_matmul_multi_impl(ctx, wtype, xtype, out_dim, in_dim, jobs, n_jobs, epilogue, images, next);
+}
+
+size_t llmr_weight_image_bytes(uint32_t out_dim, uint32_t in_dim) {
+    return in_dim % 64 ? 0u : llmr::w16_image_bytes(out_dim, in_dim, false);
+}
+
+int llmr_build_weight_image(llmr_context* ctx, const void* weight, uint32_t wtype, uint32_t xtype, uint32_t out_dim,
+                            uint32_t in_dim, uint32_t row_offset, void* image, size_t image_bytes) {
+    if (int r = check_ctx(ctx)) return r;
+    if (xtype != LLMR_GGML_F16 && xtype != LLMR_GGML_BF16)
+        return fail(LLMR_ERR_UNSUPPORTED, "weight images are built for F16 or BF16 input (got %u)", xtype);
+    if (in_dim % 64) return fail(LLMR_ERR_INVALID_ARG, "in_dim must be a multiple of 64 (got %u)", in_dim);
+    if (out_dim == 0) return ok();
+    if (int r = check_weight(weight, wtype, in_dim)) return r;
+    if ((uint64_t)row_offset + out_dim > 0xffffffffull)
+        return fail(LLMR_ERR_INVALID_ARG, "row_offset + out_dim overflows");
+    if (!image || !aligned(image, 256)) return fail(LLMR_ERR_INVALID_ARG, "image must be non-null, 256-byte aligned");
+    const size_t need = llmr::w16_image_bytes(out_dim, in_dim, false);
+    if (image_bytes < need)
+        return fail(LLMR_ERR_INVALID_ARG, "image holds %zu bytes, needs %zu", image_bytes, need);
+    const hipError_t err = llmr::launch_w16_image(weight, nullptr, wtype, xtype, image, out_dim, in_dim, row_offset,
+                                                  ctx->cur);
+    if (err != hipSuccess) return fail(LLMR_ERR_HIP, "weight image launch: %s", hipGetErrorString(err));
     return ok();
 }
 

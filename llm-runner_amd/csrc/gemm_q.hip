@@ -1649,13 +1649,13 @@ size_t fallback_t_bytes(uint32_t N, const GemmJob* jobs, uint32_t n_jobs, const 
 
 size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K,
                                           const GemmJob* jobs, uint32_t n_jobs, const GemmEpilogue& epi,
-                                          int num_cus) {
+                                          int num_cus, bool prebuilt_images) {
     const size_t t = fallback_t_bytes(N, jobs, n_jobs, epi, wtype, xtype, K, num_cus);
     size_t need = 0;
     for (uint32_t i = 0; i < n_jobs; i += 2) {
         const uint32_t n = min(2u, n_jobs - i);
         if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) {
-            if (multi_two_pass(jobs + i, n)) need = max(need, n * w16_image_bytes(N, K, false));
+            if (multi_two_pass(jobs + i, n) && !prebuilt_images) need = max(need, n * w16_image_bytes(N, K, false));
             continue;
         }
         for (uint32_t q = i; q < i + n; q++)
@@ -1664,14 +1664,38 @@ size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32
     return need;
 }
 
+// Next-group image items one idle workgroup of a two-pass GEMM takes on:
+// one per four of the GEMM's K stages (an item is 4 stages of a 256-row
+// panel, read as packed weights and written as 16-bit operands: ~6 us on a
+// CU beside the GEMM, a tile stage ~1.5 us), so the items end within the
+// idle workgroups' last-round time.
+uint32_t next_items_per_idle_wg(uint32_t K) { return max(1u, K / (uint32_t)kBK / 4u); }
+
+// The next group's images: the items [0, fused) came from the GEMM's idle
+// workgroups; the rest of each image here.
+hipError_t finish_next_images(const NextImageSet& nx, uint32_t otype, uint32_t fused, hipStream_t st) {
+    const uint32_t per = w16_image_items(nx.N, nx.K);
+    for (uint32_t i = 0; i < nx.count; i++) {
+        const uint32_t done = fused > i * per ? min(per, fused - i * per) : 0u;
+        if (done == per) continue;
+        const hipError_t e = launch_w16_image(nx.w[i], nullptr, nx.wtype, otype, nx.img[i], nx.N, nx.K,
+                                              nx.row_offset[i], st, done);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs,
                                      uint32_t n_jobs, const GemmEpilogue& epi, int num_cus, void* ws,
-                                     hipStream_t st) {
+                                     hipStream_t st, const void* const* images, const NextImageSet* next) {
+    if (next && (next->count == 0 || next->count > 2 || (xtype != kGgmlF16 && xtype != kGgmlBF16)))
+        return hipErrorInvalidValue;
+    uint32_t fused = 0;  // next-image items the last group's GEMM builds
     // a group of Q4_K projections of a few tokens (the per-block
     // modulation vectors) as one GEMV launch
     if (wtype == kGgmlQ4K && epi.kind == kEpiStore && n_jobs > 1) {
         const hipError_t e = launch_gemv_q4k_multi(xtype, jobs, n_jobs, N, K, epi.ldy, st);
-        if (e != hipErrorNotSupported) return e;
+        if (e != hipErrorNotSupported) return e != hipSuccess || !next ? e : finish_next_images(*next, xtype, 0, st);
     }
     const size_t t_bytes = fallback_t_bytes(N, jobs, n_jobs, epi, wtype, xtype, K, num_cus);
     for (uint32_t i = 0; i < n_jobs; i += 2) {
@@ -1682,10 +1706,30 @@ hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N,
             if (multi_two_pass(jobs + i, n)) {
                 const size_t img_bytes = w16_image_bytes(N, K, false);
                 for (uint32_t q = 0; q < n && e == hipSuccess; q++) {
+                    if (images) {  // built ahead by the caller (launch_w16_image, same arguments)
+                        a.p[q].W = (const uint8_t*)images[i + q];
+                        continue;
+                    }
                     void* img = (uint8_t*)ws + q * img_bytes;
                     e = launch_w16_image(jobs[i + q].w, nullptr, wtype, xtype, img, N, K, jobs[i + q].row_offset,
                                          st);
                     a.p[q].W = (const uint8_t*)img;
+                }
+                const uint64_t tiles = (uint64_t)a.tiles_m * a.tiles_n;
+                if (next && i + n == n_jobs && tiles % (uint64_t)num_cus != 0) {
+                    const uint32_t idle = num_cus - (uint32_t)(tiles % (uint64_t)num_cus);
+                    const uint32_t all = next->count * w16_image_items(next->N, next->K);
+                    fused = min(all, idle * next_items_per_idle_wg(K));
+                    NextImages& ni = a.next;
+                    for (uint32_t q = 0; q < next->count; q++) {
+                        ni.W[q] = (const uint8_t*)next->w[q];
+                        ni.img[q] = (uint8_t*)next->img[q];
+                        ni.row_offset[q] = next->row_offset[q];
+                    }
+                    ni.wtype = next->wtype;
+                    ni.N = next->N;
+                    ni.K = next->K;
+                    ni.items = fused;
                 }
                 if (e == hipSuccess) e = launch_w16_gemm(a, xtype, false, n == 2, num_cus, st);
             } else if (wtype == kGgmlQ8_0) {
@@ -1702,7 +1746,7 @@ hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N,
         }
         if (e != hipSuccess) return e;
     }
-    return hipSuccess;
+    return next ? finish_next_images(*next, xtype, fused, st) : hipSuccess;
 }
 
 }  // namespace llmr

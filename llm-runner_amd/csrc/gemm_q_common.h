@@ -22,11 +22,23 @@ struct PersistProblem {
     void* Y2;           // kEpiSplitGelu: 16-bit output
     uint32_t M, row_offset, tiles_m;
 };
+// Weight images of the next GEMM group, built by the two-pass GEMM's
+// workgroups that have no tile in its last round (items: (panel, group of 4
+// stages) of w16_image_kernel, image i's item u at i * per_image + u; the
+// first `items` of them here, the rest by w16_image_kernel after the GEMM).
+struct NextImages {
+    const uint8_t* W[2];  // raw weight blocks, row row_offset[i] is feature 0
+    uint8_t* img[2];
+    uint32_t row_offset[2];
+    uint32_t wtype, N, K;
+    uint32_t items;       // items built by the GEMM's idle workgroups (0: none)
+};
 struct PersistArgs {
     PersistProblem p[2];
     const uint8_t* W2;  // SwiGLU: the up weight (p[0].W is the gate)
     uint32_t N, K, tiles_m, tiles_n;  // tiles_m of both problems
     uint32_t epi, ldy, ldy2, split, y2_bf16;
+    NextImages next;
 };
 
 // The persistent all-DMA GEMM over weight images (gemm_w16.hip): p[i].W is
@@ -80,15 +92,54 @@ __device__ __forceinline__ u32x4 q8x8_f16(uint32_t q0, uint32_t q1, f16x2 d2) {
 // one XCD runs (dispatch is round-robin over the 8 XCDs) get 32 consecutive
 // indices, which the group-of-4-tile-rows order turns into a 4 x 8 block of
 // tiles (4 x 256 activation rows and 8 x 256 weight rows shared in the XCD's L2).
+__device__ __forceinline__ void tile_of_linear(uint32_t L, uint32_t tiles_m, uint32_t tiles_n, uint32_t& tm,
+                                               uint32_t& tn);
 __device__ __forceinline__ void map_tile_persist(uint32_t T, uint32_t G, uint32_t tiles_m, uint32_t tiles_n,
                                                  uint32_t& tm, uint32_t& tn) {
-    constexpr uint32_t kXcd = 8, kGroupM = 4;
+    constexpr uint32_t kXcd = 8;
     const uint32_t total = tiles_m * tiles_n;
     uint32_t L = T;
     if (G % kXcd == 0 && T / G < total / G) {
         const uint32_t b = T % G;
         L = (T - b) + (b % kXcd) * (G / kXcd) + b / kXcd;
     }
+    tile_of_linear(L, tiles_m, tiles_n, tm, tn);
+}
+
+// The two-pass kernel's order (grid G = the CUs, G % 8 == 0): full rounds as
+// map_tile_persist; the last, part-filled round of rem = total % G tiles is
+// split into 8 contiguous runs of rem / 8 (+1 for the first rem % 8 XCDs),
+// one per XCD, taken by that XCD's first workgroups (j = b / 8), so each
+// XCD's L2 serves neighbouring tiles and every XCD keeps the same number of
+// idle workgroups. Workgroup b's tile count, its k-th tile, and its rank
+// among the workgroups without a tile in the last round (rem > 0).
+__device__ __forceinline__ uint32_t w16_n_tiles(uint32_t b, uint32_t G, uint32_t total) {
+    const uint32_t R = total / G, rem = total % G;
+    if (G % 8u) return R + (b < rem ? 1u : 0u);
+    const uint32_t x = b % 8u, j = b / 8u;
+    return R + (j < rem / 8u + (x < rem % 8u ? 1u : 0u) ? 1u : 0u);
+}
+__device__ __forceinline__ void w16_tile(uint32_t b, uint32_t k, uint32_t G, uint32_t tiles_m, uint32_t tiles_n,
+                                         uint32_t& tm, uint32_t& tn) {
+    const uint32_t total = tiles_m * tiles_n, R = total / G, rem = total % G;
+    uint32_t L = k * G + b;
+    if (G % 8u == 0) {
+        const uint32_t x = b % 8u, j = b / 8u;
+        L = k < R ? k * G + x * (G / 8u) + j : R * G + x * (rem / 8u) + min(x, rem % 8u) + j;
+    }
+    tile_of_linear(L, tiles_m, tiles_n, tm, tn);
+}
+__device__ __forceinline__ uint32_t w16_idle_rank(uint32_t b, uint32_t G, uint32_t total) {
+    const uint32_t rem = total % G;
+    if (G % 8u) return b - rem;
+    const uint32_t x = b % 8u, j = b / 8u, q = rem / 8u, e = rem % 8u;
+    return x * (G / 8u) - x * q - min(x, e) + j - (q + (x < e ? 1u : 0u));
+}
+
+// Linear tile index -> (tile row, tile column) in groups of 4 tile rows.
+__device__ __forceinline__ void tile_of_linear(uint32_t L, uint32_t tiles_m, uint32_t tiles_n, uint32_t& tm,
+                                               uint32_t& tn) {
+    constexpr uint32_t kGroupM = 4;
     const uint32_t per_group = kGroupM * tiles_n;
     const uint32_t g = L / per_group;
     const uint32_t first_m = g * kGroupM;

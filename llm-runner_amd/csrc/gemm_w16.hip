@@ -78,10 +78,65 @@ __device__ __forceinline__ void split_bf16x8(const float (&v)[8], u32x4& hi, u32
         lo[e] = __builtin_bit_cast(uint32_t, l);
     }
 }
+// Items (panel p, group of kImgStages stages) of a weight's image:
+// panels * groups of them, item = p * groups + group.
+__host__ __device__ __forceinline__ uint32_t image_groups(uint32_t K) {
+    return (K / (uint32_t)kBK + kImgStages - 1) / kImgStages;
+}
+__host__ __device__ __forceinline__ uint32_t image_items(uint32_t N, uint32_t K) {
+    return (N + 255u) / 256u * image_groups(K);
+}
+// One item of a plain image (no SwiGLU arrangement, no LoRA) by the 256
+// threads of a workgroup (thread r: row r of the panel), through the two
+// 32 KiB LDS blocks lb0 and lb1 (one barrier per stage). Callers running
+// several items in a row put a barrier between them. NT: non-temporal
+// stores (items built beside a running GEMM: streamed, they evict less of
+// its operands from L2; Flux step 76.3 -> 75.8 ms).
+template <uint32_t WT, uint32_t OT, bool NT = false>
+__device__ __forceinline__ void image_item(const uint8_t* __restrict__ W, uint8_t* __restrict__ img, uint32_t N,
+                                           uint32_t K, uint32_t row_offset, uint32_t item, uint8_t* lb0,
+                                           uint8_t* lb1) {
+    const uint32_t S = K / kBK, groups = image_groups(K);
+    const uint32_t p = item / groups, s0 = (item % groups) * kImgStages, r = threadIdx.x;
+    const uint32_t rb = (WT == kGgmlQ8_0) ? (K / 32u) * 34u : (K / 256u) * 144u;
+    const uint32_t n0 = 256u * p;
+    const rsrc_t rs = make_rsrc(W + (uint64_t)row_offset * rb + (uint64_t)n0 * rb, (uint64_t)(N - n0) * rb);
+    WRow<WT, OT> u[kImgStages];
+#pragma unroll
+    for (uint32_t i = 0; i < kImgStages; i++)
+        if (s0 + i < S)
+            static_for<0, WRow<WT, OT>::kLoads>([&](auto L) { u[i].template load<decltype(L)::value>(rs, r * rb, s0 + i); });
+    const uint32_t base = r * 128u + (lds_swz(r) << 4);
+#pragma unroll
+    for (uint32_t i = 0; i < kImgStages; i++) {
+        if (s0 + i >= S) break;
+        uint8_t* const lb = (i & 1u) ? lb1 : lb0;
+        const auto sc = u[i].scale(s0 + i);
+        u[i].template store<0>(lb, sc, base);
+        u[i].template store<1>(lb, sc, base);
+        u[i].template store<2>(lb, sc, base);
+        u[i].template store<3>(lb, sc, base);
+        __syncthreads();
+        u32x4* const dst = (u32x4*)(img + ((uint64_t)p * S + s0 + i) * kBlk);
+#pragma unroll
+        for (uint32_t c = 0; c < kBlk / 16u / 256u; c++) {
+            if constexpr (NT)
+                __builtin_nontemporal_store(((const u32x4*)lb)[r + 256u * c], dst + r + 256u * c);
+            else
+                dst[r + 256u * c] = ((const u32x4*)lb)[r + 256u * c];
+        }
+    }
+}
+
 template <uint32_t WT, uint32_t OT, bool SW, uint32_t RS = 0>
 __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2,
                                                          uint8_t* __restrict__ img, uint32_t N, uint32_t K,
-                                                         uint32_t row_offset, const ImageLora lo) {
+                                                         uint32_t row_offset, const ImageLora lo, uint32_t item0) {
+    if constexpr (!SW && RS == 0) {  // a plain image: item item0 + blockIdx.x
+        __shared__ __attribute__((aligned(16))) uint8_t blk[2u * kBlk];
+        image_item<WT, OT>(W, img, N, K, row_offset, item0 + blockIdx.x, blk, blk + kBlk);
+        return;
+    }
     constexpr bool LORA = RS > 0;         // RS: rank steps of 16 the kernel holds (rank <= 16 RS)
     constexpr uint32_t RA = LORA ? RS : 1u;  // register array extent
     // one LDS object: two image blocks, then (LORA) the stage's a^T
@@ -359,7 +414,7 @@ __global__ void __launch_bounds__(256, 1) gemm_w16_persist(const PersistArgs arg
     const uint32_t wm = wave & 1u, wn = wave >> 1;
 
     const uint32_t G = gridDim.x, total = tiles_m * tiles_n;
-    const uint32_t n_tiles = (total - blockIdx.x + G - 1) / G;  // >= 1: grid <= total
+    const uint32_t n_tiles = w16_n_tiles(blockIdx.x, G, total);  // 0: no tile (grid = the CUs > total)
     const uint32_t S = K / kBK;
     const uint32_t SP = (S + 5u) / 6u * 6u;
     const uint32_t xrow = K * 2u;
@@ -391,7 +446,7 @@ __global__ void __launch_bounds__(256, 1) gemm_w16_persist(const PersistArgs arg
     };
     auto tile_origin = [&](uint32_t k, uint32_t& p, uint32_t& m0, uint32_t& n0) {
         uint32_t tm, tn;
-        map_tile_persist(blockIdx.x + k * G, G, tiles_m, tiles_n, tm, tn);
+        w16_tile(blockIdx.x, k, G, tiles_m, tiles_n, tm, tn);
         p = GROUPED && tm >= Tp0 ? 1u : 0u;
         m0 = (tm - (p ? Tp0 : 0u)) * 256u;
         n0 = tn * NT;
@@ -468,6 +523,7 @@ __global__ void __launch_bounds__(256, 1) gemm_w16_persist(const PersistArgs arg
                                     pick(p, Mp0, Mp1), N, m0, n0, wm, wn, l32, kh, ldy, ldy2, split, y2_bf16);
     };
 
+    if (n_tiles > 0) {
     // prologue: W(0) -> W0, X(0) -> X0, X(1) -> X1 (in the steady state's
     // order: a stage issues W(g+1), then X(g+2)); stage 0's operands have
     // landed once at most X(1)'s DMAs are in flight
@@ -548,22 +604,47 @@ __global__ void __launch_bounds__(256, 1) gemm_w16_persist(const PersistArgs arg
         store_tile(k);
     }
 #undef LLMR16_STAGE
+    }
+
+    // The next GEMM group's weight images: the workgroups without a tile in
+    // the last round build items [0, next.items) between them, through the
+    // first two ring slots (no DMA in flight into them after this wait).
+    const NextImages& ni = args.next;
+    if (ni.items > 0 && total % G != 0 && n_tiles == total / G) {
+        LLMR_WAIT_VMCNT(0);
+        __syncthreads();
+        const uint32_t idle = G - total % G, per = image_items(ni.N, ni.K);
+        for (uint32_t j = w16_idle_rank(blockIdx.x, G, total); j < ni.items; j += idle) {
+            const uint32_t i = j / per;
+            if (ni.wtype == kGgmlQ4K)
+                image_item<kGgmlQ4K, XT, true>(ni.W[i], ni.img[i], ni.N, ni.K, ni.row_offset[i], j - i * per, X0,
+                                               X1);
+            else
+                image_item<kGgmlQ8_0, XT, true>(ni.W[i], ni.img[i], ni.N, ni.K, ni.row_offset[i], j - i * per, X0,
+                                                X1);
+            __syncthreads();
+        }
+    }
     LLMR_WAIT_VMCNT(0);  // no DMA may still be writing this workgroup's LDS when it exits
 }
 
+// The image's items [item0, all) (item0 > 0 only for plain images).
 template <uint32_t WT, uint32_t OT, bool SW, uint32_t RS = 0>
 hipError_t build_image(const void* w, const void* w2, void* img, uint32_t N, uint32_t K, uint32_t row_offset,
-                       hipStream_t st, const ImageLora& lo = ImageLora{}) {
+                       hipStream_t st, const ImageLora& lo = ImageLora{}, uint32_t item0 = 0) {
     const uint32_t panels = SW ? (N + 127u) / 128u : (N + 255u) / 256u;
-    const uint32_t blocks = panels * ((K / (uint32_t)kBK + kImgStages - 1) / kImgStages);
-    hipLaunchKernelGGL((w16_image_kernel<WT, OT, SW, RS>), dim3(blocks), dim3(256), 0, st, (const uint8_t*)w,
-                       (const uint8_t*)w2, (uint8_t*)img, N, K, row_offset, lo);
+    const uint32_t blocks = panels * image_groups(K);
+    if (item0 >= blocks) return hipSuccess;
+    hipLaunchKernelGGL((w16_image_kernel<WT, OT, SW, RS>), dim3(blocks - item0), dim3(256), 0, st, (const uint8_t*)w,
+                       (const uint8_t*)w2, (uint8_t*)img, N, K, row_offset, lo, item0);
     return hipGetLastError();
 }
 
+// One workgroup per CU, also when there are fewer tiles (the workgroups
+// without one build the next group's images, or end at once).
 template <uint32_t XT, bool SW, uint32_t EPI, bool GROUPED>
 hipError_t launch_w16(const PersistArgs& a, int num_cus, hipStream_t st) {
-    const uint32_t grid = (uint32_t)min((uint64_t)a.tiles_m * a.tiles_n, (uint64_t)num_cus);
+    const uint32_t grid = (uint32_t)num_cus;
     hipLaunchKernelGGL((gemm_w16_persist<XT, SW, EPI, GROUPED>), dim3(grid), dim3(256), 0, st, a);
     return hipGetLastError();
 }
@@ -591,19 +672,24 @@ size_t w16_image_bytes(uint32_t N, uint32_t K, bool swiglu) {
 }
 
 hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
-                            uint32_t K, uint32_t row_offset, hipStream_t st) {
+                            uint32_t K, uint32_t row_offset, hipStream_t st, uint32_t item0) {
     const bool sw = w2 != nullptr;
+    if (sw && item0) return hipErrorInvalidValue;  // item offsets: plain images only
+    const ImageLora no{};
     if (wtype == kGgmlQ8_0) {
         if (otype == kGgmlBF16)
             return sw ? build_image<kGgmlQ8_0, kGgmlBF16, true>(w, w2, img, N, K, row_offset, st)
-                      : build_image<kGgmlQ8_0, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st);
+                      : build_image<kGgmlQ8_0, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
         return sw ? build_image<kGgmlQ8_0, kGgmlF16, true>(w, w2, img, N, K, row_offset, st)
-                  : build_image<kGgmlQ8_0, kGgmlF16, false>(w, w2, img, N, K, row_offset, st);
+                  : build_image<kGgmlQ8_0, kGgmlF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
     }
     if (sw) return hipErrorInvalidValue;  // the SwiGLU takes Q8_0 weights
-    if (otype == kGgmlBF16) return build_image<kGgmlQ4K, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st);
-    return build_image<kGgmlQ4K, kGgmlF16, false>(w, w2, img, N, K, row_offset, st);
+    if (otype == kGgmlBF16)
+        return build_image<kGgmlQ4K, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
+    return build_image<kGgmlQ4K, kGgmlF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
 }
+
+uint32_t w16_image_items(uint32_t N, uint32_t K) { return image_items(N, K); }
 
 hipError_t launch_w16_image_lora(const void* w, uint32_t wtype, uint32_t otype, void* img, uint32_t N, uint32_t K,
                                  uint32_t row_offset, const LoraGemm& l, hipStream_t st) {

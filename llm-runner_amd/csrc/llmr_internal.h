@@ -46,17 +46,24 @@ struct GemmJob {
 struct GemmEpilogue {
     uint32_t kind, ldy, ldy2, split, y2_type;
 };
+struct NextImageSet;  // the next GEMM group's weight images (below)
+// prebuilt_images: the caller passes the two-pass groups' weight images
+// (launch_batch_matmul_multi's `images`), so the workspace holds none.
 size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K,
                                           const GemmJob* jobs, uint32_t n_jobs, const GemmEpilogue& epi,
-                                          int num_cus);
+                                          int num_cus, bool prebuilt_images = false);
 // Q4_K projections of at most kGemvMaxTokens tokens, one launch for up to
 // 64 jobs of one shape [N, K] with plain stores (rows ldy apart);
 // hipErrorNotSupported when a job does not fit the LDS-staged kernel.
 hipError_t launch_gemv_q4k_multi(uint32_t xtype, const GemmJob* jobs, uint32_t n_jobs, uint32_t N, uint32_t K,
                                  uint32_t ldy, hipStream_t st);
+// images (null, or one per job): for jobs whose group runs two-pass, the
+// 16-bit weight image launch_w16_image built from the job's weight, wtype,
+// operand type xtype, N, K and row_offset; the group then builds none.
 hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs,
                                      uint32_t n_jobs, const GemmEpilogue& epi, int num_cus, void* ws,
-                                     hipStream_t st);
+                                     hipStream_t st, const void* const* images = nullptr,
+                                     const NextImageSet* next = nullptr);
 
 // LoRA (lora.hip): the two-hop correction appended to a base GEMM output and
 // the load-time Q8_0 merge. Ranks above kMaxLoraRank are not taken (the
@@ -99,8 +106,27 @@ size_t skinny_x_bytes(uint32_t xtype, uint32_t M, uint32_t K);
 hipError_t launch_gemm_skinny(const void* w, uint32_t wtype, const void* x, uint32_t xtype, float* y, uint32_t N,
                               uint32_t K, uint32_t M, uint32_t row_offset, uint32_t splits, void* ws,
                               hipStream_t st);
+// item0 > 0 (plain images only): items [item0, w16_image_items(N, K)) of
+// the image, the first item0 having been built elsewhere (by the GEMM before,
+// NextImageSet).
 hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
-                            uint32_t K, uint32_t row_offset, hipStream_t st);
+                            uint32_t K, uint32_t row_offset, hipStream_t st, uint32_t item0 = 0);
+// Work items (256-row panel x 4 stages) of a plain weight image.
+uint32_t w16_image_items(uint32_t N, uint32_t K);
+// Weight images of the GEMM group that follows a launch_batch_matmul_multi
+// call (plain images of `count` weights of one shape N x K for the call's
+// 16-bit input type): built in part by the two-pass GEMM's workgroups that
+// are idle in its last round, the rest right after it, so they are complete
+// when the next call on the stream starts.
+struct NextImageSet {
+    const void* w[2];
+    void* img[2];
+    uint32_t row_offset[2];
+    uint32_t count, wtype, N, K;
+};
+// The images' items from item `fused` on (items numbered across the images,
+// image i's item u = i * w16_image_items(N, K) + u), for operand type otype.
+hipError_t finish_next_images(const NextImageSet& nx, uint32_t otype, uint32_t fused, hipStream_t st);
 // A LoRA on a single GEMM (the reference's dispatch_batch_matmul with a
 // LoRA): output columns [row_offset, row_offset + b_rows) get scale *
 // b[weight_row_offset + o] . (a x).

@@ -54,6 +54,13 @@ class MatmulEpilogue(ctypes.Structure):
                 ("ldy2", ctypes.c_uint32), ("output2_type", ctypes.c_uint32)]
 
 
+class NextWeightImages(ctypes.Structure):
+    """llmr_next_weight_images: the next GEMM group's weight images."""
+    _fields_ = [("weight_type", ctypes.c_uint32), ("out_dim", ctypes.c_uint32), ("in_dim", ctypes.c_uint32),
+                ("count", ctypes.c_uint32), ("weight", ctypes.c_void_p * 2), ("row_offset", ctypes.c_uint32 * 2),
+                ("image", ctypes.c_void_p * 2), ("image_bytes", ctypes.c_size_t)]
+
+
 EPI_STORE, EPI_GATED_RESIDUAL, EPI_SPLIT_GELU = 0, 1, 2
 
 
@@ -97,6 +104,11 @@ _SIGS = {
     "llmr_batch_matmul_noalloc": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32, _u32]),
     "llmr_batch_matmul_multi": (ctypes.c_int, [_vp, _u32, _u32, _u32, _u32, ctypes.POINTER(MatmulJob), _u32,
                                                ctypes.POINTER(MatmulEpilogue)]),
+    "llmr_batch_matmul_multi_images": (ctypes.c_int, [_vp, _u32, _u32, _u32, _u32, ctypes.POINTER(MatmulJob), _u32,
+                                                      ctypes.POINTER(MatmulEpilogue), ctypes.POINTER(_vp),
+                                                      ctypes.POINTER(NextWeightImages)]),
+    "llmr_weight_image_bytes": (ctypes.c_size_t, [_u32, _u32]),
+    "llmr_build_weight_image": (ctypes.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, ctypes.c_size_t]),
     "llmr_batch_matmul_swiglu": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32]),
     "llmr_batch_matmul_swiglu_pc": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp,
                                                    ctypes.POINTER(BatchMatMulParams)]),
@@ -228,6 +240,21 @@ class Context:
         arr = (MatmulJob * len(jobs))(*jobs)
         check(lib().llmr_batch_matmul_multi(self._h, wtype, xtype, out_dim, in_dim, arr, len(jobs),
                                             ctypes.byref(epilogue) if epilogue is not None else None))
+
+    def batch_matmul_multi_images(self, wtype: int, xtype: int, out_dim: int, in_dim: int, jobs, epilogue,
+                                  images=None, next_images: NextWeightImages | None = None) -> None:
+        """As batch_matmul_multi with images[i] = device pointer of job i's weight
+        image (or None), and the next group's images built (or None)."""
+        arr = (MatmulJob * len(jobs))(*jobs)
+        imgs = (_vp * len(jobs))(*images) if images is not None else None
+        check(lib().llmr_batch_matmul_multi_images(self._h, wtype, xtype, out_dim, in_dim, arr, len(jobs),
+                                                   ctypes.byref(epilogue) if epilogue is not None else None, imgs,
+                                                   ctypes.byref(next_images) if next_images is not None else None))
+
+    def build_weight_image(self, w_ptr: int, wtype: int, xtype: int, out_dim: int, in_dim: int, row_offset: int,
+                           img_ptr: int, img_bytes: int) -> None:
+        check(lib().llmr_build_weight_image(self._h, w_ptr, wtype, xtype, out_dim, in_dim, row_offset, img_ptr,
+                                            img_bytes))
 
     def batch_matmul_swiglu(self, wg_ptr: int, wu_ptr: int, wtype: int, x_ptr: int, xtype: int,
                             y_ptr: int, out_dim: int, in_dim: int, seq_len: int) -> None:

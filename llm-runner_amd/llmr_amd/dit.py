@@ -35,8 +35,9 @@ import torch
 
 from . import capi, glue, workloads
 from .gguf import GGML_Q4_K, GGML_Q8_0
-from .ops import FlashAttentionPC, MatmulJob, RenderGraph, Tensor, default_graph, dispatch_batch_matmul, \
-    dispatch_batch_matmul_multi, dispatch_batch_matmul_swiglu, dispatch_flash_attention
+from .ops import _TORCH_GGML, FlashAttentionPC, MatmulJob, NextImages, RenderGraph, Tensor, build_weight_image, \
+    default_graph, dispatch_batch_matmul, dispatch_batch_matmul_multi, dispatch_batch_matmul_swiglu, \
+    dispatch_flash_attention, weight_image_bytes
 
 HEAD_DIM = 128
 
@@ -371,6 +372,53 @@ def flux_rope(cfg: FluxConfig, device="cuda"):
     return torch.from_numpy(cos_t).to(device), torch.from_numpy(sin_t).to(device)
 
 
+# Token count from which a GEMM runs two-pass (a 16-bit weight image, then
+# the matrix-core pass); the C-ABI makes the same choice.
+TWO_PASS_MIN_TOKENS = 2048
+
+
+class _ImageChain:
+    """Weight images of a fixed sequence of GEMM groups (one multi launch
+    each: a list of Q4_K/Q8_0 weights of one shape N x K, rows from 0), each
+    built by the call before it: that call's two-pass GEMM builds part of
+    them on its workgroups without a tile in the last round and the rest
+    right after it (NextImages); the first group's are built before it. Two
+    buffers alternate (group k reads buffer k % 2 while group k + 1's images
+    go into the other, last read by group k - 1). The results are those of
+    dispatch_batch_matmul_multi without images, bit for bit."""
+
+    def __init__(self, groups, input_dtype: int, device):
+        self.groups, self.xtype = groups, input_dtype
+        per = max(len(ws) * weight_image_bytes(N, K) for ws, N, K in groups)
+        self.bufs = [torch.empty(per, dtype=torch.uint8, device=device) for _ in range(2)]
+        self.k = 0
+        self.active = False  # between start() and the last group's take()
+
+    def _views(self, k: int):
+        ws, N, K = self.groups[k]
+        n = weight_image_bytes(N, K)
+        return [self.bufs[k % 2][i * n:(i + 1) * n] for i in range(len(ws))]
+
+    def start(self, g: RenderGraph) -> None:
+        """Before the first group: its images."""
+        self.k = 0
+        self.active = True
+        ws, N, K = self.groups[0]
+        for w, im in zip(ws, self._views(0)):
+            build_weight_image(g, w, N, K, 0, self.xtype, im)
+
+    def take(self):
+        """(images, next_images) for the next group's call."""
+        k = self.k
+        nxt = None
+        if k + 1 < len(self.groups):
+            ws, N, K = self.groups[k + 1]
+            nxt = NextImages(ws, N, K, self._views(k + 1))
+        self.k += 1
+        self.active = self.k < len(self.groups)
+        return self._views(k), nxt
+
+
 class FluxDiT:
     """One denoising forward of a Flux-shaped DiT on preallocated buffers."""
 
@@ -378,11 +426,28 @@ class FluxDiT:
     HN_EPS = 1e-6   # batch_head_norm eps (flux_dit.c3:813)
 
     def __init__(self, cfg: FluxConfig, glob: FluxGlobalWeights, doubles, singles, act_dtype=torch.bfloat16,
-                 device="cuda", g: RenderGraph | None = None):
+                 device="cuda", g: RenderGraph | None = None, images_ahead: bool = True):
         self.cfg, self.glob, self.doubles, self.singles = cfg, glob, doubles, singles
         self.g = g or default_graph()
         c, e = cfg, dict(device=device)
         S, d, m, nt = c.seq, c.dim, c.mlp, c.n_txt
+        # the blocks' GEMM groups in issue order, each group's weight images
+        # built by the call before it (when the GEMMs run two-pass)
+        self.ahead = None
+        if images_ahead and S >= TWO_PASS_MIN_TOKENS and d % 64 == 0 and m % 64 == 0 and \
+                act_dtype in (torch.float16, torch.bfloat16):
+            def q4(t, K):
+                return _qt(t, GGML_Q4_K, t.numel() // (K // 256 * 144), K)
+            groups = []
+            for w in doubles:
+                groups += [([q4(w.txt_qkv, d), q4(w.img_qkv, d)], 3 * d, d),
+                           ([q4(w.txt_proj, d), q4(w.img_proj, d)], d, d),
+                           ([q4(w.txt_mlp0, d), q4(w.img_mlp0, d)], m, d),
+                           ([q4(w.txt_mlp2, m), q4(w.img_mlp2, m)], d, m)]
+            for w in singles:
+                groups += [([q4(w.linear1, d)], 3 * d + m, d), ([q4(w.linear2, d + m)], d, d + m)]
+            if groups:
+                self.ahead = _ImageChain(groups, _TORCH_GGML[act_dtype], device)
         self.rope = flux_rope(cfg, device)
         self.hidden = torch.empty(S, d, dtype=torch.float32, **e)   # joint residual stream, text rows first
         self.xa = torch.empty(S, d, dtype=act_dtype, **e)             # GEMM inputs of width dim
@@ -447,6 +512,8 @@ class FluxDiT:
                 dispatch_batch_matmul_multi(g, jobs[k:k + 64], n, d)
         self._mm(self.glob.final_mod, GGML_Q4_K, 2 * d, d, self.vec, self.mods[:, mi * d:(mi + 2) * d])
         # 6-8: blocks (flux_dit.c3:1146-1162)
+        if self.ahead is not None:
+            self.ahead.start(g)
         mi = 0
         for w in self.doubles:
             self._double(w, self._mod(mi, 6), self._mod(mi + 6, 6))
@@ -460,6 +527,16 @@ class FluxDiT:
         self._mm(self.glob.final_linear, GGML_Q4_K, c.patch_dim, d, self.xa[nt:], self.velocity)
         glue.unpatchify(self.velocity, self.out, c.patch, g=g)
         return self.out
+
+    def _multi(self, jobs, N: int, K: int, epilogue: int = capi.EPI_STORE, split: int = 0) -> None:
+        """The blocks' next GEMM group (dispatch_batch_matmul_multi), taking its
+        weight images from the chain (and building the following group's)
+        when self.ahead is set."""
+        if self.ahead is None or not self.ahead.active:  # a block run outside forward(): no chain
+            dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split)
+            return
+        images, nxt = self.ahead.take()
+        dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split, images=images, next_images=nxt)
 
     def _attention(self, S: int) -> None:
         dispatch_flash_attention(self.g, _t(self.q), _t(self.k), _t(self.v), _t(self.o),
@@ -488,7 +565,7 @@ class FluxDiT:
             glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0],
                                  g=g)
         # Q | K | V of both streams; head norm + RoPE into the joint Q/K/V (flux_dit.c3:786-863)
-        dispatch_batch_matmul_multi(g, jobs(w.txt_qkv, w.img_qkv, d, self.xa, self.qkv), 3 * d, d)
+        self._multi(jobs(w.txt_qkv, w.img_qkv, d, self.xa, self.qkv), 3 * d, d)
         glue.qkv_heads(self.qkv[ts], H, self.q, self.k, self.v, 0, w.txt_q_norm, w.txt_k_norm, self.HN_EPS,
                        self.rope, g=g)
         glue.qkv_heads(self.qkv[im], H, self.q, self.k, self.v, nt, w.img_q_norm, w.img_k_norm, self.HN_EPS,
@@ -496,16 +573,16 @@ class FluxDiT:
         self._attention(S)
         # output projections, hidden += gate1 * proj                  (flux_dit.c3:875-898)
         glue.activation(self.o, self.xa, capi.ACT_COPY, g=g)
-        dispatch_batch_matmul_multi(g, jobs(w.txt_proj, w.img_proj, d, self.xa, self.hidden, (mt[2], mi[2])), d, d,
-                                    capi.EPI_GATED_RESIDUAL)
+        self._multi(jobs(w.txt_proj, w.img_proj, d, self.xa, self.hidden, (mt[2], mi[2])), d, d,
+                    capi.EPI_GATED_RESIDUAL)
         # MLP: LayerNorm + modulation, up + gelu, down, hidden += gate2 * down (flux_dit.c3:902-967)
         for sl, mod in ((ts, mt), (im, mi)):
             glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[4], mod_shift=mod[3],
                                  g=g)
-        dispatch_batch_matmul_multi(g, jobs(w.txt_mlp0, w.img_mlp0, d, self.xa, self.o, out2=self.fa), m, d,
-                                    capi.EPI_SPLIT_GELU, split=0)
-        dispatch_batch_matmul_multi(g, jobs(w.txt_mlp2, w.img_mlp2, m, self.fa, self.hidden, (mt[5], mi[5])), d, m,
-                                    capi.EPI_GATED_RESIDUAL)
+        self._multi(jobs(w.txt_mlp0, w.img_mlp0, d, self.xa, self.o, out2=self.fa), m, d,
+                    capi.EPI_SPLIT_GELU, split=0)
+        self._multi(jobs(w.txt_mlp2, w.img_mlp2, m, self.fa, self.hidden, (mt[5], mi[5])), d, m,
+                    capi.EPI_GATED_RESIDUAL)
 
     def _single(self, w: FluxSingleWeights, mod: torch.Tensor) -> None:
         """flux_single_stream_block (flux_dit.c3:975-1071). mod: [3, dim] (shift, scale, gate)."""
@@ -513,13 +590,12 @@ class FluxDiT:
         d, m, H, S = c.dim, c.mlp, c.n_heads, c.seq
         glue.batch_layernorm(self.hidden, self.xa, self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0], g=g)
         # linear1: Q | K | V (f32) and gelu(MLP half) straight into linear2's input (flux_dit.c3:1005-1058)
-        dispatch_batch_matmul_multi(g, [MatmulJob(_qt(w.linear1, GGML_Q4_K, 3 * d + m, d), _t(self.xa), self.qkv,
-                                                  S, 0, None, self.cat[:, d:])],
-                                    3 * d + m, d, capi.EPI_SPLIT_GELU, split=3 * d)
+        self._multi([MatmulJob(_qt(w.linear1, GGML_Q4_K, 3 * d + m, d), _t(self.xa), self.qkv,
+                               S, 0, None, self.cat[:, d:])],
+                    3 * d + m, d, capi.EPI_SPLIT_GELU, split=3 * d)
         glue.qkv_heads(self.qkv, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, self.HN_EPS, self.rope, g=g)
         self._attention(S)
         glue.activation(self.o, self.cat[:, :d], capi.ACT_COPY, g=g)
         # linear2, hidden += gate * linear2                           (flux_dit.c3:1060-1068)
-        dispatch_batch_matmul_multi(g, [MatmulJob(_qt(w.linear2, GGML_Q4_K, d, d + m), _t(self.cat), self.hidden,
-                                                  S, 0, mod[2])],
-                                    d, d + m, capi.EPI_GATED_RESIDUAL)
+        self._multi([MatmulJob(_qt(w.linear2, GGML_Q4_K, d, d + m), _t(self.cat), self.hidden, S, 0, mod[2])],
+                    d, d + m, capi.EPI_GATED_RESIDUAL)

@@ -15,6 +15,7 @@ graph's stream (the caller's current torch stream).
 """
 from __future__ import annotations
 
+import ctypes
 import dataclasses
 import math
 
@@ -218,14 +219,56 @@ class MatmulJob:
     output2: torch.Tensor | None = None
 
 
+def weight_image_bytes(out_dim: int, in_dim: int) -> int:
+    """Bytes of the 16-bit weight image of out_dim rows of in_dim (llmr_weight_image_bytes)."""
+    n = capi.lib().llmr_weight_image_bytes(out_dim, in_dim)
+    if n == 0:
+        raise ValueError("weight images need in_dim % 64 == 0")
+    return n
+
+
+def build_weight_image(g: RenderGraph, weight: Tensor, out_dim: int, in_dim: int, row_offset: int,
+                       input_dtype: int, image: torch.Tensor) -> None:
+    """Rows [row_offset, row_offset + out_dim) of `weight` dequantized into
+    `image` (a device tensor of at least weight_image_bytes bytes) as the
+    two-pass GEMM's operands for input_dtype (F16 or BF16), on the current
+    stream; pass it to dispatch_batch_matmul_multi(images=...)."""
+    _dev(weight, "weight")
+    if weight.shape[1] != in_dim or row_offset + out_dim > weight.shape[0]:
+        raise ValueError("weight shape does not cover [row_offset, row_offset+out_dim) x in_dim")
+    if not image.is_cuda or not image.is_contiguous():
+        raise ValueError("image must be a contiguous device tensor")
+    g.bind_stream()
+    g.ctx.build_weight_image(weight.ptr(), weight.dtype, input_dtype, out_dim, in_dim, row_offset,
+                             image.data_ptr(), image.numel() * image.element_size())
+
+
+@dataclasses.dataclass
+class NextImages:
+    """The weight images of the GEMM group issued next (llmr_next_weight_images):
+    its weights (one or two Tensors of one type, rows from row_offsets) and
+    out_dim x in_dim, into `images` (device tensors of weight_image_bytes)."""
+    weights: list
+    out_dim: int
+    in_dim: int
+    images: list
+    row_offsets: tuple = (0, 0)
+
+
 def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim: int,
-                                epilogue: int = capi.EPI_STORE, split: int = 0) -> None:
+                                epilogue: int = capi.EPI_STORE, split: int = 0, images=None,
+                                next_images: NextImages | None = None) -> None:
     """The jobs' GEMMs with a shared epilogue (llmr_batch_matmul_multi): a plain
     store, `output += gate * result` (gated_residual_linear), or a column split
     whose features >= split are GELU'd into output2 (linear1's MLP half feeding
     linear2, flux_dit.c3:1049-1058). Pairs of jobs run as one launch; a
     group of Q4_K jobs of at most 4 tokens with a plain store (the per-block
-    modulation projections) runs as one GEMV launch."""
+    modulation projections) runs as one GEMV launch. images: None, or one
+    device tensor per job holding the job's weight image (build_weight_image
+    or an earlier call's next_images, same weight, row_offset and input
+    type), used where a pair runs two-pass; next_images: the next group's
+    images, built partly by this call's idle workgroups and complete when
+    the stream's next call starts (llmr_batch_matmul_multi_images)."""
     if not jobs:
         return
     wtype, xtype = jobs[0].weight.dtype, jobs[0].input.dtype
@@ -279,7 +322,38 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
                                  j.seq_len, j.row_offset))
     epi = capi.MatmulEpilogue(epilogue, ldy, split, ldy2, o2type)
     g.bind_stream()
-    g.ctx.batch_matmul_multi(wtype, xtype, out_dim, in_dim, cj, epi)
+    if images is None and next_images is None:
+        g.ctx.batch_matmul_multi(wtype, xtype, out_dim, in_dim, cj, epi)
+        return
+    ptrs = None
+    if images is not None:
+        if len(images) != len(jobs):
+            raise ValueError("one weight image per job")
+        need = weight_image_bytes(out_dim, in_dim)
+        for im in images:
+            if not im.is_cuda or im.numel() * im.element_size() < need:
+                raise ValueError(f"weight images must be device tensors of at least {need} bytes")
+        ptrs = [im.data_ptr() for im in images]
+    nx = None
+    if next_images is not None:
+        n = next_images
+        if not 1 <= len(n.weights) <= 2 or len(n.images) != len(n.weights):
+            raise ValueError("next_images: one or two weights, one image each")
+        nbytes = weight_image_bytes(n.out_dim, n.in_dim)
+        nt = n.weights[0].dtype
+        for w, im, ro in zip(n.weights, n.images, n.row_offsets):
+            _dev(w, "next weight")
+            if w.dtype != nt or w.shape[1] != n.in_dim or ro + n.out_dim > w.shape[0]:
+                raise ValueError("next weights: one type, covering [row_offset, +out_dim) x in_dim")
+            if not im.is_cuda or im.numel() * im.element_size() < nbytes:
+                raise ValueError(f"next images must be device tensors of at least {nbytes} bytes")
+        k = len(n.weights)
+        nx = capi.NextWeightImages(nt, n.out_dim, n.in_dim, k,
+                                   (ctypes.c_void_p * 2)(*[w.ptr() for w in n.weights] + [None] * (2 - k)),
+                                   (ctypes.c_uint32 * 2)(*(list(n.row_offsets[:k]) + [0] * (2 - k))),
+                                   (ctypes.c_void_p * 2)(*[im.data_ptr() for im in n.images] + [None] * (2 - k)),
+                                   nbytes)
+    g.ctx.batch_matmul_multi_images(wtype, xtype, out_dim, in_dim, cj, epi, ptrs, nx)
 
 
 def dispatch_batch_matmul_swiglu(g: RenderGraph, weight_gate: Tensor, weight_up: Tensor,

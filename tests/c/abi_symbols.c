@@ -32,6 +32,9 @@ static const struct {
     {"llmr_batch_matmul_pc", (void (*)(void))(uintptr_t)llmr_batch_matmul_pc},
     {"llmr_batch_matmul_noalloc", (void (*)(void))(uintptr_t)llmr_batch_matmul_noalloc},
     {"llmr_batch_matmul_multi", (void (*)(void))(uintptr_t)llmr_batch_matmul_multi},
+    {"llmr_batch_matmul_multi_images", (void (*)(void))(uintptr_t)llmr_batch_matmul_multi_images},
+    {"llmr_weight_image_bytes", (void (*)(void))(uintptr_t)llmr_weight_image_bytes},
+    {"llmr_build_weight_image", (void (*)(void))(uintptr_t)llmr_build_weight_image},
     {"llmr_batch_matmul_swiglu", (void (*)(void))(uintptr_t)llmr_batch_matmul_swiglu},
     {"llmr_batch_matmul_swiglu_pc", (void (*)(void))(uintptr_t)llmr_batch_matmul_swiglu_pc},
     {"llmr_gguf_open", (void (*)(void))(uintptr_t)llmr_gguf_open},

@@ -53,13 +53,13 @@ def test_create_context_without_device_fails_cleanly():
 
 
 def _c_harness(name: str) -> str:
-    """tests/c/_build/<name>, built with gcc from tests/c when it is missing."""
+    """tests/c/_build/<name>, (re)built with gcc from tests/c when it is
+    missing or older than its source, the header or the library."""
     import os
     import subprocess
     cdir = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c")
     exe = os.path.join(cdir, "_build", name)
-    if not os.path.exists(exe):
-        subprocess.run(["make", "-C", cdir, f"_build/{name}"], check=True, capture_output=True)
+    subprocess.run(["make", "-C", cdir, f"_build/{name}"], check=True, capture_output=True)
     return exe
 
 

@@ -81,3 +81,31 @@ def test_flux_forward_is_deterministic(dev):
     b = model.forward(lat, txt.to(torch.bfloat16), 0.5)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_flux_images_ahead_bit_identical(dev):
+    """Each GEMM group's weight images built by the call before it (FluxDiT's
+    default from 2048 tokens: the previous two-pass GEMM's idle workgroups
+    build part of them) give the velocity of the same forward without them,
+    bit for bit, on two forwards in a row (the buffers are reused across
+    forwards). dim 1024 / mlp 4096 over 2368 tokens: the MLP-in and linear1
+    groups run two-pass on the prebuilt images, the narrower groups ignore
+    theirs but still build the next ones."""
+    from llmr_amd import dit, synth
+    cfg = dit.FluxConfig(dim=1024, n_heads=8, mlp=4096, n_double=2, n_single=2, text_dim=256, n_txt=64,
+                         latent_ch=16, latent_h=96, latent_w=96, patch=2)
+    assert cfg.seq >= dit.TWO_PASS_MIN_TOKENS
+    weights = dit.flux_weights(cfg, device=dev)
+    ahead = dit.FluxDiT(cfg, *weights, device=dev)
+    plain = dit.FluxDiT(cfg, *weights, device=dev, images_ahead=False)
+    assert ahead.ahead is not None and plain.ahead is None
+    n_lat = cfg.latent_ch * cfg.latent_h * cfg.latent_w
+    txt = torch.from_numpy(synth.normal(42, 506, cfg.n_txt * cfg.text_dim).reshape(cfg.n_txt, -1)).to(dev)
+    for rep in range(2):
+        lat = torch.from_numpy(synth.normal(42, 507 + rep, n_lat).reshape(cfg.latent_ch, cfg.latent_h,
+                                                                          cfg.latent_w)).to(dev)
+        a = ahead.forward(lat, txt.to(torch.bfloat16), 0.5).clone()
+        b = plain.forward(lat, txt.to(torch.bfloat16), 0.5).clone()
+        torch.cuda.synchronize()
+        assert torch.isfinite(a).all()
+        assert torch.equal(a, b), rep

@@ -609,6 +609,109 @@ def test_multi_two_pass_jobs_equal_single_launches(dev):
     assert (out[:, N:] == 0).all()
 
 
+@pytest.mark.parametrize("wtype,xtype", [(12, 30), (8, 1)])
+def test_multi_prebuilt_images_bit_identical(dev, wtype, xtype):
+    """llmr_batch_matmul_multi_images with weight images built ahead by
+    llmr_build_weight_image (on a second stream, ordered by an event) gives
+    the bits of llmr_batch_matmul_multi for a grouped two-pass pair (300 +
+    2000 tokens, row offsets 0 and 8) with each epilogue (strided store, gated
+    residual, split gelu); a pair too small for the persistent kernels
+    ignores its images."""
+    import torch
+    from llmr_amd import capi, ops
+    g = ops.default_graph()
+    Ms, N, K = (300, 2000), 4096, 512
+    blks, xs, wts = _multi_setup(dev, wtype, Ms, N, K, xtype, 43)
+    n = ops.weight_image_bytes(N, K)
+    imgs = [torch.full((n,), 0xAB, dtype=torch.uint8, device=dev) for _ in range(2)]
+    side = torch.cuda.Stream()
+    built = torch.cuda.Event()
+    with torch.cuda.stream(side):
+        for i in range(2):
+            ops.build_weight_image(g, wts[i], N, K, 8 * i, xtype, imgs[i])
+        built.record(side)
+    torch.cuda.current_stream().wait_event(built)
+    g.bind_stream()
+    gate = torch.randn(N, device=dev)
+    h0 = torch.randn(sum(Ms), N + 32, device=dev)
+    for epi, split in ((capi.EPI_STORE, 0), (capi.EPI_GATED_RESIDUAL, 0), (capi.EPI_SPLIT_GELU, 1536)):
+        outs = []
+        for use in (False, True):
+            out = h0.clone()
+            o2 = torch.full((sum(Ms), N - split + 16), 3.0, dtype=torch.bfloat16, device=dev)
+            jobs = [ops.MatmulJob(wts[i], ops.Tensor.from_torch(xs[i]),
+                                  (out[:Ms[0], :N], out[Ms[0]:, :N])[i], Ms[i], 8 * i,
+                                  gate if epi == capi.EPI_GATED_RESIDUAL else None,
+                                  (o2[:Ms[0], :N - split], o2[Ms[0]:, :N - split])[i]
+                                  if epi == capi.EPI_SPLIT_GELU else None) for i in range(2)]
+            ops.dispatch_batch_matmul_multi(g, jobs, N, K, epi, split, images=imgs if use else None)
+            torch.cuda.synchronize()
+            outs.append((out, o2))
+        assert torch.equal(outs[0][0], outs[1][0]), epi
+        assert torch.equal(outs[0][1], outs[1][1]), epi
+        assert not torch.equal(outs[1][0], h0), epi
+    # a pair with too few tiles for the persistent kernels runs its own path
+    small = [ops.MatmulJob(wts[i], ops.Tensor.from_torch(xs[i][:40]), torch.empty(40, 256, device=dev), 40, 8 * i)
+             for i in range(2)]
+    ref = [torch.empty(40, 256, device=dev) for _ in range(2)]
+    ops.dispatch_batch_matmul_multi(g, small, 256, K, images=imgs)
+    ops.dispatch_batch_matmul_multi(g, [ops.MatmulJob(j.weight, j.input, r, 40, j.row_offset)
+                                        for j, r in zip(small, ref)], 256, K)
+    torch.cuda.synchronize()
+    for j, r in zip(small, ref):
+        assert torch.equal(j.output, r)
+
+
+@pytest.mark.parametrize("wtype,xtype,Ms,N,K,N2,K2", [
+    (12, 30, (512, 3584), 3072, 512, 2304, 3072),   # 192 tiles: 64 tile-less workgroups
+    (12, 30, (300, 2000), 4096, 512, 1024, 4096),   # 160 tiles, next K = 4096
+    (8, 1, (4608,), 3328, 512, 640, 1536),          # 234 tiles, ragged next N (640), Q8_0
+    (12, 30, (4608,), 4096, 256, 256, 256),          # 288 tiles: a second round of 32
+    (12, 30, (2048,), 7936, 256, 1024, 3072),       # 248 tiles: 16 of 48 items fused, 32 after
+])
+def test_multi_next_images_built_by_idle_workgroups(dev, wtype, xtype, Ms, N, K, N2, K2):
+    """A call's next_images (part built by its two-pass GEMM's workgroups
+    without a tile in the last round, the rest right after) equal the images
+    llmr_build_weight_image builds, byte for byte, and the call's own output
+    is the plain call's; the next group's call on them gives the plain bits."""
+    import torch
+    from llmr_amd import capi, gguf, ops, synth
+    g = ops.default_graph()
+    blks, xs, wts = _multi_setup(dev, wtype, Ms, N, K, xtype, 47)
+    nw = [ops.Tensor.quantized(torch.from_numpy(gguf.quantize(synth.normal(47, 60 + i, (N2 + 16) * K2, 0.02),
+                                                              wtype)).to(dev), wtype, N2 + 16, K2)
+          for i in range(len(Ms))]
+    nb = ops.weight_image_bytes(N2, K2)
+    chained = [torch.zeros(nb, dtype=torch.uint8, device=dev) for _ in Ms]
+    direct = [torch.zeros(nb, dtype=torch.uint8, device=dev) for _ in Ms]
+    out_a = torch.zeros(sum(Ms), N, device=dev)
+    out_b = torch.zeros(sum(Ms), N, device=dev)
+    rows = [sum(Ms[:i]) for i in range(len(Ms) + 1)]
+
+    def jobs(out):
+        return [ops.MatmulJob(wts[i], ops.Tensor.from_torch(xs[i]), out[rows[i]:rows[i + 1]], Ms[i], 8 * i)
+                for i in range(len(Ms))]
+    nxt = ops.NextImages(nw, N2, K2, chained, row_offsets=tuple(16 * i for i in range(len(Ms))))
+    ops.dispatch_batch_matmul_multi(g, jobs(out_a), N, K, next_images=nxt)
+    ops.dispatch_batch_matmul_multi(g, jobs(out_b), N, K)
+    for i in range(len(Ms)):
+        ops.build_weight_image(g, nw[i], N2, K2, 16 * i, xtype, direct[i])
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    for i in range(len(Ms)):
+        assert torch.equal(chained[i], direct[i]), i
+    # the next group on the chained images
+    x2 = [_torch_x(synth.normal(47, 70 + i, Ms[i] * K2).reshape(Ms[i], K2), xtype, dev) for i in range(len(Ms))]
+    y_a = torch.zeros(sum(Ms), N2, device=dev)
+    y_b = torch.zeros(sum(Ms), N2, device=dev)
+    j2 = lambda y: [ops.MatmulJob(nw[i], ops.Tensor.from_torch(x2[i]), y[rows[i]:rows[i + 1]], Ms[i], 16 * i)  # noqa: E731
+                    for i in range(len(Ms))]
+    ops.dispatch_batch_matmul_multi(g, j2(y_a), N2, K2, images=chained)
+    ops.dispatch_batch_matmul_multi(g, j2(y_b), N2, K2)
+    torch.cuda.synchronize()
+    assert torch.equal(y_a, y_b)
+
+
 @pytest.mark.parametrize("wtype,M,N,K,xtype", [(8, 256, 3072, 3072, 0), (12, 300, 520, 1024, 30), (8, 96, 4096, 4096, 1)])
 def test_split_k_matches_oracle_and_repeats(orc, dev, wtype, M, N, K, xtype):
     """Launches with few tiles split K over several workgroup rows and sum the
