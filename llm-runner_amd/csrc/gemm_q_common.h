@@ -396,22 +396,68 @@ __device__ __forceinline__ void store_tile_256(f32x16 (&acc)[4][4], float* Y, co
         });
     } else if constexpr (EPI == kEpiSplitGelu) {
         uint16_t* const Y2 = (uint16_t*)Y2v;
-        each([&](uint32_t m, uint32_t n, uint32_t nw, f32x4 v) __attribute__((always_inline)) {
-            if (nw < split) {
-                *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
-            } else {
-                const f32x4 gl{gelu_tanh(v.x), gelu_tanh(v.y), gelu_tanh(v.z), gelu_tanh(v.w)};
-                u32x2 o;
-                if (y2_bf16) {
-                    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-                    o.x = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.x, (__bf16)gl.y});
-                    o.y = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.z, (__bf16)gl.w});
-                } else {
-                    o = u32x2{pack_f16x2(gl.x, gl.y), pack_f16x2(gl.z, gl.w)};
-                }
-                *(u32x2*)(Y2 + (uint64_t)m * ldy2 + (n - split)) = o;
+        // A 32-feature block wholly past the split (a uniform test: split %
+        // 8 == 0, nb uniform) with 16-byte aligned 16-bit rows: the two lanes
+        // of a token (kh = 0, 1) trade 8-byte pieces so that each holds 8
+        // consecutive features (16 bytes) twice, and a store instruction
+        // writes 32-byte pieces of 32 rows instead of 16-byte ones (Flux
+        // step 75.34 -> 75.13 ms, two runs each).
+        const bool pair_ok = (ldy2 & 7u) == 0 && ((uintptr_t)Y2 & 15u) == 0;
+        auto pack16 = [&](f32x4 v) __attribute__((always_inline)) {
+            const f32x4 gl{gelu_tanh(v.x), gelu_tanh(v.y), gelu_tanh(v.z), gelu_tanh(v.w)};
+            if (y2_bf16) {
+                typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+                return u32x2{__builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.x, (__bf16)gl.y}),
+                             __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)gl.z, (__bf16)gl.w})};
             }
-        });
+            return u32x2{pack_f16x2(gl.x, gl.y), pack_f16x2(gl.z, gl.w)};
+        };
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const uint32_t nb = n0 + wn * 128u + a * 32u;  // the block's first feature (uniform)
+            const bool paired = pair_ok && nb >= split && nb + 32u <= N;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint32_t m = m0 + wm * 128u + b * 32u + l32;
+                if (paired) {
+                    u32x2 pc[4];
+#pragma unroll
+                    for (int g = 0; g < 4; g++)
+                        pc[g] = pack16(f32x4{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2],
+                                             acc[a][b][4 * g + 3]});
+                    // lane kh holds features 8 g + 4 kh .. +3; kh = 0 gives its
+                    // g = 1, 3 pieces for the partner's g = 0, 2 pieces
+#pragma unroll
+                    for (int t = 0; t < 2; t++) {
+                        const u32x2 give = kh ? pc[2 * t] : pc[2 * t + 1];
+                        u32x2 recv;
+#pragma unroll
+                        for (int e = 0; e < 2; e++) {
+                            const auto r = __builtin_amdgcn_permlane32_swap(give[e], give[e], false, false);
+                            recv[e] = kh ? r[0] : r[1];  // the partner lane's value
+                        }
+                        // kh = 0: features 16 t + 0..7; kh = 1: 16 t + 8..15
+                        const u32x4 o = kh ? u32x4{recv.x, recv.y, pc[2 * t + 1].x, pc[2 * t + 1].y}
+                                           : u32x4{pc[2 * t].x, pc[2 * t].y, recv.x, recv.y};
+                        if (m < M) *(u32x4*)(Y2 + (uint64_t)m * ldy2 + (nb + 16u * t + 8u * kh - split)) = o;
+                    }
+                } else {
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const uint32_t nw = nb + 8u * g;
+                        const uint32_t n = nw + 4u * kh;
+                        if (m >= M || n >= N) continue;
+                        const f32x4 v{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2],
+                                      acc[a][b][4 * g + 3]};
+                        if (nw < split)
+                            *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
+                        else
+                            *(u32x2*)(Y2 + (uint64_t)m * ldy2 + (n - split)) = pack16(v);
+                    }
+                }
+                acc[a][b] = f32x16{};
+            }
+        }
     } else {
         each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
             *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
