@@ -27,6 +27,8 @@
 #include "llmr_device.h"
 #include "llmr_internal.h"
 
+#include <type_traits>
+
 #pragma clang fp contract(off)
 
 namespace llmr {
@@ -199,6 +201,62 @@ __global__ void __launch_bounds__(256) lora_up_kernel(const float* __restrict__ 
             if (h * 256u + gi < no && t < nt) ybase[(uint64_t)t * out_dim + h * 256u] = yv[h][t] + scale * acc[h][t];
 }
 
+// Hop 2 for ranks up to RK (8, 16 or 32; rank % 4 == 0): thread gi owns
+// output column o0 + gi, whose B row (rank floats) stays in registers for
+// the workgroup's kUpRegSpan tokens; the tokens' scratch rows go through LDS
+// in blocks of kUpRegTokens (broadcast reads), the block's output values are
+// read before its sums. Same arithmetic as lora_up_kernel: the sum over
+// ranks in rank order from 0, then y + scale * sum. Its LDS footprint is
+// 2 KiB (lora_up_kernel's 70 KiB held two workgroups per CU), so enough
+// workgroups share a CU to overlap their output reads and writes with the
+// FMAs of others.
+constexpr uint32_t kUpRegTokens = 16;
+constexpr uint32_t kUpRegSpan = 128;
+template <uint32_t RK>
+__global__ void __launch_bounds__(256) lora_up_reg_kernel(const float* __restrict__ B,
+                                                           const float* __restrict__ scratch, float* __restrict__ out,
+                                                           uint32_t rank, uint32_t out_dim, uint32_t seq_len,
+                                                           float scale, uint32_t row_offset, uint32_t weight_row_offset,
+                                                           uint32_t b_rows) {
+    __shared__ __attribute__((aligned(16))) float sc[kUpRegTokens][RK];
+    const uint32_t gi = threadIdx.x, o = blockIdx.x * 256u + gi;
+    const uint32_t s_begin = blockIdx.y * kUpRegSpan, s_end = min(seq_len, s_begin + kUpRegSpan);
+    const bool live = o < b_rows;
+    const uint32_t q = rank / 4u;  // 16-byte pieces of a rank row
+    float bv[RK];
+#pragma unroll
+    for (uint32_t r = 0; r < RK; r += 4) {
+        const f32x4 v = live && r < rank ? *(const f32x4*)(B + (uint64_t)(weight_row_offset + o) * rank + r)
+                                         : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        bv[r] = v.x;
+        bv[r + 1] = v.y;
+        bv[r + 2] = v.z;
+        bv[r + 3] = v.w;
+    }
+    float* const ycol = out + row_offset + o;
+    for (uint32_t s0 = s_begin; s0 < s_end; s0 += kUpRegTokens) {
+        const uint32_t nt = min(kUpRegTokens, s_end - s0);
+        for (uint32_t i = gi; i < nt * q; i += 256u) {
+            const uint32_t t = i / q, r = 4u * (i % q);
+            *(f32x4*)&sc[t][r] = *(const f32x4*)(scratch + (uint64_t)(s0 + t) * rank + r);
+        }
+        __syncthreads();
+        float yv[kUpRegTokens];
+#pragma unroll
+        for (uint32_t t = 0; t < kUpRegTokens; t++)
+            yv[t] = live && t < nt ? ycol[(uint64_t)(s0 + t) * out_dim] : 0.0f;
+#pragma unroll
+        for (uint32_t t = 0; t < kUpRegTokens; t++) {
+            float a = 0.0f;
+#pragma unroll
+            for (uint32_t r = 0; r < RK; r++)
+                if (r < rank) a = __builtin_fmaf(bv[r], sc[t][r], a);
+            if (live && t < nt) ycol[(uint64_t)(s0 + t) * out_dim] = yv[t] + scale * a;
+        }
+        __syncthreads();  // sc is refilled by the next block
+    }
+}
+
 // One 256-element chunk (8 Q8_0 blocks = 272 bytes) of LoRA row blockIdx.y:
 // thread gi owns element k = 256 blockIdx.x + gi.
 __global__ void __launch_bounds__(256) q8_lora_merge_kernel(uint8_t* __restrict__ base, const float* __restrict__ A,
@@ -260,6 +318,18 @@ hipError_t launch_lora_correction(const float* A, const float* B, uint32_t rank,
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || b_rows == 0) return e;
+    if (rank <= 32u && rank % 4u == 0u) {
+        const dim3 gr((b_rows + 255u) / 256u, (seq_len + kUpRegSpan - 1) / kUpRegSpan);
+        auto go = [&](auto rk) {
+            hipLaunchKernelGGL(lora_up_reg_kernel<decltype(rk)::value>, gr, dim3(256), 0, st, B,
+                               (const float*)scratch, out, rank, out_dim, seq_len, scale, row_offset,
+                               weight_row_offset, b_rows);
+        };
+        if (rank <= 8u) go(std::integral_constant<uint32_t, 8>{});
+        else if (rank <= 16u) go(std::integral_constant<uint32_t, 16>{});
+        else go(std::integral_constant<uint32_t, 32>{});
+        return hipGetLastError();
+    }
     const dim3 gu((b_rows + 511u) / 512u, (seq_len + kUpTokens - 1) / kUpTokens);
     hipLaunchKernelGGL(lora_up_kernel, gu, dim3(256), 0, st, B, (const float*)scratch, out, rank, out_dim, seq_len,
                        scale, row_offset, weight_row_offset, b_rows);

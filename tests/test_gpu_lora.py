@@ -30,6 +30,8 @@ def _act(x_f32, xtype, dev):
     (5, 768, 48, 1024, 256, 768, 512, 1),   # f16 input, one slot of a fused Q|K|V adapter
     (3, 256, 256, 260, 0, 0, 0, 0),         # the largest rank
     (17, 700, 1, 129, 0, 0, 0, 30),         # rank 1, ragged sizes
+    (300, 512, 16, 3072, 2000, 512, 100, 30),  # rank 16: the register-resident hop 2 over 3 token spans
+    (129, 256, 4, 520, 0, 0, 0, 1),         # rank 4, ragged columns and tokens
 ])
 def test_lora_correction_bit_exact(orc, dev, seq, in_dim, rank, out_dim, b_rows, row_off, w_off, xtype):
     import torch
