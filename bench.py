@@ -455,7 +455,7 @@ def main():
         gbs = main_r["bytes"] / (main_r["ms"] * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": _traffic(args.workload),
-                "kernel": "lora_down_kernel + lora_up_kernel", "algorithmic_bytes": main_r["bytes"]}
+                "kernel": "lora_down_kernel + lora_up_reg_kernel", "algorithmic_bytes": main_r["bytes"]}
     elif args.workload in MODEL_SETUPS:  # a composed block / step: many kernels, no single roofline
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(ach / PEAK_TFLOPS, 4), "traffic": None,
