@@ -451,6 +451,17 @@ LLMR_API int llmr_flash_attention(llmr_context* ctx, const void* q, const void* 
                                   uint32_t qkv_type, float* out, uint32_t head_dim,
                                   uint32_t n_heads, uint32_t seq_len, float scale);
 
+/* llmr_flash_attention with the output rows written straight into the next
+ * projection's input: out[s * out_stride + h * head_dim + d] of out_type
+ * (F32, or F16 / BF16 rounded to nearest even from the f32 result, the
+ * values llmr_activation's ACT_COPY gives), out_stride % 8 == 0 and >=
+ * n_heads * head_dim, out 16-byte aligned. Replaces the attention dispatch
+ * plus the copy that follows it in a block (dit.c3:1476-1487,
+ * flux_dit.c3:865-872, 1042-1047). No reference counterpart as one call. */
+LLMR_API int llmr_flash_attention_rows(llmr_context* ctx, const void* q, const void* k, const void* v,
+                                       uint32_t qkv_type, void* out, uint32_t out_type, uint32_t out_stride,
+                                       uint32_t head_dim, uint32_t n_heads, uint32_t seq_len, float scale);
+
 /* Same op with FlashAttentionPC packing (g.dispatch(&dk.flash_attention,
  * {Q, K, V, O}, &FlashAttentionPC, ceil(S/16), H)). */
 LLMR_API int llmr_flash_attention_pc(llmr_context* ctx, const void* q, const void* k,

@@ -585,9 +585,9 @@ int llmr_batch_matmul_swiglu_pc(llmr_context* ctx, const void* weight_gate, cons
                                     pc->in_dim, pc->seq_len);
 }
 
-int llmr_flash_attention(llmr_context* ctx, const void* q, const void* k, const void* v,
-                         uint32_t xtype, float* out, uint32_t head_dim, uint32_t n_heads,
-                         uint32_t seq_len, float scale) {
+static int flash_attention_impl(llmr_context* ctx, const void* q, const void* k, const void* v, uint32_t xtype,
+                                void* out, uint32_t out_type, uint32_t out_stride, uint32_t head_dim,
+                                uint32_t n_heads, uint32_t seq_len, float scale) {
     if (int r = check_ctx(ctx)) return r;
     if (head_dim != 128)
         return fail(LLMR_ERR_INVALID_ARG, "head_dim must be 128 (flash_attn.slang:20), got %u", head_dim);
@@ -604,12 +604,31 @@ int llmr_flash_attention(llmr_context* ctx, const void* q, const void* k, const 
     // one head's [S, 128] slab is addressed with 32-bit byte offsets
     if ((uint64_t)seq_len * 128u * (xtype == LLMR_GGML_F32 ? 4u : 2u) > 0xffffffffull)
         return fail(LLMR_ERR_INVALID_ARG, "seq_len %u too large: one head must span < 4 GiB", seq_len);
+    if (!is_act_type(out_type))
+        return fail(LLMR_ERR_UNSUPPORTED, "output type %u not supported (F32=0, F16=1, BF16=30)", out_type);
+    if (out_stride % 8u || (uint64_t)out_stride < (uint64_t)n_heads * head_dim)
+        return fail(LLMR_ERR_INVALID_ARG, "out_stride must be a multiple of 8 and >= n_heads * head_dim (got %u)",
+                    out_stride);
     const size_t need = llmr::flash_attention_workspace_bytes(xtype, n_heads, seq_len);
     if (int r = acquire_workspace(ctx, need)) return r;
-    hipError_t e = llmr::launch_flash_attention(q, k, v, xtype, out, n_heads, seq_len, scale, ctx->ws, ctx->cur);
+    hipError_t e = llmr::launch_flash_attention(q, k, v, xtype, out, out_type, out_stride, n_heads, seq_len, scale,
+                                                ctx->ws, ctx->cur);
     if (e != hipSuccess) return fail(LLMR_ERR_HIP, "flash_attention launch: %s", hipGetErrorString(e));
     if (int r = release_workspace(ctx, need)) return r;
     return ok();
+}
+
+int llmr_flash_attention(llmr_context* ctx, const void* q, const void* k, const void* v,
+                         uint32_t xtype, float* out, uint32_t head_dim, uint32_t n_heads,
+                         uint32_t seq_len, float scale) {
+    return flash_attention_impl(ctx, q, k, v, xtype, out, LLMR_GGML_F32, n_heads * head_dim, head_dim, n_heads,
+                                seq_len, scale);
+}
+
+int llmr_flash_attention_rows(llmr_context* ctx, const void* q, const void* k, const void* v, uint32_t xtype,
+                              void* out, uint32_t out_type, uint32_t out_stride, uint32_t head_dim,
+                              uint32_t n_heads, uint32_t seq_len, float scale) {
+    return flash_attention_impl(ctx, q, k, v, xtype, out, out_type, out_stride, head_dim, n_heads, seq_len, scale);
 }
 
 int llmr_flash_attention_pc(llmr_context* ctx, const void* q, const void* k, const void* v,

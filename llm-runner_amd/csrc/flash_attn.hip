@@ -76,9 +76,12 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // QT: type of Q (F16, or F32 / BF16 rounded to fp16 as the fragments are
 // loaded: Q is read once per workgroup, so it needs no conversion pass)
-template <int NB, uint32_t QT>  // query blocks of 32 per wave; 8 / NB waves per workgroup
+// OT: type of the output rows (F32, or F16 / BF16 rounded to nearest even)
+// at row stride ostride elements, head h at columns h * 128 of a row
+template <int NB, uint32_t QT, uint32_t OT = kGgmlF32>  // query blocks of 32 per wave; 8 / NB waves per workgroup
 __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Float16* __restrict__ K,
-                                          const _Float16* __restrict__ V, float* __restrict__ O, uint32_t S,
+                                          const _Float16* __restrict__ V, void* __restrict__ O, uint32_t ostride,
+                                          uint32_t S,
                                           uint32_t H, float scale_log2, uint32_t n_qb) {
     // K ring in slots 0..2, V ring in slots 3..5
     // (after the key loop the epilogue stages O in it: 16 KiB per 32 queries)
@@ -439,18 +442,29 @@ __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Flo
         for (int i = 0; i < 16; i++) {
             const uint32_t r = 2u * i + kh, q = q0 + 32u * b + r;
             const f32x4 v = *(const f32x4*)(ot + r * kD + ((l32 ^ r) << 2));
-            if (q < S) *(f32x4*)(O + (uint64_t)q * H * kD + (uint64_t)head * kD + 4u * l32) = v;
+            if (q >= S) continue;
+            const uint64_t at = (uint64_t)q * ostride + (uint64_t)head * kD + 4u * l32;
+            if constexpr (OT == kGgmlF32) {
+                *(f32x4*)((float*)O + at) = v;
+            } else if constexpr (OT == kGgmlBF16) {
+                typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+                *(u32x2*)((uint16_t*)O + at) = u32x2{__builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v.x, (__bf16)v.y}),
+                                                     __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v.z, (__bf16)v.w})};
+            } else {
+                *(u32x2*)((uint16_t*)O + at) = u32x2{pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w)};
+            }
         }
     }
 }
 // 8 waves of 32 queries: two waves per SIMD, so one wave's softmax runs
 // beside the other's MFMAs (measured 827 vs 737 TFLOP/s for 4 waves of 64
 // queries at H = 24, S = 4608, which also need 495 of the 512 registers)
-template <uint32_t QT>
+template <uint32_t QT, uint32_t OT = kGgmlF32>
 __global__ void __launch_bounds__(512, 1)
 flash_attn_fwd64_w8(const void* __restrict__ Q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
-                    float* __restrict__ O, uint32_t S, uint32_t H, float scale_log2, uint32_t n_qb) {
-    fa64_body<1, QT>(Q, K, V, O, S, H, scale_log2, n_qb);
+                    void* __restrict__ O, uint32_t ostride, uint32_t S, uint32_t H, float scale_log2,
+                    uint32_t n_qb) {
+    fa64_body<1, QT, OT>(Q, K, V, O, ostride, S, H, scale_log2, n_qb);
 }
 
 // K and V (blockIdx.y = 0, 1) of f32 or bf16 type -> fp16, round to nearest
@@ -479,8 +493,8 @@ size_t flash_attention_workspace_bytes(uint32_t xtype, uint32_t n_heads, uint32_
 }
 
 hipError_t launch_flash_attention(const void* q, const void* k, const void* v, uint32_t xtype,
-                                  float* o, uint32_t n_heads, uint32_t seq_len, float scale, void* ws,
-                                  hipStream_t st) {
+                                  void* o, uint32_t otype, uint32_t ostride, uint32_t n_heads, uint32_t seq_len,
+                                  float scale, void* ws, hipStream_t st) {
     if (seq_len == 0 || n_heads == 0) return hipSuccess;
     if (xtype != kGgmlF16) {  // K and V to fp16 in the workspace; Q is converted as it is loaded
         const size_t n8 = (size_t)n_heads * seq_len * kD / 8u;
@@ -498,15 +512,21 @@ hipError_t launch_flash_attention(const void* q, const void* k, const void* v, u
     const uint32_t n_qb64 = (seq_len + kBQ64 - 1) / kBQ64;
     const dim3 grid(n_qb64 * n_heads), block(512);
     const _Float16 *kh = (const _Float16*)k, *vh = (const _Float16*)v;
-    if (xtype == kGgmlF32)
-        hipLaunchKernelGGL(flash_attn_fwd64_w8<kGgmlF32>, grid, block, 0, st, q, kh, vh, o, seq_len, n_heads,
-                           scale_log2, n_qb64);
-    else if (xtype == kGgmlBF16)
-        hipLaunchKernelGGL(flash_attn_fwd64_w8<kGgmlBF16>, grid, block, 0, st, q, kh, vh, o, seq_len, n_heads,
-                           scale_log2, n_qb64);
-    else
-        hipLaunchKernelGGL(flash_attn_fwd64_w8<kGgmlF16>, grid, block, 0, st, q, kh, vh, o, seq_len, n_heads,
-                           scale_log2, n_qb64);
+    auto go = [&](auto qt, auto ot) {
+        hipLaunchKernelGGL((flash_attn_fwd64_w8<decltype(qt)::value, decltype(ot)::value>), grid, block, 0, st, q, kh,
+                           vh, o, ostride, seq_len, n_heads, scale_log2, n_qb64);
+    };
+    using F32 = std::integral_constant<uint32_t, kGgmlF32>;
+    using F16 = std::integral_constant<uint32_t, kGgmlF16>;
+    using BF16 = std::integral_constant<uint32_t, kGgmlBF16>;
+    auto by_out = [&](auto qt) {
+        if (otype == kGgmlBF16) go(qt, BF16{});
+        else if (otype == kGgmlF16) go(qt, F16{});
+        else go(qt, F32{});
+    };
+    if (xtype == kGgmlF32) by_out(F32{});
+    else if (xtype == kGgmlBF16) by_out(BF16{});
+    else by_out(F16{});
     return hipGetLastError();
 }
 

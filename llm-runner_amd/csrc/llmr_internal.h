@@ -154,9 +154,11 @@ hipError_t launch_batch_matmul_lora(const void* w, uint32_t wtype, const void* x
 // Attention (flash_attn.hip). F32 / BF16 Q, K, V are rounded to fp16 into
 // `ws` first (flash_attention_workspace_bytes; 0 for F16).
 size_t flash_attention_workspace_bytes(uint32_t xtype, uint32_t n_heads, uint32_t seq_len);
+// The output rows: o[s * ostride + h * 128 + d] of type otype (F32, F16 or
+// BF16 rounded to nearest even).
 hipError_t launch_flash_attention(const void* q, const void* k, const void* v, uint32_t xtype,
-                                  float* o, uint32_t n_heads, uint32_t seq_len, float scale, void* ws,
-                                  hipStream_t st);
+                                  void* o, uint32_t otype, uint32_t ostride, uint32_t n_heads, uint32_t seq_len,
+                                  float scale, void* ws, hipStream_t st);
 
 // --- block glue (glue.hip). Strides are in elements; the C-ABI layer checks
 // that every vector access is aligned (dims, strides and column offsets % 4,

@@ -114,6 +114,8 @@ _SIGS = {
                                                    ctypes.POINTER(BatchMatMulParams)]),
     "llmr_flash_attention": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32,
                                             ctypes.c_float]),
+    "llmr_flash_attention_rows": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _u32, _u32, _u32,
+                                                 ctypes.c_float]),
     "llmr_flash_attention_pc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _u32, _vp,
                                                ctypes.POINTER(FlashAttentionParams)]),
     "llmr_batch_rmsnorm": (ctypes.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
@@ -260,6 +262,11 @@ class Context:
                             y_ptr: int, out_dim: int, in_dim: int, seq_len: int) -> None:
         check(lib().llmr_batch_matmul_swiglu(self._h, wg_ptr, wu_ptr, wtype, x_ptr, xtype, y_ptr,
                                              out_dim, in_dim, seq_len))
+
+    def flash_attention_rows(self, q_ptr: int, k_ptr: int, v_ptr: int, xtype: int, o_ptr: int, otype: int,
+                             ostride: int, head_dim: int, n_heads: int, seq_len: int, scale: float) -> None:
+        check(lib().llmr_flash_attention_rows(self._h, q_ptr, k_ptr, v_ptr, xtype, o_ptr, otype, ostride, head_dim,
+                                              n_heads, seq_len, scale))
 
     def flash_attention(self, q_ptr: int, k_ptr: int, v_ptr: int, xtype: int, o_ptr: int,
                         head_dim: int, n_heads: int, seq_len: int, scale: float) -> None:

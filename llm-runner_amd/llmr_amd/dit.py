@@ -37,7 +37,7 @@ from . import capi, glue, workloads
 from .gguf import GGML_Q4_K, GGML_Q8_0
 from .ops import _TORCH_GGML, FlashAttentionPC, MatmulJob, NextImages, RenderGraph, Tensor, build_weight_image, \
     default_graph, dispatch_batch_matmul, dispatch_batch_matmul_multi, dispatch_batch_matmul_swiglu, \
-    dispatch_flash_attention, weight_image_bytes
+    dispatch_flash_attention, dispatch_flash_attention_rows, weight_image_bytes
 
 HEAD_DIM = 128
 
@@ -92,7 +92,6 @@ class ZImageBlock:
         self.q = torch.empty(n_heads, S, HEAD_DIM, dtype=torch.float16, **e)
         self.k = torch.empty_like(self.q)
         self.v = torch.empty_like(self.q)
-        self.o = torch.empty(S, dim, dtype=torch.float32, **e)
         self.t = torch.empty(S, dim, dtype=torch.float32, **e)      # O-proj / down outputs
         self.f = torch.empty(S, ffn_dim, dtype=torch.float32, **e)  # SwiGLU output
         self.fa = torch.empty(S, ffn_dim, dtype=act_dtype, **e)     # down-projection input
@@ -110,10 +109,11 @@ class ZImageBlock:
                               S, 0)
         # C: head norm, RoPE, head-major fp16 Q/K/V; attention         (dit.c3:1446-1483)
         glue.qkv_heads(self.qkv, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, eps, (rope_cos, rope_sin), g=g)
-        dispatch_flash_attention(g, _t(self.q), _t(self.k), _t(self.v), _t(self.o),
-                                 FlashAttentionPC(HEAD_DIM, H, S, 1.0 / math.sqrt(HEAD_DIM)))
+        # (the attention rows go straight into the O-proj input, rounded to the
+        # activation type: the reference's attention output plus its copy)
+        dispatch_flash_attention_rows(g, _t(self.q), _t(self.k), _t(self.v), self.xa,
+                                      FlashAttentionPC(HEAD_DIM, H, S, 1.0 / math.sqrt(HEAD_DIM)))
         # D: O-proj; hidden += tanh(gate_msa) * rmsnorm(o-proj)        (dit.c3:1488-1503)
-        glue.activation(self.o, self.xa, capi.ACT_COPY, g=g)
         dispatch_batch_matmul(g, _qt(w.wo, GGML_Q8_0, dim, dim), _t(self.xa), _t(self.t), dim, dim, S, 0)
         glue.gated_residual(hidden, self.t, w.adaln[1], capi.GATE_TANH, w.attn_norm2, eps, g=g)
         # E: FFN pre-norm, * (1 + scale_mlp)                           (dit.c3:1545-1554)
@@ -538,9 +538,11 @@ class FluxDiT:
         images, nxt = self.ahead.take()
         dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split, images=images, next_images=nxt)
 
-    def _attention(self, S: int) -> None:
-        dispatch_flash_attention(self.g, _t(self.q), _t(self.k), _t(self.v), _t(self.o),
-                                 FlashAttentionPC(HEAD_DIM, self.cfg.n_heads, S, 1.0 / math.sqrt(HEAD_DIM)))
+    def _attention(self, S: int, out: torch.Tensor) -> None:
+        """Attention over the joint Q/K/V, its rows written into `out` (the next
+        projection's input columns) in out's type."""
+        dispatch_flash_attention_rows(self.g, _t(self.q), _t(self.k), _t(self.v), out,
+                                      FlashAttentionPC(HEAD_DIM, self.cfg.n_heads, S, 1.0 / math.sqrt(HEAD_DIM)))
 
     def _double(self, w: FluxDoubleWeights, mi: torch.Tensor, mt: torch.Tensor) -> None:
         """flux_dual_stream_block (flux_dit.c3:746-971). mi / mt: [6, dim]
@@ -570,9 +572,9 @@ class FluxDiT:
                        self.rope, g=g)
         glue.qkv_heads(self.qkv[im], H, self.q, self.k, self.v, nt, w.img_q_norm, w.img_k_norm, self.HN_EPS,
                        self.rope, g=g)
-        self._attention(S)
+        # attention rows straight into the projection input             (flux_dit.c3:865-872)
+        self._attention(S, self.xa)
         # output projections, hidden += gate1 * proj                  (flux_dit.c3:875-898)
-        glue.activation(self.o, self.xa, capi.ACT_COPY, g=g)
         self._multi(jobs(w.txt_proj, w.img_proj, d, self.xa, self.hidden, (mt[2], mi[2])), d, d,
                     capi.EPI_GATED_RESIDUAL)
         # MLP: LayerNorm + modulation, up + gelu, down, hidden += gate2 * down (flux_dit.c3:902-967)
@@ -594,8 +596,7 @@ class FluxDiT:
                                S, 0, None, self.cat[:, d:])],
                     3 * d + m, d, capi.EPI_SPLIT_GELU, split=3 * d)
         glue.qkv_heads(self.qkv, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, self.HN_EPS, self.rope, g=g)
-        self._attention(S)
-        glue.activation(self.o, self.cat[:, :d], capi.ACT_COPY, g=g)
+        self._attention(S, self.cat[:, :d])  # rows into linear2's input  (flux_dit.c3:1042-1047)
         # linear2, hidden += gate * linear2                           (flux_dit.c3:1060-1068)
         self._multi([MatmulJob(_qt(w.linear2, GGML_Q4_K, d, d + m), _t(self.cat), self.hidden, S, 0, mod[2])],
                     d, d + m, capi.EPI_GATED_RESIDUAL)

@@ -399,6 +399,29 @@ def dispatch_flash_attention(g: RenderGraph, q: Tensor, k: Tensor, v: Tensor, ou
                           pc.seq_len, pc.scale)
 
 
+def dispatch_flash_attention_rows(g: RenderGraph, q: Tensor, k: Tensor, v: Tensor, out: torch.Tensor,
+                                  pc: FlashAttentionPC) -> None:
+    """dispatch_flash_attention with the output rows written into `out`, a 2-D
+    device view [seq_len, >= n_heads * head_dim] of f32, f16 or bf16 with
+    contiguous rows (e.g. the columns of the next projection's input),
+    rounded to nearest even (llmr_flash_attention_rows)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _dev(t, n)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, v must share a dtype")
+    ot = _TORCH_GGML.get(out.dtype)
+    if ot is None or not out.is_cuda or out.dim() != 2 or out.stride(1) != 1:
+        raise ValueError("out must be a 2-D f32/f16/bf16 device view with contiguous rows")
+    if out.shape[0] < pc.seq_len or out.shape[1] < pc.n_heads * pc.head_dim:
+        raise ValueError("out view smaller than [seq_len, n_heads * head_dim]")
+    n = pc.n_heads * pc.seq_len * pc.head_dim
+    if min(q.data.numel(), k.data.numel(), v.data.numel()) < n:
+        raise ValueError("buffers smaller than [n_heads, seq_len, head_dim]")
+    g.bind_stream()
+    g.ctx.flash_attention_rows(q.ptr(), k.ptr(), v.ptr(), q.dtype, out.data_ptr(), ot, out.stride(0), pc.head_dim,
+                               pc.n_heads, pc.seq_len, pc.scale)
+
+
 # ---- torch-tensor conveniences (tests, bench) --------------------------------
 
 _default_graph: RenderGraph | None = None

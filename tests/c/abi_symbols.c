@@ -32,6 +32,7 @@ static const struct {
     {"llmr_batch_matmul_pc", (void (*)(void))(uintptr_t)llmr_batch_matmul_pc},
     {"llmr_batch_matmul_noalloc", (void (*)(void))(uintptr_t)llmr_batch_matmul_noalloc},
     {"llmr_batch_matmul_multi", (void (*)(void))(uintptr_t)llmr_batch_matmul_multi},
+    {"llmr_flash_attention_rows", (void (*)(void))(uintptr_t)llmr_flash_attention_rows},
     {"llmr_batch_matmul_multi_images", (void (*)(void))(uintptr_t)llmr_batch_matmul_multi_images},
     {"llmr_weight_image_bytes", (void (*)(void))(uintptr_t)llmr_weight_image_bytes},
     {"llmr_build_weight_image", (void (*)(void))(uintptr_t)llmr_build_weight_image},

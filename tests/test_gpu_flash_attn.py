@@ -136,3 +136,27 @@ def test_fa_flux_full_size_sampled(orc, dev):
         err = rel_l2(got, ref.reshape(a.S, a.D)[q0:q0 + 128])
         print(f"head {h} q {q0}: rel_l2={err:.3e}")
         assert err <= TOL
+
+
+@pytest.mark.parametrize("otype,H,S,pad", [("bfloat16", 2, 300, 40), ("float16", 3, 257, 0), ("float32", 2, 129, 8),
+                                           ("bfloat16", 24, 4608, 0)])
+def test_fa_rows_equal_f32_output_rounded(dev, otype, H, S, pad):
+    """llmr_flash_attention_rows writes the f32 attention rows rounded to the
+    output type (nearest even), at a row stride with a column offset, and
+    touches nothing else of the destination: bit for bit the f32 launch
+    followed by a torch cast (the values llmr_activation's copy gives)."""
+    import torch
+    from llmr_amd import ops
+    dt = getattr(torch, otype)
+    g = ops.default_graph()
+    gen = torch.Generator(device="cpu").manual_seed(S + H)
+    q, k, v = (torch.randn(H, S, 128, generator=gen).half().to(dev) for _ in range(3))
+    pc = ops.FlashAttentionPC(128, H, S, 1.0 / 128 ** 0.5)
+    ref = torch.empty(S, H * 128, dtype=torch.float32, device=dev)
+    ops.dispatch_flash_attention(g, *(ops.Tensor.from_torch(t) for t in (q, k, v)), ops.Tensor.from_torch(ref), pc)
+    width = H * 128 + 64 + pad
+    dst = torch.full((S, width), 7.0, dtype=dt, device=dev)
+    ops.dispatch_flash_attention_rows(g, *(ops.Tensor.from_torch(t) for t in (q, k, v)), dst[:, 64:64 + H * 128], pc)
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:, 64:64 + H * 128], ref.to(dt))
+    assert (dst[:, :64] == 7.0).all() and (dst[:, 64 + H * 128:] == 7.0).all()
