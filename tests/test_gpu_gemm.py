@@ -728,3 +728,51 @@ def test_split_k_matches_oracle_and_repeats(orc, dev, wtype, M, N, K, xtype):
     print(f"split-K wtype={wtype} M={M} N={N} K={K}: rel_l2={err:.3e}")
     assert err <= TOL
     assert np.array_equal(y, y2)
+
+
+def test_weight_image_entry_points_reject_bad_arguments(dev):
+    """llmr_build_weight_image / llmr_batch_matmul_multi_images /
+    llmr_flash_attention_rows reject what they cannot take, with a message,
+    before launching anything."""
+    import ctypes
+    import torch
+    from llmr_amd import capi, gguf, ops, synth
+    g = ops.default_graph()
+    g.bind_stream()
+    N, K = 512, 512
+    blk = torch.from_numpy(gguf.quantize(synth.normal(5, 1, N * K, 0.02), 12)).to(dev)
+    w = ops.Tensor.quantized(blk, 12, N, K)
+    nb = ops.weight_image_bytes(N, K)
+    img = torch.zeros(nb + 256, dtype=torch.uint8, device=dev)
+    ctx = g.ctx
+    with pytest.raises(capi.LlmrError, match="F16 or BF16"):
+        ctx.build_weight_image(w.ptr(), 12, 0, N, K, 0, img.data_ptr(), nb)       # f32 operands
+    with pytest.raises(capi.LlmrError, match="multiple of 64"):
+        ctx.build_weight_image(w.ptr(), 12, 30, N, 256 + 32, 0, img.data_ptr(), nb)
+    with pytest.raises(capi.LlmrError, match="256-byte aligned"):
+        ctx.build_weight_image(w.ptr(), 12, 30, N, K, 0, img.data_ptr() + 16, nb)
+    with pytest.raises(capi.LlmrError, match="needs"):
+        ctx.build_weight_image(w.ptr(), 12, 30, N, K, 0, img.data_ptr(), nb - 1)
+    x = torch.zeros(2048, K, dtype=torch.bfloat16, device=dev)
+    y = torch.zeros(2048, N, device=dev)
+    job = capi.MatmulJob(w.ptr(), x.data_ptr(), y.data_ptr(), None, None, 2048, 0)
+    epi = capi.MatmulEpilogue(capi.EPI_STORE, N, 0, 0, 0)
+    with pytest.raises(capi.LlmrError, match="256-byte aligned"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, [img.data_ptr() + 16])
+    nxt = capi.NextWeightImages(12, N, K, 3, (ctypes.c_void_p * 2)(w.ptr(), None), (ctypes.c_uint32 * 2)(0, 0),
+                                (ctypes.c_void_p * 2)(img.data_ptr(), None), nb)
+    with pytest.raises(capi.LlmrError, match="count"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
+    nxt.count = 1
+    with pytest.raises(capi.LlmrError, match="also an image"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, [img.data_ptr()], nxt)
+    with pytest.raises(capi.LlmrError, match="F16 or BF16"):
+        ctx.batch_matmul_multi_images(12, 0, N, K, [job], epi, None, nxt)
+    q = torch.zeros(2, 64, 128, dtype=torch.float16, device=dev)
+    o = torch.zeros(64, 264, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(capi.LlmrError, match="out_stride"):
+        ctx.flash_attention_rows(q.data_ptr(), q.data_ptr(), q.data_ptr(), 1, o.data_ptr(), 30, 260, 128, 2, 64, 0.1)
+    with pytest.raises(capi.LlmrError, match="output type"):
+        ctx.flash_attention_rows(q.data_ptr(), q.data_ptr(), q.data_ptr(), 1, o.data_ptr(), 8, 264, 128, 2, 64, 0.1)
+    torch.cuda.synchronize()
+    assert (y == 0).all()
