@@ -79,21 +79,30 @@ __device__ __forceinline__ f32x4 ld4(const float* p) { return *(const f32x4*)p; 
 
 template <bool LN, uint32_t OT, int NV>
 __global__ void __launch_bounds__(256) row_norm_kernel(RowNormArgs a) {
+    // the modulation vectors, staged once for the workgroup's four rows
+    // (element 4k .. 4k+3 at k): the lanes keep only the row in registers
+    __shared__ f32x4 mod_lds[2][NV * 64];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (row >= a.rows) return;
-    const float* xr = a.x + (size_t)row * a.x_stride;
-    f32x4 v[NV], sc[NV], sh[NV];
+    const bool live = row < a.rows;
+    const float* xr = a.x + (size_t)(live ? row : 0u) * a.x_stride;
+    f32x4 v[NV];
     float s = 0.0f;
-    // the row and, when given, the modulation vectors all requested up
-    // front (the vectors' latency hidden behind the row's reductions)
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const uint32_t c = 4u * lane + 256u * i;
-        v[i] = c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        sc[i] = a.scale && c < a.dim ? ld4(a.scale + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        sh[i] = a.shift && c < a.dim ? ld4(a.shift + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        v[i] = live && c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    if (a.scale || a.shift) {  // uniform over the workgroup
+#pragma unroll
+        for (int j = 0; j < NV / 4; ++j) {
+            const uint32_t k = threadIdx.x + 256u * j, c = 4u * k;
+            mod_lds[0][k] = a.scale && c < a.dim ? ld4(a.scale + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            mod_lds[1][k] = a.shift && c < a.dim ? ld4(a.shift + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        __syncthreads();
+    }
+    if (!live) return;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         if constexpr (LN) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
@@ -125,8 +134,8 @@ __global__ void __launch_bounds__(256) row_norm_kernel(RowNormArgs a) {
         f32x4 y;
         if constexpr (LN) y = (v[i] - mean) * r;
         else y = (v[i] * r) * ld4(a.w + c);
-        if (a.scale) y = y * (1.0f + sc[i]);
-        if (a.shift) y = y + sh[i];
+        if (a.scale) y = y * (1.0f + mod_lds[0][lane + 64u * i]);
+        if (a.shift) y = y + mod_lds[1][lane + 64u * i];
         store4<OT>(orow, c, y);
     }
 }
