@@ -201,18 +201,39 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadsArgs a) {
 
 template <bool NORM, bool TANH, int NV>
 __global__ void __launch_bounds__(256) residual_kernel(ResidualArgs a) {
+    // the norm weights and the gate (tanh(gate) for TANH), computed once for
+    // the workgroup's four rows into LDS (element 4k .. 4k+3 at k)
+    __shared__ f32x4 vec_lds[2][NV * 64];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (row >= a.rows) return;
-    const float* xr = a.x + (size_t)row * a.x_stride;
-    float* hr = a.h + (size_t)row * a.h_stride;
+    const bool live = row < a.rows;
+    const float* xr = a.x + (size_t)(live ? row : 0u) * a.x_stride;
+    float* hr = a.h + (size_t)(live ? row : 0u) * a.h_stride;
     f32x4 v[NV];
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const uint32_t c = 4u * lane + 256u * i;
-        v[i] = c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (NORM) s += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+        v[i] = live && c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    if (NORM || a.gate) {  // uniform over the workgroup
+#pragma unroll
+        for (int j = 0; j < NV / 4; ++j) {
+            const uint32_t k = threadIdx.x + 256u * j, c = 4u * k;
+            if constexpr (NORM) vec_lds[0][k] = c < a.dim ? ld4(a.norm_w + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (a.gate) {
+                const f32x4 g = c < a.dim ? ld4(a.gate + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (TANH) vec_lds[1][k] = f32x4{tanhf(g.x), tanhf(g.y), tanhf(g.z), tanhf(g.w)};
+                else vec_lds[1][k] = g;
+            }
+        }
+        __syncthreads();
+    }
+    if (!live) return;
+    if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            s += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
     }
     float rms = 1.0f;
     if constexpr (NORM) rms = 1.0f / __builtin_sqrtf(wave_sum(s) / (float)a.dim + a.eps);
@@ -221,11 +242,11 @@ __global__ void __launch_bounds__(256) residual_kernel(ResidualArgs a) {
         const uint32_t c = 4u * lane + 256u * i;
         if (c >= a.dim) continue;
         f32x4 y = v[i];
-        if constexpr (NORM) y = (y * rms) * ld4(a.norm_w + c);
+        if constexpr (NORM) y = (y * rms) * vec_lds[0][lane + 64u * i];
         if (a.gate) {
-            const f32x4 g = ld4(a.gate + c);
+            const f32x4 g = vec_lds[1][lane + 64u * i];
             if constexpr (TANH) {
-                const f32x4 tg = {tanhf(g.x), tanhf(g.y), tanhf(g.z), tanhf(g.w)};
+                const f32x4 tg = g;
                 y = (1.0f * tg) * y;
                 y = __builtin_elementwise_min(__builtin_elementwise_max(y, f32x4(-1e10f)), f32x4(1e10f));
             } else {
