@@ -171,22 +171,35 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadsArgs a) {
         w0 = w[2u * lane];
         w1 = w[2u * lane + 1u];
     }
-    for (uint32_t h = wave; h < a.n_heads; h += 4u) {
-        const f32x2 xv = *(const f32x2*)(src + h * 128u);
-        float x0 = xv.x, x1 = xv.y;
-        if (w) {
-            const float ss = wave_sum(x0 * x0 + x1 * x1);
-            const float rms = 1.0f / __builtin_sqrtf(ss / 128.0f + a.eps);
-            x0 = (x0 * rms) * w0;
-            x1 = (x1 * rms) * w1;
+    // the wave's heads h = wave, wave + 4, ... are all requested before the
+    // first is processed (up to kHB at a time), so their loads overlap
+    constexpr uint32_t kHB = 8;
+    for (uint32_t h0 = wave; h0 < a.n_heads; h0 += 4u * kHB) {
+        f32x2 xv[kHB];
+#pragma unroll
+        for (uint32_t j = 0; j < kHB; ++j) {
+            const uint32_t h = h0 + 4u * j;
+            xv[j] = h < a.n_heads ? *(const f32x2*)(src + h * 128u) : f32x2{0.0f, 0.0f};
         }
-        if (rope) {
-            const float y0 = x0 * c - x1 * sn;
-            const float y1 = x0 * sn + x1 * c;
-            x0 = y0;
-            x1 = y1;
+#pragma unroll
+        for (uint32_t j = 0; j < kHB; ++j) {
+            const uint32_t h = h0 + 4u * j;
+            if (h >= a.n_heads) break;  // uniform over the wave
+            float x0 = xv[j].x, x1 = xv[j].y;
+            if (w) {
+                const float ss = wave_sum(x0 * x0 + x1 * x1);
+                const float rms = 1.0f / __builtin_sqrtf(ss / 128.0f + a.eps);
+                x0 = (x0 * rms) * w0;
+                x1 = (x1 * rms) * w1;
+            }
+            if (rope) {
+                const float y0 = x0 * c - x1 * sn;
+                const float y1 = x0 * sn + x1 * c;
+                x0 = y0;
+                x1 = y1;
+            }
+            store2<OT>(dst, ((size_t)h * a.dst_seq + t) * 128u + 2u * lane, x0, x1);
         }
-        store2<OT>(dst, ((size_t)h * a.dst_seq + t) * 128u + 2u * lane, x0, x1);
     }
 }
 
