@@ -34,7 +34,9 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "llm-runner_amd"))
 
 METRIC = "Q4_K/Q8_0 dequant-GEMM TFLOPS, flash-attn TFLOPS, Flux 1024² ms/step"
-PEAK_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA, published
+# MI355X dense fp16/bf16 MFMA: 256 CUs x 2.4 GHz x 4096 flop per clock
+# (the 2.5 PFLOP/s published figure, unrounded)
+PEAK_TFLOPS = 2516.6
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E, published
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 
@@ -294,8 +296,10 @@ def gemm_kernel_name(name: str, num_cus: int) -> str:
     """The kernels the library's dispatch runs for a GEMM workload (the one
     that dominates first): the two-pass path (weight image, then the all-DMA
     persistent GEMM) from 2048 tokens with at least half the CUs' worth of
-    256 x 256 tiles; the one-pass persistent kernels below 2048 tokens; the
-    few-token kernel up to 256 tokens; else the 4-wave tiled kernel."""
+    256 x 256 tiles; the one-pass persistent kernels below 2048 tokens; up to
+    256 tokens the few-token kernel (one launch) when there are at least half
+    the CUs' worth of 32 x 96 tiles, else the split-K skinny kernel; else the
+    4-wave tiled kernel."""
     from llmr_amd import gguf, workloads
     g = workloads.GEMMS[name]
     tiles = ((g.M + 255) // 256) * ((g.N + 255) // 256)
@@ -303,13 +307,18 @@ def gemm_kernel_name(name: str, num_cus: int) -> str:
         return "gemm_q_generic"
     if g.wtype == gguf.GGML_Q4_K and g.M <= 4:
         return "gemv_q4k"
-    pre = "f32->f16 conversion + " if g.xtype == gguf.GGML_F32 else ""
+    f32 = g.xtype == gguf.GGML_F32
+    cvt = "f32->bf16" if g.wtype == gguf.GGML_Q4_K else "f32->f16"
     if g.K % 64 == 0 and g.N % 4 == 0 and 2 * tiles >= num_cus:
         if g.M >= 2048:
-            return "gemm_w16_persist + w16_image_kernel" + (" + f32->f16 conversion" if pre else "")
-        return pre + ("gemm_q_persist8" if g.wtype == gguf.GGML_Q8_0 else "gemm_q_persist")
+            return "gemm_w16_persist + w16_image_kernel" + (f" + {cvt} conversion" if f32 else "")
+        return (f"{cvt} conversion + " if f32 else "") + ("gemm_q_persist8" if g.wtype == gguf.GGML_Q8_0
+                                                          else "gemm_q_persist")
+    few_tiles = ((g.M + 31) // 32) * ((g.N + 95) // 96)
+    if g.M <= 256 and g.K % 64 == 0 and 2 * few_tiles >= num_cus:
+        return "gemm_q_few"
     if g.M <= 256 and g.K % 64 == 0 and g.N % 4 == 0:
-        return "gemm_q_skinny + splitk_reduce_kernel" + (" + skinny_pack_kernel" if pre else "")
+        return "gemm_q_skinny + splitk_reduce_kernel" + (" + skinny_pack_kernel" if f32 else "")
     return "gemm_q_mfma"
 
 

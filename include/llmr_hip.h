@@ -182,12 +182,13 @@ LLMR_API int llmr_batch_matmul_pc(llmr_context* ctx, const void* weight, uint32_
  * the library's load to the end of the process. Where llmr_batch_matmul's
  * plan needs more, the call takes the form that fits: the one-pass kernels
  * instead of the weight image (the same bits), fewer K splits (the same
- * result to f32 summation order). Only f32 activations of more than 16 Mi
- * elements on a launch that converts them cannot shrink: such a call
- * returns LLMR_ERR_INVALID_ARG and launches nothing. Every call on one GPU
- * uses that GPU's one array, whose contents persist between calls: calls
- * that may overlap on a GPU (other streams, other contexts, other threads)
- * race. */
+ * result to f32 summation order), the tiled kernel reading f32 activations
+ * in place instead of their 16-bit copy (the same operands). Every call on
+ * one GPU uses that GPU's one array, whose contents persist between calls.
+ * Calls of one context on different streams (llmr_set_stream) are ordered
+ * as its workspace is: a call on another stream than the last one waits
+ * for that stream's work issued up to the switch. Calls that may overlap
+ * otherwise (other contexts, other threads) race. */
 LLMR_API int llmr_batch_matmul_noalloc(llmr_context* ctx, const void* weight, uint32_t weight_type,
                                        const void* input, uint32_t input_type, float* output,
                                        uint32_t out_dim, uint32_t in_dim, uint32_t seq_len,

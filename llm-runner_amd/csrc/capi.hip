@@ -27,6 +27,13 @@ struct llmr_context {
     hipEvent_t ws_done;
     hipStream_t ws_stream;
     bool ws_used;
+    // The same ordering for the device's fixed no-allocation scratch, as far
+    // as this context's calls go: a llmr_batch_matmul_noalloc call on another
+    // stream than the last one waits for scr_done, recorded when the context
+    // left that stream.
+    hipEvent_t scr_done;
+    hipStream_t scr_stream;
+    bool scr_used;
 };
 
 // The no-allocation GEMM's scratch (llmr_batch_matmul_noalloc): a fixed
@@ -142,8 +149,17 @@ int llmr_create_context(int device_index, llmr_context** out_ctx) {
     c->ws_bytes = 0;
     c->ws_stream = nullptr;
     c->ws_used = false;
+    c->scr_stream = nullptr;
+    c->scr_used = false;
     e = hipEventCreateWithFlags(&c->ws_done, hipEventDisableTiming);
     if (e != hipSuccess) {
+        (void)hipStreamDestroy(c->own);
+        delete c;
+        return fail(LLMR_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(e));
+    }
+    e = hipEventCreateWithFlags(&c->scr_done, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipEventDestroy(c->ws_done);
         (void)hipStreamDestroy(c->own);
         delete c;
         return fail(LLMR_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(e));
@@ -160,6 +176,7 @@ int llmr_destroy_context(llmr_context* ctx) {
     (void)hipStreamDestroy(ctx->own);
     if (ctx->ws) (void)hipFree(ctx->ws);
     (void)hipEventDestroy(ctx->ws_done);
+    (void)hipEventDestroy(ctx->scr_done);
     delete ctx;
     return ok();
 }
@@ -172,6 +189,11 @@ int llmr_set_stream(llmr_context* ctx, void* hip_stream) {
     if (s != ctx->cur && ctx->ws_used && ctx->ws_stream == ctx->cur) {
         LLMR_HIP_CHECK(hipSetDevice(ctx->device));
         LLMR_HIP_CHECK(hipEventRecord(ctx->ws_done, ctx->cur));
+    }
+    // the same for the no-allocation scratch
+    if (s != ctx->cur && ctx->scr_used && ctx->scr_stream == ctx->cur) {
+        LLMR_HIP_CHECK(hipSetDevice(ctx->device));
+        LLMR_HIP_CHECK(hipEventRecord(ctx->scr_done, ctx->cur));
     }
     ctx->cur = s;
     return ok();
@@ -329,18 +351,25 @@ int llmr_batch_matmul_noalloc(llmr_context* ctx, const void* weight, uint32_t wt
     if (int r = check_batch_matmul(ctx, weight, wtype, input, xtype, output, out_dim, in_dim, seq_len, row_offset))
         return r;
     if (seq_len == 0 || out_dim == 0) return ok();
+    // the plan keeps within the scratch: smaller forms (one-pass kernels
+    // instead of a weight image, fewer K splits, the tiled kernel reading f32
+    // activations in place) where the usual plan needs more
     const size_t need = llmr::batch_matmul_workspace_bytes(wtype, xtype, out_dim, in_dim, seq_len, ctx->num_cus,
                                                            kNoAllocScratchBytes);
     if (need > kNoAllocScratchBytes)
-        return fail(LLMR_ERR_INVALID_ARG,
-                    "this GEMM needs %zu bytes of scratch (its f32 activations as fp16), beyond the %zu the "
-                    "no-allocation entry point holds; pass 16-bit activations or call llmr_batch_matmul",
-                    need, kNoAllocScratchBytes);
+        return fail(LLMR_ERR_INVALID_ARG, "this GEMM needs %zu bytes of scratch, beyond the %zu the no-allocation "
+                    "entry point holds; call llmr_batch_matmul", need, kNoAllocScratchBytes);
     void* const ptr = scratch_ptr(ctx->device);
     if (need > 0 && !ptr) return fail(LLMR_ERR_HIP, "scratch of device %d not resolved", ctx->device);
+    if (need > 0 && ctx->scr_used && ctx->scr_stream != ctx->cur)
+        LLMR_HIP_CHECK(hipStreamWaitEvent(ctx->cur, ctx->scr_done, 0));
     hipError_t e = llmr::launch_batch_matmul(weight, wtype, input, xtype, output, out_dim, in_dim, seq_len, row_offset,
                                              ctx->num_cus, ptr, ctx->cur, kNoAllocScratchBytes);
     if (e != hipSuccess) return fail(LLMR_ERR_HIP, "batch_matmul launch: %s", hipGetErrorString(e));
+    if (need > 0) {
+        ctx->scr_stream = ctx->cur;
+        ctx->scr_used = true;
+    }
     return ok();
 }
 

@@ -48,6 +48,7 @@ struct XLoad<kGgmlBF16> {
         v = ok ? *(const u32x4*)((const uint16_t*)x + elem) : u32x4{0, 0, 0, 0};
     }
     // bf16 activations are used as bf16 operands (bf16 MFMA)
+    template <uint32_t OT>
     __device__ __forceinline__ u32x4 to_op() const { return v; }
 };
 template <>
@@ -56,10 +57,12 @@ struct XLoad<kGgmlF16> {
     __device__ __forceinline__ void load(const void* x, uint64_t elem, bool ok) {
         v = ok ? *(const u32x4*)((const uint16_t*)x + elem) : u32x4{0, 0, 0, 0};
     }
+    template <uint32_t OT>
     __device__ __forceinline__ u32x4 to_op() const { return v; }
 };
-// f32 activations: two 16-byte loads per LDS chunk, rounded to fp16 as the
-// reference's float16_t(v) (llm.slang:1673).
+// f32 activations: two 16-byte loads per LDS chunk, rounded to the operand
+// type: fp16 as the reference's float16_t(v) (llm.slang:1673) against Q8_0,
+// bf16 against Q4_K (its f32 range kept), both to nearest even.
 template <>
 struct XLoad<kGgmlF32> {
     f32x4 a, b;
@@ -68,9 +71,14 @@ struct XLoad<kGgmlF32> {
         a = ok ? *(const f32x4*)p : f32x4{0, 0, 0, 0};
         b = ok ? *(const f32x4*)(p + 4) : f32x4{0, 0, 0, 0};
     }
+    template <uint32_t OT>
     __device__ __forceinline__ u32x4 to_op() const {
-        return u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y),
-                     pack_f16x2(b.z, b.w)};
+        if constexpr (OT == kGgmlBF16)
+            return u32x4{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w), pack_bf16x2(b.x, b.y),
+                         pack_bf16x2(b.z, b.w)};
+        else
+            return u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y),
+                         pack_f16x2(b.z, b.w)};
     }
 };
 
@@ -235,7 +243,10 @@ __global__ void __launch_bounds__(256, (BM * BN >= 256 * 256) ? 1 : 2)
 gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __restrict__ Y,
             uint32_t N, uint32_t K, uint32_t M, uint32_t row_offset, uint32_t tiles_m,
             uint32_t tiles_n, uint32_t split_stages, uint64_t split_stride) {
-    constexpr uint32_t OT = (XT == kGgmlBF16) ? kGgmlBF16 : kGgmlF16;  // MFMA operand type
+    // MFMA operand type: bf16 for bf16 activations and for f32 ones against
+    // Q4_K (batch_matmul_q4k keeps x in f32, so its range is kept), fp16
+    // otherwise (the reference's float16_t(x) of batch_matmul_q8)
+    constexpr uint32_t OT = (XT == kGgmlBF16 || (XT == kGgmlF32 && WT == kGgmlQ4K)) ? kGgmlBF16 : kGgmlF16;
     constexpr int WM = BM / 2, WN = BN / 2;  // per-wave tile (tokens x features)
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr uint32_t A_BYTES = BM * kBK * 2, B_BYTES = BN * kBK * 2;
@@ -289,7 +300,7 @@ gemm_q_mfma(const uint8_t* __restrict__ W, const void* __restrict__ X, float* __
 #pragma unroll
         for (int i = 0; i < X_PER_T; i++) {
             const uint32_t r = (tid >> 3) + 32u * i, c = tid & 7u;
-            *(u32x4*)(As + lds_off(r, c)) = xl[i].to_op();
+            *(u32x4*)(As + lds_off(r, c)) = xl[i].template to_op<OT>();
         }
 #pragma unroll
         for (int i = 0; i < W_PER_T; i++) {
@@ -1190,7 +1201,11 @@ hipError_t launch_tiled(const void* w, const void* x, float* y, uint32_t N, uint
         attr_set = true;
     }
     const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const uint32_t n_stages = K / kBK, per = (n_stages + splits - 1) / splits;
+    const uint32_t n_stages = K / kBK;
+    // every split must own at least one stage: the kernel loads its first
+    // stage unconditionally
+    if (!plan::splits_nonempty(n_stages, splits) || (splits > 1 && (uint64_t)M * N % 4)) return hipErrorInvalidValue;
+    const uint32_t per = (n_stages + splits - 1) / splits;
     const uint64_t mn = (uint64_t)M * N;
     hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n, splits), dim3(256), lds, st, (const uint8_t*)w, x,
                        splits > 1 ? part : y, N, K, M, row_offset, tiles_m, tiles_n, per, splits > 1 ? mn : 0ull);
@@ -1199,28 +1214,7 @@ hipError_t launch_tiled(const void* w, const void* x, float* y, uint32_t N, uint
     return launch_splitk_reduce(part, y, mn, splits, st);
 }
 
-// Tiles of the 4-wave kernel: the largest that still gives every CU ~1.5
-// workgroups. Launches with fewer workgroups than kSplitWgsPerCu per CU
-// split K (at least kSplitMinStages stages per split, M * N % 4 == 0 for
-// the reduction) so the CUs run several short K ranges side by side
-// instead of one long chain of dependent stages each.
-constexpr uint32_t kSplitWgsPerCu = 2, kSplitMinStages = 4;
-struct TilePlan {
-    uint32_t bm, splits;
-};
-TilePlan plan_tiles(uint32_t wtype, uint32_t N, uint32_t K, uint32_t M, int num_cus) {
-    auto wgs = [&](uint32_t bm) { return (uint64_t)((M + bm - 1) / bm) * ((N + bm - 1) / bm); };
-    const uint64_t want = (uint64_t)num_cus * 3 / 2;
-    TilePlan t{64, 1};
-    if (wgs(256) >= want) t.bm = 256;
-    else if (wgs(128) >= want) t.bm = 128;
-    if (wtype == kGgmlQ8_0 && K % kBK) return t;  // the generic kernel
-    const uint64_t w = wgs(t.bm), target = (uint64_t)num_cus * kSplitWgsPerCu;
-    const uint32_t n_stages = K / kBK;
-    if (w < target && n_stages >= 2 * kSplitMinStages && ((uint64_t)M * N) % 4 == 0)
-        t.splits = (uint32_t)std::min<uint64_t>((target + w - 1) / w, n_stages / kSplitMinStages);
-    return t;
-}
+using plan::TilePlan;
 
 template <uint32_t WT, uint32_t XT>
 hipError_t dispatch_x(const void* w, const void* x, float* y, uint32_t N, uint32_t K, uint32_t M,
@@ -1291,77 +1285,11 @@ __global__ void __launch_bounds__(256) swiglu_combine_kernel(const float* __rest
     if (i < n) y[i] = silu(g[i]) * u[i];
 }
 
-size_t align256(size_t b) { return (b + 255u) / 256u * 256u; }
-
-uint64_t row_bytes_of(uint32_t wtype, uint32_t K) {
-    return (wtype == kGgmlQ8_0) ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * 144;
-}
-
-// How one GEMM runs. The persistent 256 x 256 kernels take launches with at
-// least half the CUs' worth of tiles, whole 64-wide K stages, N % 4 == 0
-// (four features per lane store) and 32-bit buffer offsets over the 16-bit
-// activations and the used weight rows. F32 activations then go through
-// the workspace as fp16 (the reference's rounding of x, llm.slang:1673).
-// From kW16MinTokens tokens the weight is dequantized once into a 16-bit
-// image (gemm_w16.hip) instead of once per 256-token tile.
-constexpr uint32_t kW16MinTokens = 2048;
-// With a workspace limit (the no-allocation entry point's fixed array) the
-// plan keeps to it where it can: the two-pass path only when its image fits,
-// split-K with as many splits as fit (none if fewer than two). Only the fp16
-// copy of f32 activations for the persistent kernels has no smaller form,
-// so a plan may still exceed the limit there (the caller refuses it).
-struct GemmPlan {
-    bool persistent, two_pass, convert_x, skinny;
-    uint32_t xt;                  // activation type the kernel reads
-    TilePlan tiles;               // the tiled kernel's tile and splits (not persistent)
-    uint32_t splits;              // the skinny kernel's K splits
-    size_t x16_off, img_off, ws;  // workspace: [x16 | image] (persistent), [packed x | partials]
-                                  // (skinny), split-K partials (tiled)
-};
-GemmPlan plan_gemm(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M, int num_cus,
-                   size_t ws_limit) {
-    GemmPlan p{};
-    const uint64_t tiles = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
-    p.persistent = (K % kBK) == 0 && N % 4 == 0 && 2 * tiles >= (uint64_t)num_cus &&
-                   (uint64_t)M * K * 2u < (1ull << 31) && (uint64_t)N * row_bytes_of(wtype, K) < (1ull << 31);
-    p.xt = xtype;
-    if (!p.persistent && M <= 256 && (K % kBK) == 0 && N % 4 == 0 && (uint64_t)M * K * 2u < (1ull << 31) &&
-        (uint64_t)N * row_bytes_of(wtype, K) < (1ull << 31)) {
-        // few tokens: the skinny kernel (one workgroup per CU: its LDS),
-        // K split so the launch fills the CUs in one round (at least
-        // kSplitMinStages stages per split), as far as the partials fit the
-        // workspace
-        const size_t x16 = skinny_x_bytes(xtype, M, K), part = (size_t)M * N * sizeof(float);
-        if (x16 <= ws_limit) {
-            const uint32_t S = K / kBK, tn = (N + 63) / 64;
-            uint32_t splits = std::max<uint32_t>(1u, std::min<uint32_t>((uint32_t)num_cus / tn, S / kSplitMinStages));
-            if (splits > 1 && x16 + splits * part > ws_limit)
-                splits = std::max<uint32_t>(1u, (uint32_t)((ws_limit - x16) / part));
-            const uint32_t per = (S + splits - 1) / splits;
-            p.skinny = true;
-            p.splits = (S + per - 1) / per;
-            p.ws = x16 + (p.splits > 1 ? p.splits * part : 0u);
-            return p;
-        }
-    }
-    if (!p.persistent) {
-        p.tiles = plan_tiles(wtype, N, K, M, num_cus);
-        const size_t part = (size_t)M * N * sizeof(float);
-        if (p.tiles.splits > 1 && (size_t)p.tiles.splits * part > ws_limit) {
-            const size_t fit = ws_limit / part;
-            p.tiles.splits = fit >= 2 ? (uint32_t)fit : 1u;
-        }
-        p.ws = p.tiles.splits > 1 ? (size_t)p.tiles.splits * part : 0u;
-        return p;
-    }
-    p.convert_x = xtype == kGgmlF32;
-    if (p.convert_x) p.xt = kGgmlF16;
-    p.x16_off = 0;
-    p.img_off = p.convert_x ? align256((size_t)M * K * 2u) : 0u;
-    p.two_pass = M >= kW16MinTokens && p.img_off + w16_image_bytes(N, K, false) <= ws_limit;
-    p.ws = p.img_off + (p.two_pass ? w16_image_bytes(N, K, false) : 0u);
-    return p;
-}
+using plan::align256;
+using plan::GemmPlan;
+using plan::kW16MinTokens;
+using plan::plan_gemm;
+using plan::row_bytes_of;
 
 // Whether the fused SwiGLU kernel takes this launch: four features per
 // lane store (N % 4 == 0) and 32-bit buffer offsets for the 16-bit
@@ -1496,6 +1424,7 @@ hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uin
     if (wtype == kGgmlQ4K && M <= kGemvMaxTokens)
         return launch_gemv_q4k(w, xtype, x, y, N, K, M, row_offset, st);
     const GemmPlan pl = plan_gemm(wtype, xtype, N, K, M, num_cus, ws_limit);
+    if (pl.few) return launch_gemm_few(w, wtype, x, xtype, y, N, K, M, row_offset, st);
     if (pl.skinny) return launch_gemm_skinny(w, wtype, x, xtype, y, N, K, M, row_offset, pl.splits, ws, st);
     if (!pl.persistent) {
         if (wtype == kGgmlQ8_0)

@@ -11,8 +11,9 @@
 // w holds tokens 32 w .. 32 w + 31 x the 64 features in two 32x32x16 MFMA
 // accumulators.
 //  * 16-bit activations are read where they are (row-major); f32 ones are
-//    first rounded to fp16 (the reference's float16_t(v)) into the
-//    workspace, stage-major, [K / 64][M][64]: a stage's slab is one
+//    first rounded to the operand type (fp16 against Q8_0: the reference's
+//    float16_t(v); bf16 against Q4_K, whose reference keeps x in f32) into
+//    the workspace, stage-major, [K / 64][M][64]: a stage's slab is one
 //    contiguous M x 128-byte block;
 //  * everything goes HBM -> LDS by buffer_load ... lds (no loads into
 //    registers in the stage loop, so the compiler adds no waits of its own):
@@ -239,41 +240,44 @@ __global__ void __launch_bounds__(512, 1)
     }
 }
 
-// x [M, K] f32 (row-major) -> fp16 [K / 64][M][64] (round to nearest even);
-// 8 values per thread
+// x [M, K] f32 (row-major) -> OT (fp16 or bf16) [K / 64][M][64] (round to
+// nearest even); 8 values per thread
+template <uint32_t OT>
 __global__ void __launch_bounds__(256) skinny_pack_kernel(const float* __restrict__ x, u32x4* __restrict__ out,
                                                           uint32_t M, uint32_t K, uint32_t n8) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
     if (i >= n8) return;
     const uint32_t e = 8u * i, m = e / K, k = e % K;
     const f32x4 a = *(const f32x4*)(x + e), b = *(const f32x4*)(x + e + 4);
-    out[((k / 64u) * M + m) * 8u + (k % 64u) / 8u] =
-        u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w), pack_f16x2(b.x, b.y), pack_f16x2(b.z, b.w)};
+    auto pk = [](float u, float v) { return OT == kGgmlBF16 ? pack_bf16x2(u, v) : pack_f16x2(u, v); };
+    out[((k / 64u) * M + m) * 8u + (k % 64u) / 8u] = u32x4{pk(a.x, a.y), pk(a.z, a.w), pk(b.x, b.y), pk(b.z, b.w)};
 }
 
 }  // namespace
-
-size_t skinny_x_bytes(uint32_t xtype, uint32_t M, uint32_t K) {
-    return xtype == kGgmlF32 ? ((size_t)M * K * 2u + 255u) / 256u * 256u : 0u;
-}
 
 hipError_t launch_gemm_skinny(const void* w, uint32_t wtype, const void* x, uint32_t xtype, float* y, uint32_t N,
                               uint32_t K, uint32_t M, uint32_t row_offset, uint32_t splits, void* ws,
                               hipStream_t st) {
     // splits > 1: the reduction takes four floats per thread (N % 4 == 0)
     if (M == 0 || M > 256 || K % kBK || splits == 0 || (splits > 1 && N % 4u)) return hipErrorInvalidValue;
-    const uint32_t S = K / kBK, per = (S + splits - 1) / splits;
-    if ((S + per - 1) / per != splits) return hipErrorInvalidValue;  // every split non-empty
-    // f32 activations: rounded to fp16, stage-major, at the start of the
-    // workspace; 16-bit ones are read in place
+    const uint32_t S = K / kBK;
+    if (!plan::splits_nonempty(S, splits)) return hipErrorInvalidValue;  // every split owns a stage
+    const uint32_t per = (S + splits - 1) / splits;
+    // f32 activations: rounded to the operand type (fp16 against Q8_0, bf16
+    // against Q4_K), stage-major, at the start of the workspace; 16-bit ones
+    // are read in place
     const bool pack = xtype == kGgmlF32;
-    const uint32_t xt = xtype == kGgmlBF16 ? kGgmlBF16 : kGgmlF16;
+    const uint32_t xt = plan::operand_type(wtype, xtype);
     const void* const x16 = pack ? ws : x;
     float* const part = (float*)((uint8_t*)ws + skinny_x_bytes(xtype, M, K));
     if (pack) {
         const uint32_t n8 = M * K / 8u;
-        hipLaunchKernelGGL(skinny_pack_kernel, dim3((n8 + 255) / 256), dim3(256), 0, st, (const float*)x, (u32x4*)ws,
-                           M, K, n8);
+        if (xt == kGgmlBF16)
+            hipLaunchKernelGGL(skinny_pack_kernel<kGgmlBF16>, dim3((n8 + 255) / 256), dim3(256), 0, st,
+                               (const float*)x, (u32x4*)ws, M, K, n8);
+        else
+            hipLaunchKernelGGL(skinny_pack_kernel<kGgmlF16>, dim3((n8 + 255) / 256), dim3(256), 0, st,
+                               (const float*)x, (u32x4*)ws, M, K, n8);
         if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
     }
     const uint64_t mn = (uint64_t)M * N;

@@ -666,11 +666,6 @@ hipError_t launch_w16_epi(const PersistArgs& a, bool grouped, int num_cus, hipSt
 
 }  // namespace
 
-size_t w16_image_bytes(uint32_t N, uint32_t K, bool swiglu) {
-    const uint64_t panels = swiglu ? (N + 127u) / 128u : (N + 255u) / 256u;
-    return (size_t)(panels * (K / (uint32_t)kBK) * kBlk);
-}
-
 hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
                             uint32_t K, uint32_t row_offset, hipStream_t st, uint32_t item0) {
     const bool sw = w2 != nullptr;

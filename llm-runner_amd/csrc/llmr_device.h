@@ -77,6 +77,11 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)a, (__bf16)b});  // nearest even (v_cvt_pk_bf16_f32)
+}
+
 // Two bf16 halves of a dword -> their f16 roundings, packed.
 __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t w) {
     return pack_f16x2(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));

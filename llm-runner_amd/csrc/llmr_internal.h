@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "gemm_plan.h"
+
 namespace llmr {
 
 // Launchers return hipSuccess or the launch error; argument validation is
@@ -22,7 +24,7 @@ hipError_t launch_dequant_operand_f16(const void* w, uint32_t wtype, uint32_t n_
 // ws_limit the plan keeps within it where a smaller form exists (the
 // one-pass kernels instead of the image, fewer splits); pass the same limit
 // to both calls.
-constexpr size_t kNoWorkspaceLimit = ~(size_t)0;
+using plan::kNoWorkspaceLimit;
 size_t batch_matmul_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, uint32_t M,
                                     int num_cus, size_t ws_limit = kNoWorkspaceLimit);
 hipError_t launch_batch_matmul(const void* w, uint32_t wtype, const void* x, uint32_t xtype,
@@ -78,7 +80,7 @@ hipError_t launch_q8_lora_merge(void* base, const float* A, const float* B, uint
 
 // Q4_K weights times at most kGemvMaxTokens tokens (gemv_q.hip): an
 // HBM-bound weight stream, taken by launch_batch_matmul for such M.
-constexpr uint32_t kGemvMaxTokens = 4;
+using plan::kGemvMaxTokens;
 hipError_t launch_gemv_q4k(const void* w, uint32_t xtype, const void* x, float* y, uint32_t N, uint32_t K,
                            uint32_t M, uint32_t row_offset, hipStream_t st);
 
@@ -94,7 +96,7 @@ hipError_t launch_batch_matmul_swiglu(const void* wg, const void* wu, uint32_t w
 // [row_offset, row_offset + N) (w2 non-null: the SwiGLU arrangement of gate
 // w and up w2), operand type otype, into `img` (w16_image_bytes). The GEMM
 // launcher itself (launch_w16_gemm) is declared in gemm_q_common.h.
-size_t w16_image_bytes(uint32_t N, uint32_t K, bool swiglu);
+using plan::w16_image_bytes;
 // y = sum of the split partials part[0 .. splits) (each mn floats, mn % 4 ==
 // 0), added in split order.
 hipError_t launch_splitk_reduce(const float* part, float* y, uint64_t mn, uint32_t splits, hipStream_t st);
@@ -102,7 +104,11 @@ hipError_t launch_splitk_reduce(const float* part, float* y, uint64_t mn, uint32
 // bf16): all M tokens x 64 features per workgroup, K in `splits` non-empty
 // ranges. Workspace: f32 activations rounded to fp16 (skinny_x_bytes), then,
 // for splits > 1, the partials (splits * M * N floats) reduced into y.
-size_t skinny_x_bytes(uint32_t xtype, uint32_t M, uint32_t K);
+using plan::skinny_x_bytes;
+// The few-token GEMM with no K split (gemm_few.hip): M <= 256, K % 64 == 0,
+// f32 / f16 / bf16 activations read in place; no workspace.
+hipError_t launch_gemm_few(const void* w, uint32_t wtype, const void* x, uint32_t xtype, float* y, uint32_t N,
+                           uint32_t K, uint32_t M, uint32_t row_offset, hipStream_t st);
 hipError_t launch_gemm_skinny(const void* w, uint32_t wtype, const void* x, uint32_t xtype, float* y, uint32_t N,
                               uint32_t K, uint32_t M, uint32_t row_offset, uint32_t splits, void* ws,
                               hipStream_t st);

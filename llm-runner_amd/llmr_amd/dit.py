@@ -407,9 +407,15 @@ class _ImageChain:
         for w, im in zip(ws, self._views(0)):
             build_weight_image(g, w, N, K, 0, self.xtype, im)
 
-    def take(self):
-        """(images, next_images) for the next group's call."""
+    def take(self, jobs, N: int, K: int):
+        """(images, next_images) for the next group's call, whose jobs must be
+        that group's GEMMs (the same weights, in order, and shape): images are
+        matched to jobs by position, which the C-ABI cannot check."""
         k = self.k
+        ws, gN, gK = self.groups[k]
+        if (gN, gK) != (N, K) or [w.ptr() for w in ws] != [j.weight.ptr() for j in jobs]:
+            self.active = False
+            raise RuntimeError(f"weight-image chain out of step: group {k} holds other weights than this call's")
         nxt = None
         if k + 1 < len(self.groups):
             ws, N, K = self.groups[k + 1]
@@ -515,12 +521,17 @@ class FluxDiT:
         if self.ahead is not None:
             self.ahead.start(g)
         mi = 0
-        for w in self.doubles:
-            self._double(w, self._mod(mi, 6), self._mod(mi + 6, 6))
-            mi += 12
-        for w in self.singles:
-            self._single(w, self._mod(mi, 3))
-            mi += 3
+        try:
+            for w in self.doubles:
+                self._double(w, self._mod(mi, 6), self._mod(mi + 6, 6))
+                mi += 12
+            for w in self.singles:
+                self._single(w, self._mod(mi, 3))
+                mi += 3
+        finally:
+            # a failed forward leaves no chain half-taken for a later call
+            if self.ahead is not None:
+                self.ahead.active = False
         # 9: final LayerNorm + adaLN (shift, scale) on the image rows, projection, unpatchify
         fm = self._mod(mi, 2)
         glue.batch_layernorm(hid_i, self.xa[nt:], self.LN_EPS, mod_scale=fm[1], mod_shift=fm[0], g=g)
@@ -535,7 +546,7 @@ class FluxDiT:
         if self.ahead is None or not self.ahead.active:  # a block run outside forward(): no chain
             dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split)
             return
-        images, nxt = self.ahead.take()
+        images, nxt = self.ahead.take(jobs, N, K)
         dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split, images=images, next_images=nxt)
 
     def _attention(self, S: int, out: torch.Tensor) -> None:

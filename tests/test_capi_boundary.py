@@ -77,3 +77,18 @@ def test_header_compiles_as_c11_and_every_entry_point_links():
     out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
     n = len(listed)
     assert out.strip() == f"{n} of {n} entry points resolved"
+
+
+def test_gemm_planner_sweep():
+    """tests/c/plan_check.cpp runs the GEMM dispatcher's planner
+    (llm-runner_amd/csrc/gemm_plan.h, host-only) over a grid of shapes, CU
+    counts and workspace limits: every split launch gives each split at least
+    one K stage (the kernels load a split's first stage unconditionally; M
+    320 x N 640 x K 3072 on 256 CUs once had an empty eleventh split), every
+    plan stays within its workspace limit, and f32 activations are rounded to
+    fp16 against Q8_0 and to bf16 against Q4_K."""
+    import subprocess
+    exe = _c_harness("plan_check")
+    out = subprocess.run([exe], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert out.stdout.startswith("plan_check: ") and out.stdout.strip().endswith("plans ok")

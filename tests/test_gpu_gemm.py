@@ -50,8 +50,15 @@ CASES = [
     (12, 3, 1000, 768, 1, 4),        # small-M Q4_K kernel, f16, row_offset
     (12, 4, 130, 512, 30, 0),        # small-M Q4_K kernel at its largest M
     (12, 5, 72, 512, 30, 0),         # one token more: the tiled kernel again
-    # few tokens, N % 4 == 0: the skinny kernel (all tokens x 64 features per
-    # workgroup, K split across workgroups)
+    # few tokens with at least half the CUs' worth of 32 x 96 tiles: the
+    # few-token kernel (one launch, the waves of a workgroup split K)
+    (8, 250, 3001, 3264, 30, 5),     # ragged M, odd N, 51 stages (not a multiple of the 8 waves), bf16
+    (12, 256, 2048, 2560, 0, 256),   # Q4_K f32 (bf16 operands), row_offset
+    (8, 129, 4000, 1024, 1, 0),      # one token in the last token tile, f16
+    (12, 64, 12288, 512, 1, 0),      # Q4_K f16, two token tiles
+    (12, 256, 3072, 3072, 30, 0),    # Q4_K bf16 at the single-linear size
+    # few tokens over few features, N % 4 == 0: the skinny kernel (all tokens x
+    # 64 features per workgroup, K split across workgroups)
     (8, 200, 1000, 768, 30, 8),      # ragged M and N, bf16, row_offset
     (8, 33, 64, 4096, 0, 0),         # one feature tile: 16 K splits, f32
     (12, 250, 3072, 3072, 1, 0),     # Q4_K f16 at the single-linear size
@@ -368,6 +375,29 @@ def test_bf16_activations_beyond_fp16_range(orc, dev, M, N, K):
     assert np.all(np.isfinite(y))
     assert np.abs(xr).max() > 65504.0
     assert rel_l2(y[rows.astype(np.int64)], ref) <= TOL
+
+
+@pytest.mark.parametrize("M,N,K,path", [(2048, 4096, 256, "two-pass"), (1024, 8192, 256, "persistent"),
+                                        (256, 3072, 256, "few-token"), (100, 256, 512, "skinny"),
+                                        (300, 520, 512, "tiled"), (3, 1000, 512, "gemv")])
+def test_q4k_f32_activations_beyond_fp16_range(orc, dev, M, N, K, path):
+    """f32 activations of magnitude ~1e5 against Q4_K weights stay finite and
+    match the oracle on every kernel path: batch_matmul_q4k multiplies x in
+    f32 (llm.slang:2300-2304), so its results are finite there; the MFMA
+    paths round such x to bf16 (fp16 would overflow past 65504), the GEMV
+    keeps f32."""
+    from llmr_amd import gguf, synth
+    blk = gguf.quantize_q4k(synth.normal(26, 1, N * K, 0.02))
+    x = synth.normal(26, 2, M * K).reshape(M, K) * np.float32(1.0e5)
+    print(f"Q4_K f32 x ~1e5 {path}: M={M} N={N} K={K}", flush=True)
+    y, xr = _run(dev, blk, 12, x, 0, N)
+    rows = np.unique(np.array([0, 1, M // 2, M - 1], np.uint32))
+    ref = orc.batch_matmul(blk, 12, xr, N, K, M, 0, rows=rows)
+    assert np.abs(xr).max() > 65504.0
+    assert np.all(np.isfinite(y))
+    err = rel_l2(y[rows.astype(np.int64)], ref)
+    print(f"  rel_l2={err:.3e}")
+    assert err <= TOL
 
 
 # ---- llmr_batch_matmul_multi: grouped jobs and fused epilogues ----------------
@@ -712,11 +742,13 @@ def test_multi_next_images_built_by_idle_workgroups(dev, wtype, xtype, Ms, N, K,
     assert torch.equal(y_a, y_b)
 
 
-@pytest.mark.parametrize("wtype,M,N,K,xtype", [(8, 256, 3072, 3072, 0), (12, 300, 520, 1024, 30), (8, 96, 4096, 4096, 1)])
+@pytest.mark.parametrize("wtype,M,N,K,xtype", [(8, 256, 3072, 3072, 0), (12, 300, 520, 1024, 30), (8, 96, 4096, 4096, 1),
+                                               (8, 64, 1024, 4096, 0), (12, 320, 640, 3072, 0)])
 def test_split_k_matches_oracle_and_repeats(orc, dev, wtype, M, N, K, xtype):
-    """Launches with few tiles split K over several workgroup rows and sum the
-    partials in split order: within the GEMM bar of the oracle, and the same
-    bits on every call."""
+    """Launches with few tiles split K over several workgroup rows (or, on the
+    few-token kernel, over the waves of a workgroup) and sum the partials in
+    split order: within the GEMM bar of the oracle, and the same bits on every
+    call. 320 x 640 x 3072 once planned an eleventh split with no K stage."""
     import torch
     from llmr_amd import gguf, synth
     blk = gguf.quantize(synth.normal(97, 2, N * K, 0.02), wtype)

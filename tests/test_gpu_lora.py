@@ -176,7 +176,7 @@ def _merged_rows(orc, blk, xs16, A, B, scale, rows_s, N, K, row_off, w_off, b_ro
 @pytest.mark.parametrize("M,N,K,rank,b_rows,row_off,w_off,xtype", [
     (2304, 4096, 512, 16, 1024, 512, 64, 30),    # bf16, a slot of the output
     (2400, 4100, 768, 48, 0, 0, 0, 1),           # f16, whole output, ragged M and N
-    (2048, 4096, 512, 64, 2000, 100, 7, 0),      # f32 input (converted to f16 first), the largest merged rank
+    (2048, 4096, 512, 64, 2000, 100, 7, 0),      # f32 input (rounded to bf16 first: Q4_K), the largest merged rank
 ])
 def test_batch_matmul_lora_fused(orc, dev, M, N, K, rank, b_rows, row_off, w_off, xtype):
     import torch
@@ -213,12 +213,14 @@ def test_batch_matmul_lora_fused(orc, dev, M, N, K, rank, b_rows, row_off, w_off
     err = rel_l2(f[:, slot], e[:, slot])
     rows_s = np.array([0, 1, M // 2, M - 1], np.int64)
     xs = xt.float().cpu().numpy()
-    xs16 = xs.astype(np.float16).astype(np.float32) if xtype == 0 else xs
-    model = _merged_rows(orc, blk, xs16, A, B, 0.7, rows_s, N, K, row_off, w_off, rows, 30 if xtype == 30 else 1)
+    # f32 activations against Q4_K weights become bf16 operands (as bf16 ones)
+    bf = xtype in (0, 30)
+    xs16 = torch.from_numpy(xs).bfloat16().float().numpy() if xtype == 0 else xs
+    model = _merged_rows(orc, blk, xs16, A, B, 0.7, rows_s, N, K, row_off, w_off, rows, 30 if bf else 1)
     err_model = rel_l2(f[rows_s], model)
     print(f"M={M} N={N} K={K} rank={rank}: vs merged-image model {err_model:.2e}, vs GEMM + correction {err:.2e}")
     assert err_model <= 2e-5
-    assert err <= (5e-3 if xtype == 30 else 1e-3)
+    assert err <= (5e-3 if bf else 1e-3)
     ref = orc.batch_matmul(blk, gguf.GGML_Q4_K, xs, N, K, M, 0, rows=rows_s.astype(np.uint32))
     s_ref = orc.lora_down(A, xs[rows_s])
     ref = orc.lora_up(B, s_ref, ref, 0.7, row_offset=row_off, weight_row_offset=w_off, b_rows=rows)
