@@ -36,24 +36,33 @@ def _mm(W, wtype, X, N, row_offset=0):
     return orc.batch_matmul(W, wtype, X, N, X.shape[1], X.shape[0], row_offset)
 
 
-def zimage_layer(w: dict, hidden: np.ndarray, n_heads: int, cos_t, sin_t, eps: float = 1e-5) -> np.ndarray:
+def zimage_layer(w: dict, hidden: np.ndarray, n_heads: int, cos_t, sin_t, eps: float = 1e-5,
+                 rows=None) -> np.ndarray:
     """w: numpy copies of llmr_amd.dit.ZImageLayerWeights fields (raw Q8_0
-    blocks, f32 vectors). Returns the updated hidden (f32 [S, dim])."""
+    blocks, f32 vectors). Returns the updated hidden (f32 [S, dim]); with
+    `rows` only those rows' updates are computed (K and V of every row, the
+    rest of the layer on the rows) and returned as [len(rows), dim]."""
     S, dim = hidden.shape
     ffn = w["w_gate"].size // (dim // 32 * 34)  # Q8_0 rows of dim/32 34-byte blocks
     h = np.array(hidden, np.float32, copy=True)
     scale_msa, gate_msa, scale_mlp, gate_mlp = (w["adaln"][i] for i in range(4))
     a = orc.modulate(orc.batch_rmsnorm(h, w["attn_norm1"], eps), scale_msa)
-    q = _mm(w["wqkv"], GGML_Q8_0, a, dim, 0)
     k = _mm(w["wqkv"], GGML_Q8_0, a, dim, dim)
     v = _mm(w["wqkv"], GGML_Q8_0, a, dim, 2 * dim)
+    if rows is None:
+        q = _mm(w["wqkv"], GGML_Q8_0, a, dim, 0)
+    else:
+        rows = np.asarray(rows)
+        q = np.zeros((S, dim), np.float32)
+        q[rows] = _mm_rows(w["wqkv"], GGML_Q8_0, a, dim, 0, rows)
+        h = h[rows]
     q = orc.batch_head_norm(q, w["q_norm"], n_heads, eps)
     k = orc.batch_head_norm(k, w["k_norm"], n_heads, eps)
-    o = _attention_rows(q, k, v, n_heads, cos_t, sin_t, None)
+    o = _attention_rows(q, k, v, n_heads, cos_t, sin_t, rows)
     t = _mm(w["wo"], GGML_Q8_0, o, dim)
     h = orc.gated_residual(h, gate_msa, orc.batch_rmsnorm(t, w["attn_norm2"], eps), True)
     a = orc.modulate(orc.batch_rmsnorm(h, w["ffn_norm1"], eps), scale_mlp)
-    f = orc.batch_matmul_swiglu_q8(w["w_gate"], w["w_up"], a, ffn, dim, S)
+    f = orc.batch_matmul_swiglu_q8(w["w_gate"], w["w_up"], a, ffn, dim, h.shape[0])
     t = _mm(w["w_down"], GGML_Q8_0, f, dim)
     return orc.gated_residual(h, gate_mlp, orc.batch_rmsnorm(t, w["ffn_norm2"], eps), True)
 

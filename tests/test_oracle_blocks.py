@@ -426,3 +426,14 @@ def test_flux_blocks_sampled_rows_match_full(orc, flux_case):
     full = blocks.flux_single_block(singles[0], h, ms, cfg.n_heads, cos_t, sin_t)
     part = blocks.flux_single_block(singles[0], h, ms, cfg.n_heads, cos_t, sin_t, rows=rows)
     np.testing.assert_array_equal(part, full[rows])
+
+
+def test_zimage_layer_sampled_rows_match_full(orc, zimage_case):
+    """The sampled-row form of the Z-Image layer (used at full size against
+    the GPU) gives the full layer's rows bit for bit."""
+    from oracle import blocks
+    w, h, H, cos_t, sin_t = zimage_case[:5]
+    full = blocks.zimage_layer(w, h, H, cos_t, sin_t)
+    rows = np.array([0, 3, 17, h.shape[0] // 2, h.shape[0] - 1])
+    part = blocks.zimage_layer(w, h, H, cos_t, sin_t, rows=rows)
+    np.testing.assert_array_equal(part, full[rows])
