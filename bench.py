@@ -265,13 +265,18 @@ def setup_zimage_block(dev):
     return step, flops, None, cfg, "bf16"
 
 
-def setup_flux_step(dev):
+def setup_flux_step(dev, mlp_act: str = "gelu"):
     """One denoising forward of the Flux-dev-shaped DiT (19 double + 38 single
     blocks, hidden 3072, 24 heads, MLP 12288, Q4_K weights generated on the
-    device, 4096 image tokens from 16x128x128 latents + 512 text tokens)."""
+    device, 4096 image tokens from 16x128x128 latents + 512 text tokens).
+    mlp_act "swiglu": the reference's own Flux.2 MLP form (linear1 [3 d +
+    2 m, d], MLP in-projections [2 m, d], silu(gate) * up in the GEMMs'
+    epilogue)."""
+    import dataclasses
+
     import torch
     from llmr_amd import dit, synth, workloads
-    cfg_m = dit.FLUX_DEV
+    cfg_m = dataclasses.replace(dit.FLUX_DEV, mlp_act=mlp_act)
     glob, doubles, singles = dit.flux_weights(cfg_m, device=dev)
     model = dit.FluxDiT(cfg_m, glob, doubles, singles, act_dtype=torch.bfloat16, device=dev)
     lat = torch.from_numpy(synth.normal(workloads.SEED, 30, cfg_m.latent_ch * cfg_m.latent_h * cfg_m.latent_w)
@@ -282,14 +287,16 @@ def setup_flux_step(dev):
     def step():
         model.forward(lat, txt, 0.5)
 
-    cfg = {"workload": "flux_step", "double_blocks": cfg_m.n_double, "single_blocks": cfg_m.n_single,
-           "hidden": cfg_m.dim, "heads": cfg_m.n_heads, "mlp": cfg_m.mlp, "img_tokens": cfg_m.n_img,
-           "txt_tokens": cfg_m.n_txt, "weights": "Q4_K (img_in Q8_0)", "activations": "bf16",
-           "timestep": 0.5, "mlp_act": "gelu-tanh", "modulation": "per block"}
+    cfg = {"workload": "flux_step" if mlp_act == "gelu" else "flux2_step", "double_blocks": cfg_m.n_double,
+           "single_blocks": cfg_m.n_single, "hidden": cfg_m.dim, "heads": cfg_m.n_heads, "mlp": cfg_m.mlp,
+           "img_tokens": cfg_m.n_img, "txt_tokens": cfg_m.n_txt, "weights": "Q4_K (img_in Q8_0)",
+           "activations": "bf16", "timestep": 0.5,
+           "mlp_act": "gelu-tanh" if mlp_act == "gelu" else "swiglu (silu(gate) * up)", "modulation": "per block"}
     return step, cfg_m.gemm_flops(), None, cfg, "bf16"
 
 
-MODEL_SETUPS = {"zimage_block": setup_zimage_block, "flux_step": setup_flux_step}
+MODEL_SETUPS = {"zimage_block": setup_zimage_block, "flux_step": setup_flux_step,
+                "flux2_step": lambda dev: setup_flux_step(dev, "swiglu")}
 
 
 def gemm_kernel_name(name: str, num_cus: int) -> str:
@@ -423,7 +430,8 @@ def main():
     ap.add_argument("--workload", default="flux_attention")
     ap.add_argument("--components",
                     default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu,flux_linear1_f32,"
-                            "flux_linear2_f32,flux_attention_f32,lora_flux_linear1,flux_linear1_lora,zimage_block,flux_step")
+                            "flux_linear2_f32,flux_attention_f32,lora_flux_linear1,flux_linear1_lora,zimage_block,flux_step,"
+                            "flux2_step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--hbm-copy-calibration", action="store_true",
                     help="time a plain 1 GiB device copy (reference for the FETCH_SIZE/WRITE_SIZE counters)")

@@ -206,7 +206,7 @@ typedef struct llmr_matmul_job {
     uint32_t row_offset;
 } llmr_matmul_job;
 
-enum { LLMR_EPI_STORE = 0, LLMR_EPI_GATED_RESIDUAL = 1, LLMR_EPI_SPLIT_GELU = 2 };
+enum { LLMR_EPI_STORE = 0, LLMR_EPI_GATED_RESIDUAL = 1, LLMR_EPI_SPLIT_GELU = 2, LLMR_EPI_SPLIT_SWIGLU = 3 };
 
 /* How the f32 result r[m, n] of a job reaches memory:
  *   STORE            output[m*ldy + n] = r
@@ -214,9 +214,15 @@ enum { LLMR_EPI_STORE = 0, LLMR_EPI_GATED_RESIDUAL = 1, LLMR_EPI_SPLIT_GELU = 2 
  *   SPLIT_GELU       n <  split: output[m*ldy + n] = r
  *                    n >= split: output2[m*ldy2 + n - split] = gelu_tanh(r)
  *                    rounded to output2_type (split % 8 == 0)
- * ldy 0 means out_dim (SPLIT_GELU: split); ldy2 0 means out_dim - split.
- * Strides are multiples of 4; out_dim % 4 == 0 unless the epilogue is a
- * STORE with ldy == out_dim. */
+ *   SPLIT_SWIGLU     out_dim = split + 2 f: weight rows [split, split + f)
+ *                    are a SwiGLU gate, [split + f, split + 2 f) its up:
+ *                    n < split: output[m*ldy + n] = r;
+ *                    o < f: output2[m*ldy2 + o] = silu(r[split + o]) *
+ *                    r[split + f + o] rounded to output2_type
+ *                    (split % 256 == 0, f % 8 == 0; not with weight images)
+ * ldy 0 means out_dim (SPLIT_*: split); ldy2 0 means out_dim - split
+ * (SPLIT_SWIGLU: f). Strides are multiples of 4; out_dim % 4 == 0 unless the
+ * epilogue is a STORE with ldy == out_dim. */
 typedef struct llmr_matmul_epilogue {
     uint32_t kind;
     uint32_t ldy;
@@ -236,7 +242,11 @@ typedef struct llmr_matmul_epilogue {
  *   - gated_residual_linear after a projection (flux_dit.c3:891-898, 1064-1068);
  *   - the single block's linear1 slots plus silu/gelu and concat_rows_copy
  *     (flux_dit.c3:1005-1018, 1049-1058): Q | K | V to `output`, the
- *     activated MLP half straight into linear2's input;
+ *     activated MLP half straight into linear2's input (SPLIT_SWIGLU: the
+ *     reference's Flux.2 block, silu(gate) * up of linear1's last 2 f rows,
+ *     flux_dit.c3:1013-1018, 1049-1055; SPLIT_GELU: the Flux.1 form);
+ *   - a double block's MLP in-projection and its SwiGLU (SPLIT_SWIGLU with
+ *     split 0: flux_dit.c3:917-931, 945-955), both streams in one launch;
  *   - the modulation projections of one step (the reference makes three
  *     shared ones, flux_dit.c3:1131-1140; a Flux.1-dev model has one per block):
  *     Q4_K jobs of at most 4 tokens with LLMR_EPI_STORE run as one launch

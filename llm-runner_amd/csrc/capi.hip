@@ -491,13 +491,21 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
     if (!jobs) return fail(LLMR_ERR_INVALID_ARG, "null jobs");
     if (n_jobs > 64) return fail(LLMR_ERR_INVALID_ARG, "at most 64 jobs per call (got %u)", n_jobs);
     llmr_matmul_epilogue e = epilogue ? *epilogue : llmr_matmul_epilogue{LLMR_EPI_STORE, 0, 0, 0, 0};
-    if (e.kind > LLMR_EPI_SPLIT_GELU) return fail(LLMR_ERR_INVALID_ARG, "unknown epilogue kind %u", e.kind);
-    const bool split = e.kind == LLMR_EPI_SPLIT_GELU;
+    if (e.kind > LLMR_EPI_SPLIT_SWIGLU) return fail(LLMR_ERR_INVALID_ARG, "unknown epilogue kind %u", e.kind);
+    const bool swiglu = e.kind == LLMR_EPI_SPLIT_SWIGLU;
+    const bool split = e.kind == LLMR_EPI_SPLIT_GELU || swiglu;
     if (!split) e.split = out_dim;
     if (split && (e.split > out_dim || e.split % 8))
         return fail(LLMR_ERR_INVALID_ARG, "split must be a multiple of 8 and <= out_dim (got %u)", e.split);
+    // SPLIT_SWIGLU: out_dim = split + 2 f, whole 256-row panels below split
+    const uint32_t f2 = out_dim - e.split, n2 = swiglu ? f2 / 2u : f2;  // output2 columns
+    if (swiglu && (e.split % 256 || f2 % 16 || f2 == 0))
+        return fail(LLMR_ERR_INVALID_ARG, "SPLIT_SWIGLU needs split %% 256 == 0 and out_dim - split = 2 f, "
+                    "f %% 8 == 0, f > 0 (got split %u, out_dim %u)", e.split, out_dim);
+    if (swiglu && (images || next))
+        return fail(LLMR_ERR_INVALID_ARG, "SPLIT_SWIGLU takes no weight images");
     if (e.ldy == 0) e.ldy = split ? e.split : out_dim;
-    if (e.ldy2 == 0) e.ldy2 = out_dim - e.split;
+    if (e.ldy2 == 0) e.ldy2 = n2;
     const uint32_t width = split ? e.split : out_dim;
     const bool plain = e.kind == LLMR_EPI_STORE && e.ldy == out_dim;
     if (!plain && out_dim % 4) return fail(LLMR_ERR_INVALID_ARG, "this epilogue needs out_dim %% 4 == 0");
@@ -506,8 +514,8 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
     if (e.kind == LLMR_EPI_GATED_RESIDUAL && out_dim > llmr::kRowNormMaxDim)
         return fail(LLMR_ERR_INVALID_ARG, "GATED_RESIDUAL needs out_dim <= %u", llmr::kRowNormMaxDim);
     const bool has2 = split && e.split < out_dim;
-    if (has2 && (e.ldy2 % 4 || e.ldy2 < out_dim - e.split))
-        return fail(LLMR_ERR_INVALID_ARG, "ldy2 must be a multiple of 4 and >= out_dim - split");
+    if (has2 && (e.ldy2 % 4 || e.ldy2 < n2))
+        return fail(LLMR_ERR_INVALID_ARG, "ldy2 must be a multiple of 4 and >= %u", n2);
     if (has2 && e.output2_type != LLMR_GGML_BF16 && e.output2_type != LLMR_GGML_F16)
         return fail(LLMR_ERR_UNSUPPORTED, "output2_type must be BF16 or F16 (got %u)", e.output2_type);
     if ((uint64_t)e.ldy > 0xffffffffull / 4) return fail(LLMR_ERR_INVALID_ARG, "ldy too large");
@@ -515,7 +523,7 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
     for (uint32_t i = 0; i < n_jobs; i++) {
         const llmr_matmul_job& j = jobs[i];
         if (int r = check_weight(j.weight, wtype, in_dim)) return r;
-        if (j.seq_len && (!j.input || !j.output))
+        if (j.seq_len && (!j.input || (!j.output && !(swiglu && e.split == 0))))
             return fail(LLMR_ERR_INVALID_ARG, "job %u: null input/output pointer", i);
         if (!aligned(j.input, 16) || !aligned(j.output, 16))
             return fail(LLMR_ERR_INVALID_ARG, "job %u: input/output pointers must be 16-byte aligned", i);

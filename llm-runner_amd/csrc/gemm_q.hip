@@ -1496,6 +1496,37 @@ bool multi_two_pass(const GemmJob* jobs, uint32_t n) {
     return m >= kW16MinTokens;
 }
 
+// Split-SwiGLU jobs (kEpiSplitSwiglu): N = split + 2 f weight rows, f gate
+// rows after the plain ones, then f up rows. Their two-pass image is the
+// plain image of the first split rows followed by the SwiGLU-arranged image
+// of the gate and up rows (128 outputs per 256-row panel).
+uint32_t swiglu_outputs(const GemmEpilogue& epi, uint32_t N) { return (N - epi.split) / 2u; }
+size_t multi_image_bytes(const GemmEpilogue& epi, uint32_t N, uint32_t K) {
+    if (epi.kind == kEpiSplitSwiglu)
+        return w16_image_bytes(epi.split, K, false) + w16_image_bytes(swiglu_outputs(epi, N), K, true);
+    return w16_image_bytes(N, K, false);
+}
+hipError_t build_split_swiglu_image(const GemmJob& j, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
+                                    uint32_t K, uint32_t split, hipStream_t st) {
+    const uint64_t rb = row_bytes_of(wtype, K);
+    const uint8_t* const w = (const uint8_t*)j.w + (uint64_t)j.row_offset * rb;
+    const uint32_t f = (N - split) / 2u;
+    if (split > 0)
+        if (hipError_t e = launch_w16_image(w, nullptr, wtype, otype, img, split, K, 0u, st); e != hipSuccess)
+            return e;
+    return launch_w16_image(w + (uint64_t)split * rb, w + (uint64_t)(split + f) * rb, wtype, otype,
+                            (uint8_t*)img + w16_image_bytes(split, K, false), f, K, 0u, st);
+}
+
+// Whether jobs [j0, j0 + n) run fused in one launch: the persistent
+// kernels take them (split-SwiGLU: the two-pass one only, the one-pass
+// kernels have no such epilogue).
+bool multi_fused(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n,
+                 const GemmEpilogue& epi, int num_cus) {
+    if (!multi_persistent(wtype, xtype, N, K, jobs, n, num_cus)) return false;
+    return epi.kind != kEpiSplitSwiglu || multi_two_pass(jobs, n);
+}
+
 PersistArgs multi_args(uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n, const GemmEpilogue& epi) {
     PersistArgs a{};
     const uint32_t tiles_n = (N + 255) / 256;
@@ -1513,8 +1544,10 @@ PersistArgs multi_args(uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n, 
     a.epi = epi.kind;
     a.ldy = epi.ldy;
     a.ldy2 = epi.ldy2;
-    a.split = epi.kind == kEpiSplitGelu ? epi.split : N;
+    a.split = epi.kind == kEpiSplitGelu || epi.kind == kEpiSplitSwiglu ? epi.split : N;
     a.y2_bf16 = epi.y2_type == kGgmlBF16 ? 1u : 0u;
+    if (epi.kind == kEpiSplitSwiglu)  // the plain panels, then the SwiGLU ones
+        a.tiles_n = epi.split / 256u + (swiglu_outputs(epi, N) + 127u) / 128u;
     return a;
 }
 
@@ -1548,6 +1581,15 @@ hipError_t run_job_fallback(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t
         const ResidualArgs r{j.y, t, nullptr, j.gate, epi.ldy, N, j.M, N, 0.0f};
         return launch_residual(r, false, st);
     }
+    if (epi.kind == kEpiSplitSwiglu) {  // columns [0, split) copied, then silu(gate) * up
+        const uint32_t f = swiglu_outputs(epi, N);
+        if (epi.split > 0) {
+            const ActColsArgs c{t, j.y, N, 0u, 0u, epi.ldy, 0u, j.M, epi.split};
+            if ((e = launch_act_cols(c, kActCopy, kGgmlF32, st)) != hipSuccess) return e;
+        }
+        const ActColsArgs c{t, j.y2, N, epi.split, epi.split + f, epi.ldy2, 0u, j.M, f};
+        return launch_act_cols(c, kActSiluMul, epi.y2_type, st);
+    }
     const uint32_t split = epi.kind == kEpiSplitGelu ? epi.split : N;
     if (split > 0) {
         const ActColsArgs c{t, j.y, N, 0u, 0u, epi.ldy, 0u, j.M, split};
@@ -1567,7 +1609,7 @@ size_t fallback_t_bytes(uint32_t N, const GemmJob* jobs, uint32_t n_jobs, const 
     size_t t = 0;
     for (uint32_t i = 0; i < n_jobs; i += 2) {
         const uint32_t n = min(2u, n_jobs - i);
-        if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) continue;
+        if (multi_fused(wtype, xtype, N, K, jobs + i, n, epi, num_cus)) continue;
         if (epi.kind == kEpiStore && epi.ldy == N) continue;
         for (uint32_t q = i; q < i + n; q++) t = max(t, align256((size_t)jobs[q].M * N * sizeof(float)));
     }
@@ -1583,8 +1625,8 @@ size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32
     size_t need = 0;
     for (uint32_t i = 0; i < n_jobs; i += 2) {
         const uint32_t n = min(2u, n_jobs - i);
-        if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) {
-            if (multi_two_pass(jobs + i, n) && !prebuilt_images) need = max(need, n * w16_image_bytes(N, K, false));
+        if (multi_fused(wtype, xtype, N, K, jobs + i, n, epi, num_cus)) {
+            if (multi_two_pass(jobs + i, n) && !prebuilt_images) need = max(need, n * multi_image_bytes(epi, N, K));
             continue;
         }
         for (uint32_t q = i; q < i + n; q++)
@@ -1630,18 +1672,20 @@ hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N,
     for (uint32_t i = 0; i < n_jobs; i += 2) {
         const uint32_t n = min(2u, n_jobs - i);
         hipError_t e = hipSuccess;
-        if (multi_persistent(wtype, xtype, N, K, jobs + i, n, num_cus)) {
+        if (multi_fused(wtype, xtype, N, K, jobs + i, n, epi, num_cus)) {
             PersistArgs a = multi_args(N, K, jobs + i, n, epi);
             if (multi_two_pass(jobs + i, n)) {
-                const size_t img_bytes = w16_image_bytes(N, K, false);
+                const size_t img_bytes = multi_image_bytes(epi, N, K);
                 for (uint32_t q = 0; q < n && e == hipSuccess; q++) {
                     if (images) {  // built ahead by the caller (launch_w16_image, same arguments)
                         a.p[q].W = (const uint8_t*)images[i + q];
                         continue;
                     }
                     void* img = (uint8_t*)ws + q * img_bytes;
-                    e = launch_w16_image(jobs[i + q].w, nullptr, wtype, xtype, img, N, K, jobs[i + q].row_offset,
-                                         st);
+                    e = epi.kind == kEpiSplitSwiglu
+                            ? build_split_swiglu_image(jobs[i + q], wtype, xtype, img, N, K, epi.split, st)
+                            : launch_w16_image(jobs[i + q].w, nullptr, wtype, xtype, img, N, K,
+                                               jobs[i + q].row_offset, st);
                     a.p[q].W = (const uint8_t*)img;
                 }
                 const uint64_t tiles = (uint64_t)a.tiles_m * a.tiles_n;

@@ -329,8 +329,13 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 //   kEpiResidual   Y[m, n] += gate[n] * acc  (gate 1 when null)
 //   kEpiSplitGelu  n < split: Y[m, n] = acc; n >= split: Y2[m, n - split] =
 //                  16-bit gelu(acc)   (split % 8 == 0)
+//   kEpiSplitSwiglu  tiles below split (split % 256 == 0): Y[m, n] = acc;
+//                  the tiles past it are SwiGLU tiles of the weight image
+//                  (256 rows: gate and up rows of 128 outputs, the
+//                  arrangement of the SwiGLU kernel): Y2[m, o] = 16-bit
+//                  silu(gate) * up, o < (N - split) / 2 (two-pass kernel)
 // with row strides ldy (Y) and ldy2 (Y2).
-constexpr uint32_t kEpiStore = 0, kEpiResidual = 1, kEpiSplitGelu = 2;
+constexpr uint32_t kEpiStore = 0, kEpiResidual = 1, kEpiSplitGelu = 2, kEpiSplitSwiglu = 3;
 
 template <typename T>
 __device__ __forceinline__ T pick(uint32_t p, T a, T b) {
@@ -388,6 +393,38 @@ __device__ __forceinline__ void store_tile_256(f32x16 (&acc)[4][4], float* Y, co
                 acc[a][b] = f32x16{};
             }
     };
+    if constexpr (EPI == kEpiSplitSwiglu) {
+        if (n0 < split) {  // a plain tile (a uniform test: split % 256 == 0)
+            each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
+                *(f32x4*)(Y + (uint64_t)m * ldy + n) = v;
+            });
+            return;
+        }
+        // a SwiGLU tile: wave wn's 128 weight rows are gate rows 64 wn .. + 63
+        // of the tile's 128 outputs (acc[0..1]) and the same outputs' up rows
+        // (acc[2..3])
+        uint16_t* const Y2 = (uint16_t*)Y2v;
+        const uint32_t n_sw = (N - split) / 2u, o0 = (n0 - split) / 2u;
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint32_t m = m0 + wm * 128u + b * 32u + l32;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const uint32_t o = o0 + wn * 64u + a * 32u + 8u * g + 4u * kh;
+                    f32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = silu(acc[a][b][4 * g + e]) * acc[a + 2][b][4 * g + e];
+                    const u32x2 pk = y2_bf16 ? u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)}
+                                             : u32x2{pack_f16x2(v.x, v.y), pack_f16x2(v.z, v.w)};
+                    if (m < M && o < n_sw) *(u32x2*)(Y2 + (uint64_t)m * ldy2 + o) = pk;
+                }
+                acc[a][b] = f32x16{};
+                acc[a + 2][b] = f32x16{};
+            }
+        return;
+    }
     if constexpr (EPI == kEpiResidual) {
         each([&](uint32_t m, uint32_t n, uint32_t, f32x4 v) __attribute__((always_inline)) {
             f32x4* const h = (f32x4*)(Y + (uint64_t)m * ldy + n);

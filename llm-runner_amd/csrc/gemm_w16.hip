@@ -658,6 +658,9 @@ hipError_t launch_w16_epi(const PersistArgs& a, bool grouped, int num_cus, hipSt
         case kEpiSplitGelu:
             return grouped ? launch_w16<XT, false, kEpiSplitGelu, true>(a, num_cus, st)
                            : launch_w16<XT, false, kEpiSplitGelu, false>(a, num_cus, st);
+        case kEpiSplitSwiglu:
+            return grouped ? launch_w16<XT, false, kEpiSplitSwiglu, true>(a, num_cus, st)
+                           : launch_w16<XT, false, kEpiSplitSwiglu, false>(a, num_cus, st);
         default:
             return grouped ? launch_w16<XT, false, kEpiStore, true>(a, num_cus, st)
                            : launch_w16<XT, false, kEpiStore, false>(a, num_cus, st);
@@ -678,7 +681,9 @@ hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint3
         return sw ? build_image<kGgmlQ8_0, kGgmlF16, true>(w, w2, img, N, K, row_offset, st)
                   : build_image<kGgmlQ8_0, kGgmlF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
     }
-    if (sw) return hipErrorInvalidValue;  // the SwiGLU takes Q8_0 weights
+    if (sw)
+        return otype == kGgmlBF16 ? build_image<kGgmlQ4K, kGgmlBF16, true>(w, w2, img, N, K, row_offset, st)
+                                  : build_image<kGgmlQ4K, kGgmlF16, true>(w, w2, img, N, K, row_offset, st);
     if (otype == kGgmlBF16)
         return build_image<kGgmlQ4K, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
     return build_image<kGgmlQ4K, kGgmlF16, false>(w, w2, img, N, K, row_offset, st, no, item0);

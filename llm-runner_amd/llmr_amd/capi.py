@@ -61,7 +61,7 @@ class NextWeightImages(ctypes.Structure):
                 ("image", ctypes.c_void_p * 2), ("image_bytes", ctypes.c_size_t)]
 
 
-EPI_STORE, EPI_GATED_RESIDUAL, EPI_SPLIT_GELU = 0, 1, 2
+EPI_STORE, EPI_GATED_RESIDUAL, EPI_SPLIT_GELU, EPI_SPLIT_SWIGLU = 0, 1, 2, 3
 
 
 class GgufTensorInfo(ctypes.Structure):

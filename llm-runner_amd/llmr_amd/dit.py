@@ -173,6 +173,15 @@ class FluxConfig:
     t_emb_dim: int = 256
     axes: tuple = (16, 56, 56)
     theta: float = 10000.0
+    # "gelu": the Flux.1-dev MLP (in-projection [mlp, dim], GELU); "swiglu":
+    # the reference's own Flux.2 MLP (in-projection [2 mlp, dim]: gate rows,
+    # then up rows; silu(gate) * up, flux_dit.c3:917-931, 1013-1018, 1049-1055)
+    mlp_act: str = "gelu"
+
+    @property
+    def mlp_in(self) -> int:
+        """Rows of a block's MLP in-projection (and of linear1 past 3 dim)."""
+        return 2 * self.mlp if self.mlp_act == "swiglu" else self.mlp
 
     @property
     def patch_dim(self) -> int:
@@ -189,10 +198,10 @@ class FluxConfig:
     def gemm_flops(self) -> float:
         """2MNK over every token-wise GEMM plus 4*H*S^2*D per attention (the
         modulation and timestep projections, M = 1, are not counted)."""
-        d, m, ni, nt, S = self.dim, self.mlp, self.n_img, self.n_txt, self.seq
-        per_stream = 3 * d * d + d * d + 2 * d * m
+        d, m, mi, ni, nt, S = self.dim, self.mlp, self.mlp_in, self.n_img, self.n_txt, self.seq
+        per_stream = 3 * d * d + d * d + mi * d + d * m
         double = 2.0 * (ni + nt) * per_stream + 4.0 * self.n_heads * S * S * HEAD_DIM
-        single = 2.0 * S * ((3 * d + m) * d + d * (d + m)) + 4.0 * self.n_heads * S * S * HEAD_DIM
+        single = 2.0 * S * ((3 * d + mi) * d + d * (d + m)) + 4.0 * self.n_heads * S * S * HEAD_DIM
         io = 2.0 * ni * self.patch_dim * d + 2.0 * nt * self.text_dim * d + 2.0 * ni * d * self.patch_dim
         return self.n_double * double + self.n_single * single + io
 
@@ -208,7 +217,7 @@ class FluxDoubleWeights:
     txt_qkv: torch.Tensor
     img_proj: torch.Tensor  # Q4_K [dim, dim]
     txt_proj: torch.Tensor
-    img_mlp0: torch.Tensor  # Q4_K [mlp, dim]
+    img_mlp0: torch.Tensor  # Q4_K [mlp, dim] (swiglu: [2 mlp, dim], gate rows then up rows)
     txt_mlp0: torch.Tensor
     img_mlp2: torch.Tensor  # Q4_K [dim, mlp]
     txt_mlp2: torch.Tensor
@@ -221,7 +230,7 @@ class FluxDoubleWeights:
 @dataclasses.dataclass
 class FluxSingleWeights:
     mod: torch.Tensor       # Q4_K [3*dim, dim]
-    linear1: torch.Tensor   # Q4_K [3*dim + mlp, dim]
+    linear1: torch.Tensor   # Q4_K [3*dim + mlp, dim] (swiglu: [3*dim + 2 mlp, dim])
     linear2: torch.Tensor   # Q4_K [dim, dim + mlp]
     q_norm: torch.Tensor
     k_norm: torch.Tensor
@@ -254,10 +263,11 @@ def flux_weights(cfg: FluxConfig, device="cuda", seed: int = workloads.SEED, g: 
         counter[0] += 1
         return torch.from_numpy(1.0 + synth.normal(seed, counter[0], HEAD_DIM, 0.1)).to(device)
 
+    mi = cfg.mlp_in
     doubles = [FluxDoubleWeights(q4(6 * d, d), q4(6 * d, d), q4(3 * d, d), q4(3 * d, d), q4(d, d), q4(d, d),
-                                 q4(m, d), q4(m, d), q4(d, m), q4(d, m), norm(), norm(), norm(), norm())
+                                 q4(mi, d), q4(mi, d), q4(d, m), q4(d, m), norm(), norm(), norm(), norm())
                for _ in range(cfg.n_double)]
-    singles = [FluxSingleWeights(q4(3 * d, d), q4(3 * d + m, d), q4(d, d + m), norm(), norm())
+    singles = [FluxSingleWeights(q4(3 * d, d), q4(3 * d + mi, d), q4(d, d + m), norm(), norm())
                for _ in range(cfg.n_single)]
     w_in = synth.normal(seed, 999, d * cfg.patch_dim, 0.02).reshape(d, cfg.patch_dim)
     glob = FluxGlobalWeights(torch.from_numpy(gguf.quantize(w_in, GGML_Q8_0)).to(device), q4(d, cfg.text_dim),
@@ -267,11 +277,13 @@ def flux_weights(cfg: FluxConfig, device="cuda", seed: int = workloads.SEED, g: 
 
 # Checkpoint tensor names: the BFL Flux.1-dev layout this model uses (per-block
 # img_mod / txt_mod / modulation weights, a GELU MLP with img_mlp.0 of
-# [mlp, dim], linear1 of [3 dim + mlp, dim]). The reference's loader
-# (load_flux_dit, flux_dit.c3:664-744) reads the Flux Klein layout instead:
+# [mlp, dim], linear1 of [3 dim + mlp, dim]; with mlp_act "swiglu" the same
+# names hold the SwiGLU halves, img_mlp.0 of [2 mlp, dim] and linear1 of
+# [3 dim + 2 mlp, dim]). The reference's loader (load_flux_dit,
+# flux_dit.c3:664-744) reads the Flux Klein layout: the SwiGLU halves, and
 # shared double_stream_modulation_img/txt and single_stream_modulation
-# weights and SwiGLU halves (img_mlp.0 of [2 mlp, dim], linear1 of
-# [3 dim + 2 mlp, dim]), so its checkpoints do not load here unchanged.
+# weights instead of per-block ones, so its checkpoints do not load here
+# unchanged.
 _FLUX_GLOBAL = {"img_in": "img_in.weight", "txt_in": "txt_in.weight", "time_in0": "time_in.in_layer.weight",
                 "time_in1": "time_in.out_layer.weight", "final_mod": "final_layer.adaLN_modulation.1.weight",
                 "final_linear": "final_layer.linear.weight"}
@@ -287,13 +299,13 @@ _FLUX_SINGLE = {"mod": "modulation.lin.weight", "linear1": "linear1.weight", "li
 
 
 def _flux_shapes(cfg: FluxConfig):
-    d, m = cfg.dim, cfg.mlp
+    d, m, mi = cfg.dim, cfg.mlp, cfg.mlp_in
     glob = {"img_in": (d, cfg.patch_dim), "txt_in": (d, cfg.text_dim), "time_in0": (d, cfg.t_emb_dim),
             "time_in1": (d, d), "final_mod": (2 * d, d), "final_linear": (cfg.patch_dim, d)}
     dbl = {"img_mod": (6 * d, d), "txt_mod": (6 * d, d), "img_qkv": (3 * d, d), "txt_qkv": (3 * d, d),
-           "img_proj": (d, d), "txt_proj": (d, d), "img_mlp0": (m, d), "txt_mlp0": (m, d),
+           "img_proj": (d, d), "txt_proj": (d, d), "img_mlp0": (mi, d), "txt_mlp0": (mi, d),
            "img_mlp2": (d, m), "txt_mlp2": (d, m)}
-    sgl = {"mod": (3 * d, d), "linear1": (3 * d + m, d), "linear2": (d, d + m)}
+    sgl = {"mod": (3 * d, d), "linear1": (3 * d + mi, d), "linear2": (d, d + m)}
     return glob, dbl, sgl
 
 
@@ -439,9 +451,11 @@ class FluxDiT:
         S, d, m, nt = c.seq, c.dim, c.mlp, c.n_txt
         # the blocks' GEMM groups in issue order, each group's weight images
         # built by the call before it (when the GEMMs run two-pass)
+        # (the SwiGLU form's in-projections build their own images: plain rows
+        # and SwiGLU-arranged gate / up rows, which the chain does not make)
         self.ahead = None
         if images_ahead and S >= TWO_PASS_MIN_TOKENS and d % 64 == 0 and m % 64 == 0 and \
-                act_dtype in (torch.float16, torch.bfloat16):
+                act_dtype in (torch.float16, torch.bfloat16) and cfg.mlp_act == "gelu":
             def q4(t, K):
                 return _qt(t, GGML_Q4_K, t.numel() // (K // 256 * 144), K)
             groups = []
@@ -588,12 +602,17 @@ class FluxDiT:
         # output projections, hidden += gate1 * proj                  (flux_dit.c3:875-898)
         self._multi(jobs(w.txt_proj, w.img_proj, d, self.xa, self.hidden, (mt[2], mi[2])), d, d,
                     capi.EPI_GATED_RESIDUAL)
-        # MLP: LayerNorm + modulation, up + gelu, down, hidden += gate2 * down (flux_dit.c3:902-967)
+        # MLP: LayerNorm + modulation, up + gelu (swiglu: gate and up, silu(gate) * up), down,
+        # hidden += gate2 * down (flux_dit.c3:902-967)
         for sl, mod in ((ts, mt), (im, mi)):
             glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[4], mod_shift=mod[3],
                                  g=g)
-        self._multi(jobs(w.txt_mlp0, w.img_mlp0, d, self.xa, self.o, out2=self.fa), m, d,
-                    capi.EPI_SPLIT_GELU, split=0)
+        if c.mlp_act == "swiglu":
+            self._multi(jobs(w.txt_mlp0, w.img_mlp0, d, self.xa, self.o, out2=self.fa), 2 * m, d,
+                        capi.EPI_SPLIT_SWIGLU, split=0)
+        else:
+            self._multi(jobs(w.txt_mlp0, w.img_mlp0, d, self.xa, self.o, out2=self.fa), m, d,
+                        capi.EPI_SPLIT_GELU, split=0)
         self._multi(jobs(w.txt_mlp2, w.img_mlp2, m, self.fa, self.hidden, (mt[5], mi[5])), d, m,
                     capi.EPI_GATED_RESIDUAL)
 
@@ -602,10 +621,12 @@ class FluxDiT:
         c, g = self.cfg, self.g
         d, m, H, S = c.dim, c.mlp, c.n_heads, c.seq
         glue.batch_layernorm(self.hidden, self.xa, self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0], g=g)
-        # linear1: Q | K | V (f32) and gelu(MLP half) straight into linear2's input (flux_dit.c3:1005-1058)
-        self._multi([MatmulJob(_qt(w.linear1, GGML_Q4_K, 3 * d + m, d), _t(self.xa), self.qkv,
-                               S, 0, None, self.cat[:, d:])],
-                    3 * d + m, d, capi.EPI_SPLIT_GELU, split=3 * d)
+        # linear1: Q | K | V (f32) and the activated MLP half (gelu; swiglu: silu(gate) * up)
+        # straight into linear2's input                               (flux_dit.c3:1005-1058)
+        n1 = 3 * d + c.mlp_in
+        self._multi([MatmulJob(_qt(w.linear1, GGML_Q4_K, n1, d), _t(self.xa), self.qkv, S, 0, None,
+                               self.cat[:, d:])],
+                    n1, d, capi.EPI_SPLIT_SWIGLU if c.mlp_act == "swiglu" else capi.EPI_SPLIT_GELU, split=3 * d)
         glue.qkv_heads(self.qkv, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, self.HN_EPS, self.rope, g=g)
         self._attention(S, self.cat[:, :d])  # rows into linear2's input  (flux_dit.c3:1042-1047)
         # linear2, hidden += gate * linear2                           (flux_dit.c3:1060-1068)

@@ -259,9 +259,12 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
                                 epilogue: int = capi.EPI_STORE, split: int = 0, images=None,
                                 next_images: NextImages | None = None) -> None:
     """The jobs' GEMMs with a shared epilogue (llmr_batch_matmul_multi): a plain
-    store, `output += gate * result` (gated_residual_linear), or a column split
+    store, `output += gate * result` (gated_residual_linear), a column split
     whose features >= split are GELU'd into output2 (linear1's MLP half feeding
-    linear2, flux_dit.c3:1049-1058). Pairs of jobs run as one launch; a
+    linear2, flux_dit.c3:1049-1058), or a column split whose last 2 f
+    features are a SwiGLU gate and up, silu(gate) * up into output2's f
+    columns (the Flux.2 linear1 and MLP in-projection, flux_dit.c3:917-931,
+    1013-1018; output may be None when split is 0). Pairs of jobs run as one launch; a
     group of Q4_K jobs of at most 4 tokens with a plain store (the per-block
     modulation projections) runs as one GEMV launch. images: None, or one
     device tensor per job holding the job's weight image (build_weight_image
@@ -285,7 +288,12 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
             raise ValueError(f"{what} views must share one row stride")
         return strides.pop() if strides else (views[0].shape[1] + 3) // 4 * 4
 
-    ldy = common_stride([j.output for j in jobs], "output")
+    swiglu = epilogue == capi.EPI_SPLIT_SWIGLU
+    no_out = swiglu and split == 0
+    if no_out:
+        ldy = 0
+    else:
+        ldy = common_stride([j.output for j in jobs], "output")
     has2 = [j.output2 is not None for j in jobs]
     if any(has2) and not all(has2):
         raise ValueError("either every job has output2 or none")
@@ -301,25 +309,27 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
             raise ValueError("weight shape does not cover [row_offset, row_offset+out_dim) x in_dim")
         if j.input.data.numel() < j.seq_len * in_dim:
             raise ValueError("input smaller than [seq_len, in_dim]")
-        if not j.output.is_cuda or j.output.dtype != torch.float32:
-            raise ValueError("outputs must be f32 device views")
-        width = split if epilogue == capi.EPI_SPLIT_GELU else out_dim
-        if j.output.shape[0] < j.seq_len or j.output.shape[1] < width:
-            raise ValueError("output view smaller than [seq_len, out_dim]")
+        if not no_out:
+            if not j.output.is_cuda or j.output.dtype != torch.float32:
+                raise ValueError("outputs must be f32 device views")
+            width = split if epilogue in (capi.EPI_SPLIT_GELU, capi.EPI_SPLIT_SWIGLU) else out_dim
+            if j.output.shape[0] < j.seq_len or j.output.shape[1] < width:
+                raise ValueError("output view smaller than [seq_len, out_dim]")
         o2 = 0
         if j.output2 is not None:
             if _TORCH_GGML.get(j.output2.dtype) != o2type:
                 raise ValueError("output2 views must share one dtype")
-            if j.output2.shape[0] < j.seq_len or j.output2.shape[1] < out_dim - split:
-                raise ValueError("output2 view smaller than [seq_len, out_dim - split]")
+            width2 = (out_dim - split) // 2 if swiglu else out_dim - split
+            if j.output2.shape[0] < j.seq_len or j.output2.shape[1] < width2:
+                raise ValueError(f"output2 view smaller than [seq_len, {width2}]")
             o2 = j.output2.data_ptr()
         gp = 0
         if j.gate is not None:
             if j.gate.dtype != torch.float32 or not j.gate.is_contiguous() or j.gate.numel() < out_dim:
                 raise ValueError("gate must be a contiguous f32 vector of out_dim elements")
             gp = j.gate.data_ptr()
-        cj.append(capi.MatmulJob(j.weight.ptr(), j.input.ptr(), j.output.data_ptr(), gp or None, o2 or None,
-                                 j.seq_len, j.row_offset))
+        cj.append(capi.MatmulJob(j.weight.ptr(), j.input.ptr(), None if no_out else j.output.data_ptr(),
+                                 gp or None, o2 or None, j.seq_len, j.row_offset))
     epi = capi.MatmulEpilogue(epilogue, ldy, split, ldy2, o2type)
     g.bind_stream()
     if images is None and next_images is None:

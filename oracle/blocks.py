@@ -16,9 +16,10 @@ llm.slang:2264-2365; flash_attention_v2: fp16 Q/K/V, flash_attn.slang:38-241).
                  batch_rmsnorm, scale_modulate, batch_matmul_swiglu_q8, down
                  GEMM, batch_rmsnorm, gated_residual.
   flux_forward   FluxDiTModel.forward (dependencies/flux.c3l/flux_dit.c3:
-                 1075-1210) with the Flux.1-dev choices of llmr_amd.dit.FluxDiT
-                 (GELU MLP, per-block modulation), each block the reference's
-                 dispatch order (flux_dit.c3:746-1071).
+                 1075-1210) with the choices of llmr_amd.dit.FluxDiT (per-block
+                 modulation; the Flux.1-dev GELU MLP or the reference's own
+                 SwiGLU MLP, cfg.mlp_act), each block the reference's dispatch
+                 order (flux_dit.c3:746-1071).
 """
 from __future__ import annotations
 
@@ -111,17 +112,32 @@ def _mm_rows(W, wtype, X, N, row_offset, rows):
     return orc.batch_matmul(W, wtype, X, N, X.shape[1], X.shape[0], row_offset, rows=np.asarray(rows))
 
 
+def _mlp_in(W, a, m, mlp_act, row0=0, rows=None):
+    """The MLP in-projection of a block and its activation: GELU of m rows
+    from row0 (the Flux.1-dev form), or silu(gate) * up of the m gate rows
+    from row0 and the m up rows after them (the reference's Flux.2 form:
+    flux_matmul of the gate and up slots, then silu and elemwise_mul in f32,
+    flux_dit.c3:917-931, 1013-1018, 1049-1055)."""
+    if mlp_act == "gelu":
+        return orc.gelu(_mm_rows(W, GGML_Q4_K, a, m, row0, rows))
+    g = _mm_rows(W, GGML_Q4_K, a, m, row0, rows)
+    u = _mm_rows(W, GGML_Q4_K, a, m, row0 + m, rows)
+    return orc.silu(g) * u
+
+
 def flux_double_block(w: dict, txt_h: np.ndarray, img: np.ndarray, mt: np.ndarray, mi: np.ndarray, n_heads: int,
-                      cos_t, sin_t, rows=None):
-    """flux_dual_stream_block (flux_dit.c3:746-971) with the Flux.1-dev GELU
-    MLP. txt_h [n_txt, d] / img [n_img, d]: the two residual streams; mt / mi
-    [6, d]: (shift1, scale1, gate1, shift2, scale2, gate2) of each stream.
-    Returns the updated (txt_h, img); with `rows` (joint row indices, text
-    rows first) only those rows' updates are computed and returned as one
-    [len(rows), d] array in joint order."""
+                      cos_t, sin_t, rows=None, mlp_act: str = "gelu"):
+    """flux_dual_stream_block (flux_dit.c3:746-971). mlp_act "gelu": the
+    Flux.1-dev GELU MLP ([m, d] in-projection); "swiglu": the reference's own
+    SwiGLU MLP ([2 m, d]: gate rows, then up rows). txt_h [n_txt, d] / img
+    [n_img, d]: the two residual streams; mt / mi [6, d]: (shift1, scale1,
+    gate1, shift2, scale2, gate2) of each stream. Returns the updated (txt_h,
+    img); with `rows` (joint row indices, text rows first) only those rows'
+    updates are computed and returned as one [len(rows), d] array in joint
+    order."""
     d = txt_h.shape[1]
     nt, ni = txt_h.shape[0], img.shape[0]
-    m = w["img_mlp0"].size // (d // 256 * 144)
+    m = w["img_mlp0"].size // (d // 256 * 144) // (2 if mlp_act == "swiglu" else 1)
     eps_hn = 1e-6
     a_i = _ln_mod(img, mi[0], mi[1])
     a_t = _ln_mod(txt_h, mt[0], mt[1])
@@ -150,7 +166,7 @@ def flux_double_block(w: dict, txt_h: np.ndarray, img: np.ndarray, mt: np.ndarra
         """Attention projection + gated residual, then the MLP half."""
         h = orc.gated_residual(h, mod[2], _mm(wp, GGML_Q4_K, o_s, d), False)
         a = _ln_mod(h, mod[3], mod[4])
-        return orc.gated_residual(h, mod[5], _mm(w2, GGML_Q4_K, orc.gelu(_mm(w0, GGML_Q4_K, a, m)), d), False)
+        return orc.gated_residual(h, mod[5], _mm(w2, GGML_Q4_K, _mlp_in(w0, a, m, mlp_act), d), False)
 
     if rows is None:
         txt_h = stream(txt_h, mt, w["txt_proj"], w["txt_mlp0"], w["txt_mlp2"], o[:nt])
@@ -165,25 +181,28 @@ def flux_double_block(w: dict, txt_h: np.ndarray, img: np.ndarray, mt: np.ndarra
     return out
 
 
-def flux_single_block(w: dict, h: np.ndarray, ms: np.ndarray, n_heads: int, cos_t, sin_t, rows=None):
-    """flux_single_stream_block (flux_dit.c3:975-1071) with the Flux.1-dev
-    GELU MLP half of linear1. h [S, d] joint stream (text rows first); ms [3, d]
-    (shift, scale, gate). Returns the updated h, or with `rows` the updated
-    rows [len(rows), d]."""
+def flux_single_block(w: dict, h: np.ndarray, ms: np.ndarray, n_heads: int, cos_t, sin_t, rows=None,
+                      mlp_act: str = "gelu"):
+    """flux_single_stream_block (flux_dit.c3:975-1071). mlp_act "gelu": the
+    Flux.1-dev GELU MLP half of linear1 ([3 d + m, d]); "swiglu": the
+    reference's own form, linear1 [3 d + 2 m, d] whose last 2 m rows are a
+    SwiGLU gate and up (flux_dit.c3:1013-1018, 1049-1055). h [S, d] joint
+    stream (text rows first); ms [3, d] (shift, scale, gate). Returns the
+    updated h, or with `rows` the updated rows [len(rows), d]."""
     S, d = h.shape
-    m = w["linear1"].size // (d // 256 * 144) - 3 * d
+    m = (w["linear1"].size // (d // 256 * 144) - 3 * d) // (2 if mlp_act == "swiglu" else 1)
     eps_hn = 1e-6
     a = _ln_mod(h, ms[0], ms[1])
     k, v = (_mm(w["linear1"], GGML_Q4_K, a, d, r * d) for r in (1, 2))
     if rows is None:
         q = _mm(w["linear1"], GGML_Q4_K, a, d, 0)
-        mlp = orc.gelu(_mm(w["linear1"], GGML_Q4_K, a, m, 3 * d))
+        mlp = _mlp_in(w["linear1"], a, m, mlp_act, 3 * d)
         h_r = h
     else:
         rows = np.asarray(rows)
         q = np.zeros((S, d), np.float32)
         q[rows] = _mm_rows(w["linear1"], GGML_Q4_K, a, d, 0, rows)
-        mlp = orc.gelu(_mm_rows(w["linear1"], GGML_Q4_K, a, m, 3 * d, rows))
+        mlp = _mlp_in(w["linear1"], a, m, mlp_act, 3 * d, rows)
         h_r = h[rows]
     q = orc.batch_head_norm(q, w["q_norm"], n_heads, eps_hn)
     k = orc.batch_head_norm(k, w["k_norm"], n_heads, eps_hn)
@@ -205,11 +224,13 @@ def flux_forward(cfg, glob: dict, doubles: list, singles: list, latent: np.ndarr
     vec = _mm(glob["time_in1"], GGML_Q4_K, orc.silu(_mm(glob["time_in0"], GGML_Q4_K, temb, d)), d)
     vec = orc.silu(vec)
     mod = lambda W, n: _mm(W, GGML_Q4_K, vec, n * d).reshape(n, d)  # noqa: E731
+    act = getattr(cfg, "mlp_act", "gelu")
     for w in doubles:
-        txt_h, img = flux_double_block(w, txt_h, img, mod(w["txt_mod"], 6), mod(w["img_mod"], 6), H, cos_t, sin_t)
+        txt_h, img = flux_double_block(w, txt_h, img, mod(w["txt_mod"], 6), mod(w["img_mod"], 6), H, cos_t, sin_t,
+                                       mlp_act=act)
     h = np.concatenate([txt_h, img])
     for w in singles:
-        h = flux_single_block(w, h, mod(w["mod"], 3), H, cos_t, sin_t)
+        h = flux_single_block(w, h, mod(w["mod"], 3), H, cos_t, sin_t, mlp_act=act)
     fm = mod(glob["final_mod"], 2)
     a = _ln_mod(h[nt:], fm[0], fm[1])
     vel = _mm(glob["final_linear"], GGML_Q4_K, a, cfg.patch_dim)

@@ -39,17 +39,21 @@ def test_zimage_block_vs_oracle(dev, act):
     assert err < (3e-3 if act == torch.float16 else 1e-2)
 
 
-def _small_flux():
+def _small_flux(mlp_act="gelu"):
     from llmr_amd import dit
     return dit.FluxConfig(dim=256, n_heads=2, mlp=512, n_double=2, n_single=2, text_dim=256, n_txt=40,
-                          latent_ch=16, latent_h=16, latent_w=16, patch=2)
+                          latent_ch=16, latent_h=16, latent_w=16, patch=2, mlp_act=mlp_act)
 
 
-@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
-def test_flux_forward_vs_oracle(dev, act):
+@pytest.mark.parametrize("act,mlp_act", [(torch.float16, "gelu"), (torch.bfloat16, "gelu"),
+                                         (torch.bfloat16, "swiglu")])
+def test_flux_forward_vs_oracle(dev, act, mlp_act):
+    """The composed forward against the oracle's: the Flux.1-dev GELU MLP,
+    and the reference's own Flux.2 SwiGLU MLP (linear1 [3 d + 2 m, d], MLP
+    in-projection [2 m, d])."""
     from llmr_amd import dit, synth
     from oracle import blocks
-    cfg = _small_flux()
+    cfg = _small_flux(mlp_act)
     glob, doubles, singles = dit.flux_weights(cfg, device=dev)
     model = dit.FluxDiT(cfg, glob, doubles, singles, act_dtype=act, device=dev)
     lat = synth.normal(42, 501, cfg.latent_ch * cfg.latent_h * cfg.latent_w).reshape(
@@ -64,7 +68,7 @@ def test_flux_forward_vs_oracle(dev, act):
                               txt_t.float().cpu().numpy(), 0.5, cos_t, sin_t)
     got = _np(out)
     err = rel_l2(got, ref)
-    print(f"flux forward act={act}: velocity rel L2 {err:.2e}")
+    print(f"flux forward act={act} mlp={mlp_act}: velocity rel L2 {err:.2e}")
     assert np.isfinite(got).all()
     assert err < (5e-3 if act == torch.float16 else 1e-2)  # measured 2.9e-4 / 3.3e-3
 

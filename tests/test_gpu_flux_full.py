@@ -77,6 +77,57 @@ def test_flux_single_block_full_shape_vs_oracle(flux1):
     assert err < 1e-2
 
 
+@pytest.fixture(scope="module")
+def flux2(dev):
+    """The same at full shape with the reference's own Flux.2 MLP form:
+    linear1 [3 dim + 2 mlp, dim] and MLP in-projections [2 mlp, dim] whose
+    gate and up halves the GEMMs' split-SwiGLU epilogue combines."""
+    from llmr_amd import dit, synth
+    cfg = dit.FluxConfig(n_double=1, n_single=1, mlp_act="swiglu")
+    glob, doubles, singles = dit.flux_weights(cfg, device=dev)
+    model = dit.FluxDiT(cfg, glob, doubles, singles, device=dev)
+    h0 = synth.normal(42, 720, cfg.seq * cfg.dim).reshape(cfg.seq, cfg.dim)
+    mods = synth.normal(42, 721, model.mods.numel(), 0.5).reshape(1, -1)
+    model.mods.copy_(torch.from_numpy(mods))
+    cos_t, sin_t = (_np(t) for t in model.rope)
+    return cfg, model, doubles[0], singles[0], h0, cos_t, sin_t
+
+
+def test_flux2_double_block_full_shape_vs_oracle(flux2):
+    from oracle import blocks
+    cfg, model, w, _, h0, cos_t, sin_t = flux2
+    nt = cfg.n_txt
+    model.hidden.copy_(torch.from_numpy(h0))
+    mi, mt = model._mod(0, 6), model._mod(6, 6)
+    print(f"Flux.2 double block: S={cfg.seq} dim={cfg.dim} rows={ROWS.tolist()}", flush=True)
+    model._double(w, mi, mt)
+    torch.cuda.synchronize()
+    got = _np(model.hidden)[ROWS]
+    ref = blocks.flux_double_block(_as_np(w), h0[:nt], h0[nt:], _np(mt), _np(mi), cfg.n_heads, cos_t, sin_t,
+                                   rows=ROWS, mlp_act="swiglu")
+    assert np.isfinite(got).all()
+    for name, sel in (("text", ROWS < nt), ("image", ROWS >= nt)):
+        err = rel_l2(got[sel] - h0[ROWS[sel]], ref[sel] - h0[ROWS[sel]])
+        print(f"Flux.2 double block {name} rows: update rel L2 {err:.2e}")
+        assert err < 1e-2
+
+
+def test_flux2_single_block_full_shape_vs_oracle(flux2):
+    from oracle import blocks
+    cfg, model, _, w, h0, cos_t, sin_t = flux2
+    model.hidden.copy_(torch.from_numpy(h0))
+    ms = model._mod(12, 3)
+    print(f"Flux.2 single block: S={cfg.seq} dim={cfg.dim} rows={ROWS.tolist()}", flush=True)
+    model._single(w, ms)
+    torch.cuda.synchronize()
+    got = _np(model.hidden)[ROWS]
+    ref = blocks.flux_single_block(_as_np(w), h0, _np(ms), cfg.n_heads, cos_t, sin_t, rows=ROWS, mlp_act="swiglu")
+    assert np.isfinite(got).all()
+    err = rel_l2(got - h0[ROWS], ref - h0[ROWS])
+    print(f"Flux.2 single block: update rel L2 {err:.2e}")
+    assert err < 1e-2
+
+
 def test_flux_dev_step_full_size_finite_and_deterministic(dev):
     """The whole 19 + 38 block step (the bench's flux_step) twice on the same
     inputs: finite, bit-identical, and not degenerate."""

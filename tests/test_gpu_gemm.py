@@ -482,6 +482,55 @@ def test_multi_gemv_group(orc, dev, xtype, pad):
         assert (out[i, M:] == 7.0).all() and (out[i, :, N:] == 7.0).all(), i
 
 
+@pytest.mark.parametrize("Ms,split,f,K,xtype,o2", [
+    ((4608,), 768, 1024, 512, 30, 30),     # one job on the two-pass kernel: Q|K|V part + SwiGLU part
+    ((512, 3584), 0, 1024, 512, 30, 1),    # two jobs (text + image stream), SwiGLU only, f16 output2
+    ((1000,), 256, 512, 512, 30, 30),      # fewer tokens: the GEMM into the workspace, then the glue
+    ((2304,), 512, 760, 768, 0, 30),       # f32 activations (bf16 operands against Q4_K): the glue path
+])
+def test_multi_split_swiglu(orc, dev, Ms, split, f, K, xtype, o2):
+    """LLMR_EPI_SPLIT_SWIGLU, the reference's Flux.2 linear1 and MLP
+    in-projection (flux_dit.c3:917-931, 1013-1018, 1049-1055): weight rows
+    [split, split + f) are a SwiGLU gate, the next f its up; features below
+    split are stored in f32, silu(gate) * up of every output into a 16-bit
+    buffer. Against the oracle's GEMM of all rows, then silu and the product
+    in f32, on sampled rows of every job."""
+    import torch
+    from llmr_amd import capi, gguf, ops, synth
+    N = split + 2 * f
+    g = ops.default_graph()
+    odt = torch.bfloat16 if o2 == 30 else torch.float16
+    blks, xs, jobs, ys, y2s = [], [], [], [], []
+    for i, M in enumerate(Ms):
+        blk = gguf.quantize(synth.normal(80 + i, 2, N * K, 0.02), gguf.GGML_Q4_K)
+        x = _torch_x(synth.normal(90 + i, 1, M * K).reshape(M, K), xtype, dev)
+        y = torch.full((M, max(split, 4)), 7.0, device=dev)
+        y2 = torch.zeros((M, f), dtype=odt, device=dev)
+        blks.append(blk)
+        xs.append(x)
+        ys.append(y)
+        y2s.append(y2)
+        w = ops.Tensor.quantized(torch.from_numpy(blk).to(dev), 12, N, K)
+        jobs.append(ops.MatmulJob(w, ops.Tensor.from_torch(x), y[:, :split] if split else None, M, 0,
+                                  None, y2))
+    print(f"split swiglu: jobs {Ms} split {split} f {f} K {K} x {xtype} output2 {o2}", flush=True)
+    ops.dispatch_batch_matmul_multi(g, jobs, N, K, capi.EPI_SPLIT_SWIGLU, split)
+    torch.cuda.synchronize()
+    for i, M in enumerate(Ms):
+        rows = _sample_rows(M)
+        ref = orc.batch_matmul(blks[i], 12, _x_as_f32(xs[i]), N, K, M, 0, rows=rows.astype(np.uint32))
+        ref2 = orc.silu(ref[:, split:split + f]) * ref[:, split + f:]
+        got2 = y2s[i].float().cpu().numpy()[rows]
+        err2 = rel_l2(got2, ref2)
+        print(f"  job {i}: silu(gate) * up rel L2 {err2:.2e}", end="")
+        assert np.all(np.isfinite(got2)) and err2 <= TOL
+        if split:
+            err = rel_l2(ys[i].cpu().numpy()[rows, :split], ref[:, :split])
+            print(f", plain part rel L2 {err:.2e}", end="")
+            assert err <= TOL
+        print()
+
+
 @pytest.mark.parametrize("N,xtype", [(18432, 30), (9216, 0)])
 def test_multi_gemv_group_flux_modulation(orc, dev, N, xtype):
     """The Flux.1-dev modulation projections of one step at full size: 38

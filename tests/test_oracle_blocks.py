@@ -133,12 +133,28 @@ def _timestep(dim, t):
 
 
 def flux_f64(orc, cfg, glob, doubles, singles, latent, txt, sigma, cos_t, sin_t, mistake=None):
-    """FluxDiTModel.forward (flux_dit.c3:1075-1210) in float64 with the
-    Flux.1-dev GELU MLP and per-block modulation. Chunks per stream of a
+    """FluxDiTModel.forward (flux_dit.c3:1075-1210) in float64 with
+    per-block modulation and cfg.mlp_act's MLP: the Flux.1-dev GELU, or the
+    reference's SwiGLU (silu of the gate rows times the up rows after them,
+    flux_dit.c3:917-931, 1013-1018, 1049-1055). Chunks per stream of a
     double block: shift1, scale1, gate1, shift2, scale2, gate2
     (flux_dit.c3:764-765,889,905-906,936); single block: shift, scale, gate
     (:988-989,1064); final layer: shift, scale (:1183-1185)."""
     d, m, H, nt = cfg.dim, cfg.mlp, cfg.n_heads, cfg.n_txt
+    swiglu = cfg.mlp_act == "swiglu"
+
+    def mlp_in(a, W):
+        """a @ W.T of the MLP in-projection rows W, activated."""
+        if not swiglu:
+            return _gelu(a @ W.T)
+        g, u = a @ W[:m].T, a @ W[m:].T
+        if mistake == "swiglu_halves":
+            g, u = u, g
+        if mistake == "swiglu_gelu":
+            return _gelu(g) * u
+        if mistake == "swiglu_no_gate":
+            return u
+        return _silu(g) * u
     G = lambda blocks, wt, n, k: _deq(orc, blocks, wt, n, k)  # noqa: E731
     eps = 1e-6
     img = _patchify(np.asarray(latent, np.float64), cfg.patch) @ G(glob["img_in"], Q8, d, cfg.patch_dim).T
@@ -181,15 +197,16 @@ def flux_f64(orc, cfg, glob, doubles, singles, latent, txt, sigma, cos_t, sin_t,
         txt_h = txt_h + mt[g1] * (o[:nt] @ G(w["txt_proj"], Q4K, d, d).T)
         img = img + mi[g1] * (o[nt:] @ G(w["img_proj"], Q4K, d, d).T)
         a_i, a_t = ln_mod(img, mi[3], mi[4]), ln_mod(txt_h, mt[3], mt[4])
-        img = img + mi[g2] * (_gelu(a_i @ G(w["img_mlp0"], Q4K, m, d).T) @ G(w["img_mlp2"], Q4K, d, m).T)
-        txt_h = txt_h + mt[g2] * (_gelu(a_t @ G(w["txt_mlp0"], Q4K, m, d).T) @ G(w["txt_mlp2"], Q4K, d, m).T)
+        mi_rows = cfg.mlp_in
+        img = img + mi[g2] * (mlp_in(a_i, G(w["img_mlp0"], Q4K, mi_rows, d)) @ G(w["img_mlp2"], Q4K, d, m).T)
+        txt_h = txt_h + mt[g2] * (mlp_in(a_t, G(w["txt_mlp0"], Q4K, mi_rows, d)) @ G(w["txt_mlp2"], Q4K, d, m).T)
     h = np.concatenate([txt_h, img])
     for w in singles:
         ms = mod(w["mod"], 3)
         a = ln_mod(h, ms[0], ms[1])
-        l1 = G(w["linear1"], Q4K, 3 * d + m, d)
+        l1 = G(w["linear1"], Q4K, 3 * d + cfg.mlp_in, d)
         q, k, v = (a @ l1[r * d:(r + 1) * d].T for r in range(3))
-        mlp = _gelu(a @ l1[3 * d:].T)
+        mlp = mlp_in(a, l1[3 * d:])
         q = _head_norm(q, np.asarray(w["q_norm"], np.float64), H, eps)
         k = _head_norm(k, np.asarray(w["k_norm"], np.float64), H, eps)
         o = _attention(_rope(q, cos64, sin64), _rope(k, cos64, sin64), v, H)
@@ -301,10 +318,10 @@ def test_zimage_layer_zero_qk_is_mean_of_v(orc):
 # Flux forward
 # ---------------------------------------------------------------------------
 
-def _flux_cfg():
+def _flux_cfg(mlp_act="gelu"):
     from llmr_amd import dit
     return dit.FluxConfig(dim=256, n_heads=2, mlp=512, n_double=2, n_single=2, text_dim=256, n_txt=24,
-                          latent_ch=16, latent_h=12, latent_w=12, patch=2)
+                          latent_ch=16, latent_h=12, latent_w=12, patch=2, mlp_act=mlp_act)
 
 
 def _flux_weights(r, cfg, zero_gates=False):
@@ -313,7 +330,7 @@ def _flux_weights(r, cfg, zero_gates=False):
     are O(1) and distinct; with zero_gates every gate chunk's rows are zero
     blocks."""
     from llmr_amd import gguf
-    d, m = cfg.dim, cfg.mlp
+    d, m, mi = cfg.dim, cfg.mlp, cfg.mlp_in
 
     def q(n, k, std=0.05, wt=gguf.GGML_Q4_K):
         return gguf.quantize((std * r.standard_normal((n, k))).astype(np.float32), wt)
@@ -329,10 +346,10 @@ def _flux_weights(r, cfg, zero_gates=False):
     def norm():
         return (1.0 + 0.1 * r.standard_normal(128)).astype(np.float32)
     doubles = [dict(img_mod=mod(6, (2, 5)), txt_mod=mod(6, (2, 5)), img_qkv=q(3 * d, d), txt_qkv=q(3 * d, d),
-                    img_proj=q(d, d), txt_proj=q(d, d), img_mlp0=q(m, d), txt_mlp0=q(m, d), img_mlp2=q(d, m),
+                    img_proj=q(d, d), txt_proj=q(d, d), img_mlp0=q(mi, d), txt_mlp0=q(mi, d), img_mlp2=q(d, m),
                     txt_mlp2=q(d, m), img_q_norm=norm(), img_k_norm=norm(), txt_q_norm=norm(),
                     txt_k_norm=norm()) for _ in range(cfg.n_double)]
-    singles = [dict(mod=mod(3, (2,)), linear1=q(3 * d + m, d), linear2=q(d, d + m), q_norm=norm(), k_norm=norm())
+    singles = [dict(mod=mod(3, (2,)), linear1=q(3 * d + mi, d), linear2=q(d, d + m), q_norm=norm(), k_norm=norm())
                for _ in range(cfg.n_single)]
     glob = dict(img_in=q(d, cfg.patch_dim, 0.1, gguf.GGML_Q8_0), txt_in=q(d, cfg.text_dim, 0.1),
                 time_in0=q(d, cfg.t_emb_dim, 0.1), time_in1=q(d, d, 0.1), final_mod=q(2 * d, d, 0.1),
@@ -436,4 +453,63 @@ def test_zimage_layer_sampled_rows_match_full(orc, zimage_case):
     full = blocks.zimage_layer(w, h, H, cos_t, sin_t)
     rows = np.array([0, 3, 17, h.shape[0] // 2, h.shape[0] - 1])
     part = blocks.zimage_layer(w, h, H, cos_t, sin_t, rows=rows)
+    np.testing.assert_array_equal(part, full[rows])
+
+
+# ---------------------------------------------------------------------------
+# the reference's own Flux.2 MLP form (SwiGLU halves)
+# ---------------------------------------------------------------------------
+
+FLUX_SWIGLU_MISTAKES = ["swiglu_halves", "swiglu_gelu", "swiglu_no_gate", "cat_order", "gate_chunks"]
+
+
+@pytest.fixture(scope="module")
+def flux_swiglu_case(orc):
+    from oracle import blocks
+    cfg = _flux_cfg("swiglu")
+    r = np.random.default_rng(31)
+    glob, doubles, singles = _flux_weights(r, cfg)
+    lat, txt, cos_t, sin_t = _flux_inputs(r, cfg)
+    got = blocks.flux_forward(cfg, glob, doubles, singles, lat, txt, 0.5, cos_t, sin_t)
+    return cfg, glob, doubles, singles, lat, txt, cos_t, sin_t, got
+
+
+def test_flux_swiglu_forward_vs_float64(orc, flux_swiglu_case):
+    """The SwiGLU MLP form of both block types (linear1 [3 d + 2 m, d], MLP
+    in-projection [2 m, d]) against the float64 restatement."""
+    cfg, glob, doubles, singles, lat, txt, cos_t, sin_t, got = flux_swiglu_case
+    ref = flux_f64(orc, cfg, glob, doubles, singles, lat, txt, 0.5, cos_t, sin_t)
+    err = rel_l2(got, ref)
+    print(f"flux (swiglu) forward velocity: rel L2 {err:.2e}")
+    assert err < FLUX_TOL
+
+
+@pytest.mark.parametrize("mistake", FLUX_SWIGLU_MISTAKES)
+def test_flux_swiglu_forward_catches_planted_mistake(orc, flux_swiglu_case, mistake):
+    cfg, glob, doubles, singles, lat, txt, cos_t, sin_t, got = flux_swiglu_case
+    bad = flux_f64(orc, cfg, glob, doubles, singles, lat, txt, 0.5, cos_t, sin_t, mistake=mistake)
+    err = rel_l2(got, bad)
+    print(f"{mistake}: rel L2 {err:.2e}")
+    assert err > 10 * FLUX_TOL
+
+
+def test_flux_swiglu_blocks_sampled_rows_match_full(orc, flux_swiglu_case):
+    """The sampled-row forms of the SwiGLU blocks give the full blocks' rows
+    bit for bit."""
+    from oracle import blocks
+    cfg, glob, doubles, singles, lat, txt, cos_t, sin_t, _ = flux_swiglu_case
+    d, nt = cfg.dim, cfg.n_txt
+    r = np.random.default_rng(33)
+    txt_h = r.standard_normal((nt, d)).astype(np.float32)
+    img = r.standard_normal((cfg.n_img, d)).astype(np.float32)
+    mt, mi = (r.standard_normal((6, d)).astype(np.float32) for _ in range(2))
+    ft, fi = blocks.flux_double_block(doubles[0], txt_h, img, mt, mi, cfg.n_heads, cos_t, sin_t, mlp_act="swiglu")
+    rows = np.array([0, 5, nt - 1, nt, nt + 17, nt + cfg.n_img - 1])
+    part = blocks.flux_double_block(doubles[0], txt_h, img, mt, mi, cfg.n_heads, cos_t, sin_t, rows=rows,
+                                    mlp_act="swiglu")
+    np.testing.assert_array_equal(part, np.concatenate([ft, fi])[rows])
+    h = np.concatenate([txt_h, img])
+    ms = r.standard_normal((3, d)).astype(np.float32)
+    full = blocks.flux_single_block(singles[0], h, ms, cfg.n_heads, cos_t, sin_t, mlp_act="swiglu")
+    part = blocks.flux_single_block(singles[0], h, ms, cfg.n_heads, cos_t, sin_t, rows=rows, mlp_act="swiglu")
     np.testing.assert_array_equal(part, full[rows])
