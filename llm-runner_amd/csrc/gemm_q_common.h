@@ -376,11 +376,17 @@ __device__ __forceinline__ void store_tile_256(f32x16 (&acc)[4][4], float* Y, co
             }
         return;
     }
+    // The empty asm statement before each 32 x 32 block ("+a": the block's
+    // accumulators are in AGPRs there and may change) keeps the compiler from
+    // copying every accumulator into VGPRs at the top of the epilogue, which
+    // spilled the gated-residual and split-SwiGLU variants to scratch; each
+    // block is now copied out when it is stored.
     auto each = [&](auto&& f) __attribute__((always_inline)) {
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
             for (int b = 0; b < 4; b++) {
+                asm volatile("" : "+a"(acc[a][b]));
                 const uint32_t m = m0 + wm * 128u + b * 32u + l32;
 #pragma unroll
                 for (int g = 0; g < 4; g++) {
@@ -409,6 +415,7 @@ __device__ __forceinline__ void store_tile_256(f32x16 (&acc)[4][4], float* Y, co
         for (int a = 0; a < 2; a++)
 #pragma unroll
             for (int b = 0; b < 4; b++) {
+                asm volatile("" : "+a"(acc[a][b]), "+a"(acc[a + 2][b]));
                 const uint32_t m = m0 + wm * 128u + b * 32u + l32;
 #pragma unroll
                 for (int g = 0; g < 4; g++) {
