@@ -308,6 +308,47 @@ LLMR_API int llmr_batch_matmul_multi_images(llmr_context* ctx, uint32_t weight_t
                                             uint32_t n_jobs, const llmr_matmul_epilogue* epilogue,
                                             const void* const* images, const llmr_next_weight_images* next);
 
+/* Head routing of a QKV projection's result, per job (NULL: no norms, row0 0). */
+typedef struct llmr_qkv_heads_job {
+    const float* q_norm; /* [128] or NULL (16-byte aligned) */
+    const float* k_norm; /* [128] or NULL */
+    uint32_t row0;       /* sequence position of the job's token 0 */
+} llmr_qkv_heads_job;
+
+/* The Q | K | V columns of a QKV projection routed to the attention's
+ * head-major inputs, as llmr_qkv_heads does from the f32 result. */
+typedef struct llmr_qkv_heads_out {
+    void* q;                        /* [n_heads, seq_len, 128] of out_type each, 16-byte aligned */
+    void* k;
+    void* v;
+    uint32_t out_type;              /* LLMR_GGML_F16 or LLMR_GGML_BF16 */
+    uint32_t n_heads;
+    uint32_t seq_len;
+    float eps;
+    const float* rope_cos;          /* [seq_len, 64] f32, or both NULL */
+    const float* rope_sin;
+    const llmr_qkv_heads_job* jobs; /* n_jobs entries, or NULL */
+} llmr_qkv_heads_out;
+
+/* llmr_batch_matmul_multi_images, with the result's first 3 * n_heads * 128
+ * columns (Q | K | V; the whole result for a STORE epilogue, [0, split) for
+ * SPLIT_GELU and SPLIT_SWIGLU, GATED_RESIDUAL not taken) written through
+ * `heads` instead of to the jobs' `output` (which may then be NULL): for
+ * job i, llmr_qkv_heads(result rows, n_heads, jobs[i].q_norm, jobs[i].k_norm,
+ * eps, rope tables, q, k, v, out_type, seq_len, jobs[i].row0), bit for bit
+ * (the row's sum of squares in the same order). row0 + seq_len of each job
+ * <= heads->seq_len. The persistent GEMM launches do it in their epilogue,
+ * so the f32 Q | K | V never reaches memory; other job groups run the GEMM
+ * into the context workspace and then llmr_qkv_heads. Replaces a QKV
+ * dispatch_batch_matmul followed by batch_head_norm x2 + transpose_heads x3
+ * + mrope x2 (dependencies/zimage.c3l/dit.c3:1434-1473,
+ * dependencies/flux.c3l/flux_dit.c3:786-863, 1005-1040). */
+LLMR_API int llmr_batch_matmul_multi_qkv(llmr_context* ctx, uint32_t weight_type, uint32_t input_type,
+                                         uint32_t out_dim, uint32_t in_dim, const llmr_matmul_job* jobs,
+                                         uint32_t n_jobs, const llmr_matmul_epilogue* epilogue,
+                                         const llmr_qkv_heads_out* heads, const void* const* images,
+                                         const llmr_next_weight_images* next);
+
 /* SwiGLU feed-forward in-projection, both matmuls and the activation in one op:
  *   g = input · weight_gate^T,  u = input · weight_up^T,
  *   output[s, o] = silu(g[s, o]) * u[s, o],  silu(g) = g / (1 + e^-g)

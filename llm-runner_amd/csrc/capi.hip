@@ -98,6 +98,20 @@ int check_ctx(llmr_context* ctx) {
 
 bool is_act_type(uint32_t t) { return t == LLMR_GGML_F32 || t == LLMR_GGML_F16 || t == LLMR_GGML_BF16; }
 
+int check_rows(const void* p, const char* what, uint32_t stride, uint32_t width) {
+    if (!p) return fail(LLMR_ERR_INVALID_ARG, "null %s pointer", what);
+    if (!aligned(p, 16)) return fail(LLMR_ERR_INVALID_ARG, "%s pointer must be 16-byte aligned", what);
+    if (stride % 4) return fail(LLMR_ERR_INVALID_ARG, "%s row stride must be a multiple of 4 (got %u)", what, stride);
+    if (stride < width) return fail(LLMR_ERR_INVALID_ARG, "%s row stride %u < row width %u", what, stride, width);
+    return LLMR_OK;
+}
+
+int check_vec(const void* p, const char* what, bool required) {
+    if (!p) return required ? fail(LLMR_ERR_INVALID_ARG, "null %s pointer", what) : LLMR_OK;
+    if (!aligned(p, 16)) return fail(LLMR_ERR_INVALID_ARG, "%s pointer must be 16-byte aligned", what);
+    return LLMR_OK;
+}
+
 // Weight-type and in_dim preconditions shared by dequant and GEMM
 // (the reference assumes K % 32 for Q8_0 and K % 256 for Q4_K: llm.slang:1650,2284).
 int check_weight(const void* w, uint32_t wtype, uint32_t in_dim) {
@@ -447,10 +461,50 @@ int llmr_q8_lora_merge(llmr_context* ctx, void* weight, const float* a, const fl
     return ok();
 }
 
+// The head routing of llmr_batch_matmul_multi_qkv: checks `heads` against
+// the call and turns a STORE epilogue into SPLIT_GELU with split = out_dim
+// (no gelu columns), the form the kernels take.
+static int check_qkv_heads(const llmr_qkv_heads_out* h, uint32_t out_dim, const llmr_matmul_job* jobs,
+                           uint32_t n_jobs, llmr_matmul_epilogue& e) {
+    if (h->n_heads == 0 || h->n_heads > 1024) return fail(LLMR_ERR_INVALID_ARG, "heads: n_heads must be in [1, 1024]");
+    const uint32_t qkv = 3u * h->n_heads * 128u;
+    if (e.kind == LLMR_EPI_GATED_RESIDUAL)
+        return fail(LLMR_ERR_INVALID_ARG, "heads: not with a GATED_RESIDUAL epilogue");
+    if (e.kind == LLMR_EPI_STORE) {
+        if (out_dim != qkv)
+            return fail(LLMR_ERR_INVALID_ARG, "heads: a STORE epilogue needs out_dim = 3 * n_heads * 128 = %u "
+                        "(got %u)", qkv, out_dim);
+        e = llmr_matmul_epilogue{LLMR_EPI_SPLIT_GELU, 0, out_dim, 0, LLMR_GGML_BF16};
+    } else if (e.split != qkv) {
+        return fail(LLMR_ERR_INVALID_ARG, "heads: split must be 3 * n_heads * 128 = %u (got %u)", qkv, e.split);
+    }
+    if (h->out_type != LLMR_GGML_F16 && h->out_type != LLMR_GGML_BF16)
+        return fail(LLMR_ERR_UNSUPPORTED, "heads: out_type must be F16 or BF16 (got %u)", h->out_type);
+    if (!(h->eps >= 0.0f) || !std::isfinite(h->eps))
+        return fail(LLMR_ERR_INVALID_ARG, "heads: eps must be finite and >= 0");
+    if (int r = check_vec(h->q, "heads q", true)) return r;
+    if (int r = check_vec(h->k, "heads k", true)) return r;
+    if (int r = check_vec(h->v, "heads v", true)) return r;
+    if ((h->rope_cos == nullptr) != (h->rope_sin == nullptr))
+        return fail(LLMR_ERR_INVALID_ARG, "heads: rope_cos and rope_sin must both be given or both be null");
+    if (int r = check_vec(h->rope_cos, "heads rope_cos", false)) return r;
+    if (int r = check_vec(h->rope_sin, "heads rope_sin", false)) return r;
+    if ((uint64_t)h->seq_len * 256u > 0xffffffffull) return fail(LLMR_ERR_INVALID_ARG, "heads: seq_len too large");
+    for (uint32_t i = 0; i < n_jobs; i++) {
+        const llmr_qkv_heads_job hj = h->jobs ? h->jobs[i] : llmr_qkv_heads_job{nullptr, nullptr, 0};
+        if (int r = check_vec(hj.q_norm, "heads q_norm", false)) return r;
+        if (int r = check_vec(hj.k_norm, "heads k_norm", false)) return r;
+        if ((uint64_t)hj.row0 + jobs[i].seq_len > h->seq_len)
+            return fail(LLMR_ERR_INVALID_ARG, "heads: job %u: row0 + seq_len (%llu) > seq_len %u", i,
+                        (unsigned long long)hj.row0 + jobs[i].seq_len, h->seq_len);
+    }
+    return LLMR_OK;
+}
+
 static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t xtype, uint32_t out_dim,
                                    uint32_t in_dim, const llmr_matmul_job* jobs, uint32_t n_jobs,
                                    const llmr_matmul_epilogue* epilogue, const void* const* images,
-                                   const llmr_next_weight_images* next) {
+                                   const llmr_next_weight_images* next, const llmr_qkv_heads_out* heads = nullptr) {
     if (int r = check_ctx(ctx)) return r;
     llmr::NextImageSet nx{};
     if (next) {
@@ -492,6 +546,8 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
     if (n_jobs > 64) return fail(LLMR_ERR_INVALID_ARG, "at most 64 jobs per call (got %u)", n_jobs);
     llmr_matmul_epilogue e = epilogue ? *epilogue : llmr_matmul_epilogue{LLMR_EPI_STORE, 0, 0, 0, 0};
     if (e.kind > LLMR_EPI_SPLIT_SWIGLU) return fail(LLMR_ERR_INVALID_ARG, "unknown epilogue kind %u", e.kind);
+    if (heads)
+        if (int r = check_qkv_heads(heads, out_dim, jobs, n_jobs, e)) return r;
     const bool swiglu = e.kind == LLMR_EPI_SPLIT_SWIGLU;
     const bool split = e.kind == LLMR_EPI_SPLIT_GELU || swiglu;
     if (!split) e.split = out_dim;
@@ -523,7 +579,7 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
     for (uint32_t i = 0; i < n_jobs; i++) {
         const llmr_matmul_job& j = jobs[i];
         if (int r = check_weight(j.weight, wtype, in_dim)) return r;
-        if (j.seq_len && (!j.input || (!j.output && !(swiglu && e.split == 0))))
+        if (j.seq_len && (!j.input || (!j.output && !heads && !(swiglu && e.split == 0))))
             return fail(LLMR_ERR_INVALID_ARG, "job %u: null input/output pointer", i);
         if (!aligned(j.input, 16) || !aligned(j.output, 16))
             return fail(LLMR_ERR_INVALID_ARG, "job %u: input/output pointers must be 16-byte aligned", i);
@@ -537,10 +593,20 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
             return fail(LLMR_ERR_INVALID_ARG, "job %u: weight image must be non-null and 256-byte aligned", i);
         gj[i] = llmr::GemmJob{j.weight, j.input, j.output, e.kind == LLMR_EPI_GATED_RESIDUAL ? j.gate : nullptr,
                               has2 ? j.output2 : nullptr, j.seq_len, j.row_offset};
+        if (heads && heads->jobs) {
+            gj[i].q_norm = heads->jobs[i].q_norm;
+            gj[i].k_norm = heads->jobs[i].k_norm;
+            gj[i].row0 = heads->jobs[i].row0;
+        }
     }
     if (images && (xtype == LLMR_GGML_F32 || in_dim % 64))
         return fail(LLMR_ERR_INVALID_ARG, "weight images need F16/BF16 input and in_dim %% 64 == 0");
-    const llmr::GemmEpilogue ge{e.kind, e.ldy, e.ldy2, e.split, has2 ? e.output2_type : (uint32_t)LLMR_GGML_BF16};
+    llmr::GemmHeads gh{};
+    if (heads)
+        gh = llmr::GemmHeads{heads->q,       heads->k,        heads->v,        heads->rope_cos, heads->rope_sin,
+                             heads->n_heads, heads->seq_len, heads->out_type, heads->eps};
+    const llmr::GemmEpilogue ge{e.kind, e.ldy, e.ldy2, e.split, has2 ? e.output2_type : (uint32_t)LLMR_GGML_BF16,
+                                heads ? &gh : nullptr};
     const size_t need = llmr::batch_matmul_multi_workspace_bytes(wtype, xtype, out_dim, in_dim, gj, n_jobs, ge,
                                                                  ctx->num_cus, images != nullptr);
     if (int r = acquire_workspace(ctx, need)) return r;
@@ -561,6 +627,14 @@ int llmr_batch_matmul_multi_images(llmr_context* ctx, uint32_t wtype, uint32_t x
                                    const llmr_matmul_epilogue* epilogue, const void* const* images,
                                    const llmr_next_weight_images* next) {
     return batch_matmul_multi_impl(ctx, wtype, xtype, out_dim, in_dim, jobs, n_jobs, epilogue, images, next);
+}
+
+int llmr_batch_matmul_multi_qkv(llmr_context* ctx, uint32_t wtype, uint32_t xtype, uint32_t out_dim,
+                                uint32_t in_dim, const llmr_matmul_job* jobs, uint32_t n_jobs,
+                                const llmr_matmul_epilogue* epilogue, const llmr_qkv_heads_out* heads,
+                                const void* const* images, const llmr_next_weight_images* next) {
+    if (!heads) return fail(LLMR_ERR_INVALID_ARG, "null heads");
+    return batch_matmul_multi_impl(ctx, wtype, xtype, out_dim, in_dim, jobs, n_jobs, epilogue, images, next, heads);
 }
 
 size_t llmr_weight_image_bytes(uint32_t out_dim, uint32_t in_dim) {
@@ -682,20 +756,6 @@ int llmr_flash_attention_pc(llmr_context* ctx, const void* q, const void* k, con
 namespace {
 
 // A row-major [rows, stride] operand accessed in 4-element vectors over `width` columns.
-int check_rows(const void* p, const char* what, uint32_t stride, uint32_t width) {
-    if (!p) return fail(LLMR_ERR_INVALID_ARG, "null %s pointer", what);
-    if (!aligned(p, 16)) return fail(LLMR_ERR_INVALID_ARG, "%s pointer must be 16-byte aligned", what);
-    if (stride % 4) return fail(LLMR_ERR_INVALID_ARG, "%s row stride must be a multiple of 4 (got %u)", what, stride);
-    if (stride < width) return fail(LLMR_ERR_INVALID_ARG, "%s row stride %u < row width %u", what, stride, width);
-    return LLMR_OK;
-}
-
-int check_vec(const void* p, const char* what, bool required) {
-    if (!p) return required ? fail(LLMR_ERR_INVALID_ARG, "null %s pointer", what) : LLMR_OK;
-    if (!aligned(p, 16)) return fail(LLMR_ERR_INVALID_ARG, "%s pointer must be 16-byte aligned", what);
-    return LLMR_OK;
-}
-
 int check_dim(uint32_t dim) {
     if (dim == 0 || dim % 4 || dim > llmr::kRowNormMaxDim)
         return fail(LLMR_ERR_INVALID_ARG, "dim must be a positive multiple of 4 and <= %u (got %u)",

@@ -615,7 +615,7 @@ __global__ void __launch_bounds__(256, 1) gemm_q_persist(const PersistArgs args)
         uint32_t p, m0, n0;
         tile_origin(k, p, m0, n0);
         store_tile_256<SW, EPI>(acc, pick(p, Yp0, Yp1), pick(p, Gp0, Gp1), pick(p, Y2p0, Y2p1), pick(p, Mp0, Mp1), N,
-                                m0, n0, wm, wn, l32, kh, ldy, ldy2, split, y2_bf16);
+                                m0, n0, wm, wn, l32, kh, ldy, ldy2, split, y2_bf16, args.heads, p);
     };
 
     // prologue, issued in the steady state's order (a stage issues the
@@ -1524,6 +1524,8 @@ hipError_t build_split_swiglu_image(const GemmJob& j, uint32_t wtype, uint32_t o
 bool multi_fused(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n,
                  const GemmEpilogue& epi, int num_cus) {
     if (!multi_persistent(wtype, xtype, N, K, jobs, n, num_cus)) return false;
+    // head routing: the 4-wave kernels (two-pass, or one-pass Q4_K)
+    if (epi.heads && wtype == kGgmlQ8_0 && !multi_two_pass(jobs, n)) return false;
     return epi.kind != kEpiSplitSwiglu || multi_two_pass(jobs, n);
 }
 
@@ -1546,6 +1548,15 @@ PersistArgs multi_args(uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n, 
     a.ldy2 = epi.ldy2;
     a.split = epi.kind == kEpiSplitGelu || epi.kind == kEpiSplitSwiglu ? epi.split : N;
     a.y2_bf16 = epi.y2_type == kGgmlBF16 ? 1u : 0u;
+    if (const GemmHeads* h = epi.heads) {
+        a.heads = HeadsEpi{h->q, h->k, h->v, h->cos, h->sin, {}, {}, {}, h->n_heads, h->seq,
+                           h->otype == kGgmlBF16 ? 1u : 0u, h->eps};
+        for (uint32_t i = 0; i < n; i++) {
+            a.heads.qn[i] = jobs[i].q_norm;
+            a.heads.kn[i] = jobs[i].k_norm;
+            a.heads.row0[i] = jobs[i].row0;
+        }
+    }
     if (epi.kind == kEpiSplitSwiglu)  // the plain panels, then the SwiGLU ones
         a.tiles_n = epi.split / 256u + (swiglu_outputs(epi, N) + 127u) / 128u;
     return a;
@@ -1581,9 +1592,14 @@ hipError_t run_job_fallback(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t
         const ResidualArgs r{j.y, t, nullptr, j.gate, epi.ldy, N, j.M, N, 0.0f};
         return launch_residual(r, false, st);
     }
+    if (const GemmHeads* h = epi.heads) {  // columns [0, split) into the heads
+        const QkvHeadsArgs q{t, j.q_norm, j.k_norm, h->cos, h->sin, h->q, h->k, h->v, N, j.M, h->n_heads, h->seq,
+                             j.row0, h->eps};
+        if ((e = launch_qkv_heads(q, h->otype, st)) != hipSuccess) return e;
+    }
     if (epi.kind == kEpiSplitSwiglu) {  // columns [0, split) copied, then silu(gate) * up
         const uint32_t f = swiglu_outputs(epi, N);
-        if (epi.split > 0) {
+        if (epi.split > 0 && !epi.heads) {
             const ActColsArgs c{t, j.y, N, 0u, 0u, epi.ldy, 0u, j.M, epi.split};
             if ((e = launch_act_cols(c, kActCopy, kGgmlF32, st)) != hipSuccess) return e;
         }
@@ -1591,7 +1607,7 @@ hipError_t run_job_fallback(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t
         return launch_act_cols(c, kActSiluMul, epi.y2_type, st);
     }
     const uint32_t split = epi.kind == kEpiSplitGelu ? epi.split : N;
-    if (split > 0) {
+    if (split > 0 && !epi.heads) {
         const ActColsArgs c{t, j.y, N, 0u, 0u, epi.ldy, 0u, j.M, split};
         if ((e = launch_act_cols(c, kActCopy, kGgmlF32, st)) != hipSuccess) return e;
     }

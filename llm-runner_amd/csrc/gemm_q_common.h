@@ -33,11 +33,29 @@ struct NextImages {
     uint32_t wtype, N, K;
     uint32_t items;       // items built by the GEMM's idle workgroups (0: none)
 };
+// Head routing of the split-epilogue GEMMs' first `split` = 3 H 128 output
+// features (q non-null): feature slot * H * 128 + head * 128 + f (slot Q, K,
+// V) of token m of problem p goes, per-head RMS-normalised (Q, K with a norm
+// weight) and rotated (Q, K with tables), to dst_slot[head, row0[p] + m, f]
+// in 16 bits instead of to Y.
+struct HeadsEpi {
+    void* q;  // [n_heads, seq, 128] each; null: no head routing
+    void* k;
+    void* v;
+    const float* cos;  // [seq, 64] or null
+    const float* sin;
+    const float* qn[2];  // per problem: [128] or null
+    const float* kn[2];
+    uint32_t row0[2];
+    uint32_t n_heads, seq, out_bf16;
+    float eps;
+};
 struct PersistArgs {
     PersistProblem p[2];
     const uint8_t* W2;  // SwiGLU: the up weight (p[0].W is the gate)
     uint32_t N, K, tiles_m, tiles_n;  // tiles_m of both problems
     uint32_t epi, ldy, ldy2, split, y2_bf16;
+    HeadsEpi heads;
     NextImages next;
 };
 
@@ -343,6 +361,102 @@ __device__ __forceinline__ T pick(uint32_t p, T a, T b) {
 }
 
 
+// Head routing of one wave's 128 features n0w .. n0w + 127, one head of one
+// Q/K/V slot (split % 128 == 0), for its 128 tokens, as qkv_heads_kernel
+// computes it from the f32 GEMM output, bit for bit: per token the sum of
+// the squares of its 64 pairs (2j, 2j + 1) in the same tree as that
+// kernel's butterfly over pairs (a lane holds pairs j = 16 a + 4 g + 2 kh +
+// e, so the levels across a, g are in the lane, the level across kh is the
+// partner lane's, and the level across e comes last), x * rms * norm[f],
+// pairs rotated by cos/sin[t, j], rounded to 16 bits into dst[head, t, f].
+__device__ __forceinline__ void store_heads(f32x16 (&acc)[4][4], const HeadsEpi& h, uint32_t p, uint32_t M,
+                                            uint32_t m0, uint32_t n0w, uint32_t wm, uint32_t l32, uint32_t kh) {
+#pragma clang fp contract(off)
+    const uint32_t hs = n0w / 128u, slot = hs / h.n_heads, head = hs - slot * h.n_heads;
+    uint16_t* const dst = (uint16_t*)(slot == 0 ? h.q : slot == 1 ? h.k : h.v) + (uint64_t)head * h.seq * 128u;
+    const float* const nw = slot == 0 ? pick(p, h.qn[0], h.qn[1]) : slot == 1 ? pick(p, h.kn[0], h.kn[1]) : nullptr;
+    const bool rope = slot < 2 && h.cos != nullptr;
+    const uint32_t row0 = pick(p, h.row0[0], h.row0[1]);
+    // buffer loads: 32-bit offsets whose constant parts fold into the
+    // instructions (per-lane 64-bit pointers for the 16 (a, g) pieces were
+    // hoisted out of the tile loop and spilled)
+    const rsrc_t nr = make_rsrc(nw, nw ? 512u : 0u);
+    const rsrc_t cr = make_rsrc(h.cos, rope ? (uint64_t)h.seq * 256u : 0u);
+    const rsrc_t sr = make_rsrc(h.sin, rope ? (uint64_t)h.seq * 256u : 0u);
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        asm volatile("" : "+a"(acc[0][b]), "+a"(acc[1][b]), "+a"(acc[2][b]), "+a"(acc[3][b]));
+        const uint32_t m = m0 + wm * 128u + b * 32u + l32;
+        const uint32_t t = row0 + m;            // < seq for m < M (host-checked)
+        const uint32_t tt = m < M ? t : row0;   // the table row read
+        float rms = 1.0f;
+        if (nw) {
+            float t4[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                float t3[2];
+#pragma unroll
+                for (int gl = 0; gl < 2; gl++) {
+                    float t2[2];
+#pragma unroll
+                    for (int gh = 0; gh < 2; gh++) {
+                        const int g = 2 * gh + gl;
+                        float t1[2];
+#pragma unroll
+                        for (int al = 0; al < 2; al++) {
+                            float sq[2];
+#pragma unroll
+                            for (int ah = 0; ah < 2; ah++) {
+                                const float x0 = acc[2 * ah + al][b][4 * g + 2 * e];
+                                const float x1 = acc[2 * ah + al][b][4 * g + 2 * e + 1];
+                                sq[ah] = x0 * x0 + x1 * x1;
+                            }
+                            t1[al] = sq[0] + sq[1];
+                        }
+                        t2[gh] = t1[0] + t1[1];
+                    }
+                    t3[gl] = t2[0] + t2[1];
+                }
+                t4[e] = t3[0] + t3[1];
+            }
+            float t5[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(t4[e]), __float_as_uint(t4[e]),
+                                                                false, false);
+                t5[e] = t4[e] + __uint_as_float(kh ? r[0] : r[1]);  // plus the partner lane's
+            }
+            rms = 1.0f / __builtin_sqrtf((t5[0] + t5[1]) / 128.0f + h.eps);
+        }
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const uint32_t f = 32u * a + 8u * g + 4u * kh;
+                f32x4 x{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
+                // the (a, g) part of each offset as the constant soffset
+                if (nw) {
+                    const f32x4 w = __builtin_bit_cast(
+                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(nr, 16u * kh, 128u * a + 32u * g, 0));
+#pragma unroll
+                    for (int e = 0; e < 4; e++) x[e] = (x[e] * rms) * w[e];
+                }
+                if (rope) {
+                    const uint32_t co = tt * 256u + 8u * kh, cs = 64u * a + 16u * g;
+                    const f32x2 c = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(cr, co, cs, 0));
+                    const f32x2 sn = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(sr, co, cs, 0));
+                    x = f32x4{x.x * c.x - x.y * sn.x, x.x * sn.x + x.y * c.x, x.z * c.y - x.w * sn.y,
+                              x.z * sn.y + x.w * c.y};
+                }
+                const u32x2 pk = h.out_bf16 ? u32x2{pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w)}
+                                            : u32x2{pack_f16x2(x.x, x.y), pack_f16x2(x.z, x.w)};
+                if (m < M) *(u32x2*)(dst + (uint64_t)t * 128u + f) = pk;
+            }
+#pragma unroll
+        for (int a = 0; a < 4; a++) acc[a][b] = f32x16{};
+    }
+}
+
 // Stores (through the epilogue EPI) and clears the accumulators of one
 // 256 x 256 tile of the 4-wave persistent kernels: wave (wm, wn) holds
 // tokens m0 + 128 wm + 32 b + l32 and features n0 + 128 wn + 32 a + 8 g +
@@ -356,7 +470,16 @@ template <bool SW, uint32_t EPI>
 __device__ __forceinline__ void store_tile_256(f32x16 (&acc)[4][4], float* Y, const float* gate, void* Y2v,
                                                uint32_t M, uint32_t N, uint32_t m0, uint32_t n0, uint32_t wm,
                                                uint32_t wn, uint32_t l32, uint32_t kh, uint32_t ldy, uint32_t ldy2,
-                                               uint32_t split, uint32_t y2_bf16) {
+                                               uint32_t split, uint32_t y2_bf16, const HeadsEpi& hd, uint32_t p) {
+    if constexpr (EPI == kEpiSplitGelu || EPI == kEpiSplitSwiglu) {
+        // a wave's 128 features lie wholly below or above split (split % 128
+        // == 0 with head routing; split % 256 == 0 for SwiGLU, where the
+        // tiles past split hold other rows)
+        if (hd.q != nullptr && n0 + wn * 128u < split) {
+            store_heads(acc, hd, p, M, m0, n0 + wn * 128u, wm, l32, kh);
+            return;
+        }
+    }
     if constexpr (SW) {
 #pragma unroll
         for (int a = 0; a < 2; a++)
@@ -462,6 +585,7 @@ __device__ __forceinline__ void store_tile_256(f32x16 (&acc)[4][4], float* Y, co
             const bool paired = pair_ok && nb >= split && nb + 32u <= N;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
+                asm volatile("" : "+a"(acc[a][b]));
                 const uint32_t m = m0 + wm * 128u + b * 32u + l32;
                 if (paired) {
                     u32x2 pc[4];

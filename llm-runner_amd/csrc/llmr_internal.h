@@ -44,9 +44,25 @@ struct GemmJob {
     const float* gate;
     void* y2;
     uint32_t M, row_offset;
+    const float* q_norm;  // head routing (GemmEpilogue::heads): [128] or null
+    const float* k_norm;
+    uint32_t row0;        // sequence position of token 0
+};
+// Head routing of the split epilogues' first `split` = 3 n_heads 128
+// columns (Q | K | V) into q, k, v [n_heads, seq, 128] of otype (16-bit):
+// per job, what launch_qkv_heads computes from the f32 result.
+struct GemmHeads {
+    void* q;
+    void* k;
+    void* v;
+    const float* cos;  // [seq, 64] or null
+    const float* sin;
+    uint32_t n_heads, seq, otype;
+    float eps;
 };
 struct GemmEpilogue {
     uint32_t kind, ldy, ldy2, split, y2_type;
+    const GemmHeads* heads;  // null, or (kind kEpiSplitGelu / kEpiSplitSwiglu) the Q | K | V routing
 };
 struct NextImageSet;  // the next GEMM group's weight images (below)
 // prebuilt_images: the caller passes the two-pass groups' weight images

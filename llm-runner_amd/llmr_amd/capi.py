@@ -64,6 +64,19 @@ class NextWeightImages(ctypes.Structure):
 EPI_STORE, EPI_GATED_RESIDUAL, EPI_SPLIT_GELU, EPI_SPLIT_SWIGLU = 0, 1, 2, 3
 
 
+class QkvHeadsJob(ctypes.Structure):
+    """llmr_qkv_heads_job: one job's head norms and first sequence position."""
+    _fields_ = [("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p), ("row0", ctypes.c_uint32)]
+
+
+class QkvHeadsOut(ctypes.Structure):
+    """llmr_qkv_heads_out: the Q | K | V routing of llmr_batch_matmul_multi_qkv."""
+    _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("out_type", ctypes.c_uint32), ("n_heads", ctypes.c_uint32), ("seq_len", ctypes.c_uint32),
+                ("eps", ctypes.c_float), ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
+                ("jobs", ctypes.POINTER(QkvHeadsJob))]
+
+
 class GgufTensorInfo(ctypes.Structure):
     """llmr_gguf_tensor_info."""
     _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_uint32), ("n_dims", ctypes.c_uint32),
@@ -107,6 +120,9 @@ _SIGS = {
     "llmr_batch_matmul_multi_images": (ctypes.c_int, [_vp, _u32, _u32, _u32, _u32, ctypes.POINTER(MatmulJob), _u32,
                                                       ctypes.POINTER(MatmulEpilogue), ctypes.POINTER(_vp),
                                                       ctypes.POINTER(NextWeightImages)]),
+    "llmr_batch_matmul_multi_qkv": (ctypes.c_int, [_vp, _u32, _u32, _u32, _u32, ctypes.POINTER(MatmulJob), _u32,
+                                                   ctypes.POINTER(MatmulEpilogue), ctypes.POINTER(QkvHeadsOut),
+                                                   ctypes.POINTER(_vp), ctypes.POINTER(NextWeightImages)]),
     "llmr_weight_image_bytes": (ctypes.c_size_t, [_u32, _u32]),
     "llmr_build_weight_image": (ctypes.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, ctypes.c_size_t]),
     "llmr_batch_matmul_swiglu": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32]),
@@ -252,6 +268,21 @@ class Context:
         check(lib().llmr_batch_matmul_multi_images(self._h, wtype, xtype, out_dim, in_dim, arr, len(jobs),
                                                    ctypes.byref(epilogue) if epilogue is not None else None, imgs,
                                                    ctypes.byref(next_images) if next_images is not None else None))
+
+    def batch_matmul_multi_qkv(self, wtype: int, xtype: int, out_dim: int, in_dim: int, jobs, epilogue,
+                               heads: QkvHeadsOut, head_jobs=None, images=None,
+                               next_images: NextWeightImages | None = None) -> None:
+        """As batch_matmul_multi_images with the Q | K | V columns routed by
+        `heads`; head_jobs: one QkvHeadsJob per job, or None."""
+        arr = (MatmulJob * len(jobs))(*jobs)
+        imgs = (_vp * len(jobs))(*images) if images is not None else None
+        hj = (QkvHeadsJob * len(jobs))(*head_jobs) if head_jobs is not None else None
+        h = QkvHeadsOut(heads.q, heads.k, heads.v, heads.out_type, heads.n_heads, heads.seq_len, heads.eps,
+                        heads.rope_cos, heads.rope_sin, hj)
+        check(lib().llmr_batch_matmul_multi_qkv(self._h, wtype, xtype, out_dim, in_dim, arr, len(jobs),
+                                                ctypes.byref(epilogue) if epilogue is not None else None,
+                                                ctypes.byref(h), imgs,
+                                                ctypes.byref(next_images) if next_images is not None else None))
 
     def build_weight_image(self, w_ptr: int, wtype: int, xtype: int, out_dim: int, in_dim: int, row_offset: int,
                            img_ptr: int, img_bytes: int) -> None:

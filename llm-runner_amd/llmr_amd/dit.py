@@ -35,9 +35,9 @@ import torch
 
 from . import capi, glue, workloads
 from .gguf import GGML_Q4_K, GGML_Q8_0
-from .ops import _TORCH_GGML, FlashAttentionPC, MatmulJob, NextImages, RenderGraph, Tensor, build_weight_image, \
-    default_graph, dispatch_batch_matmul, dispatch_batch_matmul_multi, dispatch_batch_matmul_swiglu, \
-    dispatch_flash_attention, dispatch_flash_attention_rows, weight_image_bytes
+from .ops import _TORCH_GGML, FlashAttentionPC, MatmulJob, NextImages, QkvHeads, RenderGraph, Tensor, \
+    build_weight_image, default_graph, dispatch_batch_matmul, dispatch_batch_matmul_multi, \
+    dispatch_batch_matmul_swiglu, dispatch_flash_attention, dispatch_flash_attention_rows, weight_image_bytes
 
 HEAD_DIM = 128
 
@@ -88,7 +88,6 @@ class ZImageBlock:
         S = seq_len
         e = dict(device=device)
         self.xa = torch.empty(S, dim, dtype=act_dtype, **e)          # GEMM inputs of width dim
-        self.qkv = torch.empty(S, 3 * dim, dtype=torch.float32, **e)
         self.q = torch.empty(n_heads, S, HEAD_DIM, dtype=torch.float16, **e)
         self.k = torch.empty_like(self.q)
         self.v = torch.empty_like(self.q)
@@ -104,11 +103,12 @@ class ZImageBlock:
             raise ValueError("hidden must be f32 [seq_len, dim]")
         # A: pre-attention RMSNorm, * (1 + scale_msa)                 (dit.c3:1421-1432)
         glue.batch_rmsnorm(hidden, w.attn_norm1, self.xa, eps, mod_scale=w.adaln[0], g=g)
-        # B: Q | K | V in one call over the fused weight               (dit.c3:1435-1443)
-        dispatch_batch_matmul(g, _qt(w.wqkv, GGML_Q8_0, 3 * dim, dim), _t(self.xa), _t(self.qkv), 3 * dim, dim,
-                              S, 0)
-        # C: head norm, RoPE, head-major fp16 Q/K/V; attention         (dit.c3:1446-1483)
-        glue.qkv_heads(self.qkv, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, eps, (rope_cos, rope_sin), g=g)
+        # B, C: Q | K | V in one call over the fused weight, with the head
+        # norm, RoPE and head-major fp16 Q/K/V done on its result
+        # (dit.c3:1435-1473); attention                               (dit.c3:1476-1483)
+        dispatch_batch_matmul_multi(g, [MatmulJob(_qt(w.wqkv, GGML_Q8_0, 3 * dim, dim), _t(self.xa), None, S)],
+                                    3 * dim, dim, heads=QkvHeads(self.q, self.k, self.v, H, [(w.q_norm, w.k_norm, 0)],
+                                                                 eps, (rope_cos, rope_sin)))
         # (the attention rows go straight into the O-proj input, rounded to the
         # activation type: the reference's attention output plus its copy)
         dispatch_flash_attention_rows(g, _t(self.q), _t(self.k), _t(self.v), self.xa,
@@ -472,7 +472,6 @@ class FluxDiT:
         self.hidden = torch.empty(S, d, dtype=torch.float32, **e)   # joint residual stream, text rows first
         self.xa = torch.empty(S, d, dtype=act_dtype, **e)             # GEMM inputs of width dim
         self.patches = torch.empty(c.n_img, c.patch_dim, dtype=act_dtype, **e)
-        self.qkv = torch.empty(S, 3 * d, dtype=torch.float32, **e)   # Q | K | V rows (both block types)
         self.q = torch.empty(c.n_heads, S, HEAD_DIM, dtype=torch.float16, **e)
         self.k = torch.empty_like(self.q)
         self.v = torch.empty_like(self.q)
@@ -553,15 +552,22 @@ class FluxDiT:
         glue.unpatchify(self.velocity, self.out, c.patch, g=g)
         return self.out
 
-    def _multi(self, jobs, N: int, K: int, epilogue: int = capi.EPI_STORE, split: int = 0) -> None:
+    def _multi(self, jobs, N: int, K: int, epilogue: int = capi.EPI_STORE, split: int = 0,
+               heads: QkvHeads | None = None) -> None:
         """The blocks' next GEMM group (dispatch_batch_matmul_multi), taking its
         weight images from the chain (and building the following group's)
         when self.ahead is set."""
         if self.ahead is None or not self.ahead.active:  # a block run outside forward(): no chain
-            dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split)
+            dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split, heads=heads)
             return
         images, nxt = self.ahead.take(jobs, N, K)
-        dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split, images=images, next_images=nxt)
+        dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split, images=images, next_images=nxt,
+                                    heads=heads)
+
+    def _heads(self, norms) -> QkvHeads:
+        """The joint Q/K/V as the QKV projections' head routing; norms: per job
+        (q_norm, k_norm, first sequence row)."""
+        return QkvHeads(self.q, self.k, self.v, self.cfg.n_heads, norms, self.HN_EPS, self.rope)
 
     def _attention(self, S: int, out: torch.Tensor) -> None:
         """Attention over the joint Q/K/V, its rows written into `out` (the next
@@ -575,28 +581,26 @@ class FluxDiT:
         stream. Each projection multiplies both streams in one launch
         (text rows first, each with its own weight)."""
         c, g = self.cfg, self.g
-        d, m, nt, H, S = c.dim, c.mlp, c.n_txt, c.n_heads, c.seq
+        d, m, nt, S = c.dim, c.mlp, c.n_txt, c.seq
         ts, im = slice(0, nt), slice(nt, S)
         ni = S - nt
 
         def jobs(wt, wi, K, x, out, gates=(None, None), out2=None):
             """[text job, image job]: rows ts / im of x, out (and out2)."""
             rows = wt.numel() // (K // 256 * 144)
-            return [MatmulJob(_qt(wt, GGML_Q4_K, rows, K), _t(x[ts]), out[ts], nt, 0, gates[0],
-                              None if out2 is None else out2[ts]),
-                    MatmulJob(_qt(wi, GGML_Q4_K, rows, K), _t(x[im]), out[im], ni, 0, gates[1],
-                              None if out2 is None else out2[im])]
+            return [MatmulJob(_qt(wt, GGML_Q4_K, rows, K), _t(x[ts]), None if out is None else out[ts], nt, 0,
+                              gates[0], None if out2 is None else out2[ts]),
+                    MatmulJob(_qt(wi, GGML_Q4_K, rows, K), _t(x[im]), None if out is None else out[im], ni, 0,
+                              gates[1], None if out2 is None else out2[im])]
 
         # LayerNorm + modulation of each stream                      (flux_dit.c3:761-779)
         for sl, mod in ((ts, mt), (im, mi)):
             glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0],
                                  g=g)
-        # Q | K | V of both streams; head norm + RoPE into the joint Q/K/V (flux_dit.c3:786-863)
-        self._multi(jobs(w.txt_qkv, w.img_qkv, d, self.xa, self.qkv), 3 * d, d)
-        glue.qkv_heads(self.qkv[ts], H, self.q, self.k, self.v, 0, w.txt_q_norm, w.txt_k_norm, self.HN_EPS,
-                       self.rope, g=g)
-        glue.qkv_heads(self.qkv[im], H, self.q, self.k, self.v, nt, w.img_q_norm, w.img_k_norm, self.HN_EPS,
-                       self.rope, g=g)
+        # Q | K | V of both streams, head norm + RoPE into the joint Q/K/V (text
+        # rows first) on the projections' result                 (flux_dit.c3:786-863)
+        self._multi(jobs(w.txt_qkv, w.img_qkv, d, self.xa, None), 3 * d, d,
+                    heads=self._heads([(w.txt_q_norm, w.txt_k_norm, 0), (w.img_q_norm, w.img_k_norm, nt)]))
         # attention rows straight into the projection input             (flux_dit.c3:865-872)
         self._attention(S, self.xa)
         # output projections, hidden += gate1 * proj                  (flux_dit.c3:875-898)
@@ -619,15 +623,15 @@ class FluxDiT:
     def _single(self, w: FluxSingleWeights, mod: torch.Tensor) -> None:
         """flux_single_stream_block (flux_dit.c3:975-1071). mod: [3, dim] (shift, scale, gate)."""
         c, g = self.cfg, self.g
-        d, m, H, S = c.dim, c.mlp, c.n_heads, c.seq
+        d, m, S = c.dim, c.mlp, c.seq
         glue.batch_layernorm(self.hidden, self.xa, self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0], g=g)
-        # linear1: Q | K | V (f32) and the activated MLP half (gelu; swiglu: silu(gate) * up)
-        # straight into linear2's input                               (flux_dit.c3:1005-1058)
+        # linear1: Q | K | V head-normed and rotated into the joint Q/K/V, and
+        # the activated MLP half (gelu; swiglu: silu(gate) * up) straight into
+        # linear2's input                                             (flux_dit.c3:1005-1058)
         n1 = 3 * d + c.mlp_in
-        self._multi([MatmulJob(_qt(w.linear1, GGML_Q4_K, n1, d), _t(self.xa), self.qkv, S, 0, None,
-                               self.cat[:, d:])],
-                    n1, d, capi.EPI_SPLIT_SWIGLU if c.mlp_act == "swiglu" else capi.EPI_SPLIT_GELU, split=3 * d)
-        glue.qkv_heads(self.qkv, H, self.q, self.k, self.v, 0, w.q_norm, w.k_norm, self.HN_EPS, self.rope, g=g)
+        self._multi([MatmulJob(_qt(w.linear1, GGML_Q4_K, n1, d), _t(self.xa), None, S, 0, None, self.cat[:, d:])],
+                    n1, d, capi.EPI_SPLIT_SWIGLU if c.mlp_act == "swiglu" else capi.EPI_SPLIT_GELU, split=3 * d,
+                    heads=self._heads([(w.q_norm, w.k_norm, 0)]))
         self._attention(S, self.cat[:, :d])  # rows into linear2's input  (flux_dit.c3:1042-1047)
         # linear2, hidden += gate * linear2                           (flux_dit.c3:1060-1068)
         self._multi([MatmulJob(_qt(w.linear2, GGML_Q4_K, d, d + m), _t(self.cat), self.hidden, S, 0, mod[2])],

@@ -244,6 +244,50 @@ def build_weight_image(g: RenderGraph, weight: Tensor, out_dim: int, in_dim: int
 
 
 @dataclasses.dataclass
+class QkvHeads:
+    """Head routing of a QKV projection's Q | K | V columns (llmr_qkv_heads_out):
+    q, k, v [n_heads, seq, 128] f16 / bf16 device tensors, the RoPE tables
+    (cos, sin f32 [seq, 64]) or None, and per job (q_norm, k_norm, row0):
+    its head-norm weights ([128] f32 or None) and the sequence position of its
+    token 0."""
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    n_heads: int
+    jobs: list
+    eps: float = 1e-6
+    rope: tuple | None = None
+
+
+def _qkv_heads_out(h: QkvHeads, n_jobs: int) -> tuple:
+    H, S, D = h.q.shape
+    if D != 128 or H != h.n_heads or h.k.shape != h.q.shape or h.v.shape != h.q.shape:
+        raise ValueError("q/k/v must be [n_heads, seq, 128] alike")
+    if not (h.q.dtype == h.k.dtype == h.v.dtype) or h.q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("q/k/v must share one dtype, float16 or bfloat16")
+    if not all(t.is_contiguous() and t.is_cuda for t in (h.q, h.k, h.v)):
+        raise ValueError("q/k/v must be contiguous device tensors")
+    if len(h.jobs) != n_jobs:
+        raise ValueError("one (q_norm, k_norm, row0) per job")
+
+    def vec(t, what, n):
+        if t is None:
+            return None
+        if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous() or t.numel() < n:
+            raise ValueError(f"{what} must be a contiguous f32 device tensor of {n} elements")
+        return t.data_ptr()
+
+    cos_p = sin_p = None
+    if h.rope is not None:
+        cos_p = vec(h.rope[0], "rope_cos", S * 64)
+        sin_p = vec(h.rope[1], "rope_sin", S * 64)
+    hj = [capi.QkvHeadsJob(vec(qn, "q_norm", 128), vec(kn, "k_norm", 128), row0) for qn, kn, row0 in h.jobs]
+    out = capi.QkvHeadsOut(h.q.data_ptr(), h.k.data_ptr(), h.v.data_ptr(), _TORCH_GGML[h.q.dtype], H, S,
+                           float(h.eps), cos_p, sin_p, None)
+    return out, hj
+
+
+@dataclasses.dataclass
 class NextImages:
     """The weight images of the GEMM group issued next (llmr_next_weight_images):
     its weights (one or two Tensors of one type, rows from row_offsets) and
@@ -257,7 +301,7 @@ class NextImages:
 
 def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim: int,
                                 epilogue: int = capi.EPI_STORE, split: int = 0, images=None,
-                                next_images: NextImages | None = None) -> None:
+                                next_images: NextImages | None = None, heads: QkvHeads | None = None) -> None:
     """The jobs' GEMMs with a shared epilogue (llmr_batch_matmul_multi): a plain
     store, `output += gate * result` (gated_residual_linear), a column split
     whose features >= split are GELU'd into output2 (linear1's MLP half feeding
@@ -271,7 +315,11 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
     or an earlier call's next_images, same weight, row_offset and input
     type), used where a pair runs two-pass; next_images: the next group's
     images, built partly by this call's idle workgroups and complete when
-    the stream's next call starts (llmr_batch_matmul_multi_images)."""
+    the stream's next call starts (llmr_batch_matmul_multi_images). heads: the
+    Q | K | V columns (all of a plain store, [0, split) of a split) head-normed,
+    rotated and written head-major into heads.q/k/v instead of `output`, which
+    may then be None (llmr_batch_matmul_multi_qkv; batch_head_norm +
+    transpose_heads + mrope after the QKV projection, flux_dit.c3:786-863)."""
     if not jobs:
         return
     wtype, xtype = jobs[0].weight.dtype, jobs[0].input.dtype
@@ -289,7 +337,7 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
         return strides.pop() if strides else (views[0].shape[1] + 3) // 4 * 4
 
     swiglu = epilogue == capi.EPI_SPLIT_SWIGLU
-    no_out = swiglu and split == 0
+    no_out = (swiglu and split == 0) or heads is not None
     if no_out:
         ldy = 0
     else:
@@ -331,8 +379,9 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
         cj.append(capi.MatmulJob(j.weight.ptr(), j.input.ptr(), None if no_out else j.output.data_ptr(),
                                  gp or None, o2 or None, j.seq_len, j.row_offset))
     epi = capi.MatmulEpilogue(epilogue, ldy, split, ldy2, o2type)
+    hout = _qkv_heads_out(heads, len(jobs)) if heads is not None else None
     g.bind_stream()
-    if images is None and next_images is None:
+    if images is None and next_images is None and hout is None:
         g.ctx.batch_matmul_multi(wtype, xtype, out_dim, in_dim, cj, epi)
         return
     ptrs = None
@@ -363,7 +412,10 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
                                    (ctypes.c_uint32 * 2)(*(list(n.row_offsets[:k]) + [0] * (2 - k))),
                                    (ctypes.c_void_p * 2)(*[im.data_ptr() for im in n.images] + [None] * (2 - k)),
                                    nbytes)
-    g.ctx.batch_matmul_multi_images(wtype, xtype, out_dim, in_dim, cj, epi, ptrs, nx)
+    if hout is not None:
+        g.ctx.batch_matmul_multi_qkv(wtype, xtype, out_dim, in_dim, cj, epi, hout[0], hout[1], ptrs, nx)
+    else:
+        g.ctx.batch_matmul_multi_images(wtype, xtype, out_dim, in_dim, cj, epi, ptrs, nx)
 
 
 def dispatch_batch_matmul_swiglu(g: RenderGraph, weight_gate: Tensor, weight_up: Tensor,
