@@ -265,6 +265,68 @@ def setup_zimage_block(dev):
     return step, flops, None, cfg, "bf16"
 
 
+def setup_zimage_block_c3(dev):
+    """The Z-Image block at the same full size as a compiled C caller with the
+    reference's buffer types issues it: the call order of the C11 harness
+    tests/c/zimage_layer.c (dit.c3:1421-1610), f32 activation buffers
+    throughout, each GEMM through llmr_batch_matmul_pc (the QKV projection
+    over the fused weight), the SwiGLU through llmr_batch_matmul_swiglu_pc,
+    head norm + RoPE + transpose into f32 Q/K/V by llmr_qkv_heads, attention
+    through llmr_flash_attention_pc, norms and gated residuals by the glue
+    entry points. Device pointers and push constants are resolved once."""
+    import ctypes
+
+    import torch
+    from llmr_amd import capi, dit, synth, workloads
+    from llmr_amd.gguf import GGML_Q8_0
+    dim, H, ffn = 3840, 30, 10240
+    a = workloads.ZIMAGE_ATTENTION
+    S, eps = a.S, dit.ZImageBlock.EPS
+    w = dit.zimage_layer_weights(dim, H, ffn, device=dev)
+    cos_t, sin_t = (torch.from_numpy(t).to(dev) for t in
+                    workloads.rope_tables(workloads.attention_positions(a), a.axes, a.theta))
+    hidden = torch.from_numpy(synth.normal(workloads.SEED, 10, S * dim).reshape(S, dim)).to(dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    buf_a, qkv, attn, t = (torch.empty(S, n, **f32) for n in (dim, 3 * dim, dim, dim))
+    f = torch.empty(S, ffn, **f32)
+    qh, kh, vh = (torch.empty(H, S, 128, **f32) for _ in range(3))
+    ctx = _bound_ctx()
+    lib, h, F32, Q8 = capi.lib(), ctx.handle, 0, GGML_Q8_0
+    p = {k: v.data_ptr() for k, v in vars(w).items() if isinstance(v, torch.Tensor)}
+    pc_qkv = capi.BatchMatMulParams(3 * dim, dim, S, 0)
+    pc_o = capi.BatchMatMulParams(dim, dim, S, 0)
+    pc_sw = capi.BatchMatMulParams(ffn, dim, S, 0)
+    pc_down = capi.BatchMatMulParams(dim, ffn, S, 0)
+    fa = capi.FlashAttentionParams(128, H, S, 1.0 / math.sqrt(128.0))
+    ad = p["adaln"]
+    hp, ap, qp, atp, tp, fp = (x.data_ptr() for x in (hidden, buf_a, qkv, attn, t, f))
+
+    def step():
+        ck = capi.check
+        ck(lib.llmr_batch_rmsnorm(h, hp, dim, p["attn_norm1"], ad, None, ap, F32, dim, dim, S, ctypes.c_float(eps)))
+        ck(lib.llmr_batch_matmul_pc(h, p["wqkv"], Q8, ap, F32, qp, ctypes.byref(pc_qkv)))
+        ck(lib.llmr_qkv_heads(h, qp, 3 * dim, S, H, p["q_norm"], p["k_norm"], ctypes.c_float(eps), cos_t.data_ptr(),
+                              sin_t.data_ptr(), qh.data_ptr(), kh.data_ptr(), vh.data_ptr(), F32, S, 0))
+        ck(lib.llmr_flash_attention_pc(h, qh.data_ptr(), kh.data_ptr(), vh.data_ptr(), F32, atp, ctypes.byref(fa)))
+        ck(lib.llmr_batch_matmul_pc(h, p["wo"], Q8, atp, F32, tp, ctypes.byref(pc_o)))
+        ck(lib.llmr_gated_residual(h, hp, dim, tp, dim, p["attn_norm2"], ad + 4 * dim, capi.GATE_TANH, dim, S,
+                                   ctypes.c_float(eps)))
+        ck(lib.llmr_batch_rmsnorm(h, hp, dim, p["ffn_norm1"], ad + 8 * dim, None, ap, F32, dim, dim, S,
+                                  ctypes.c_float(eps)))
+        ck(lib.llmr_batch_matmul_swiglu_pc(h, p["w_gate"], p["w_up"], Q8, ap, F32, fp, ctypes.byref(pc_sw)))
+        ck(lib.llmr_batch_matmul_pc(h, p["w_down"], Q8, fp, F32, tp, ctypes.byref(pc_down)))
+        ck(lib.llmr_gated_residual(h, hp, dim, tp, dim, p["ffn_norm2"], ad + 12 * dim, capi.GATE_TANH, dim, S,
+                                   ctypes.c_float(eps)))
+
+    flops = 2.0 * S * dim * (3 * dim + dim + 2 * ffn + ffn) + a.flops
+    cfg = {"workload": "zimage_block_c3", "hidden": dim, "heads": H, "head_dim": 128, "ffn": ffn, "seq_len": S,
+           "weights": "Q8_0", "activations": "f32 (every buffer, as the reference's)",
+           "calls": "tests/c/zimage_layer.c order: rmsnorm, batch_matmul_pc (QKV), qkv_heads (f32), "
+           "flash_attention_pc (f32), batch_matmul_pc (O), gated_residual, rmsnorm, batch_matmul_swiglu_pc, "
+           "batch_matmul_pc (down), gated_residual"}
+    return step, flops, None, cfg, "f32"
+
+
 def setup_flux_step(dev, mlp_act: str = "gelu"):
     """One denoising forward of the Flux-dev-shaped DiT (19 double + 38 single
     blocks, hidden 3072, 24 heads, MLP 12288, Q4_K weights generated on the
@@ -295,7 +357,8 @@ def setup_flux_step(dev, mlp_act: str = "gelu"):
     return step, cfg_m.gemm_flops(), None, cfg, "bf16"
 
 
-MODEL_SETUPS = {"zimage_block": setup_zimage_block, "flux_step": setup_flux_step,
+MODEL_SETUPS = {"zimage_block": setup_zimage_block, "zimage_block_c3": setup_zimage_block_c3,
+                "flux_step": setup_flux_step,
                 "flux2_step": lambda dev: setup_flux_step(dev, "swiglu")}
 
 
@@ -430,7 +493,8 @@ def main():
     ap.add_argument("--workload", default="flux_attention")
     ap.add_argument("--components",
                     default="flux_linear1,flux_linear2,q8_linear,zimage_qkv,zimage_swiglu,flux_linear1_f32,"
-                            "flux_linear2_f32,flux_attention_f32,lora_flux_linear1,flux_linear1_lora,zimage_block,flux_step,"
+                            "flux_linear2_f32,flux_attention_f32,lora_flux_linear1,flux_linear1_lora,zimage_block,"
+                            "zimage_block_c3,flux_step,"
                             "flux2_step")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--hbm-copy-calibration", action="store_true",

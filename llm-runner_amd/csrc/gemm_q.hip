@@ -615,7 +615,7 @@ __global__ void __launch_bounds__(256, 1) gemm_q_persist(const PersistArgs args)
         uint32_t p, m0, n0;
         tile_origin(k, p, m0, n0);
         store_tile_256<SW, EPI>(acc, pick(p, Yp0, Yp1), pick(p, Gp0, Gp1), pick(p, Y2p0, Y2p1), pick(p, Mp0, Mp1), N,
-                                m0, n0, wm, wn, l32, kh, ldy, ldy2, split, y2_bf16, args.heads, p);
+                                m0, n0, wm, wn, l32, kh, ldy, ldy2, split, y2_bf16);
     };
 
     // prologue, issued in the steady state's order (a stage issues the
@@ -1524,8 +1524,8 @@ hipError_t build_split_swiglu_image(const GemmJob& j, uint32_t wtype, uint32_t o
 bool multi_fused(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs, uint32_t n,
                  const GemmEpilogue& epi, int num_cus) {
     if (!multi_persistent(wtype, xtype, N, K, jobs, n, num_cus)) return false;
-    // head routing: the 4-wave kernels (two-pass, or one-pass Q4_K)
-    if (epi.heads && wtype == kGgmlQ8_0 && !multi_two_pass(jobs, n)) return false;
+    // head routing: the two-pass kernel's epilogue
+    if (epi.heads && !multi_two_pass(jobs, n)) return false;
     return epi.kind != kEpiSplitSwiglu || multi_two_pass(jobs, n);
 }
 

@@ -369,26 +369,54 @@ __device__ __forceinline__ T pick(uint32_t p, T a, T b) {
 // e, so the levels across a, g are in the lane, the level across kh is the
 // partner lane's, and the level across e comes last), x * rms * norm[f],
 // pairs rotated by cos/sin[t, j], rounded to 16 bits into dst[head, t, f].
+// A block's 32 tokens are consecutive rows of the RoPE tables, 8 KiB of
+// each: they are DMA'd whole into lc / ls (the wave's own 8 KiB of LDS
+// each), row r's logical 16-byte chunk c at physical chunk c ^ (r % 16), and
+// each lane reads its pairs from there (read from memory per lane, a row per
+// lane per load, the tables cost ~20 us per tile); a block's DMAs are issued
+// before its sums of squares. The norm weights are read as scalar loads
+// (both lanes' halves, selected by kh): as vector loads per block, their
+// latency cost ~9 us per tile.
 __device__ __forceinline__ void store_heads(f32x16 (&acc)[4][4], const HeadsEpi& h, uint32_t p, uint32_t M,
-                                            uint32_t m0, uint32_t n0w, uint32_t wm, uint32_t l32, uint32_t kh) {
+                                            uint32_t m0, uint32_t n0w, uint32_t wm, uint32_t l32, uint32_t kh,
+                                            uint8_t* lc, uint8_t* ls) {
 #pragma clang fp contract(off)
+    typedef __attribute__((address_space(4))) const float cfloat;
     const uint32_t hs = n0w / 128u, slot = hs / h.n_heads, head = hs - slot * h.n_heads;
     uint16_t* const dst = (uint16_t*)(slot == 0 ? h.q : slot == 1 ? h.k : h.v) + (uint64_t)head * h.seq * 128u;
-    const float* const nw = slot == 0 ? pick(p, h.qn[0], h.qn[1]) : slot == 1 ? pick(p, h.kn[0], h.kn[1]) : nullptr;
+    const float* const nwp = slot == 0 ? pick(p, h.qn[0], h.qn[1]) : slot == 1 ? pick(p, h.kn[0], h.kn[1]) : nullptr;
+    cfloat* const nw0 = (cfloat*)nwp;
     const bool rope = slot < 2 && h.cos != nullptr;
-    const uint32_t row0 = pick(p, h.row0[0], h.row0[1]);
-    // buffer loads: 32-bit offsets whose constant parts fold into the
-    // instructions (per-lane 64-bit pointers for the 16 (a, g) pieces were
-    // hoisted out of the tile loop and spilled)
-    const rsrc_t nr = make_rsrc(nw, nw ? 512u : 0u);
+    const uint32_t row0 = __builtin_amdgcn_readfirstlane(pick(p, h.row0[0], h.row0[1]));
     const rsrc_t cr = make_rsrc(h.cos, rope ? (uint64_t)h.seq * 256u : 0u);
     const rsrc_t sr = make_rsrc(h.sin, rope ? (uint64_t)h.seq * 256u : 0u);
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         asm volatile("" : "+a"(acc[0][b]), "+a"(acc[1][b]), "+a"(acc[2][b]), "+a"(acc[3][b]));
+        // the lane index opaque per block, so the 8 DMA and 16 LDS offsets
+        // derived from it are computed here, not kept live across the tile
+        // loop (which spilled the SwiGLU variants)
+        uint32_t lane = l32 + 32u * kh;
+        asm volatile("" : "+v"(lane));
+        const uint32_t r32 = lane & 31u, sw = lane & 15u;
+        // the norm pointer opaque per block too: its scalar loads stay here
+        // (hoisted out of the tile loop, they took SGPRs the loop needs)
+        cfloat* nw = nw0;
+        asm volatile("" : "+s"(nw));
         const uint32_t m = m0 + wm * 128u + b * 32u + l32;
-        const uint32_t t = row0 + m;            // < seq for m < M (host-checked)
-        const uint32_t tt = m < M ? t : row0;   // the table row read
+        const uint32_t t = row0 + m;  // < seq for m < M (host-checked)
+        if (rope) {
+            // DMA i: LDS rows 4 i .. 4 i + 3 (lane: row 4 i + lane / 16,
+            // physical chunk lane % 16); rows past the tables read zero
+            const uint32_t t0 = row0 + m0 + wm * 128u + b * 32u;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t r = 4u * i + (lane >> 4);
+                const uint32_t vo = r * 256u + (((lane & 15u) ^ (r & 15u)) << 4);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(cr, (lds_void*)(lc + 1024u * i), 16, vo, t0 * 256u, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_void*)(ls + 1024u * i), 16, vo, t0 * 256u, 0, 0);
+            }
+        }
         float rms = 1.0f;
         if (nw) {
             float t4[2];
@@ -428,23 +456,28 @@ __device__ __forceinline__ void store_heads(f32x16 (&acc)[4][4], const HeadsEpi&
             }
             rms = 1.0f / __builtin_sqrtf((t5[0] + t5[1]) / 128.0f + h.eps);
         }
+        if (rope) {  // this block's table rows have landed (its DMAs are the wave's only loads in flight)
+            asm volatile("" ::: "memory");
+            LLMR_WAIT_VMCNT(0);
+            asm volatile("" ::: "memory");
+        }
 #pragma unroll
         for (int a = 0; a < 4; a++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 const uint32_t f = 32u * a + 8u * g + 4u * kh;
                 f32x4 x{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
-                // the (a, g) part of each offset as the constant soffset
                 if (nw) {
-                    const f32x4 w = __builtin_bit_cast(
-                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(nr, 16u * kh, 128u * a + 32u * g, 0));
 #pragma unroll
-                    for (int e = 0; e < 4; e++) x[e] = (x[e] * rms) * w[e];
+                    for (int e = 0; e < 4; e++) {
+                        const float wl = nw[32 * a + 8 * g + e], wh = nw[32 * a + 8 * g + 4 + e];
+                        x[e] = (x[e] * rms) * (kh ? wh : wl);
+                    }
                 }
-                if (rope) {
-                    const uint32_t co = tt * 256u + 8u * kh, cs = 64u * a + 16u * g;
-                    const f32x2 c = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(cr, co, cs, 0));
-                    const f32x2 sn = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(sr, co, cs, 0));
+                if (rope) {  // pairs 16 a + 4 g + 2 kh + 0, 1: logical chunk 4 a + g of row l32, half kh
+                    const uint32_t lo = r32 * 256u + (((4u * a + g) ^ sw) << 4) + 8u * kh;
+                    const f32x2 c = *(const f32x2*)(lc + lo);
+                    const f32x2 sn = *(const f32x2*)(ls + lo);
                     x = f32x4{x.x * c.x - x.y * sn.x, x.x * sn.x + x.y * c.x, x.z * c.y - x.w * sn.y,
                               x.z * sn.y + x.w * c.y};
                 }
@@ -454,29 +487,28 @@ __device__ __forceinline__ void store_heads(f32x16 (&acc)[4][4], const HeadsEpi&
             }
 #pragma unroll
         for (int a = 0; a < 4; a++) acc[a][b] = f32x16{};
+        if (rope) {  // the reads of this block's rows are done before the next block's DMAs
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            asm volatile("" ::: "memory");
+        }
     }
 }
 
-// Stores (through the epilogue EPI) and clears the accumulators of one
-// 256 x 256 tile of the 4-wave persistent kernels: wave (wm, wn) holds
-// tokens m0 + 128 wm + 32 b + l32 and features n0 + 128 wn + 32 a + 8 g +
-// 4 kh + 0..3 in acc[a][b][4 g .. 4 g + 3]. SW: a 128-feature SwiGLU tile,
-// acc[a] (gate) and acc[a + 2] (up) of the same features, y = silu(g) * u.
-// N % 4 == 0 (host-checked): a lane's four consecutive features are all in
-// range or none. nw = n - 4 kh is the same for the whole wave; with split %
-// 8 == 0 (host-checked) nw < split decides the side of split for both kh, as
-// a uniform branch.
-template <bool SW, uint32_t EPI>
+// HEADS (the two-pass kernel): head routing of the split epilogues, the
+// wave's 8 KiB LDS regions lc, ls free for it (no DMA in flight into them).
+template <bool SW, uint32_t EPI, bool HEADS = false>
 __device__ __forceinline__ void store_tile_256(f32x16 (&acc)[4][4], float* Y, const float* gate, void* Y2v,
                                                uint32_t M, uint32_t N, uint32_t m0, uint32_t n0, uint32_t wm,
                                                uint32_t wn, uint32_t l32, uint32_t kh, uint32_t ldy, uint32_t ldy2,
-                                               uint32_t split, uint32_t y2_bf16, const HeadsEpi& hd, uint32_t p) {
-    if constexpr (EPI == kEpiSplitGelu || EPI == kEpiSplitSwiglu) {
+                                               uint32_t split, uint32_t y2_bf16, const HeadsEpi* hd = nullptr,
+                                               uint32_t p = 0, uint8_t* lc = nullptr, uint8_t* ls = nullptr) {
+    if constexpr (HEADS && (EPI == kEpiSplitGelu || EPI == kEpiSplitSwiglu)) {
         // a wave's 128 features lie wholly below or above split (split % 128
         // == 0 with head routing; split % 256 == 0 for SwiGLU, where the
         // tiles past split hold other rows)
-        if (hd.q != nullptr && n0 + wn * 128u < split) {
-            store_heads(acc, hd, p, M, m0, n0 + wn * 128u, wm, l32, kh);
+        if (hd->q != nullptr && n0 + wn * 128u < split) {
+            store_heads(acc, *hd, p, M, m0, n0 + wn * 128u, wm, l32, kh, lc, ls);
             return;
         }
     }

@@ -519,9 +519,9 @@ __global__ void __launch_bounds__(256, 1) gemm_w16_persist(const PersistArgs arg
             store_tile_rows(acc, pick(p, Yp0, Yp1), pick(p, Mp0, Mp1), N, m0, n0, wm, wn, lane, ldy,
                             X2 + wave * 8192u);
         else
-            store_tile_256<SW, EPI>(acc, pick(p, Yp0, Yp1), pick(p, Gp0, Gp1), pick(p, Y2p0, Y2p1),
-                                    pick(p, Mp0, Mp1), N, m0, n0, wm, wn, l32, kh, ldy, ldy2, split, y2_bf16,
-                                    args.heads, p);
+            store_tile_256<SW, EPI, true>(acc, pick(p, Yp0, Yp1), pick(p, Gp0, Gp1), pick(p, Y2p0, Y2p1),
+                                          pick(p, Mp0, Mp1), N, m0, n0, wm, wn, l32, kh, ldy, ldy2, split, y2_bf16,
+                                          &args.heads, p, X2 + wave * 8192u, W1 + wave * 8192u);
     };
 
     if (n_tiles > 0) {

@@ -3,8 +3,9 @@ and head-major Q/K/V done on its result in the GEMM epilogue
 (flux_dit.c3:786-863, 1005-1040; dit.c3:1434-1473), against the unfused
 composition: llmr_batch_matmul_multi, then llmr_qkv_heads on its f32
 result (each of which the oracle checks: test_gpu_gemm.py, test_gpu_glue.py).
-Bit for bit on every path the call takes: the two-pass and the one-pass
-persistent kernels, and the GEMM into the workspace plus the glue pass. The
+Bit for bit on both paths the call takes: the two-pass persistent kernel's
+epilogue (from a few thousand tokens), and the GEMM into the workspace plus
+the glue pass. The
 cases cover pairs of jobs with their own norms and first rows; the STORE,
 SPLIT_GELU and SPLIT_SWIGLU epilogues; an odd head count, where a tile
 straddles the Q | K | V end; and f16 and bf16 Q/K/V."""
@@ -38,8 +39,8 @@ def _weight(seed, wtype, N, K, dev):
     (12, 30, (4096,), 4, 512, GELU, 1024, True, "qk", "f16", False),        # two-pass, linear1 with gelu
     (12, 30, (4096,), 4, 512, SWIGLU, 512, True, "qk", "bf16", False),      # two-pass, linear1 with SwiGLU
     (8, 30, (4096,), 6, 768, STORE, 0, True, "qk", "f16", False),           # two-pass Q8_0 (Z-Image QKV)
-    (12, 1, (1536,), 16, 256, STORE, 0, True, "qk", "bf16", False),         # one-pass Q4_K kernel
-    (8, 30, (1536,), 16, 256, STORE, 0, True, "qk", "f16", False),          # one-pass Q8_0: GEMM + glue
+    (12, 1, (1536,), 16, 256, STORE, 0, True, "qk", "bf16", False),         # one-pass sizes: GEMM + glue
+    (8, 30, (1536,), 16, 256, STORE, 0, True, "qk", "f16", False),          # the same for Q8_0
     (12, 30, (5120,), 3, 256, GELU, 512, False, "q", "f16", False),         # odd H: a straddling tile
     (12, 30, (100, 37), 2, 512, STORE, 0, True, "qk", "f16", False),        # few tokens: GEMM + glue
     (12, 0, (2048,), 4, 512, STORE, 0, True, "", "f16", False),             # f32 activations: GEMM + glue
