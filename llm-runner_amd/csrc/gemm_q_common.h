@@ -462,10 +462,10 @@ __device__ __forceinline__ void store_heads(f32x16 (&acc)[4][4], const HeadsEpi&
             asm volatile("" ::: "memory");
         }
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+        for (int a = 0; a < 4; a++) {
+            u32x2 pc[4];
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const uint32_t f = 32u * a + 8u * g + 4u * kh;
                 f32x4 x{acc[a][b][4 * g], acc[a][b][4 * g + 1], acc[a][b][4 * g + 2], acc[a][b][4 * g + 3]};
                 if (nw) {
 #pragma unroll
@@ -481,10 +481,27 @@ __device__ __forceinline__ void store_heads(f32x16 (&acc)[4][4], const HeadsEpi&
                     x = f32x4{x.x * c.x - x.y * sn.x, x.x * sn.x + x.y * c.x, x.z * c.y - x.w * sn.y,
                               x.z * sn.y + x.w * c.y};
                 }
-                const u32x2 pk = h.out_bf16 ? u32x2{pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w)}
-                                            : u32x2{pack_f16x2(x.x, x.y), pack_f16x2(x.z, x.w)};
-                if (m < M) *(u32x2*)(dst + (uint64_t)t * 128u + f) = pk;
+                pc[g] = h.out_bf16 ? u32x2{pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w)}
+                                   : u32x2{pack_f16x2(x.x, x.y), pack_f16x2(x.z, x.w)};
             }
+            // lane kh holds features 32 a + 8 g + 4 kh .. + 3; the two lanes
+            // of a token trade pieces (kh = 0 gives its g = 1, 3 ones) so that
+            // each stores 8 consecutive features, 16 bytes, per instruction
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const u32x2 give = kh ? pc[2 * q] : pc[2 * q + 1];
+                u32x2 recv;
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const auto r = __builtin_amdgcn_permlane32_swap(give[e], give[e], false, false);
+                    recv[e] = kh ? r[0] : r[1];  // the partner lane's value
+                }
+                // kh = 0: features 32 a + 16 q + 0..7; kh = 1: + 8..15
+                const u32x4 o = kh ? u32x4{recv.x, recv.y, pc[2 * q + 1].x, pc[2 * q + 1].y}
+                                   : u32x4{pc[2 * q].x, pc[2 * q].y, recv.x, recv.y};
+                if (m < M) *(u32x4*)(dst + (uint64_t)t * 128u + 32u * a + 16u * q + 8u * kh) = o;
+            }
+        }
 #pragma unroll
         for (int a = 0; a < 4; a++) acc[a][b] = f32x16{};
         if (rope) {  // the reads of this block's rows are done before the next block's DMAs
