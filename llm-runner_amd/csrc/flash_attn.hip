@@ -117,18 +117,43 @@ __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Flo
 #pragma unroll
                 for (int st = 0; st < 2; st++) {
                     const uint32_t off = ((q0 + 32u * b + l32) * kD + 32u * c + 16u * kh + 8u * st) * QB;
+                    f32x4 a, e;  // the 8 elements as f32 (exact for f16 / bf16 inputs)
                     if constexpr (QT == kGgmlF32) {
-                        const f32x4 a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
-                        const f32x4 e = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off + 16u, 0, 0));
-                        qf[b][c][st] = __builtin_bit_cast(f16x8, u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w),
-                                                                      pack_f16x2(e.x, e.y), pack_f16x2(e.z, e.w)});
-                    } else if constexpr (QT == kGgmlBF16) {
-                        const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
-                        qf[b][c][st] = __builtin_bit_cast(f16x8, u32x4{bf16x2_to_f16x2(w.x), bf16x2_to_f16x2(w.y),
-                                                                      bf16x2_to_f16x2(w.z), bf16x2_to_f16x2(w.w)});
+                        a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+                        e = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off + 16u, 0, 0));
                     } else {
-                        qf[b][c][st] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+                        const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(qr, off, 0, 0));
+                        // the components by name: indexed as w[k] in this
+                        // unrolled loop, hipcc read w[0] for every k
+                        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+                        float x[8];
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            if constexpr (QT == kGgmlBF16) {
+                                x[2 * k] = __uint_as_float(wd[k] << 16);
+                                x[2 * k + 1] = __uint_as_float(wd[k] & 0xffff0000u);
+                            } else {
+                                const f16x2 hw = __builtin_bit_cast(f16x2, wd[k]);
+                                x[2 * k] = (float)hw.x;
+                                x[2 * k + 1] = (float)hw.y;
+                            }
+                        }
+                        a = f32x4{x[0], x[1], x[2], x[3]};
+                        e = f32x4{x[4], x[5], x[6], x[7]};
                     }
+                    if constexpr (QT != kGgmlF16) {  // rounded to fp16 first, as the fp16 inputs are
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            a[k] = (float)(_Float16)a[k];
+                            e[k] = (float)(_Float16)e[k];
+                        }
+                    }
+                    // the softmax scale (log2 domain) carried by Q: the score
+                    // MFMAs then produce exp2's argument
+                    a *= scale_log2;
+                    e *= scale_log2;
+                    qf[b][c][st] = __builtin_bit_cast(f16x8, u32x4{pack_f16x2(a.x, a.y), pack_f16x2(a.z, a.w),
+                                                                  pack_f16x2(e.x, e.y), pack_f16x2(e.z, e.w)});
                 }
     }
 
@@ -175,11 +200,14 @@ __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Flo
         for (int dt = 0; dt < 4; dt++) vto[dt] = kr * ROW + (((4u * dt + x) ^ vswz(kr)) << 4) + 8u * half;
     }
 
+    // Scores are kept relative to m_ref, the max the exponentials use (log2
+    // domain; Q carries the scale): the score MFMAs start from -m_ref
+    // instead of zero, so a score is exp2's argument as it stands.
     f32x16 o[4][NB];
-    float m_ref[NB], l_i[NB];  // max used by the exponentials (log2 domain); this lane's partial row sums
+    float m_ref[NB], l_i[NB];  // this lane's query's m_ref; its partial row sums
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-        m_ref[b] = -1.0e30f;
+        m_ref[b] = 0.0f;
         l_i[b] = 0.0f;
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) o[dt][b] = f32x16{};
@@ -231,43 +259,50 @@ __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Flo
             }
         }
     };
-    // row max of a tile (log2 domain), both halves of the wave combined
+    // row max of a tile's scores (relative to m_ref), both halves of the wave
+    // combined
     auto rowmax = [&](const f32x16 (&h0)[NB], const f32x16 (&h1)[NB], float (&mx)[NB]) {
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             float m = h0[b][0];
 #pragma unroll
             for (int i = 0; i < 16; i++) m = fmaxf(fmaxf(m, h0[b][i]), h1[b][i]);
-            mx[b] = xhalf_max(m) * scale_log2;
+            mx[b] = xhalf_max(m);
         }
     };
-    // raise the running max where a tile exceeds it by more than 2^8
-    auto rescale = [&](const float (&mx)[NB]) {
+    // raise m_ref where the tile whose scores are in (n0, n1) exceeds it by
+    // more than 2^8 (lazily: exp2 of at most 2^8 cannot overflow), and shift
+    // those scores to the new m_ref (the next tile's MFMAs start from it)
+    auto rescale = [&](const float (&mx)[NB], f32x16 (&n0)[NB], f32x16 (&n1)[NB]) {
         bool grow = false;
 #pragma unroll
-        for (int b = 0; b < NB; b++) grow = grow || mx[b] > m_ref[b] + 8.0f;
+        for (int b = 0; b < NB; b++) grow = grow || mx[b] > 8.0f;
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                const float m2 = fmaxf(m_ref[b], mx[b]);
-                const float alpha = __builtin_amdgcn_exp2f(m_ref[b] - m2);
-                m_ref[b] = m2;
+                const float d = fmaxf(mx[b], 0.0f);
+                const float alpha = __builtin_amdgcn_exp2f(-d);
+                m_ref[b] += d;
                 l_i[b] *= alpha;
 #pragma unroll
                 for (int dt = 0; dt < 4; dt++) o[dt][b] *= alpha;
+                n0[b] -= d;
+                n1[b] -= d;
             }
         }
     };
-    // P = exp2(S scale - m_ref) of score pair `item` (query block item/8,
-    // keys 2(item%8), +1) of half h (key block kb) into the fp16 operand p
-    // (p[b][kb][c] holds keys 16c..16c+15 of the block); row sums into rs
+    // P = exp2(score) of score pair `item` (query block item/8, keys
+    // 2(item%8), +1) of half h (key block kb) into the fp16 operand p
+    // (p[b][kb][c] holds keys 16c..16c+15 of the block); the row sums of
+    // the fp16 P (the values O accumulates) into rs, by one dot2 per pair
     auto exp_pair = [&](const f32x16 (&h)[NB], int kb, int item, f16x8 (&p)[NB][2][2], float (&rs)[NB]) {
         const int b = item / 8, i = 2 * (item % 8);
-        const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(h[b][i], scale_log2, -m_ref[b]));
-        const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(h[b][i + 1], scale_log2, -m_ref[b]));
-        rs[b] += e0 + e1;
-        p[b][kb][i >> 3][i & 7] = (_Float16)e0;
-        p[b][kb][i >> 3][(i & 7) + 1] = (_Float16)e1;
+        const float e0 = __builtin_amdgcn_exp2f(h[b][i]);
+        const float e1 = __builtin_amdgcn_exp2f(h[b][i + 1]);
+        const f16x2 pe{(_Float16)e0, (_Float16)e1};
+        rs[b] = __builtin_amdgcn_fdot2(pe, f16x2{(_Float16)1.0f, (_Float16)1.0f}, rs[b], false);
+        p[b][kb][i >> 3][i & 7] = pe.x;
+        p[b][kb][i >> 3][(i & 7) + 1] = pe.y;
     };
 
     // One tile t. S(t) is in (c0, c1); S(t+1) = K(t+1) Q^T goes to (n0, c0)
@@ -305,7 +340,8 @@ __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Flo
                 if constexpr (b == 0 && f + PF < 16) kf[(f + PF) % (PF + 1)] = kfrag(Ks, f + PF);
                 f32x16& s = kb == 0 ? n0[b] : c0[b];
                 s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[f % (PF + 1)], qf[b][c][st],
-                                                           (c == 0 && st == 0) ? f32x16{} : s, 0, 0, 0);
+                                                           (c == 0 && st == 0) ? f32x16{} - m_ref[b] : s, 0, 0,
+                                                           0);
             } else {
                 constexpr int f = (j - QS) / NB, b = j % NB, kb = f / 8, c = (f % 8) / 4, dt = f % 4;
                 if constexpr (b == 0 && f + PF < 16) vf[(f + PF) % (PF + 1)] = vfrag(Vs, f + PF);
@@ -328,9 +364,9 @@ __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Flo
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             l_i[b] += rs[b];
-            mx[b] = xhalf_max(mt[b]) * scale_log2;
+            mx[b] = xhalf_max(mt[b]);
         }
-        rescale(mx);
+        rescale(mx, n0, c0);
         LLMR_STAGE_BARRIER(4 * NB);
     };
 
@@ -347,12 +383,17 @@ __device__ __forceinline__ void fa64_body(const void* __restrict__ Q, const _Flo
     dma(Kh, kvo, 2, 2);
     LLMR_STAGE_BARRIER(8 * NB);  // K(0) has landed
     f32x16 h0[NB], h1[NB], h2[NB];
-    {
+    {   // S(0) from zero; its row max becomes m_ref, S(0) relative to it
         float mx[NB];
         qk_all(lds, h0, h1);
         if (n_tiles == 1u && partial) mask(h0, h1, 0);
         rowmax(h0, h1, mx);
-        rescale(mx);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            m_ref[b] = mx[b];
+            h0[b] -= mx[b];
+            h1[b] -= mx[b];
+        }
     }
     LLMR_STAGE_BARRIER(4 * NB);  // K(1), V(0) have landed; every wave is done with K(0)
 
