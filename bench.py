@@ -71,22 +71,33 @@ def _device_warmup(fn, min_ms: float = DEVICE_WARMUP_MS):
     return n + 1
 
 
-def _time_steps(fn, steps: int, warmup: int):
-    """Runs warmup + timed steps; returns (total ms over `steps`, per-step ms list)."""
+def _time_steps(fn, steps: int, warmup: int, per_step: bool = False):
+    """Runs warmup + timed steps; returns (total ms over `steps`, per-step ms
+    list or None). The total is timed between two events only: an event
+    recorded after every step adds a few microseconds of stream time per
+    step, a sixth of a 16 us launch. With per_step, `steps` more steps run
+    with an event after each, for the per-step list."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    torch.cuda.synchronize()
-    evs[0].record(st)
-    for i in range(steps):
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(steps):
         fn()
-        evs[i + 1].record(st)
+    b.record(st)
     torch.cuda.synchronize()
-    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
-    return evs[0].elapsed_time(evs[-1]), per
+    per = None
+    if per_step:
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        evs[0].record(st)
+        for i in range(steps):
+            fn()
+            evs[i + 1].record(st)
+        torch.cuda.synchronize()
+        per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
+    return a.elapsed_time(b), per
 
 
 def _traffic(name: str):
@@ -424,10 +435,9 @@ def measure(dev, name, steps, warmup, cold: bool = False):
     if cold:  # W warmup + K timed steps straight after set-up, before the device warm-up
         cold_ms = _time_steps(step, steps, warmup)[0] / steps
     _device_warmup(step)
-    total_ms, per = _time_steps(step, steps, warmup)
+    total_ms, per = _time_steps(step, steps, warmup, per_step=name in MODEL_SETUPS)
     ms = total_ms / steps
-    per.sort()
-    med = per[len(per) // 2]
+    med = sorted(per)[len(per) // 2] if per else ms
     tflops = flops / (ms * 1e-3) / 1e12
     return {"name": name, "ms": ms, "median_ms": med, "tflops": tflops, "flops": flops,
             "bytes": nbytes, "cfg": cfg, "dtype": dtype, "cold_ms": cold_ms}
