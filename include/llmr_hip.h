@@ -262,9 +262,10 @@ LLMR_API int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t weight_type, ui
  * runs in two passes: its weight rows are first dequantized into a 16-bit
  * image (laid out as the GEMM's LDS tiles), which the matrix-core pass then
  * streams. A caller that knows its next GEMM group (a whole denoising step)
- * can have each call build the next group's images: the current GEMM's
- * workgroups that have no tile in its last round build part of them, the
- * rest runs right after it. No reference counterpart (the reference
+ * can have each call build the next group's images, or the next two groups'
+ * where its idle workgroups have room: the current GEMM's workgroups that
+ * have no tile in its last round build what fits, the rest runs right after
+ * it. No reference counterpart (the reference
  * dequantizes inside every matmul dispatch, llm.slang:1677-1705, 2321-2328);
  * the results are bit-identical to llmr_batch_matmul_multi.
  *
@@ -279,18 +280,24 @@ LLMR_API int llmr_build_weight_image(llmr_context* ctx, const void* weight, uint
                                      uint32_t input_type, uint32_t out_dim, uint32_t in_dim, uint32_t row_offset,
                                      void* image, size_t image_bytes);
 
-/* The weight images of the GEMM group a caller issues next: `count` (1 or 2)
- * weights of weight_type with out_dim rows from row_offset[i] and in_dim
- * columns, for the same input_type as the call that builds them. */
+/* One weight image a call builds for a later call: rows [row_offset,
+ * row_offset + out_dim) of a weight with in_dim columns. */
+typedef struct llmr_next_weight_image {
+    const void* weight;
+    uint32_t out_dim;
+    uint32_t in_dim;     /* % 64 == 0 */
+    uint32_t row_offset;
+    void* image;         /* 256-byte aligned */
+    size_t image_bytes;  /* >= llmr_weight_image_bytes(out_dim, in_dim) */
+} llmr_next_weight_image;
+
+/* The weight images of the GEMM groups a caller issues next (the next
+ * group's, or the next two groups'): `count` (1 to 4) images of weights of
+ * weight_type, for the same input_type as the call that builds them. */
 typedef struct llmr_next_weight_images {
     uint32_t weight_type;
-    uint32_t out_dim;
-    uint32_t in_dim;  /* % 64 == 0 */
     uint32_t count;
-    const void* weight[2];
-    uint32_t row_offset[2];
-    void* image[2];   /* 256-byte aligned, image_bytes each */
-    size_t image_bytes;
+    llmr_next_weight_image image[4];
 } llmr_next_weight_images;
 
 /* llmr_batch_matmul_multi, plus:
@@ -300,8 +307,11 @@ typedef struct llmr_next_weight_images {
  *     row_offset (the weight unchanged since; the call cannot check the
  *     contents). Job groups that run two-pass use them instead of building
  *     their own; other groups ignore them.
- *   next (NULL or the next group's images): built before the call returns
- *     its work to the stream, partly by this call's idle workgroups.
+ *   next (NULL or images of later groups): all built before the call
+ *     returns its work to the stream, as many items as fit by this call's
+ *     idle workgroups (the workgroups without a tile in the GEMM's last
+ *     round), the rest by an image launch right after the GEMM. None may be
+ *     an image this call reads.
  * Either needs input_type F16 or BF16. */
 LLMR_API int llmr_batch_matmul_multi_images(llmr_context* ctx, uint32_t weight_type, uint32_t input_type,
                                             uint32_t out_dim, uint32_t in_dim, const llmr_matmul_job* jobs,

@@ -510,30 +510,36 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
     if (next) {
         if (xtype != LLMR_GGML_F16 && xtype != LLMR_GGML_BF16)
             return fail(LLMR_ERR_INVALID_ARG, "next weight images need F16 or BF16 input");
-        if (next->count == 0 || next->count > 2) return fail(LLMR_ERR_INVALID_ARG, "next: count must be 1 or 2");
-        if (next->in_dim % 64 || next->out_dim == 0)
-            return fail(LLMR_ERR_INVALID_ARG, "next: in_dim %% 64 == 0 and out_dim > 0 needed");
-        const size_t need = llmr::w16_image_bytes(next->out_dim, next->in_dim, false);
-        if (next->image_bytes < need)
-            return fail(LLMR_ERR_INVALID_ARG, "next: images hold %zu bytes, need %zu", next->image_bytes, need);
+        if (next->count == 0 || next->count > llmr::kMaxNextImages)
+            return fail(LLMR_ERR_INVALID_ARG, "next: count must be 1 to %u", llmr::kMaxNextImages);
         for (uint32_t i = 0; i < next->count; i++) {
-            if (int r = check_weight(next->weight[i], next->weight_type, next->in_dim)) return r;
-            if ((uint64_t)next->row_offset[i] + next->out_dim > 0xffffffffull)
-                return fail(LLMR_ERR_INVALID_ARG, "next: row_offset + out_dim overflows");
-            if (!next->image[i] || !aligned(next->image[i], 256))
-                return fail(LLMR_ERR_INVALID_ARG, "next: image %u must be non-null and 256-byte aligned", i);
+            const llmr_next_weight_image& m = next->image[i];
+            if (m.in_dim % 64 || m.out_dim == 0)
+                return fail(LLMR_ERR_INVALID_ARG, "next image %u: in_dim %% 64 == 0 and out_dim > 0 needed", i);
+            const size_t need = llmr::w16_image_bytes(m.out_dim, m.in_dim, false);
+            if (m.image_bytes < need)
+                return fail(LLMR_ERR_INVALID_ARG, "next image %u holds %zu bytes, needs %zu", i, m.image_bytes,
+                            need);
+            if (int r = check_weight(m.weight, next->weight_type, m.in_dim)) return r;
+            if ((uint64_t)m.row_offset + m.out_dim > 0xffffffffull)
+                return fail(LLMR_ERR_INVALID_ARG, "next image %u: row_offset + out_dim overflows", i);
+            if (!m.image || !aligned(m.image, 256))
+                return fail(LLMR_ERR_INVALID_ARG, "next image %u must be non-null and 256-byte aligned", i);
+            for (uint32_t j = 0; j < i; j++)
+                if (next->image[j].image == m.image)
+                    return fail(LLMR_ERR_INVALID_ARG, "next images %u and %u are the same buffer", j, i);
             if (images)
                 for (uint32_t j = 0; j < n_jobs; j++)
-                    if (images[j] == next->image[i])
+                    if (images[j] == m.image)
                         return fail(LLMR_ERR_INVALID_ARG, "next: image %u is also an image of this call", i);
-            nx.w[i] = next->weight[i];
-            nx.img[i] = next->image[i];
-            nx.row_offset[i] = next->row_offset[i];
+            nx.w[i] = m.weight;
+            nx.img[i] = m.image;
+            nx.row_offset[i] = m.row_offset;
+            nx.N[i] = m.out_dim;
+            nx.K[i] = m.in_dim;
         }
         nx.count = next->count;
         nx.wtype = next->weight_type;
-        nx.N = next->out_dim;
-        nx.K = next->in_dim;
     }
     if (!is_act_type(xtype))
         return fail(LLMR_ERR_UNSUPPORTED, "input type %u not supported (F32=0, F16=1, BF16=30)", xtype);

@@ -1658,14 +1658,22 @@ size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32
 // idle workgroups' last-round time.
 uint32_t next_items_per_idle_wg(uint32_t K) { return max(1u, K / (uint32_t)kBK / 4u); }
 
-// The next group's images: the items [0, fused) came from the GEMM's idle
+uint32_t next_image_items(const NextImageSet& nx) {
+    uint32_t all = 0;
+    for (uint32_t i = 0; i < nx.count; i++) all += w16_image_items(nx.N[i], nx.K[i]);
+    return all;
+}
+
+// Later groups' images: the items [0, fused) came from the GEMM's idle
 // workgroups; the rest of each image here.
 hipError_t finish_next_images(const NextImageSet& nx, uint32_t otype, uint32_t fused, hipStream_t st) {
-    const uint32_t per = w16_image_items(nx.N, nx.K);
+    uint32_t first = 0;
     for (uint32_t i = 0; i < nx.count; i++) {
-        const uint32_t done = fused > i * per ? min(per, fused - i * per) : 0u;
+        const uint32_t per = w16_image_items(nx.N[i], nx.K[i]);
+        const uint32_t done = fused > first ? min(per, fused - first) : 0u;
+        first += per;
         if (done == per) continue;
-        const hipError_t e = launch_w16_image(nx.w[i], nullptr, nx.wtype, otype, nx.img[i], nx.N, nx.K,
+        const hipError_t e = launch_w16_image(nx.w[i], nullptr, nx.wtype, otype, nx.img[i], nx.N[i], nx.K[i],
                                               nx.row_offset[i], st, done);
         if (e != hipSuccess) return e;
     }
@@ -1675,7 +1683,7 @@ hipError_t finish_next_images(const NextImageSet& nx, uint32_t otype, uint32_t f
 hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t K, const GemmJob* jobs,
                                      uint32_t n_jobs, const GemmEpilogue& epi, int num_cus, void* ws,
                                      hipStream_t st, const void* const* images, const NextImageSet* next) {
-    if (next && (next->count == 0 || next->count > 2 || (xtype != kGgmlF16 && xtype != kGgmlBF16)))
+    if (next && (next->count == 0 || next->count > kMaxNextImages || (xtype != kGgmlF16 && xtype != kGgmlBF16)))
         return hipErrorInvalidValue;
     uint32_t fused = 0;  // next-image items the last group's GEMM builds
     // a group of Q4_K projections of a few tokens (the per-block
@@ -1707,17 +1715,20 @@ hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N,
                 const uint64_t tiles = (uint64_t)a.tiles_m * a.tiles_n;
                 if (next && i + n == n_jobs && tiles % (uint64_t)num_cus != 0) {
                     const uint32_t idle = num_cus - (uint32_t)(tiles % (uint64_t)num_cus);
-                    const uint32_t all = next->count * w16_image_items(next->N, next->K);
-                    fused = min(all, idle * next_items_per_idle_wg(K));
+                    fused = min(next_image_items(*next), idle * next_items_per_idle_wg(K));
                     NextImages& ni = a.next;
+                    uint32_t first = 0;
                     for (uint32_t q = 0; q < next->count; q++) {
                         ni.W[q] = (const uint8_t*)next->w[q];
                         ni.img[q] = (uint8_t*)next->img[q];
                         ni.row_offset[q] = next->row_offset[q];
+                        ni.N[q] = next->N[q];
+                        ni.K[q] = next->K[q];
+                        ni.first[q] = first;
+                        first += w16_image_items(next->N[q], next->K[q]);
                     }
+                    ni.count = next->count;
                     ni.wtype = next->wtype;
-                    ni.N = next->N;
-                    ni.K = next->K;
                     ni.items = fused;
                 }
                 if (e == hipSuccess) e = launch_w16_gemm(a, xtype, false, n == 2, num_cus, st);

@@ -22,15 +22,16 @@ struct PersistProblem {
     void* Y2;           // kEpiSplitGelu: 16-bit output
     uint32_t M, row_offset, tiles_m;
 };
-// Weight images of the next GEMM group, built by the two-pass GEMM's
+// Weight images of later GEMM groups, built by the two-pass GEMM's
 // workgroups that have no tile in its last round (items: (panel, group of 4
-// stages) of w16_image_kernel, image i's item u at i * per_image + u; the
-// first `items` of them here, the rest by w16_image_kernel after the GEMM).
+// stages) of w16_image_kernel, numbered across the images in order, image
+// i's item u at first[i] + u; the first `items` of them here, the rest by
+// w16_image_kernel after the GEMM).
 struct NextImages {
-    const uint8_t* W[2];  // raw weight blocks, row row_offset[i] is feature 0
-    uint8_t* img[2];
-    uint32_t row_offset[2];
-    uint32_t wtype, N, K;
+    const uint8_t* W[4];  // raw weight blocks, row row_offset[i] is feature 0
+    uint8_t* img[4];
+    uint32_t row_offset[4], N[4], K[4], first[4];
+    uint32_t count, wtype;
     uint32_t items;       // items built by the GEMM's idle workgroups (0: none)
 };
 // Head routing of the split-epilogue GEMMs' first `split` = 3 H 128 output

@@ -607,22 +607,23 @@ __global__ void __launch_bounds__(256, 1) gemm_w16_persist(const PersistArgs arg
 #undef LLMR16_STAGE
     }
 
-    // The next GEMM group's weight images: the workgroups without a tile in
-    // the last round build items [0, next.items) between them, through the
+    // Later groups' weight images: the workgroups without a tile in the
+    // last round build items [0, next.items) between them, through the
     // first two ring slots (no DMA in flight into them after this wait).
     const NextImages& ni = args.next;
     if (ni.items > 0 && total % G != 0 && n_tiles == total / G) {
         LLMR_WAIT_VMCNT(0);
         __syncthreads();
-        const uint32_t idle = G - total % G, per = image_items(ni.N, ni.K);
+        const uint32_t idle = G - total % G;
         for (uint32_t j = w16_idle_rank(blockIdx.x, G, total); j < ni.items; j += idle) {
-            const uint32_t i = j / per;
+            uint32_t i = 0;  // the image of item j (uniform)
+            while (i + 1u < ni.count && j >= ni.first[i + 1u]) i++;
             if (ni.wtype == kGgmlQ4K)
-                image_item<kGgmlQ4K, XT, true>(ni.W[i], ni.img[i], ni.N, ni.K, ni.row_offset[i], j - i * per, X0,
-                                               X1);
+                image_item<kGgmlQ4K, XT, true>(ni.W[i], ni.img[i], ni.N[i], ni.K[i], ni.row_offset[i],
+                                               j - ni.first[i], X0, X1);
             else
-                image_item<kGgmlQ8_0, XT, true>(ni.W[i], ni.img[i], ni.N, ni.K, ni.row_offset[i], j - i * per, X0,
-                                                X1);
+                image_item<kGgmlQ8_0, XT, true>(ni.W[i], ni.img[i], ni.N[i], ni.K[i], ni.row_offset[i],
+                                                j - ni.first[i], X0, X1);
             __syncthreads();
         }
     }

@@ -140,14 +140,17 @@ uint32_t w16_image_items(uint32_t N, uint32_t K);
 // 16-bit input type): built in part by the two-pass GEMM's workgroups that
 // are idle in its last round, the rest right after it, so they are complete
 // when the next call on the stream starts.
+constexpr uint32_t kMaxNextImages = 4;
 struct NextImageSet {
-    const void* w[2];
-    void* img[2];
-    uint32_t row_offset[2];
-    uint32_t count, wtype, N, K;
+    const void* w[kMaxNextImages];
+    void* img[kMaxNextImages];
+    uint32_t row_offset[kMaxNextImages], N[kMaxNextImages], K[kMaxNextImages];
+    uint32_t count, wtype;
 };
-// The images' items from item `fused` on (items numbered across the images,
-// image i's item u = i * w16_image_items(N, K) + u), for operand type otype.
+// Items of the images, numbered across them in order (image i's item u =
+// the items of images 0..i-1 + u); the images' items from item `fused` on,
+// for operand type otype.
+uint32_t next_image_items(const NextImageSet& nx);
 hipError_t finish_next_images(const NextImageSet& nx, uint32_t otype, uint32_t fused, hipStream_t st);
 // A LoRA on a single GEMM (the reference's dispatch_batch_matmul with a
 // LoRA): output columns [row_offset, row_offset + b_rows) get scale *

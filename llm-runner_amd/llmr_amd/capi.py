@@ -54,11 +54,15 @@ class MatmulEpilogue(ctypes.Structure):
                 ("ldy2", ctypes.c_uint32), ("output2_type", ctypes.c_uint32)]
 
 
+class NextWeightImage(ctypes.Structure):
+    """llmr_next_weight_image: one weight image a call builds for a later call."""
+    _fields_ = [("weight", ctypes.c_void_p), ("out_dim", ctypes.c_uint32), ("in_dim", ctypes.c_uint32),
+                ("row_offset", ctypes.c_uint32), ("image", ctypes.c_void_p), ("image_bytes", ctypes.c_size_t)]
+
+
 class NextWeightImages(ctypes.Structure):
-    """llmr_next_weight_images: the next GEMM group's weight images."""
-    _fields_ = [("weight_type", ctypes.c_uint32), ("out_dim", ctypes.c_uint32), ("in_dim", ctypes.c_uint32),
-                ("count", ctypes.c_uint32), ("weight", ctypes.c_void_p * 2), ("row_offset", ctypes.c_uint32 * 2),
-                ("image", ctypes.c_void_p * 2), ("image_bytes", ctypes.c_size_t)]
+    """llmr_next_weight_images: weight images of later GEMM groups (1 to 4)."""
+    _fields_ = [("weight_type", ctypes.c_uint32), ("count", ctypes.c_uint32), ("image", NextWeightImage * 4)]
 
 
 EPI_STORE, EPI_GATED_RESIDUAL, EPI_SPLIT_GELU, EPI_SPLIT_SWIGLU = 0, 1, 2, 3

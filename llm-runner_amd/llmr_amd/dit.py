@@ -391,31 +391,72 @@ TWO_PASS_MIN_TOKENS = 2048
 
 class _ImageChain:
     """Weight images of a fixed sequence of GEMM groups (one multi launch
-    each: a list of Q4_K/Q8_0 weights of one shape N x K, rows from 0), each
-    built by the call before it: that call's two-pass GEMM builds part of
-    them on its workgroups without a tile in the last round and the rest
-    right after it (NextImages); the first group's are built before it. Two
-    buffers alternate (group k reads buffer k % 2 while group k + 1's images
-    go into the other, last read by group k - 1). The results are those of
-    dispatch_batch_matmul_multi without images, bit for bit."""
+    each: one or two Q4_K/Q8_0 weights of one shape N x K, rows from 0, and
+    the token counts of its jobs), built ahead: group k's images by call
+    k - 1, or by call k - 2 when that call's idle workgroups (those without
+    a tile in its GEMM's last round) have room for all of them after group
+    k - 1's. A call's NextImages are built as far as its idle workgroups
+    reach and the rest right after it; the first group's are built before
+    it. Three buffers rotate (group k in buffer k % 3: at most two groups
+    are built ahead of the one running, none into the buffer it reads). The
+    room is estimated here from the launch's tile count; a wrong estimate
+    only moves items into the image launch after the GEMM. The results are
+    those of dispatch_batch_matmul_multi without images, bit for bit."""
 
-    def __init__(self, groups, input_dtype: int, device):
+    def __init__(self, groups, input_dtype: int, device, cus: int):
         self.groups, self.xtype = groups, input_dtype
-        per = max(len(ws) * weight_image_bytes(N, K) for ws, N, K in groups)
-        self.bufs = [torch.empty(per, dtype=torch.uint8, device=device) for _ in range(2)]
+        per = max(len(ws) * weight_image_bytes(N, K) for ws, N, K, _ in groups)
+        self.bufs = [torch.empty(per, dtype=torch.uint8, device=device) for _ in range(3)]
+        self.builds = self.plan(groups, cus)  # call k -> the groups whose images it builds
         self.k = 0
         self.active = False  # between start() and the last group's take()
 
+    @classmethod
+    def plan(cls, groups, cus: int):
+        """For each call, the later groups whose images it builds: group k + 1
+        unless call k - 1 built it, then group k + 2 if all of its items fit
+        in what is left of the call's room."""
+        n = len(groups)
+        builds = [[] for _ in range(n)]
+        built = [False] * n
+        for c in range(n - 1):
+            room = cls._room(groups[c], cus)
+            for j in (c + 1, c + 2):
+                if j >= n or built[j]:
+                    continue
+                need = cls._items(groups[j])
+                if j > c + 1 and need > room:
+                    break
+                builds[c].append(j)
+                built[j] = True
+                room -= need
+        return builds
+
+    @staticmethod
+    def _items(group) -> int:
+        """Image items of a group: (256-row panel, 4 K stages) each."""
+        ws, N, K, _ = group
+        return len(ws) * -(-N // 256) * -(-(K // 64) // 4)
+
+    @staticmethod
+    def _room(group, cus: int) -> int:
+        """Items the group's GEMM can build on its workgroups without a tile
+        in the last round: one per four of its K stages each."""
+        ws, N, K, Ms = group
+        tiles = sum(-(-M // 256) for M in Ms) * -(-N // 256)
+        rem = tiles % cus
+        return 0 if rem == 0 else (cus - rem) * max(1, K // 256)
+
     def _views(self, k: int):
-        ws, N, K = self.groups[k]
+        ws, N, K, _ = self.groups[k]
         n = weight_image_bytes(N, K)
-        return [self.bufs[k % 2][i * n:(i + 1) * n] for i in range(len(ws))]
+        return [self.bufs[k % 3][i * n:(i + 1) * n] for i in range(len(ws))]
 
     def start(self, g: RenderGraph) -> None:
         """Before the first group: its images."""
         self.k = 0
         self.active = True
-        ws, N, K = self.groups[0]
+        ws, N, K, _ = self.groups[0]
         for w, im in zip(ws, self._views(0)):
             build_weight_image(g, w, N, K, 0, self.xtype, im)
 
@@ -424,14 +465,15 @@ class _ImageChain:
         that group's GEMMs (the same weights, in order, and shape): images are
         matched to jobs by position, which the C-ABI cannot check."""
         k = self.k
-        ws, gN, gK = self.groups[k]
+        ws, gN, gK, _ = self.groups[k]
         if (gN, gK) != (N, K) or [w.ptr() for w in ws] != [j.weight.ptr() for j in jobs]:
             self.active = False
             raise RuntimeError(f"weight-image chain out of step: group {k} holds other weights than this call's")
         nxt = None
-        if k + 1 < len(self.groups):
-            ws, N, K = self.groups[k + 1]
-            nxt = NextImages(ws, N, K, self._views(k + 1))
+        for j in self.builds[k]:
+            jw, jN, jK, _ = self.groups[j]
+            part = NextImages.group(jw, jN, jK, self._views(j), (0,) * len(jw))
+            nxt = part if nxt is None else nxt + part
         self.k += 1
         self.active = self.k < len(self.groups)
         return self._views(k), nxt
@@ -459,15 +501,17 @@ class FluxDiT:
             def q4(t, K):
                 return _qt(t, GGML_Q4_K, t.numel() // (K // 256 * 144), K)
             groups = []
+            two = (nt, S - nt)  # a double block's text and image jobs
             for w in doubles:
-                groups += [([q4(w.txt_qkv, d), q4(w.img_qkv, d)], 3 * d, d),
-                           ([q4(w.txt_proj, d), q4(w.img_proj, d)], d, d),
-                           ([q4(w.txt_mlp0, d), q4(w.img_mlp0, d)], m, d),
-                           ([q4(w.txt_mlp2, m), q4(w.img_mlp2, m)], d, m)]
+                groups += [([q4(w.txt_qkv, d), q4(w.img_qkv, d)], 3 * d, d, two),
+                           ([q4(w.txt_proj, d), q4(w.img_proj, d)], d, d, two),
+                           ([q4(w.txt_mlp0, d), q4(w.img_mlp0, d)], m, d, two),
+                           ([q4(w.txt_mlp2, m), q4(w.img_mlp2, m)], d, m, two)]
             for w in singles:
-                groups += [([q4(w.linear1, d)], 3 * d + m, d), ([q4(w.linear2, d + m)], d, d + m)]
+                groups += [([q4(w.linear1, d)], 3 * d + m, d, (S,)), ([q4(w.linear2, d + m)], d, d + m, (S,))]
             if groups:
-                self.ahead = _ImageChain(groups, _TORCH_GGML[act_dtype], device)
+                cus = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
+                self.ahead = _ImageChain(groups, _TORCH_GGML[act_dtype], device, cus)
         self.rope = flux_rope(cfg, device)
         self.hidden = torch.empty(S, d, dtype=torch.float32, **e)   # joint residual stream, text rows first
         self.xa = torch.empty(S, d, dtype=act_dtype, **e)             # GEMM inputs of width dim

@@ -288,15 +288,30 @@ def _qkv_heads_out(h: QkvHeads, n_jobs: int) -> tuple:
 
 
 @dataclasses.dataclass
-class NextImages:
-    """The weight images of the GEMM group issued next (llmr_next_weight_images):
-    its weights (one or two Tensors of one type, rows from row_offsets) and
-    out_dim x in_dim, into `images` (device tensors of weight_image_bytes)."""
-    weights: list
+class NextImage:
+    """One weight image a call builds for a later call: rows [row_offset,
+    row_offset + out_dim) of `weight` (a quantized Tensor) with in_dim
+    columns, into `image` (a device tensor of weight_image_bytes)."""
+    weight: Tensor
     out_dim: int
     in_dim: int
-    images: list
-    row_offsets: tuple = (0, 0)
+    image: object
+    row_offset: int = 0
+
+
+@dataclasses.dataclass
+class NextImages:
+    """Weight images of the GEMM groups issued next (llmr_next_weight_images):
+    1 to 4 NextImage entries, weights of one type."""
+    entries: list
+
+    @classmethod
+    def group(cls, weights, out_dim: int, in_dim: int, images, row_offsets=(0, 0)) -> "NextImages":
+        """One group's images: its weights, out_dim x in_dim each."""
+        return cls([NextImage(w, out_dim, in_dim, im, ro) for w, im, ro in zip(weights, images, row_offsets)])
+
+    def __add__(self, other: "NextImages") -> "NextImages":
+        return NextImages(self.entries + other.entries)
 
 
 def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim: int,
@@ -313,9 +328,10 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
     modulation projections) runs as one GEMV launch. images: None, or one
     device tensor per job holding the job's weight image (build_weight_image
     or an earlier call's next_images, same weight, row_offset and input
-    type), used where a pair runs two-pass; next_images: the next group's
-    images, built partly by this call's idle workgroups and complete when
-    the stream's next call starts (llmr_batch_matmul_multi_images). heads: the
+    type), used where a pair runs two-pass; next_images: images of later
+    groups (NextImages), built partly by this call's idle workgroups and
+    complete when the stream's next call starts
+    (llmr_batch_matmul_multi_images). heads: the
     Q | K | V columns (all of a plain store, [0, split) of a split) head-normed,
     rotated and written head-major into heads.q/k/v instead of `output`, which
     may then be None (llmr_batch_matmul_multi_qkv; batch_head_norm +
@@ -395,23 +411,23 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
         ptrs = [im.data_ptr() for im in images]
     nx = None
     if next_images is not None:
-        n = next_images
-        if not 1 <= len(n.weights) <= 2 or len(n.images) != len(n.weights):
-            raise ValueError("next_images: one or two weights, one image each")
-        nbytes = weight_image_bytes(n.out_dim, n.in_dim)
-        nt = n.weights[0].dtype
-        for w, im, ro in zip(n.weights, n.images, n.row_offsets):
-            _dev(w, "next weight")
-            if w.dtype != nt or w.shape[1] != n.in_dim or ro + n.out_dim > w.shape[0]:
+        es = next_images.entries
+        if not 1 <= len(es) <= 4:
+            raise ValueError("next_images: one to four images")
+        if len(es) != len(set(e.image.data_ptr() for e in es)):
+            raise ValueError("next_images: one buffer per image")
+        nt = es[0].weight.dtype
+        arr = (capi.NextWeightImage * 4)()
+        for i, e in enumerate(es):
+            _dev(e.weight, "next weight")
+            nbytes = weight_image_bytes(e.out_dim, e.in_dim)
+            if e.weight.dtype != nt or e.weight.shape[1] != e.in_dim or e.row_offset + e.out_dim > e.weight.shape[0]:
                 raise ValueError("next weights: one type, covering [row_offset, +out_dim) x in_dim")
-            if not im.is_cuda or im.numel() * im.element_size() < nbytes:
+            if not e.image.is_cuda or e.image.numel() * e.image.element_size() < nbytes:
                 raise ValueError(f"next images must be device tensors of at least {nbytes} bytes")
-        k = len(n.weights)
-        nx = capi.NextWeightImages(nt, n.out_dim, n.in_dim, k,
-                                   (ctypes.c_void_p * 2)(*[w.ptr() for w in n.weights] + [None] * (2 - k)),
-                                   (ctypes.c_uint32 * 2)(*(list(n.row_offsets[:k]) + [0] * (2 - k))),
-                                   (ctypes.c_void_p * 2)(*[im.data_ptr() for im in n.images] + [None] * (2 - k)),
-                                   nbytes)
+            arr[i] = capi.NextWeightImage(e.weight.ptr(), e.out_dim, e.in_dim, e.row_offset, e.image.data_ptr(),
+                                          e.image.numel() * e.image.element_size())
+        nx = capi.NextWeightImages(nt, len(es), arr)
     if hout is not None:
         g.ctx.batch_matmul_multi_qkv(wtype, xtype, out_dim, in_dim, cj, epi, hout[0], hout[1], ptrs, nx)
     else:

@@ -770,7 +770,7 @@ def test_multi_next_images_built_by_idle_workgroups(dev, wtype, xtype, Ms, N, K,
     def jobs(out):
         return [ops.MatmulJob(wts[i], ops.Tensor.from_torch(xs[i]), out[rows[i]:rows[i + 1]], Ms[i], 8 * i)
                 for i in range(len(Ms))]
-    nxt = ops.NextImages(nw, N2, K2, chained, row_offsets=tuple(16 * i for i in range(len(Ms))))
+    nxt = ops.NextImages.group(nw, N2, K2, chained, row_offsets=tuple(16 * i for i in range(len(Ms))))
     ops.dispatch_batch_matmul_multi(g, jobs(out_a), N, K, next_images=nxt)
     ops.dispatch_batch_matmul_multi(g, jobs(out_b), N, K)
     for i in range(len(Ms)):
@@ -840,9 +840,19 @@ def test_weight_image_entry_points_reject_bad_arguments(dev):
     epi = capi.MatmulEpilogue(capi.EPI_STORE, N, 0, 0, 0)
     with pytest.raises(capi.LlmrError, match="256-byte aligned"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, [img.data_ptr() + 16])
-    nxt = capi.NextWeightImages(12, N, K, 3, (ctypes.c_void_p * 2)(w.ptr(), None), (ctypes.c_uint32 * 2)(0, 0),
-                                (ctypes.c_void_p * 2)(img.data_ptr(), None), nb)
+    img2 = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    one = capi.NextWeightImage(w.ptr(), N, K, 0, img.data_ptr(), nb)
+    nxt = capi.NextWeightImages(12, 5, (capi.NextWeightImage * 4)(one, one, one, one))
     with pytest.raises(capi.LlmrError, match="count"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
+    nxt.count = 2  # images 0 and 1 in one buffer
+    with pytest.raises(capi.LlmrError, match="same buffer"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, img2.data_ptr(), nb - 1)
+    with pytest.raises(capi.LlmrError, match="needs"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, 256 + 32, 0, img2.data_ptr(), nb)
+    with pytest.raises(capi.LlmrError, match="in_dim"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
     nxt.count = 1
     with pytest.raises(capi.LlmrError, match="also an image"):
@@ -857,3 +867,43 @@ def test_weight_image_entry_points_reject_bad_arguments(dev):
         ctx.flash_attention_rows(q.data_ptr(), q.data_ptr(), q.data_ptr(), 1, o.data_ptr(), 8, 264, 128, 2, 64, 0.1)
     torch.cuda.synchronize()
     assert (y == 0).all()
+
+
+@pytest.mark.parametrize("wtype,xtype,Ms,N,K", [
+    (12, 30, (512, 4096), 9216, 3072),   # the Flux double block's QKV: 648 tiles, room for all 73 items
+    (8, 1, (4608,), 3328, 512),           # 234 tiles: room for 44 of the 73 items, the rest after the GEMM
+])
+def test_multi_next_images_of_two_groups(dev, wtype, xtype, Ms, N, K):
+    """next_images of the two groups after this call (the Flux double block's
+    QKV builds the projection's and the MLP-in's): four images of two shapes
+    (N2 x K2, N3 x K3, with row offsets), numbered across all four, built
+    as far as the call's idle workgroups reach and the rest after the GEMM,
+    equal llmr_build_weight_image's bytes; the call's own output is the
+    plain call's."""
+    import torch
+    from llmr_amd import gguf, ops, synth
+    g = ops.default_graph()
+    blks, xs, wts = _multi_setup(dev, wtype, Ms, N, K, xtype, 53)
+    # (N2, K2, row_offset): 9 + 12 + 48 + 4 items of (256-row panel, 4 K stages)
+    shapes = [(640, 768, 0), (1000, 768, 8), (1536, 2048, 0), (256, 1024, 16)]
+    nw = [ops.Tensor.quantized(torch.from_numpy(gguf.quantize(synth.normal(53, 60 + i, (n + ro) * k, 0.02),
+                                                              wtype)).to(dev), wtype, n + ro, k)
+          for i, (n, k, ro) in enumerate(shapes)]
+    chained = [torch.zeros(ops.weight_image_bytes(n, k), dtype=torch.uint8, device=dev) for n, k, _ in shapes]
+    direct = [torch.zeros_like(c) for c in chained]
+    out_a = torch.zeros(sum(Ms), N, device=dev)
+    out_b = torch.zeros(sum(Ms), N, device=dev)
+    rows = [sum(Ms[:i]) for i in range(len(Ms) + 1)]
+
+    def jobs(out):
+        return [ops.MatmulJob(wts[i], ops.Tensor.from_torch(xs[i]), out[rows[i]:rows[i + 1]], Ms[i], 8 * i)
+                for i in range(len(Ms))]
+    nxt = ops.NextImages([ops.NextImage(w, n, k, im, ro) for w, (n, k, ro), im in zip(nw, shapes, chained)])
+    ops.dispatch_batch_matmul_multi(g, jobs(out_a), N, K, next_images=nxt)
+    ops.dispatch_batch_matmul_multi(g, jobs(out_b), N, K)
+    for w, (n, k, ro), im in zip(nw, shapes, direct):
+        ops.build_weight_image(g, w, n, k, ro, xtype, im)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    for i in range(len(shapes)):
+        assert torch.equal(chained[i], direct[i]), i
