@@ -9,10 +9,14 @@
 // activations it needs (a 64-element slice per token at a time); the 16
 // partial sums of a row are reduced with lane shuffles. When the
 // activations fit in 48 KiB of LDS the variant below is used (activations
-// staged in LDS, 64-element units spread over all 16 lanes). Arithmetic is the
-// reference's f32 path (batch_matmul_q4k, llm.slang:2264-2365): weight
+// staged in LDS, 64-element units spread over all 16 lanes). Arithmetic is
+// f32 throughout, as the reference's batch_matmul_q4k (llm.slang:2264-2365)
+// with activations in f32: the register variant forms each weight as
 // (d*sc)*q - dmin*mn with one rounding (the FMA below; both products are
-// exact), activations in f32, f32 accumulation (in a different order).
+// exact), as the reference does; the LDS variant sums the same products as
+// d*sc * sum q x - dmin*mn * sum x per 32-element sub-block (the activation
+// sums shared by a lane's rows), one FMA per weight instead of two VALU
+// operations (double-block modulation launch 379-416 -> 342-371 us).
 #include <hip/hip_runtime.h>
 
 #include "llmr_device.h"
@@ -220,6 +224,13 @@ __global__ void __launch_bounds__(256) gemv_q4k_lds_kernel(const GemvJobs<CAP> j
                 xl[c] = xr[c];
                 xh[c] = xr[c + 8];
             }
+            // the sub-blocks' activation sums, shared by the lane's rows
+            float sxl = 0.0f, sxh = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                sxl += (xl[c].x + xl[c].y) + (xl[c].z + xl[c].w);
+                sxh += (xh[c].x + xh[c].y) + (xh[c].z + xh[c].w);
+            }
 #pragma unroll
             for (int i = 0; i < RPL; ++i) {
                 const float d = f16_bits_to_f32(cur.hdr[i].x & 0xffffu), dmin = f16_bits_to_f32(cur.hdr[i].x >> 16);
@@ -228,20 +239,28 @@ __global__ void __launch_bounds__(256) gemv_q4k_lds_kernel(const GemvJobs<CAP> j
                 q4k_scale_min(2u * j + 1u, cur.hdr[i].y, cur.hdr[i].z, cur.hdr[i].w, sc1, mn1);
                 const float d0 = d * (float)sc0, m0 = dmin * (float)mn0;
                 const float d1 = d * (float)sc1, m1 = dmin * (float)mn1;
+                // sum (d0 q - m0) x = d0 sum q x - m0 sum x per 32-element
+                // sub-block: one FMA per weight on the nibble as a float
+                float ql = 0.0f, qh = 0.0f;
 #pragma unroll
                 for (int c = 0; c < 8; c++) {
                     const uint32_t word = c < 4 ? cur.qa[i][c] : cur.qb[i][c - 4];
-                    f32x4 wl, wh;
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const uint32_t q = (word >> (8 * k)) & 0xffu;
-                        wl[k] = __builtin_fmaf((float)(q & 15u), d0, -m0);
-                        wh[k] = __builtin_fmaf((float)(q >> 4), d1, -m1);
-                    }
+                    // nibbles in the bytes of lo / hi; hidden from the compiler's
+                    // known bits so each byte converts with one v_cvt_f32_ubyteN
+                    // (seen as a 4-bit field it extracts with v_bfe_u32 first)
+                    uint32_t lo = word & 0x0f0f0f0fu, hi = (word >> 4) & 0x0f0f0f0fu;
+                    asm("" : "+v"(lo), "+v"(hi));
                     const f32x4 a = xl[c], h = xh[c];
-                    acc[i][m] += (wl.x * a.x + wl.y * a.y) + (wl.z * a.z + wl.w * a.w) +
-                                 ((wh.x * h.x + wh.y * h.y) + (wh.z * h.z + wh.w * h.w));
+                    ql = __builtin_fmaf((float)(lo & 0xffu), a.x, ql);
+                    ql = __builtin_fmaf((float)((lo >> 8) & 0xffu), a.y, ql);
+                    ql = __builtin_fmaf((float)((lo >> 16) & 0xffu), a.z, ql);
+                    ql = __builtin_fmaf((float)(lo >> 24), a.w, ql);
+                    qh = __builtin_fmaf((float)(hi & 0xffu), h.x, qh);
+                    qh = __builtin_fmaf((float)((hi >> 8) & 0xffu), h.y, qh);
+                    qh = __builtin_fmaf((float)((hi >> 16) & 0xffu), h.z, qh);
+                    qh = __builtin_fmaf((float)(hi >> 24), h.w, qh);
                 }
+                acc[i][m] += (d0 * ql - m0 * sxl) + (d1 * qh - m1 * sxh);
             }
         }
         cur = nxt;

@@ -70,9 +70,11 @@ CASES = [
 
 @pytest.mark.parametrize("M,N,K,row_offset", [(1, 18432, 3072, 0), (1, 3072, 256, 0), (4, 264, 4096, 16)])
 def test_small_m_q4k_f32_matches_reference_arithmetic(orc, dev, M, N, K, row_offset):
-    """M <= 4 Q4_K launches keep the activations in f32 and dequantize in
-    f32 like batch_matmul_q4k, so only the summation order differs from the
-    oracle: far inside the GEMM bar (the modulation-projection shape first)."""
+    """M <= 4 Q4_K launches keep the activations in f32 and sum the
+    f32 products of batch_matmul_q4k's dequantized weights (per sub-block as
+    d*sc * sum q x - dmin*mn * sum x): only the rounding order differs from
+    the oracle, far inside the GEMM bar (the modulation-projection shape
+    first)."""
     from llmr_amd import gguf, synth
     blk = gguf.quantize(synth.normal(21, 2, (N + row_offset) * K, 0.02), 12)
     x = synth.normal(21, 1, M * K).reshape(M, K)
