@@ -69,6 +69,9 @@ class ZImageLayerWeights:
     q_norm: torch.Tensor    # f32 [128]
     k_norm: torch.Tensor
     adaln: torch.Tensor     # f32 [4, dim]: scale_msa, gate_msa, scale_mlp, gate_mlp
+    # w_gate's rows followed by w_up's in one buffer (w_gate and w_up are then
+    # views of it; a loader concatenates the two tensors' blocks once), or None
+    w_gate_up: torch.Tensor | None = None
 
 
 class ZImageBlock:
@@ -119,9 +122,17 @@ class ZImageBlock:
         # E: FFN pre-norm, * (1 + scale_mlp)                           (dit.c3:1545-1554)
         glue.batch_rmsnorm(hidden, w.ffn_norm1, self.xa, eps, mod_scale=w.adaln[2], g=g)
         # F: SwiGLU in-projection, down-projection                     (dit.c3:1562-1596)
-        dispatch_batch_matmul_swiglu(g, _qt(w.w_gate, GGML_Q8_0, ffn, dim), _qt(w.w_up, GGML_Q8_0, ffn, dim),
-                                     _t(self.xa), _t(self.f), ffn, dim, S)
-        glue.activation(self.f, self.fa, capi.ACT_COPY, g=g)
+        if w.w_gate_up is not None:
+            # gate | up in one weight: silu(gate) * up straight into the
+            # down-projection input in the activation type (the split-SwiGLU
+            # epilogue with no plain columns); on the two-pass kernel bit for
+            # bit the SwiGLU's f32 output and its copy below
+            dispatch_batch_matmul_multi(g, [MatmulJob(_qt(w.w_gate_up, GGML_Q8_0, 2 * ffn, dim), _t(self.xa), None,
+                                                      S, 0, None, self.fa)], 2 * ffn, dim, capi.EPI_SPLIT_SWIGLU, 0)
+        else:
+            dispatch_batch_matmul_swiglu(g, _qt(w.w_gate, GGML_Q8_0, ffn, dim), _qt(w.w_up, GGML_Q8_0, ffn, dim),
+                                         _t(self.xa), _t(self.f), ffn, dim, S)
+            glue.activation(self.f, self.fa, capi.ACT_COPY, g=g)
         dispatch_batch_matmul(g, _qt(w.w_down, GGML_Q8_0, dim, ffn), _t(self.fa), _t(self.t), dim, ffn, S, 0)
         # G: hidden += tanh(gate_mlp) * rmsnorm(down)                  (dit.c3:1600-1610)
         glue.gated_residual(hidden, self.t, w.adaln[3], capi.GATE_TANH, w.ffn_norm2, eps, g=g)
@@ -144,13 +155,15 @@ def zimage_layer_weights(dim: int, n_heads: int, ffn: int, device="cuda", seed: 
         return torch.from_numpy(mean + synth.normal(seed, stream, n, std)).to(device)
 
     b = base_stream
+    gate_up = torch.cat([q8(ffn, dim, b + 6), q8(ffn, dim, b + 7)])  # gate rows, then up rows
+    half = gate_up.numel() // 2
     return ZImageLayerWeights(
-        wqkv=q8(3 * dim, dim, b + 1), wo=q8(dim, dim, b + 3), w_gate=q8(ffn, dim, b + 6),
-        w_up=q8(ffn, dim, b + 7), w_down=q8(dim, ffn, b + 5),
+        wqkv=q8(3 * dim, dim, b + 1), wo=q8(dim, dim, b + 3), w_gate=gate_up[:half], w_up=gate_up[half:],
+        w_down=q8(dim, ffn, b + 5),
         attn_norm1=vec(dim, b + 20, 1.0, 0.1), attn_norm2=vec(dim, b + 21, 1.0, 0.1),
         ffn_norm1=vec(dim, b + 22, 1.0, 0.1), ffn_norm2=vec(dim, b + 23, 1.0, 0.1),
         q_norm=vec(HEAD_DIM, b + 24, 1.0, 0.1), k_norm=vec(HEAD_DIM, b + 25, 1.0, 0.1),
-        adaln=vec(4 * dim, b + 26, 0.0, 0.5).reshape(4, dim))
+        adaln=vec(4 * dim, b + 26, 0.0, 0.5).reshape(4, dim), w_gate_up=gate_up)
 
 
 # ---------------------------------------------------------------------------

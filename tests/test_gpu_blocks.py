@@ -39,6 +39,33 @@ def test_zimage_block_vs_oracle(dev, act):
     assert err < (3e-3 if act == torch.float16 else 1e-2)
 
 
+def test_zimage_block_fused_swiglu_bit_identical(dev):
+    """With gate and up in one weight (w_gate_up) the block's SwiGLU is one
+    split-SwiGLU launch writing silu(gate) * up straight into the
+    down-projection input: where both run the two-pass kernel (2304 tokens,
+    144 tiles) bit for bit the SwiGLU's f32 output followed by the copy to
+    the activation type. (With too few tiles for the persistent kernels the
+    split launch falls back to a GEMM and the glue's reference silu, which
+    rounds differently: test_zimage_block_vs_oracle covers that shape.)"""
+    import dataclasses
+    from llmr_amd import dit, synth, workloads
+    dim, H, ffn, S = 512, 4, 2048, 2304
+    w = dit.zimage_layer_weights(dim, H, ffn, device=dev, base_stream=700)
+    att = workloads.Attention("z", H, S, 128, 24, 11, 16, (32, 48, 48), 256.0)
+    rope = tuple(torch.from_numpy(t).to(dev)
+                 for t in workloads.rope_tables(workloads.attention_positions(att), att.axes, att.theta))
+    h0 = torch.from_numpy(synth.normal(42, 701, S * dim).reshape(S, dim)).to(dev)
+    out = []
+    for ww in (w, dataclasses.replace(w, w_gate_up=None)):
+        blk = dit.ZImageBlock(dim, H, ffn, S, act_dtype=torch.bfloat16, device=dev)
+        h = h0.clone()
+        blk.forward(ww, h, *rope)
+        out.append(h)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out[0]).all() and not torch.equal(out[0], h0)
+    assert torch.equal(out[0], out[1])
+
+
 def _small_flux(mlp_act="gelu"):
     from llmr_amd import dit
     return dit.FluxConfig(dim=256, n_heads=2, mlp=512, n_double=2, n_single=2, text_dim=256, n_txt=40,
