@@ -219,7 +219,7 @@ enum { LLMR_EPI_STORE = 0, LLMR_EPI_GATED_RESIDUAL = 1, LLMR_EPI_SPLIT_GELU = 2,
  *                    n < split: output[m*ldy + n] = r;
  *                    o < f: output2[m*ldy2 + o] = silu(r[split + o]) *
  *                    r[split + f + o] rounded to output2_type
- *                    (split % 256 == 0, f % 8 == 0; not with weight images)
+ *                    (split % 256 == 0, f % 8 == 0)
  * ldy 0 means out_dim (SPLIT_*: split); ldy2 0 means out_dim - split
  * (SPLIT_SWIGLU: f). Strides are multiples of 4; out_dim % 4 == 0 unless the
  * epilogue is a STORE with ldy == out_dim. */
@@ -276,19 +276,29 @@ LLMR_API int llmr_batch_matmul_multi(llmr_context* ctx, uint32_t weight_type, ui
  * above), as operands for input_type F16 or BF16, on the context's current
  * stream. */
 LLMR_API size_t llmr_weight_image_bytes(uint32_t out_dim, uint32_t in_dim);
+/* Bytes of the SwiGLU-arranged image of n_out outputs (gate and up rows
+ * interleaved per 128 outputs; 0 when in_dim % 64 != 0). */
+LLMR_API size_t llmr_swiglu_weight_image_bytes(uint32_t n_out, uint32_t in_dim);
 LLMR_API int llmr_build_weight_image(llmr_context* ctx, const void* weight, uint32_t weight_type,
                                      uint32_t input_type, uint32_t out_dim, uint32_t in_dim, uint32_t row_offset,
                                      void* image, size_t image_bytes);
 
-/* One weight image a call builds for a later call: rows [row_offset,
- * row_offset + out_dim) of a weight with in_dim columns. */
+/* One weight image a call builds for a later call, of a weight with in_dim
+ * columns. swiglu 0: rows [row_offset, row_offset + out_dim) (sized by
+ * llmr_weight_image_bytes). swiglu 1: the SwiGLU arrangement of out_dim
+ * outputs, gate rows [row_offset, row_offset + out_dim) and up rows
+ * [row_offset + out_dim, row_offset + 2 out_dim) (sized by
+ * llmr_swiglu_weight_image_bytes): what a SPLIT_SWIGLU job reads after the
+ * plain image of its first `split` rows, at llmr_weight_image_bytes(split,
+ * in_dim) into its image. */
 typedef struct llmr_next_weight_image {
     const void* weight;
     uint32_t out_dim;
     uint32_t in_dim;     /* % 64 == 0 */
     uint32_t row_offset;
+    uint32_t swiglu;
     void* image;         /* 256-byte aligned */
-    size_t image_bytes;  /* >= llmr_weight_image_bytes(out_dim, in_dim) */
+    size_t image_bytes;
 } llmr_next_weight_image;
 
 /* The weight images of the GEMM groups a caller issues next (the next
@@ -305,8 +315,11 @@ typedef struct llmr_next_weight_images {
  *     built by llmr_build_weight_image or by the `next` of an earlier call
  *     with the job's weight, weight_type, input_type, out_dim, in_dim and
  *     row_offset (the weight unchanged since; the call cannot check the
- *     contents). Job groups that run two-pass use them instead of building
- *     their own; other groups ignore them.
+ *     contents). SPLIT_SWIGLU: the image of rows [row_offset, + split) (none
+ *     when split == 0), then at llmr_weight_image_bytes(split, in_dim) the
+ *     SwiGLU image of the job's f outputs (a `next` entry with swiglu 1,
+ *     out_dim f, row_offset + split). Job groups that run two-pass use them
+ *     instead of building their own; other groups ignore them.
  *   next (NULL or images of later groups): all built before the call
  *     returns its work to the stream, as many items as fit by this call's
  *     idle workgroups (the workgroups without a tile in the GEMM's last

@@ -516,13 +516,14 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
             const llmr_next_weight_image& m = next->image[i];
             if (m.in_dim % 64 || m.out_dim == 0)
                 return fail(LLMR_ERR_INVALID_ARG, "next image %u: in_dim %% 64 == 0 and out_dim > 0 needed", i);
-            const size_t need = llmr::w16_image_bytes(m.out_dim, m.in_dim, false);
+            if (m.swiglu > 1) return fail(LLMR_ERR_INVALID_ARG, "next image %u: swiglu must be 0 or 1", i);
+            const size_t need = llmr::w16_image_bytes(m.out_dim, m.in_dim, m.swiglu != 0);
             if (m.image_bytes < need)
                 return fail(LLMR_ERR_INVALID_ARG, "next image %u holds %zu bytes, needs %zu", i, m.image_bytes,
                             need);
             if (int r = check_weight(m.weight, next->weight_type, m.in_dim)) return r;
-            if ((uint64_t)m.row_offset + m.out_dim > 0xffffffffull)
-                return fail(LLMR_ERR_INVALID_ARG, "next image %u: row_offset + out_dim overflows", i);
+            if ((uint64_t)m.row_offset + (m.swiglu ? 2ull : 1ull) * m.out_dim > 0xffffffffull)
+                return fail(LLMR_ERR_INVALID_ARG, "next image %u: its last row overflows 32 bits", i);
             if (!m.image || !aligned(m.image, 256))
                 return fail(LLMR_ERR_INVALID_ARG, "next image %u must be non-null and 256-byte aligned", i);
             for (uint32_t j = 0; j < i; j++)
@@ -537,6 +538,7 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
             nx.row_offset[i] = m.row_offset;
             nx.N[i] = m.out_dim;
             nx.K[i] = m.in_dim;
+            nx.sw[i] = m.swiglu;
         }
         nx.count = next->count;
         nx.wtype = next->weight_type;
@@ -564,8 +566,6 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
     if (swiglu && (e.split % 256 || f2 % 16 || f2 == 0))
         return fail(LLMR_ERR_INVALID_ARG, "SPLIT_SWIGLU needs split %% 256 == 0 and out_dim - split = 2 f, "
                     "f %% 8 == 0, f > 0 (got split %u, out_dim %u)", e.split, out_dim);
-    if (swiglu && (images || next))
-        return fail(LLMR_ERR_INVALID_ARG, "SPLIT_SWIGLU takes no weight images");
     if (e.ldy == 0) e.ldy = split ? e.split : out_dim;
     if (e.ldy2 == 0) e.ldy2 = n2;
     const uint32_t width = split ? e.split : out_dim;
@@ -645,6 +645,10 @@ int llmr_batch_matmul_multi_qkv(llmr_context* ctx, uint32_t wtype, uint32_t xtyp
 
 size_t llmr_weight_image_bytes(uint32_t out_dim, uint32_t in_dim) {
     return in_dim % 64 ? 0u : llmr::w16_image_bytes(out_dim, in_dim, false);
+}
+
+size_t llmr_swiglu_weight_image_bytes(uint32_t n_out, uint32_t in_dim) {
+    return in_dim % 64 ? 0u : llmr::w16_image_bytes(n_out, in_dim, true);
 }
 
 int llmr_build_weight_image(llmr_context* ctx, const void* weight, uint32_t wtype, uint32_t xtype, uint32_t out_dim,

@@ -1660,8 +1660,21 @@ uint32_t next_items_per_idle_wg(uint32_t K) { return max(1u, K / (uint32_t)kBK /
 
 uint32_t next_image_items(const NextImageSet& nx) {
     uint32_t all = 0;
-    for (uint32_t i = 0; i < nx.count; i++) all += w16_image_items(nx.N[i], nx.K[i]);
+    for (uint32_t i = 0; i < nx.count; i++) all += w16_image_items(nx.N[i], nx.K[i], nx.sw[i] != 0);
     return all;
+}
+
+// The raw rows of next image i: plain, w at its row_offset (g, u null
+// pointers returned as g = w); SwiGLU, its gate rows g and up rows u.
+static void next_image_rows(const NextImageSet& nx, uint32_t i, const void*& g, const void*& u) {
+    if (!nx.sw[i]) {
+        g = nx.w[i];
+        u = nullptr;
+        return;
+    }
+    const uint64_t rb = row_bytes_of(nx.wtype, nx.K[i]);
+    g = (const uint8_t*)nx.w[i] + (uint64_t)nx.row_offset[i] * rb;
+    u = (const uint8_t*)g + (uint64_t)nx.N[i] * rb;
 }
 
 // Later groups' images: the items [0, fused) came from the GEMM's idle
@@ -1669,12 +1682,14 @@ uint32_t next_image_items(const NextImageSet& nx) {
 hipError_t finish_next_images(const NextImageSet& nx, uint32_t otype, uint32_t fused, hipStream_t st) {
     uint32_t first = 0;
     for (uint32_t i = 0; i < nx.count; i++) {
-        const uint32_t per = w16_image_items(nx.N[i], nx.K[i]);
+        const uint32_t per = w16_image_items(nx.N[i], nx.K[i], nx.sw[i] != 0);
         const uint32_t done = fused > first ? min(per, fused - first) : 0u;
         first += per;
         if (done == per) continue;
-        const hipError_t e = launch_w16_image(nx.w[i], nullptr, nx.wtype, otype, nx.img[i], nx.N[i], nx.K[i],
-                                              nx.row_offset[i], st, done);
+        const void *g, *u;
+        next_image_rows(nx, i, g, u);
+        const hipError_t e = launch_w16_image(g, u, nx.wtype, otype, nx.img[i], nx.N[i], nx.K[i],
+                                              nx.sw[i] ? 0u : nx.row_offset[i], st, done);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -1719,13 +1734,16 @@ hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N,
                     NextImages& ni = a.next;
                     uint32_t first = 0;
                     for (uint32_t q = 0; q < next->count; q++) {
-                        ni.W[q] = (const uint8_t*)next->w[q];
+                        const void *g, *u;
+                        next_image_rows(*next, q, g, u);
+                        ni.W[q] = (const uint8_t*)g;
+                        ni.W2[q] = (const uint8_t*)u;
                         ni.img[q] = (uint8_t*)next->img[q];
-                        ni.row_offset[q] = next->row_offset[q];
+                        ni.row_offset[q] = next->sw[q] ? 0u : next->row_offset[q];
                         ni.N[q] = next->N[q];
                         ni.K[q] = next->K[q];
                         ni.first[q] = first;
-                        first += w16_image_items(next->N[q], next->K[q]);
+                        first += w16_image_items(next->N[q], next->K[q], next->sw[q] != 0);
                     }
                     ni.count = next->count;
                     ni.wtype = next->wtype;

@@ -79,33 +79,51 @@ __device__ __forceinline__ void split_bf16x8(const float (&v)[8], u32x4& hi, u32
     }
 }
 // Items (panel p, group of kImgStages stages) of a weight's image:
-// panels * groups of them, item = p * groups + group.
+// panels * groups of them, item = p * groups + group; a panel is 256 rows
+// (SwiGLU: 128 outputs, their gate and up rows).
 __host__ __device__ __forceinline__ uint32_t image_groups(uint32_t K) {
     return (K / (uint32_t)kBK + kImgStages - 1) / kImgStages;
 }
-__host__ __device__ __forceinline__ uint32_t image_items(uint32_t N, uint32_t K) {
-    return (N + 255u) / 256u * image_groups(K);
+__host__ __device__ __forceinline__ uint32_t image_items(uint32_t N, uint32_t K, bool sw = false) {
+    return (sw ? (N + 127u) / 128u : (N + 255u) / 256u) * image_groups(K);
 }
-// One item of a plain image (no SwiGLU arrangement, no LoRA) by the 256
-// threads of a workgroup (thread r: row r of the panel), through the two
-// 32 KiB LDS blocks lb0 and lb1 (one barrier per stage). Callers running
-// several items in a row put a barrier between them. NT: non-temporal
-// stores (items built beside a running GEMM: streamed, they evict less of
-// its operands from L2; Flux step 76.3 -> 75.8 ms).
-template <uint32_t WT, uint32_t OT, bool NT = false>
-__device__ __forceinline__ void image_item(const uint8_t* __restrict__ W, uint8_t* __restrict__ img, uint32_t N,
-                                           uint32_t K, uint32_t row_offset, uint32_t item, uint8_t* lb0,
-                                           uint8_t* lb1) {
+// One item of an image without LoRA by the 256 threads of a workgroup
+// (thread r: row r of the panel), through the two 32 KiB LDS blocks lb0 and
+// lb1 (one barrier per stage). Callers running several items in a row put
+// a barrier between them. Plain (SW false): rows row_offset + 256 p + r of
+// W. SW: the SwiGLU arrangement of N outputs, W the gate rows and W2 the up
+// rows of output 0 (row_offset unused): panel p holds outputs 128 p .. +
+// 127, its rows gate 0-63 | up 0-63 | gate 64-127 | up 64-127 (wave q of
+// the workgroup: gate or up by q % 2, outputs 64 (q / 2) ..), the
+// arrangement of the fused SwiGLU kernel. NT: non-temporal stores (items
+// built beside a running GEMM: streamed, they evict less of its operands
+// from L2; Flux step 76.3 -> 75.8 ms).
+template <uint32_t WT, uint32_t OT, bool NT = false, bool SW = false>
+__device__ __forceinline__ void image_item(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2,
+                                           uint8_t* __restrict__ img, uint32_t N, uint32_t K, uint32_t row_offset,
+                                           uint32_t item, uint8_t* lb0, uint8_t* lb1) {
     const uint32_t S = K / kBK, groups = image_groups(K);
     const uint32_t p = item / groups, s0 = (item % groups) * kImgStages, r = threadIdx.x;
     const uint32_t rb = (WT == kGgmlQ8_0) ? (K / 32u) * 34u : (K / 256u) * 144u;
-    const uint32_t n0 = 256u * p;
-    const rsrc_t rs = make_rsrc(W + (uint64_t)row_offset * rb + (uint64_t)n0 * rb, (uint64_t)(N - n0) * rb);
+    const uint8_t* src;
+    uint32_t n0, row;  // the panel's first feature, this thread's row of it
+    if constexpr (SW) {
+        const uint32_t q = __builtin_amdgcn_readfirstlane(r >> 6);
+        n0 = 128u * p;
+        src = (q & 1u) ? W2 : W;
+        row = (q >> 1) * 64u + (r & 63u);
+    } else {
+        n0 = 256u * p;
+        src = W + (uint64_t)row_offset * rb;
+        row = r;
+    }
+    const rsrc_t rs = make_rsrc(src + (uint64_t)n0 * rb, (uint64_t)(N - n0) * rb);
     WRow<WT, OT> u[kImgStages];
 #pragma unroll
     for (uint32_t i = 0; i < kImgStages; i++)
         if (s0 + i < S)
-            static_for<0, WRow<WT, OT>::kLoads>([&](auto L) { u[i].template load<decltype(L)::value>(rs, r * rb, s0 + i); });
+            static_for<0, WRow<WT, OT>::kLoads>(
+                [&](auto L) { u[i].template load<decltype(L)::value>(rs, row * rb, s0 + i); });
     const uint32_t base = r * 128u + (lds_swz(r) << 4);
 #pragma unroll
     for (uint32_t i = 0; i < kImgStages; i++) {
@@ -132,9 +150,9 @@ template <uint32_t WT, uint32_t OT, bool SW, uint32_t RS = 0>
 __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2,
                                                          uint8_t* __restrict__ img, uint32_t N, uint32_t K,
                                                          uint32_t row_offset, const ImageLora lo, uint32_t item0) {
-    if constexpr (!SW && RS == 0) {  // a plain image: item item0 + blockIdx.x
+    if constexpr (RS == 0) {  // no LoRA: item item0 + blockIdx.x
         __shared__ __attribute__((aligned(16))) uint8_t blk[2u * kBlk];
-        image_item<WT, OT>(W, img, N, K, row_offset, item0 + blockIdx.x, blk, blk + kBlk);
+        image_item<WT, OT, false, SW>(W, W2, img, N, K, row_offset, item0 + blockIdx.x, blk, blk + kBlk);
         return;
     }
     constexpr bool LORA = RS > 0;         // RS: rank steps of 16 the kernel holds (rank <= 16 RS)
@@ -618,19 +636,26 @@ __global__ void __launch_bounds__(256, 1) gemm_w16_persist(const PersistArgs arg
         for (uint32_t j = w16_idle_rank(blockIdx.x, G, total); j < ni.items; j += idle) {
             uint32_t i = 0;  // the image of item j (uniform)
             while (i + 1u < ni.count && j >= ni.first[i + 1u]) i++;
-            if (ni.wtype == kGgmlQ4K)
-                image_item<kGgmlQ4K, XT, true>(ni.W[i], ni.img[i], ni.N[i], ni.K[i], ni.row_offset[i],
-                                               j - ni.first[i], X0, X1);
-            else
-                image_item<kGgmlQ8_0, XT, true>(ni.W[i], ni.img[i], ni.N[i], ni.K[i], ni.row_offset[i],
-                                                j - ni.first[i], X0, X1);
+            const uint32_t u = j - ni.first[i];
+            if (ni.W2[i] == nullptr) {
+                if (ni.wtype == kGgmlQ4K)
+                    image_item<kGgmlQ4K, XT, true>(ni.W[i], nullptr, ni.img[i], ni.N[i], ni.K[i], ni.row_offset[i],
+                                                   u, X0, X1);
+                else
+                    image_item<kGgmlQ8_0, XT, true>(ni.W[i], nullptr, ni.img[i], ni.N[i], ni.K[i],
+                                                    ni.row_offset[i], u, X0, X1);
+            } else if (ni.wtype == kGgmlQ4K) {
+                image_item<kGgmlQ4K, XT, true, true>(ni.W[i], ni.W2[i], ni.img[i], ni.N[i], ni.K[i], 0u, u, X0, X1);
+            } else {
+                image_item<kGgmlQ8_0, XT, true, true>(ni.W[i], ni.W2[i], ni.img[i], ni.N[i], ni.K[i], 0u, u, X0, X1);
+            }
             __syncthreads();
         }
     }
     LLMR_WAIT_VMCNT(0);  // no DMA may still be writing this workgroup's LDS when it exits
 }
 
-// The image's items [item0, all) (item0 > 0 only for plain images).
+// The image's items [item0, all) (item0 > 0 only without LoRA).
 template <uint32_t WT, uint32_t OT, bool SW, uint32_t RS = 0>
 hipError_t build_image(const void* w, const void* w2, void* img, uint32_t N, uint32_t K, uint32_t row_offset,
                        hipStream_t st, const ImageLora& lo = ImageLora{}, uint32_t item0 = 0) {
@@ -674,24 +699,23 @@ hipError_t launch_w16_epi(const PersistArgs& a, bool grouped, int num_cus, hipSt
 hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
                             uint32_t K, uint32_t row_offset, hipStream_t st, uint32_t item0) {
     const bool sw = w2 != nullptr;
-    if (sw && item0) return hipErrorInvalidValue;  // item offsets: plain images only
     const ImageLora no{};
     if (wtype == kGgmlQ8_0) {
         if (otype == kGgmlBF16)
-            return sw ? build_image<kGgmlQ8_0, kGgmlBF16, true>(w, w2, img, N, K, row_offset, st)
+            return sw ? build_image<kGgmlQ8_0, kGgmlBF16, true>(w, w2, img, N, K, row_offset, st, no, item0)
                       : build_image<kGgmlQ8_0, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
-        return sw ? build_image<kGgmlQ8_0, kGgmlF16, true>(w, w2, img, N, K, row_offset, st)
+        return sw ? build_image<kGgmlQ8_0, kGgmlF16, true>(w, w2, img, N, K, row_offset, st, no, item0)
                   : build_image<kGgmlQ8_0, kGgmlF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
     }
     if (sw)
-        return otype == kGgmlBF16 ? build_image<kGgmlQ4K, kGgmlBF16, true>(w, w2, img, N, K, row_offset, st)
-                                  : build_image<kGgmlQ4K, kGgmlF16, true>(w, w2, img, N, K, row_offset, st);
+        return otype == kGgmlBF16 ? build_image<kGgmlQ4K, kGgmlBF16, true>(w, w2, img, N, K, row_offset, st, no, item0)
+                                  : build_image<kGgmlQ4K, kGgmlF16, true>(w, w2, img, N, K, row_offset, st, no, item0);
     if (otype == kGgmlBF16)
         return build_image<kGgmlQ4K, kGgmlBF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
     return build_image<kGgmlQ4K, kGgmlF16, false>(w, w2, img, N, K, row_offset, st, no, item0);
 }
 
-uint32_t w16_image_items(uint32_t N, uint32_t K) { return image_items(N, K); }
+uint32_t w16_image_items(uint32_t N, uint32_t K, bool sw) { return image_items(N, K, sw); }
 
 hipError_t launch_w16_image_lora(const void* w, uint32_t wtype, uint32_t otype, void* img, uint32_t N, uint32_t K,
                                  uint32_t row_offset, const LoraGemm& l, hipStream_t st) {

@@ -128,23 +128,27 @@ hipError_t launch_gemm_few(const void* w, uint32_t wtype, const void* x, uint32_
 hipError_t launch_gemm_skinny(const void* w, uint32_t wtype, const void* x, uint32_t xtype, float* y, uint32_t N,
                               uint32_t K, uint32_t M, uint32_t row_offset, uint32_t splits, void* ws,
                               hipStream_t st);
-// item0 > 0 (plain images only): items [item0, w16_image_items(N, K)) of
-// the image, the first item0 having been built elsewhere (by the GEMM before,
+// item0 > 0: items [item0, w16_image_items(N, K, w2 != nullptr)) of the
+// image, the first item0 having been built elsewhere (by the GEMM before,
 // NextImageSet).
 hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint32_t otype, void* img, uint32_t N,
                             uint32_t K, uint32_t row_offset, hipStream_t st, uint32_t item0 = 0);
-// Work items (256-row panel x 4 stages) of a plain weight image.
-uint32_t w16_image_items(uint32_t N, uint32_t K);
+// Work items (256-row panel x 4 stages) of a weight image (sw: the SwiGLU
+// arrangement of N outputs, 128 outputs a panel).
+uint32_t w16_image_items(uint32_t N, uint32_t K, bool sw = false);
 // Weight images of the GEMM group that follows a launch_batch_matmul_multi
-// call (plain images of `count` weights of one shape N x K for the call's
-// 16-bit input type): built in part by the two-pass GEMM's workgroups that
-// are idle in its last round, the rest right after it, so they are complete
-// when the next call on the stream starts.
+// call and the one after (up to four images, each its own shape, for the
+// call's 16-bit input type): built in part by the two-pass GEMM's
+// workgroups that are idle in its last round, the rest right after it, so
+// they are complete when the next call on the stream starts. Image i: the
+// plain image of rows [row_offset, + N) of w (sw 0), or the SwiGLU
+// arrangement of N outputs whose gate rows are [row_offset, + N) and up
+// rows [row_offset + N, + N) (sw 1).
 constexpr uint32_t kMaxNextImages = 4;
 struct NextImageSet {
     const void* w[kMaxNextImages];
     void* img[kMaxNextImages];
-    uint32_t row_offset[kMaxNextImages], N[kMaxNextImages], K[kMaxNextImages];
+    uint32_t row_offset[kMaxNextImages], N[kMaxNextImages], K[kMaxNextImages], sw[kMaxNextImages];
     uint32_t count, wtype;
 };
 // Items of the images, numbered across them in order (image i's item u =

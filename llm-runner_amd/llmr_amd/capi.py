@@ -57,7 +57,8 @@ class MatmulEpilogue(ctypes.Structure):
 class NextWeightImage(ctypes.Structure):
     """llmr_next_weight_image: one weight image a call builds for a later call."""
     _fields_ = [("weight", ctypes.c_void_p), ("out_dim", ctypes.c_uint32), ("in_dim", ctypes.c_uint32),
-                ("row_offset", ctypes.c_uint32), ("image", ctypes.c_void_p), ("image_bytes", ctypes.c_size_t)]
+                ("row_offset", ctypes.c_uint32), ("swiglu", ctypes.c_uint32), ("image", ctypes.c_void_p),
+                ("image_bytes", ctypes.c_size_t)]
 
 
 class NextWeightImages(ctypes.Structure):
@@ -128,6 +129,7 @@ _SIGS = {
                                                    ctypes.POINTER(MatmulEpilogue), ctypes.POINTER(QkvHeadsOut),
                                                    ctypes.POINTER(_vp), ctypes.POINTER(NextWeightImages)]),
     "llmr_weight_image_bytes": (ctypes.c_size_t, [_u32, _u32]),
+    "llmr_swiglu_weight_image_bytes": (ctypes.c_size_t, [_u32, _u32]),
     "llmr_build_weight_image": (ctypes.c_int, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, ctypes.c_size_t]),
     "llmr_batch_matmul_swiglu": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp, _u32, _u32, _u32]),
     "llmr_batch_matmul_swiglu_pc": (ctypes.c_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp,

@@ -36,8 +36,9 @@ import torch
 from . import capi, glue, workloads
 from .gguf import GGML_Q4_K, GGML_Q8_0
 from .ops import _TORCH_GGML, FlashAttentionPC, MatmulJob, NextImages, QkvHeads, RenderGraph, Tensor, \
-    build_weight_image, default_graph, dispatch_batch_matmul, dispatch_batch_matmul_multi, \
-    dispatch_batch_matmul_swiglu, dispatch_flash_attention, dispatch_flash_attention_rows, weight_image_bytes
+    build_next_images, default_graph, dispatch_batch_matmul, dispatch_batch_matmul_multi, \
+    dispatch_batch_matmul_swiglu, dispatch_flash_attention, dispatch_flash_attention_rows, \
+    split_swiglu_image_bytes, weight_image_bytes
 
 HEAD_DIM = 128
 
@@ -404,89 +405,137 @@ TWO_PASS_MIN_TOKENS = 2048
 
 class _ImageChain:
     """Weight images of a fixed sequence of GEMM groups (one multi launch
-    each: one or two Q4_K/Q8_0 weights of one shape N x K, rows from 0, and
-    the token counts of its jobs), built ahead: group k's images by call
-    k - 1, or by call k - 2 when that call's idle workgroups (those without
-    a tile in its GEMM's last round) have room for all of them after group
-    k - 1's. A call's NextImages are built as far as its idle workgroups
-    reach and the rest right after it; the first group's are built before
-    it. Three buffers rotate (group k in buffer k % 3: at most two groups
-    are built ahead of the one running, none into the buffer it reads). The
-    room is estimated here from the launch's tile count; a wrong estimate
-    only moves items into the image launch after the GEMM. The results are
-    those of dispatch_batch_matmul_multi without images, bit for bit."""
+    each: one or two Q4_K/Q8_0 weights of one shape N x K, rows from 0, the
+    token counts of its jobs and, for a SPLIT_SWIGLU group, its split (a
+    weight's image then the plain image of its first split rows followed by
+    the SwiGLU image of its (N - split) / 2 outputs: two next images), built
+    ahead image by image: each of group k's images by call k - 1, or by call
+    k - 2 when that call's idle workgroups (those without a tile in its
+    GEMM's last round) have room for all of its items after what the call
+    builds before it. A call's NextImages are built as far as its idle
+    workgroups reach and the rest right after it; the first group's are
+    built before it. Three buffers rotate (group k in buffer k % 3: at most
+    two groups are built ahead of the one running, none into the buffer it
+    reads). The room is estimated here from the launch's tile count; a wrong
+    estimate only moves items into the image launch after the GEMM. The
+    results are those of dispatch_batch_matmul_multi without images, bit
+    for bit."""
 
     def __init__(self, groups, input_dtype: int, device, cus: int):
+        if any(self._entries(gr) > 4 for gr in groups):
+            raise ValueError("a group's images must fit one call's four next images")
         self.groups, self.xtype = groups, input_dtype
-        per = max(len(ws) * weight_image_bytes(N, K) for ws, N, K, _ in groups)
+        per = max(len(gr[0]) * self._image_bytes(gr) for gr in groups)
         self.bufs = [torch.empty(per, dtype=torch.uint8, device=device) for _ in range(3)]
-        self.builds = self.plan(groups, cus)  # call k -> the groups whose images it builds
+        self.builds = self.plan(groups, cus)  # call k -> the (group, image) pairs it builds
+        self.images = [self._next(k).entries for k in range(len(groups))]  # group k's NextImage entries
         self.k = 0
         self.active = False  # between start() and the last group's take()
 
     @classmethod
     def plan(cls, groups, cus: int):
-        """For each call, the later groups whose images it builds: group k + 1
-        unless call k - 1 built it, then group k + 2 if all of its items fit
-        in what is left of the call's room."""
+        """For each call k, the images (group j, image e) it builds, in order:
+        those of group k + 1 that call k - 1 did not build, then group k + 2's
+        in order while all items of the next one fit in what is left of the
+        call's room and a next image of the call's four is left."""
         n = len(groups)
         builds = [[] for _ in range(n)]
-        built = [False] * n
+        done = [0] * n  # images of each group assigned so far (in order)
         for c in range(n - 1):
-            room = cls._room(groups[c], cus)
+            room, slots = cls._room(groups[c], cus), 4
             for j in (c + 1, c + 2):
-                if j >= n or built[j]:
-                    continue
-                need = cls._items(groups[j])
-                if j > c + 1 and need > room:
+                if j >= n:
                     break
-                builds[c].append(j)
-                built[j] = True
-                room -= need
+                items = cls._entry_items(groups[j])
+                while done[j] < len(items):
+                    if j > c + 1 and (items[done[j]] > room or slots == 0):
+                        break
+                    builds[c].append((j, done[j]))
+                    room -= items[done[j]]
+                    slots -= 1
+                    done[j] += 1
         return builds
 
     @staticmethod
-    def _items(group) -> int:
-        """Image items of a group: (256-row panel, 4 K stages) each."""
-        ws, N, K, _ = group
-        return len(ws) * -(-N // 256) * -(-(K // 64) // 4)
+    def _split(group):
+        return group[4] if len(group) > 4 else None
 
-    @staticmethod
-    def _room(group, cus: int) -> int:
+    @classmethod
+    def _entry_items(cls, group) -> list:
+        """Image items ((256-row panel, 4 K stages) each) of the group's next
+        images in order: one image per weight; a split SwiGLU weight's plain
+        rows (when split > 0), then its SwiGLU rows."""
+        ws, N, K = group[:3]
+        stages = -(-(K // 64) // 4)
+        split = cls._split(group)
+        if split is None:
+            return [-(-N // 256) * stages] * len(ws)
+        one = ([split // 256 * stages] if split else []) + [-(-((N - split) // 2) // 128) * stages]
+        return one * len(ws)
+
+    @classmethod
+    def _entries(cls, group) -> int:
+        """Next images of a group."""
+        return len(cls._entry_items(group))
+
+    @classmethod
+    def _panels(cls, group) -> int:
+        """256-row panels of one weight's image (SwiGLU: 128 outputs each),
+        also the GEMM's column tiles."""
+        N, split = group[1], cls._split(group)
+        if split is None:
+            return -(-N // 256)
+        return split // 256 + -(-((N - split) // 2) // 128)
+
+    @classmethod
+    def _image_bytes(cls, group) -> int:
+        ws, N, K = group[:3]
+        split = cls._split(group)
+        return weight_image_bytes(N, K) if split is None else split_swiglu_image_bytes(split, (N - split) // 2, K)
+
+    @classmethod
+    def _items(cls, group) -> int:
+        """Image items of a group: (256-row panel, 4 K stages) each."""
+        return sum(cls._entry_items(group))
+
+    @classmethod
+    def _room(cls, group, cus: int) -> int:
         """Items the group's GEMM can build on its workgroups without a tile
         in the last round: one per four of its K stages each."""
-        ws, N, K, Ms = group
-        tiles = sum(-(-M // 256) for M in Ms) * -(-N // 256)
+        K, Ms = group[2], group[3]
+        tiles = sum(-(-M // 256) for M in Ms) * cls._panels(group)
         rem = tiles % cus
         return 0 if rem == 0 else (cus - rem) * max(1, K // 256)
 
     def _views(self, k: int):
-        ws, N, K, _ = self.groups[k]
-        n = weight_image_bytes(N, K)
-        return [self.bufs[k % 3][i * n:(i + 1) * n] for i in range(len(ws))]
+        n = self._image_bytes(self.groups[k])
+        return [self.bufs[k % 3][i * n:(i + 1) * n] for i in range(len(self.groups[k][0]))]
+
+    def _next(self, k: int) -> NextImages:
+        ws, N, K = self.groups[k][:3]
+        split = self._split(self.groups[k])
+        if split is None:
+            return NextImages.group(ws, N, K, self._views(k), (0,) * len(ws))
+        return NextImages.split_swiglu(ws, split, (N - split) // 2, K, self._views(k), (0,) * len(ws))
 
     def start(self, g: RenderGraph) -> None:
         """Before the first group: its images."""
         self.k = 0
         self.active = True
-        ws, N, K, _ = self.groups[0]
-        for w, im in zip(ws, self._views(0)):
-            build_weight_image(g, w, N, K, 0, self.xtype, im)
+        build_next_images(g, NextImages(self.images[0]), self.xtype)
 
     def take(self, jobs, N: int, K: int):
         """(images, next_images) for the next group's call, whose jobs must be
         that group's GEMMs (the same weights, in order, and shape): images are
         matched to jobs by position, which the C-ABI cannot check."""
         k = self.k
-        ws, gN, gK, _ = self.groups[k]
+        ws, gN, gK = self.groups[k][:3]
         if (gN, gK) != (N, K) or [w.ptr() for w in ws] != [j.weight.ptr() for j in jobs]:
             self.active = False
             raise RuntimeError(f"weight-image chain out of step: group {k} holds other weights than this call's")
         nxt = None
-        for j in self.builds[k]:
-            jw, jN, jK, _ = self.groups[j]
-            part = NextImages.group(jw, jN, jK, self._views(j), (0,) * len(jw))
-            nxt = part if nxt is None else nxt + part
+        if self.builds[k]:
+            nxt = NextImages([self.images[j][e] for j, e in self.builds[k]])
         self.k += 1
         self.active = self.k < len(self.groups)
         return self._views(k), nxt
@@ -505,23 +554,26 @@ class FluxDiT:
         c, e = cfg, dict(device=device)
         S, d, m, nt = c.seq, c.dim, c.mlp, c.n_txt
         # the blocks' GEMM groups in issue order, each group's weight images
-        # built by the call before it (when the GEMMs run two-pass)
-        # (the SwiGLU form's in-projections build their own images: plain rows
-        # and SwiGLU-arranged gate / up rows, which the chain does not make)
+        # built by the call before it (when the GEMMs run two-pass); the
+        # SwiGLU form's in-projections are SPLIT_SWIGLU groups (plain rows,
+        # then SwiGLU-arranged gate / up rows)
         self.ahead = None
         if images_ahead and S >= TWO_PASS_MIN_TOKENS and d % 64 == 0 and m % 64 == 0 and \
-                act_dtype in (torch.float16, torch.bfloat16) and cfg.mlp_act == "gelu":
+                act_dtype in (torch.float16, torch.bfloat16):
             def q4(t, K):
                 return _qt(t, GGML_Q4_K, t.numel() // (K // 256 * 144), K)
+            sw = cfg.mlp_act == "swiglu"
+            rows, sp0, sp1 = (2 * m, (0,), (3 * d,)) if sw else (m, (), ())  # MLP-in rows, splits
             groups = []
             two = (nt, S - nt)  # a double block's text and image jobs
             for w in doubles:
                 groups += [([q4(w.txt_qkv, d), q4(w.img_qkv, d)], 3 * d, d, two),
                            ([q4(w.txt_proj, d), q4(w.img_proj, d)], d, d, two),
-                           ([q4(w.txt_mlp0, d), q4(w.img_mlp0, d)], m, d, two),
+                           ([q4(w.txt_mlp0, d), q4(w.img_mlp0, d)], rows, d, two) + sp0,
                            ([q4(w.txt_mlp2, m), q4(w.img_mlp2, m)], d, m, two)]
             for w in singles:
-                groups += [([q4(w.linear1, d)], 3 * d + m, d, (S,)), ([q4(w.linear2, d + m)], d, d + m, (S,))]
+                groups += [([q4(w.linear1, d)], 3 * d + rows, d, (S,)) + sp1,
+                           ([q4(w.linear2, d + m)], d, d + m, (S,))]
             if groups:
                 cus = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
                 self.ahead = _ImageChain(groups, _TORCH_GGML[act_dtype], device, cus)

@@ -227,6 +227,21 @@ def weight_image_bytes(out_dim: int, in_dim: int) -> int:
     return n
 
 
+def swiglu_weight_image_bytes(n_out: int, in_dim: int) -> int:
+    """Bytes of the SwiGLU-arranged image of n_out outputs (their gate and up
+    rows) of in_dim (llmr_swiglu_weight_image_bytes)."""
+    n = capi.lib().llmr_swiglu_weight_image_bytes(n_out, in_dim)
+    if n == 0:
+        raise ValueError("weight images need in_dim % 64 == 0")
+    return n
+
+
+def split_swiglu_image_bytes(split: int, f: int, in_dim: int) -> int:
+    """Bytes of a SPLIT_SWIGLU job's image: the plain image of its first
+    `split` rows, then the SwiGLU image of its f outputs."""
+    return (weight_image_bytes(split, in_dim) if split else 0) + swiglu_weight_image_bytes(f, in_dim)
+
+
 def build_weight_image(g: RenderGraph, weight: Tensor, out_dim: int, in_dim: int, row_offset: int,
                        input_dtype: int, image: torch.Tensor) -> None:
     """Rows [row_offset, row_offset + out_dim) of `weight` dequantized into
@@ -291,12 +306,21 @@ def _qkv_heads_out(h: QkvHeads, n_jobs: int) -> tuple:
 class NextImage:
     """One weight image a call builds for a later call: rows [row_offset,
     row_offset + out_dim) of `weight` (a quantized Tensor) with in_dim
-    columns, into `image` (a device tensor of weight_image_bytes)."""
+    columns, into `image` (a device tensor of weight_image_bytes); swiglu:
+    the SwiGLU arrangement of out_dim outputs whose gate rows start at
+    row_offset and up rows at row_offset + out_dim (swiglu_weight_image_bytes)."""
     weight: Tensor
     out_dim: int
     in_dim: int
     image: object
     row_offset: int = 0
+    swiglu: bool = False
+
+    def nbytes(self) -> int:
+        return (swiglu_weight_image_bytes if self.swiglu else weight_image_bytes)(self.out_dim, self.in_dim)
+
+    def rows(self) -> int:
+        return self.row_offset + (2 if self.swiglu else 1) * self.out_dim
 
 
 @dataclasses.dataclass
@@ -310,8 +334,51 @@ class NextImages:
         """One group's images: its weights, out_dim x in_dim each."""
         return cls([NextImage(w, out_dim, in_dim, im, ro) for w, im, ro in zip(weights, images, row_offsets)])
 
+    @classmethod
+    def split_swiglu(cls, weights, split: int, f: int, in_dim: int, images, row_offsets=(0, 0)) -> "NextImages":
+        """A SPLIT_SWIGLU group's images (out_dim = split + 2 f): per weight,
+        the plain image of its first split rows (none when split is 0) and,
+        in the same buffer right after it, the SwiGLU image of its f outputs."""
+        es = []
+        for w, im, ro in zip(weights, images, row_offsets):
+            flat = im.view(torch.uint8).reshape(-1)
+            plain = weight_image_bytes(split, in_dim) if split else 0
+            if split:
+                es.append(NextImage(w, split, in_dim, flat[:plain], ro))
+            es.append(NextImage(w, f, in_dim, flat[plain:], ro + split, True))
+        return cls(es)
+
     def __add__(self, other: "NextImages") -> "NextImages":
         return NextImages(self.entries + other.entries)
+
+
+def _next_images_struct(next_images: NextImages) -> capi.NextWeightImages:
+    es = next_images.entries
+    if not 1 <= len(es) <= 4:
+        raise ValueError("next_images: one to four images")
+    if len(es) != len(set(e.image.data_ptr() for e in es)):
+        raise ValueError("next_images: one buffer per image")
+    nt = es[0].weight.dtype
+    arr = (capi.NextWeightImage * 4)()
+    for i, e in enumerate(es):
+        _dev(e.weight, "next weight")
+        nbytes = e.nbytes()
+        if e.weight.dtype != nt or e.weight.shape[1] != e.in_dim or e.rows() > e.weight.shape[0]:
+            raise ValueError("next weights: one type, covering the image's rows x in_dim")
+        if not e.image.is_cuda or e.image.numel() * e.image.element_size() < nbytes:
+            raise ValueError(f"next images must be device tensors of at least {nbytes} bytes")
+        arr[i] = capi.NextWeightImage(e.weight.ptr(), e.out_dim, e.in_dim, e.row_offset, int(e.swiglu),
+                                      e.image.data_ptr(), e.image.numel() * e.image.element_size())
+    return capi.NextWeightImages(nt, len(es), arr)
+
+
+def build_next_images(g: RenderGraph, next_images: NextImages, input_dtype: int) -> None:
+    """The images of next_images built now, on the current stream, for
+    input_dtype (F16 or BF16): a llmr_batch_matmul_multi_images call with no
+    jobs (plain and SwiGLU-arranged images alike)."""
+    nx = _next_images_struct(next_images)
+    g.bind_stream()
+    g.ctx.batch_matmul_multi_images(next_images.entries[0].weight.dtype, input_dtype, 0, 0, [], None, None, nx)
 
 
 def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim: int,
@@ -404,30 +471,15 @@ def dispatch_batch_matmul_multi(g: RenderGraph, jobs: list, out_dim: int, in_dim
     if images is not None:
         if len(images) != len(jobs):
             raise ValueError("one weight image per job")
-        need = weight_image_bytes(out_dim, in_dim)
+        if epilogue == capi.EPI_SPLIT_SWIGLU:
+            need = split_swiglu_image_bytes(split, (out_dim - split) // 2, in_dim)
+        else:
+            need = weight_image_bytes(out_dim, in_dim)
         for im in images:
             if not im.is_cuda or im.numel() * im.element_size() < need:
                 raise ValueError(f"weight images must be device tensors of at least {need} bytes")
         ptrs = [im.data_ptr() for im in images]
-    nx = None
-    if next_images is not None:
-        es = next_images.entries
-        if not 1 <= len(es) <= 4:
-            raise ValueError("next_images: one to four images")
-        if len(es) != len(set(e.image.data_ptr() for e in es)):
-            raise ValueError("next_images: one buffer per image")
-        nt = es[0].weight.dtype
-        arr = (capi.NextWeightImage * 4)()
-        for i, e in enumerate(es):
-            _dev(e.weight, "next weight")
-            nbytes = weight_image_bytes(e.out_dim, e.in_dim)
-            if e.weight.dtype != nt or e.weight.shape[1] != e.in_dim or e.row_offset + e.out_dim > e.weight.shape[0]:
-                raise ValueError("next weights: one type, covering [row_offset, +out_dim) x in_dim")
-            if not e.image.is_cuda or e.image.numel() * e.image.element_size() < nbytes:
-                raise ValueError(f"next images must be device tensors of at least {nbytes} bytes")
-            arr[i] = capi.NextWeightImage(e.weight.ptr(), e.out_dim, e.in_dim, e.row_offset, e.image.data_ptr(),
-                                          e.image.numel() * e.image.element_size())
-        nx = capi.NextWeightImages(nt, len(es), arr)
+    nx = _next_images_struct(next_images) if next_images is not None else None
     if hout is not None:
         g.ctx.batch_matmul_multi_qkv(wtype, xtype, out_dim, in_dim, cj, epi, hout[0], hout[1], ptrs, nx)
     else:

@@ -36,6 +36,7 @@ static const struct {
     {"llmr_batch_matmul_multi_images", (void (*)(void))(uintptr_t)llmr_batch_matmul_multi_images},
     {"llmr_batch_matmul_multi_qkv", (void (*)(void))(uintptr_t)llmr_batch_matmul_multi_qkv},
     {"llmr_weight_image_bytes", (void (*)(void))(uintptr_t)llmr_weight_image_bytes},
+    {"llmr_swiglu_weight_image_bytes", (void (*)(void))(uintptr_t)llmr_swiglu_weight_image_bytes},
     {"llmr_build_weight_image", (void (*)(void))(uintptr_t)llmr_build_weight_image},
     {"llmr_batch_matmul_swiglu", (void (*)(void))(uintptr_t)llmr_batch_matmul_swiglu},
     {"llmr_batch_matmul_swiglu_pc", (void (*)(void))(uintptr_t)llmr_batch_matmul_swiglu_pc},

@@ -114,17 +114,19 @@ def test_flux_forward_is_deterministic(dev):
     assert torch.equal(a, b)
 
 
-def test_flux_images_ahead_bit_identical(dev):
+@pytest.mark.parametrize("act", ["gelu", "swiglu"])
+def test_flux_images_ahead_bit_identical(dev, act):
     """Each GEMM group's weight images built by the call before it (FluxDiT's
     default from 2048 tokens: the previous two-pass GEMM's idle workgroups
     build part of them) give the velocity of the same forward without them,
     bit for bit, on two forwards in a row (the buffers are reused across
     forwards). dim 1024 / mlp 4096 over 2368 tokens: the MLP-in and linear1
     groups run two-pass on the prebuilt images, the narrower groups ignore
-    theirs but still build the next ones."""
+    theirs but still build the next ones. swiglu: the Flux.2 form, whose
+    MLP-in and linear1 images hold SwiGLU-arranged gate / up rows."""
     from llmr_amd import dit, synth
     cfg = dit.FluxConfig(dim=1024, n_heads=8, mlp=4096, n_double=2, n_single=2, text_dim=256, n_txt=64,
-                         latent_ch=16, latent_h=96, latent_w=96, patch=2)
+                         latent_ch=16, latent_h=96, latent_w=96, patch=2, mlp_act=act)
     assert cfg.seq >= dit.TWO_PASS_MIN_TOKENS
     weights = dit.flux_weights(cfg, device=dev)
     ahead = dit.FluxDiT(cfg, *weights, device=dev)

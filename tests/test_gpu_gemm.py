@@ -843,17 +843,25 @@ def test_weight_image_entry_points_reject_bad_arguments(dev):
     with pytest.raises(capi.LlmrError, match="256-byte aligned"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, [img.data_ptr() + 16])
     img2 = torch.zeros(nb, dtype=torch.uint8, device=dev)
-    one = capi.NextWeightImage(w.ptr(), N, K, 0, img.data_ptr(), nb)
+    one = capi.NextWeightImage(w.ptr(), N, K, 0, 0, img.data_ptr(), nb)
     nxt = capi.NextWeightImages(12, 5, (capi.NextWeightImage * 4)(one, one, one, one))
     with pytest.raises(capi.LlmrError, match="count"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
     nxt.count = 2  # images 0 and 1 in one buffer
     with pytest.raises(capi.LlmrError, match="same buffer"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
-    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, img2.data_ptr(), nb - 1)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, 0, img2.data_ptr(), nb - 1)
     with pytest.raises(capi.LlmrError, match="needs"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
-    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, 256 + 32, 0, img2.data_ptr(), nb)
+    # a SwiGLU image of N outputs: twice the panels of the plain one
+    assert ops.swiglu_weight_image_bytes(N, K) > nb
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, 1, img2.data_ptr(), nb)
+    with pytest.raises(capi.LlmrError, match="needs"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, 2, img2.data_ptr(), nb)
+    with pytest.raises(capi.LlmrError, match="swiglu must be 0 or 1"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, 256 + 32, 0, 0, img2.data_ptr(), nb)
     with pytest.raises(capi.LlmrError, match="in_dim"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
     nxt.count = 1
@@ -909,3 +917,68 @@ def test_multi_next_images_of_two_groups(dev, wtype, xtype, Ms, N, K):
     assert torch.equal(out_a, out_b)
     for i in range(len(shapes)):
         assert torch.equal(chained[i], direct[i]), i
+
+
+@pytest.mark.parametrize("wtype,xtype,Ms,N,K", [
+    (12, 30, (4608,), 3328, 512),        # 234 tiles: room for 44 of the 51 items, the SwiGLU image's last 7 after
+    (8, 1, (512, 4096), 9216, 3072),     # 648 tiles: room for all of them
+])
+def test_multi_next_swiglu_images(dev, wtype, xtype, Ms, N, K):
+    """next_images with SwiGLU-arranged entries (the Flux.2 linear1 and MLP
+    in-projection): a SPLIT_SWIGLU weight's plain rows and its SwiGLU image
+    in one buffer, a second weight's SwiGLU image alone (split 0, row offset)
+    and a plain image, built as far as the call's idle workgroups reach and
+    the rest after the GEMM, equal the same images built by a call without
+    jobs byte for byte; a SPLIT_SWIGLU GEMM reading the first buffer equals
+    the one that builds its own image, bit for bit."""
+    import torch
+    from llmr_amd import capi, gguf, ops, synth
+    g = ops.default_graph()
+    _, xs, wts = _multi_setup(dev, wtype, Ms, N, K, xtype, 71)
+    split, f, K1 = 512, 1000, 768          # 6 plain + 24 SwiGLU items (f % 128 != 0: a ragged panel)
+    f2, K2, ro2 = 264, 1024, 16            # 12 SwiGLU items
+    n3, K3, ro3 = 640, 768, 8              # 9 plain items
+
+    def qw(seed, rows, k):
+        blk = gguf.quantize(synth.normal(71, seed, rows * k, 0.02), wtype)
+        return ops.Tensor.quantized(torch.from_numpy(blk).to(dev), wtype, rows, k)
+    w1, w2, w3 = qw(40, split + 2 * f, K1), qw(41, ro2 + 2 * f2, K2), qw(42, ro3 + n3, K3)
+
+    def bufs():
+        return [torch.zeros(ops.split_swiglu_image_bytes(split, f, K1), dtype=torch.uint8, device=dev),
+                torch.zeros(ops.swiglu_weight_image_bytes(f2, K2), dtype=torch.uint8, device=dev),
+                torch.zeros(ops.weight_image_bytes(n3, K3), dtype=torch.uint8, device=dev)]
+
+    def nxt(b):
+        return (ops.NextImages.split_swiglu([w1], split, f, K1, [b[0]]) +
+                ops.NextImages([ops.NextImage(w3, n3, K3, b[2], ro3)]) +
+                ops.NextImages.split_swiglu([w2], 0, f2, K2, [b[1]], (ro2,)))
+    chained, direct = bufs(), bufs()
+    assert len(nxt(chained).entries) == 4
+    out_a = torch.zeros(sum(Ms), N, device=dev)
+    out_b = torch.zeros(sum(Ms), N, device=dev)
+    rows = [sum(Ms[:i]) for i in range(len(Ms) + 1)]
+
+    def jobs(out):
+        return [ops.MatmulJob(wts[i], ops.Tensor.from_torch(xs[i]), out[rows[i]:rows[i + 1]], Ms[i], 8 * i)
+                for i in range(len(Ms))]
+    print(f"next swiglu images: w{wtype} x{xtype} jobs {Ms} {N}x{K}", flush=True)
+    ops.dispatch_batch_matmul_multi(g, jobs(out_a), N, K, next_images=nxt(chained))
+    ops.dispatch_batch_matmul_multi(g, jobs(out_b), N, K)
+    ops.build_next_images(g, nxt(direct), xtype)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    for i in range(3):
+        assert torch.equal(chained[i], direct[i]), i
+    # the split-SwiGLU GEMM on the chained image and on its own
+    M = 2304
+    x = _torch_x(synth.normal(71, 50, M * K1).reshape(M, K1), xtype, dev)
+    odt = torch.float16 if xtype == 1 else torch.bfloat16
+    ys = [torch.full((M, split), 7.0, device=dev) for _ in range(2)]
+    y2s = [torch.zeros((M, f), dtype=odt, device=dev) for _ in range(2)]
+    for y, y2, im in ((ys[0], y2s[0], [chained[0]]), (ys[1], y2s[1], None)):
+        ops.dispatch_batch_matmul_multi(g, [ops.MatmulJob(w1, ops.Tensor.from_torch(x), y, M, 0, None, y2)],
+                                        split + 2 * f, K1, capi.EPI_SPLIT_SWIGLU, split, images=im)
+    torch.cuda.synchronize()
+    assert torch.equal(ys[0], ys[1]) and torch.equal(y2s[0], y2s[1])
+    assert torch.isfinite(y2s[0].float()).all() and y2s[0].float().abs().max() > 0
