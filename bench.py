@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
                     [--components a,b,...] [--no-cpu-baseline]
+    python bench.py --library-baselines [--steps K] [--warmup W]
 
 A step is one pass of the hot path over one batch of synthetic input already
 resident in HBM: for the default workload `flux_attention` one non-causal
@@ -443,6 +444,51 @@ def measure(dev, name, steps, warmup, cold: bool = False):
             "bytes": nbytes, "cfg": cfg, "dtype": dtype, "cold_ms": cold_ms}
 
 
+def library_baselines(steps: int, warmup: int) -> int:
+    """The vendor libraries on the same shapes, timed as the workloads are
+    (device warm-up, W warmup and K timed steps between two HIP events),
+    each beside this library's own call in the same process: hipBLASLt
+    (torch.mm) on plain bf16 operands (no dequantization) with f32 and with
+    bf16 output, against the Q4_K / Q8_0 dequant-GEMM with its f32 output;
+    PyTorch's scaled_dot_product_attention (flash backend) against the flash
+    attention call. One JSON line per shape."""
+    import torch
+    import torch.nn.functional as F
+    from llmr_amd import workloads
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(42)
+    for name in ("flux_linear1", "flux_linear2", "zimage_qkv"):
+        g = workloads.GEMMS[name]
+        r = measure(dev, name, steps, warmup)
+        x = torch.randn(g.M, g.K, dtype=torch.bfloat16, device=dev, generator=gen)
+        wt = (torch.randn(g.N, g.K, dtype=torch.bfloat16, device=dev, generator=gen) * 0.02).t()
+        flops = 2.0 * g.M * g.N * g.K
+        line = {"shape": name, "M": g.M, "N": g.N, "K": g.K}
+        for key, fn in (("hipblaslt_bf16_to_f32", lambda: torch.mm(x, wt, out_dtype=torch.float32)),
+                        ("hipblaslt_bf16_to_bf16", lambda: torch.mm(x, wt))):
+            _device_warmup(fn)
+            ms = _time_steps(fn, steps, warmup)[0] / steps
+            line[key] = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+        del x, wt
+        line["llmr_" + r["dtype"]] = {"ms": round(r["ms"], 4), "tflops": round(r["tflops"], 1),
+                                      "weight": r["cfg"].get("weight"), "output": "f32"}
+        print(json.dumps(line), flush=True)
+    a = workloads.FLUX_ATTENTION
+    r = measure(dev, "flux_attention", steps, warmup)
+    q, k, v = (torch.randn(1, a.H, a.S, a.D, dtype=torch.float16, device=dev, generator=gen) for _ in range(3))
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    flops = 4.0 * a.H * a.S * a.S * a.D
+    line = {"shape": "flux_attention", "H": a.H, "S": a.S, "D": a.D}
+    with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+        fn = lambda: F.scaled_dot_product_attention(q, k, v)
+        _device_warmup(fn)
+        ms = _time_steps(fn, steps, warmup)[0] / steps
+    line["torch_sdpa_flash_f16"] = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+    line["llmr_f16"] = {"ms": round(r["ms"], 4), "tflops": round(r["tflops"], 1)}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def cpu_baseline(name: str, budget_s: float = 10.0):
     """The oracle (the C restatement, OpenMP on the host cores) on a bounded
     sample of the same workload: whole heads (attention) or token blocks
@@ -509,6 +555,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--hbm-copy-calibration", action="store_true",
                     help="time a plain 1 GiB device copy (reference for the FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--library-baselines", action="store_true",
+                    help="time hipBLASLt GEMMs and PyTorch's flash attention on the same shapes beside this library")
     args = ap.parse_args()
     if args.hbm_copy_calibration:
         return copy_calibration(args.steps, args.warmup)
@@ -524,6 +572,8 @@ def main():
     dev = torch.device("cuda:0")
     from llmr_amd import capi
     capi.lib()  # fail loudly if the HIP library is missing
+    if args.library_baselines:
+        return library_baselines(args.steps, args.warmup)
 
     main_r = measure(dev, args.workload, args.steps, args.warmup, cold=True)
     comps = {}
