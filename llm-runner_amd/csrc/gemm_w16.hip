@@ -89,8 +89,9 @@ __host__ __device__ __forceinline__ uint32_t image_items(uint32_t N, uint32_t K,
 }
 // One item of an image without LoRA by the 256 threads of a workgroup
 // (thread r: row r of the panel), through the two 32 KiB LDS blocks lb0 and
-// lb1 (one barrier per stage). Callers running several items in a row put
-// a barrier between them. Plain (SW false): rows row_offset + 256 p + r of
+// lb1 (one barrier per stage), or through one (ONE: lb0 == lb1, a second
+// barrier per stage). Callers running several items in a row put a barrier
+// between them. Plain (SW false): rows row_offset + 256 p + r of
 // W. SW: the SwiGLU arrangement of N outputs, W the gate rows and W2 the up
 // rows of output 0 (row_offset unused): panel p holds outputs 128 p .. +
 // 127, its rows gate 0-63 | up 0-63 | gate 64-127 | up 64-127 (wave q of
@@ -98,7 +99,7 @@ __host__ __device__ __forceinline__ uint32_t image_items(uint32_t N, uint32_t K,
 // arrangement of the fused SwiGLU kernel. NT: non-temporal stores (items
 // built beside a running GEMM: streamed, they evict less of its operands
 // from L2; Flux step 76.3 -> 75.8 ms).
-template <uint32_t WT, uint32_t OT, bool NT = false, bool SW = false>
+template <uint32_t WT, uint32_t OT, bool NT = false, bool SW = false, bool ONE = false>
 __device__ __forceinline__ void image_item(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2,
                                            uint8_t* __restrict__ img, uint32_t N, uint32_t K, uint32_t row_offset,
                                            uint32_t item, uint8_t* lb0, uint8_t* lb1) {
@@ -143,6 +144,8 @@ __device__ __forceinline__ void image_item(const uint8_t* __restrict__ W, const 
             else
                 dst[r + 256u * c] = ((const u32x4*)lb)[r + 256u * c];
         }
+        if constexpr (ONE)
+            if (i + 1u < kImgStages) __syncthreads();  // the block is read out before the next stage's stores
     }
 }
 
@@ -150,9 +153,9 @@ template <uint32_t WT, uint32_t OT, bool SW, uint32_t RS = 0>
 __global__ void __launch_bounds__(256) w16_image_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2,
                                                          uint8_t* __restrict__ img, uint32_t N, uint32_t K,
                                                          uint32_t row_offset, const ImageLora lo, uint32_t item0) {
-    if constexpr (RS == 0) {  // no LoRA: item item0 + blockIdx.x
-        __shared__ __attribute__((aligned(16))) uint8_t blk[2u * kBlk];
-        image_item<WT, OT, false, SW>(W, W2, img, N, K, row_offset, item0 + blockIdx.x, blk, blk + kBlk);
+    if constexpr (RS == 0) {  // no LoRA: item item0 + blockIdx.x, through one 32 KiB block
+        __shared__ __attribute__((aligned(16))) uint8_t blk[kBlk];
+        image_item<WT, OT, false, SW, true>(W, W2, img, N, K, row_offset, item0 + blockIdx.x, blk, blk);
         return;
     }
     constexpr bool LORA = RS > 0;         // RS: rank steps of 16 the kernel holds (rank <= 16 RS)
