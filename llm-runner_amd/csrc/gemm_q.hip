@@ -1652,11 +1652,14 @@ size_t batch_matmul_multi_workspace_bytes(uint32_t wtype, uint32_t xtype, uint32
 }
 
 // Next-group image items one idle workgroup of a two-pass GEMM takes on:
-// one per four of the GEMM's K stages (an item is 4 stages of a 256-row
-// panel, read as packed weights and written as 16-bit operands: ~6 us on a
-// CU beside the GEMM, a tile stage ~1.5 us), so the items end within the
-// idle workgroups' last-round time.
-uint32_t next_items_per_idle_wg(uint32_t K) { return max(1u, K / (uint32_t)kBK / 4u); }
+// one per four of the GEMM's K stages for Q4_K items (an item is 4 stages
+// of a 256-row panel, read as packed weights and written as 16-bit
+// operands: ~6 us on a CU beside the GEMM, a tile stage ~1.5 us), one per
+// eight for Q8_0 items (68 bytes a row and stage against 36), so the items
+// end within the idle workgroups' last-round time.
+uint32_t next_items_per_idle_wg(uint32_t K, uint32_t wtype) {
+    return max(1u, K / (uint32_t)kBK / (wtype == kGgmlQ8_0 ? 8u : 4u));
+}
 
 uint32_t next_image_items(const NextImageSet& nx) {
     uint32_t all = 0;
@@ -1730,7 +1733,7 @@ hipError_t launch_batch_matmul_multi(uint32_t wtype, uint32_t xtype, uint32_t N,
                 const uint64_t tiles = (uint64_t)a.tiles_m * a.tiles_n;
                 if (next && i + n == n_jobs && tiles % (uint64_t)num_cus != 0) {
                     const uint32_t idle = num_cus - (uint32_t)(tiles % (uint64_t)num_cus);
-                    fused = min(next_image_items(*next), idle * next_items_per_idle_wg(K));
+                    fused = min(next_image_items(*next), idle * next_items_per_idle_wg(K, next->wtype));
                     NextImages& ni = a.next;
                     uint32_t first = 0;
                     for (uint32_t q = 0; q < next->count; q++) {

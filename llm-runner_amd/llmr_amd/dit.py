@@ -84,13 +84,23 @@ class ZImageBlock:
     EPS = 1e-5  # batch_rmsnorm and batch_head_norm eps (dit.c3:1423, 1447)
 
     def __init__(self, dim: int, n_heads: int, ffn_dim: int, seq_len: int, act_dtype=torch.bfloat16,
-                 device="cuda", g: RenderGraph | None = None):
+                 device="cuda", g: RenderGraph | None = None, images_ahead: bool = True):
         if dim != n_heads * HEAD_DIM:
             raise ValueError("dim must be n_heads * 128")
         self.dim, self.n_heads, self.ffn, self.S = dim, n_heads, ffn_dim, seq_len
         self.g = g or default_graph()
         S = seq_len
         e = dict(device=device)
+        # the block's four GEMMs (QKV, O-proj, gate | up SwiGLU, down) as an
+        # image chain when they run two-pass: each call builds the next one's
+        # weight images (the SwiGLU's idle workgroups the down projection's)
+        self.ahead = None
+        if images_ahead and S >= TWO_PASS_MIN_TOKENS and dim % 64 == 0 and ffn_dim % 64 == 0 and \
+                act_dtype in (torch.float16, torch.bfloat16):
+            cus = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
+            self.ahead = _ImageChain([([None], 3 * dim, dim, (S,)), ([None], dim, dim, (S,)),
+                                      ([None], 2 * ffn_dim, dim, (S,), 0), ([None], dim, ffn_dim, (S,))],
+                                     _TORCH_GGML[act_dtype], device, cus, GGML_Q8_0)
         self.xa = torch.empty(S, dim, dtype=act_dtype, **e)          # GEMM inputs of width dim
         self.q = torch.empty(n_heads, S, HEAD_DIM, dtype=torch.float16, **e)
         self.k = torch.empty_like(self.q)
@@ -105,20 +115,46 @@ class ZImageBlock:
         g, S, dim, H, ffn, eps = self.g, self.S, self.dim, self.n_heads, self.ffn, self.EPS
         if hidden.shape != (S, dim) or hidden.dtype != torch.float32:
             raise ValueError("hidden must be f32 [seq_len, dim]")
+        ch = self.ahead if w.w_gate_up is not None else None
+        wqkv, wo = _qt(w.wqkv, GGML_Q8_0, 3 * dim, dim), _qt(w.wo, GGML_Q8_0, dim, dim)
+        wdown = _qt(w.w_down, GGML_Q8_0, dim, ffn)
+        if ch is not None:
+            wgu = _qt(w.w_gate_up, GGML_Q8_0, 2 * ffn, dim)
+            ch.bind([[wqkv], [wo], [wgu], [wdown]])
+            ch.start(g)
+
+        def mm(jobs, N, K, epilogue=capi.EPI_STORE, split=0, heads=None):
+            if ch is None:
+                if epilogue == capi.EPI_STORE and heads is None:  # the plain projections
+                    j = jobs[0]
+                    dispatch_batch_matmul(g, j.weight, j.input, _t(j.output), N, K, j.seq_len, 0)
+                else:
+                    dispatch_batch_matmul_multi(g, jobs, N, K, epilogue, split, heads=heads)
+                return
+            images, nxt = ch.take(jobs, N, K)
+            dispatch_batch_matmul_multi(g, jobs, N, K, epilogue, split, images=images, next_images=nxt,
+                                        heads=heads)
+        try:
+            return self._forward(w, hidden, rope_cos, rope_sin, wqkv, wo, wdown, mm)
+        finally:
+            if ch is not None:  # a failed forward leaves no chain half-taken
+                ch.active = False
+
+    def _forward(self, w, hidden, rope_cos, rope_sin, wqkv, wo, wdown, mm):
+        g, S, dim, H, ffn, eps = self.g, self.S, self.dim, self.n_heads, self.ffn, self.EPS
         # A: pre-attention RMSNorm, * (1 + scale_msa)                 (dit.c3:1421-1432)
         glue.batch_rmsnorm(hidden, w.attn_norm1, self.xa, eps, mod_scale=w.adaln[0], g=g)
         # B, C: Q | K | V in one call over the fused weight, with the head
         # norm, RoPE and head-major fp16 Q/K/V done on its result
         # (dit.c3:1435-1473); attention                               (dit.c3:1476-1483)
-        dispatch_batch_matmul_multi(g, [MatmulJob(_qt(w.wqkv, GGML_Q8_0, 3 * dim, dim), _t(self.xa), None, S)],
-                                    3 * dim, dim, heads=QkvHeads(self.q, self.k, self.v, H, [(w.q_norm, w.k_norm, 0)],
-                                                                 eps, (rope_cos, rope_sin)))
+        mm([MatmulJob(wqkv, _t(self.xa), None, S)], 3 * dim, dim,
+           heads=QkvHeads(self.q, self.k, self.v, H, [(w.q_norm, w.k_norm, 0)], eps, (rope_cos, rope_sin)))
         # (the attention rows go straight into the O-proj input, rounded to the
         # activation type: the reference's attention output plus its copy)
         dispatch_flash_attention_rows(g, _t(self.q), _t(self.k), _t(self.v), self.xa,
                                       FlashAttentionPC(HEAD_DIM, H, S, 1.0 / math.sqrt(HEAD_DIM)))
         # D: O-proj; hidden += tanh(gate_msa) * rmsnorm(o-proj)        (dit.c3:1488-1503)
-        dispatch_batch_matmul(g, _qt(w.wo, GGML_Q8_0, dim, dim), _t(self.xa), _t(self.t), dim, dim, S, 0)
+        mm([MatmulJob(wo, _t(self.xa), self.t, S)], dim, dim)
         glue.gated_residual(hidden, self.t, w.adaln[1], capi.GATE_TANH, w.attn_norm2, eps, g=g)
         # E: FFN pre-norm, * (1 + scale_mlp)                           (dit.c3:1545-1554)
         glue.batch_rmsnorm(hidden, w.ffn_norm1, self.xa, eps, mod_scale=w.adaln[2], g=g)
@@ -128,13 +164,13 @@ class ZImageBlock:
             # down-projection input in the activation type (the split-SwiGLU
             # epilogue with no plain columns); on the two-pass kernel bit for
             # bit the SwiGLU's f32 output and its copy below
-            dispatch_batch_matmul_multi(g, [MatmulJob(_qt(w.w_gate_up, GGML_Q8_0, 2 * ffn, dim), _t(self.xa), None,
-                                                      S, 0, None, self.fa)], 2 * ffn, dim, capi.EPI_SPLIT_SWIGLU, 0)
+            mm([MatmulJob(_qt(w.w_gate_up, GGML_Q8_0, 2 * ffn, dim), _t(self.xa), None, S, 0, None, self.fa)],
+               2 * ffn, dim, capi.EPI_SPLIT_SWIGLU, 0)
         else:
             dispatch_batch_matmul_swiglu(g, _qt(w.w_gate, GGML_Q8_0, ffn, dim), _qt(w.w_up, GGML_Q8_0, ffn, dim),
                                          _t(self.xa), _t(self.f), ffn, dim, S)
             glue.activation(self.f, self.fa, capi.ACT_COPY, g=g)
-        dispatch_batch_matmul(g, _qt(w.w_down, GGML_Q8_0, dim, ffn), _t(self.fa), _t(self.t), dim, ffn, S, 0)
+        mm([MatmulJob(wdown, _t(self.fa), self.t, S)], dim, ffn)
         # G: hidden += tanh(gate_mlp) * rmsnorm(down)                  (dit.c3:1600-1610)
         glue.gated_residual(hidden, self.t, w.adaln[3], capi.GATE_TANH, w.ffn_norm2, eps, g=g)
         return hidden
@@ -419,21 +455,31 @@ class _ImageChain:
     reads). The room is estimated here from the launch's tile count; a wrong
     estimate only moves items into the image launch after the GEMM. The
     results are those of dispatch_batch_matmul_multi without images, bit
-    for bit."""
+    for bit. A group's weights may be None at construction (the shapes
+    alone plan the chain); bind() then sets them before start()."""
 
-    def __init__(self, groups, input_dtype: int, device, cus: int):
+    def __init__(self, groups, input_dtype: int, device, cus: int, wtype: int = GGML_Q4_K):
         if any(self._entries(gr) > 4 for gr in groups):
             raise ValueError("a group's images must fit one call's four next images")
-        self.groups, self.xtype = groups, input_dtype
+        self.groups, self.xtype = list(groups), input_dtype
         per = max(len(gr[0]) * self._image_bytes(gr) for gr in groups)
         self.bufs = [torch.empty(per, dtype=torch.uint8, device=device) for _ in range(3)]
-        self.builds = self.plan(groups, cus)  # call k -> the (group, image) pairs it builds
-        self.images = [self._next(k).entries for k in range(len(groups))]  # group k's NextImage entries
+        self.builds = self.plan(groups, cus, wtype)  # call k -> the (group, image) pairs it builds
+        self.images = None
+        if all(w is not None for gr in groups for w in gr[0]):
+            self.bind([gr[0] for gr in groups])
         self.k = 0
         self.active = False  # between start() and the last group's take()
 
+    def bind(self, weights) -> None:
+        """The weights of each group (a list per group, as many as planned)."""
+        if len(weights) != len(self.groups) or any(len(w) != len(gr[0]) for w, gr in zip(weights, self.groups)):
+            raise ValueError("one weight list per group, as many weights as planned")
+        self.groups = [(list(w),) + tuple(gr[1:]) for w, gr in zip(weights, self.groups)]
+        self.images = [self._next(k).entries for k in range(len(self.groups))]  # group k's NextImage entries
+
     @classmethod
-    def plan(cls, groups, cus: int):
+    def plan(cls, groups, cus: int, wtype: int = GGML_Q4_K):
         """For each call k, the images (group j, image e) it builds, in order:
         those of group k + 1 that call k - 1 did not build, then group k + 2's
         in order while all items of the next one fit in what is left of the
@@ -442,7 +488,7 @@ class _ImageChain:
         builds = [[] for _ in range(n)]
         done = [0] * n  # images of each group assigned so far (in order)
         for c in range(n - 1):
-            room, slots = cls._room(groups[c], cus), 4
+            room, slots = cls._room(groups[c], cus, wtype), 4
             for j in (c + 1, c + 2):
                 if j >= n:
                     break
@@ -499,13 +545,14 @@ class _ImageChain:
         return sum(cls._entry_items(group))
 
     @classmethod
-    def _room(cls, group, cus: int) -> int:
-        """Items the group's GEMM can build on its workgroups without a tile
-        in the last round: one per four of its K stages each."""
+    def _room(cls, group, cus: int, wtype: int = GGML_Q4_K) -> int:
+        """Items of weight type wtype the group's GEMM can build on its
+        workgroups without a tile in the last round: one per four of its K
+        stages each (Q8_0: per eight)."""
         K, Ms = group[2], group[3]
         tiles = sum(-(-M // 256) for M in Ms) * cls._panels(group)
         rem = tiles % cus
-        return 0 if rem == 0 else (cus - rem) * max(1, K // 256)
+        return 0 if rem == 0 else (cus - rem) * max(1, K // (512 if wtype == GGML_Q8_0 else 256))
 
     def _views(self, k: int):
         n = self._image_bytes(self.groups[k])
@@ -520,6 +567,8 @@ class _ImageChain:
 
     def start(self, g: RenderGraph) -> None:
         """Before the first group: its images."""
+        if self.images is None:
+            raise RuntimeError("weight-image chain started before its weights were bound")
         self.k = 0
         self.active = True
         build_next_images(g, NextImages(self.images[0]), self.xtype)

@@ -66,6 +66,35 @@ def test_zimage_block_fused_swiglu_bit_identical(dev):
     assert torch.equal(out[0], out[1])
 
 
+def test_zimage_block_images_ahead_bit_identical(dev):
+    """The block's four GEMMs as an image chain (ZImageBlock's default from
+    2048 tokens: the QKV's images built first, each GEMM building the next
+    one's, the SwiGLU's idle workgroups the down projection's) give the
+    hidden state of the same block without it, bit for bit, over two layers
+    of different weights run through one block object (the chain rebinds its
+    weights and reuses its buffers) and twice in a row. dim 2048 / FFN 4096
+    over 4352 tokens: all four GEMMs run two-pass on the chain's images."""
+    from llmr_amd import dit, synth, workloads
+    dim, H, ffn, S = 2048, 16, 4096, 4352
+    layers = [dit.zimage_layer_weights(dim, H, ffn, device=dev, base_stream=b) for b in (700, 800)]
+    att = workloads.Attention("z", H, S, 128, 256, 64, 64, (32, 48, 48), 256.0)
+    rope = tuple(torch.from_numpy(t).to(dev)
+                 for t in workloads.rope_tables(workloads.attention_positions(att), att.axes, att.theta))
+    h0 = torch.from_numpy(synth.normal(42, 702, S * dim).reshape(S, dim)).to(dev)
+    ahead = dit.ZImageBlock(dim, H, ffn, S, act_dtype=torch.bfloat16, device=dev)
+    plain = dit.ZImageBlock(dim, H, ffn, S, act_dtype=torch.bfloat16, device=dev, images_ahead=False)
+    assert ahead.ahead is not None and plain.ahead is None
+    ha, hb = h0.clone(), h0.clone()
+    for rep in range(2):
+        for i, w in enumerate(layers):
+            ahead.forward(w, ha, *rope)
+            plain.forward(w, hb, *rope)
+            torch.cuda.synchronize()
+            assert torch.isfinite(ha).all()
+            assert torch.equal(ha, hb), (rep, i)
+    assert not torch.equal(ha, h0)
+
+
 def _small_flux(mlp_act="gelu"):
     from llmr_amd import dit
     return dit.FluxConfig(dim=256, n_heads=2, mlp=512, n_double=2, n_single=2, text_dim=256, n_txt=40,
