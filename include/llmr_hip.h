@@ -579,6 +579,19 @@ LLMR_API int llmr_batch_layernorm(llmr_context* ctx, const float* x, uint32_t x_
                                   const float* mod_shift, void* out, uint32_t out_type, uint32_t out_stride,
                                   uint32_t dim, uint32_t n_rows, float eps);
 
+/* llmr_batch_layernorm over rows that belong to two streams with their own
+ * modulation: rows [0, split_row) take mod_scale / mod_shift, rows
+ * [split_row, n_rows) mod_scale2 / mod_shift2 (each pair may hold nulls);
+ * split_row % 4 == 0. One launch for the Flux double block's text and image
+ * streams, which the reference normalizes by two batch_layernorm +
+ * adaln_modulate dispatches each (dependencies/flux.c3l/flux_dit.c3:761-779,
+ * 903-909, 939-945); the rows equal those two calls' bit for bit. */
+LLMR_API int llmr_batch_layernorm_split(llmr_context* ctx, const float* x, uint32_t x_stride,
+                                        const float* mod_scale, const float* mod_shift, uint32_t split_row,
+                                        const float* mod_scale2, const float* mod_shift2, void* out,
+                                        uint32_t out_type, uint32_t out_stride, uint32_t dim, uint32_t n_rows,
+                                        float eps);
+
 /* Per-head RMSNorm + rotary embedding + head-major transpose of a QKV GEMM
  * output. qkv f32 [n_rows, qkv_stride] holds Q | K | V, each n_heads*128
  * wide, starting at column 0. For row r (sequence position t = row0 + r),

@@ -780,7 +780,8 @@ int launched(hipError_t e, const char* op) {
 
 int row_norm_common(llmr_context* ctx, bool ln, const float* x, uint32_t x_stride, const float* weight,
                     const float* mod_scale, const float* mod_shift, void* out, uint32_t out_type,
-                    uint32_t out_stride, uint32_t dim, uint32_t n_rows, float eps) {
+                    uint32_t out_stride, uint32_t dim, uint32_t n_rows, float eps, uint32_t split = ~0u,
+                    const float* mod_scale2 = nullptr, const float* mod_shift2 = nullptr) {
     if (int r = check_ctx(ctx)) return r;
     if (!is_act_type(out_type)) return fail(LLMR_ERR_UNSUPPORTED, "output type %u not supported", out_type);
     if (int r = check_dim(dim)) return r;
@@ -792,7 +793,10 @@ int row_norm_common(llmr_context* ctx, bool ln, const float* x, uint32_t x_strid
     if (ln && weight) return fail(LLMR_ERR_INVALID_ARG, "batch_layernorm has no affine weight (pass null)");
     if (int r = check_vec(mod_scale, "mod_scale", false)) return r;
     if (int r = check_vec(mod_shift, "mod_shift", false)) return r;
-    llmr::RowNormArgs a{x, weight, mod_scale, mod_shift, out, x_stride, out_stride, n_rows, dim, eps};
+    if (int r = check_vec(mod_scale2, "mod_scale2", false)) return r;
+    if (int r = check_vec(mod_shift2, "mod_shift2", false)) return r;
+    llmr::RowNormArgs a{x, weight, mod_scale, mod_shift, out, x_stride, out_stride, n_rows, dim, eps,
+                        mod_scale2, mod_shift2, split};
     return launched(llmr::launch_row_norm(a, ln, out_type, ctx->cur), ln ? "batch_layernorm" : "batch_rmsnorm");
 }
 
@@ -812,6 +816,17 @@ int llmr_batch_layernorm(llmr_context* ctx, const float* x, uint32_t x_stride, c
                          uint32_t n_rows, float eps) {
     return row_norm_common(ctx, true, x, x_stride, nullptr, mod_scale, mod_shift, out, out_type, out_stride, dim,
                            n_rows, eps);
+}
+
+int llmr_batch_layernorm_split(llmr_context* ctx, const float* x, uint32_t x_stride, const float* mod_scale,
+                               const float* mod_shift, uint32_t split_row, const float* mod_scale2,
+                               const float* mod_shift2, void* out, uint32_t out_type, uint32_t out_stride,
+                               uint32_t dim, uint32_t n_rows, float eps) {
+    if (split_row % 4 || split_row > n_rows)
+        return fail(LLMR_ERR_INVALID_ARG, "split_row must be a multiple of 4 and <= n_rows (got %u of %u)", split_row,
+                    n_rows);
+    return row_norm_common(ctx, true, x, x_stride, nullptr, mod_scale, mod_shift, out, out_type, out_stride, dim,
+                           n_rows, eps, split_row, mod_scale2, mod_shift2);
 }
 
 int llmr_qkv_heads(llmr_context* ctx, const float* qkv, uint32_t qkv_stride, uint32_t n_rows, uint32_t n_heads,

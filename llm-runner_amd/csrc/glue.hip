@@ -84,6 +84,10 @@ __global__ void __launch_bounds__(256) row_norm_kernel(RowNormArgs a) {
     __shared__ f32x4 mod_lds[2][NV * 64];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
+    // the workgroup's four rows lie on one side of the split (a multiple of 4)
+    const bool second = blockIdx.x * 4u >= a.split;
+    const float* const scale = second ? a.scale2 : a.scale;
+    const float* const shift = second ? a.shift2 : a.shift;
     const bool live = row < a.rows;
     const float* xr = a.x + (size_t)(live ? row : 0u) * a.x_stride;
     f32x4 v[NV];
@@ -93,12 +97,12 @@ __global__ void __launch_bounds__(256) row_norm_kernel(RowNormArgs a) {
         const uint32_t c = 4u * lane + 256u * i;
         v[i] = live && c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    if (a.scale || a.shift) {  // uniform over the workgroup
+    if (scale || shift) {  // uniform over the workgroup
 #pragma unroll
         for (int j = 0; j < NV / 4; ++j) {
             const uint32_t k = threadIdx.x + 256u * j, c = 4u * k;
-            mod_lds[0][k] = a.scale && c < a.dim ? ld4(a.scale + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            mod_lds[1][k] = a.shift && c < a.dim ? ld4(a.shift + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            mod_lds[0][k] = scale && c < a.dim ? ld4(scale + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            mod_lds[1][k] = shift && c < a.dim ? ld4(shift + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         __syncthreads();
     }
@@ -134,8 +138,8 @@ __global__ void __launch_bounds__(256) row_norm_kernel(RowNormArgs a) {
         f32x4 y;
         if constexpr (LN) y = (v[i] - mean) * r;
         else y = (v[i] * r) * ld4(a.w + c);
-        if (a.scale) y = y * (1.0f + mod_lds[0][lane + 64u * i]);
-        if (a.shift) y = y + mod_lds[1][lane + 64u * i];
+        if (scale) y = y * (1.0f + mod_lds[0][lane + 64u * i]);
+        if (shift) y = y + mod_lds[1][lane + 64u * i];
         store4<OT>(orow, c, y);
     }
 }

@@ -201,6 +201,10 @@ struct RowNormArgs {
     void* out;            // [rows, out_stride] of the output type
     uint32_t x_stride, out_stride, rows, dim;
     float eps;
+    // rows from `split` on (a multiple of 4) take scale2 / shift2 instead
+    const float* scale2 = nullptr;
+    const float* shift2 = nullptr;
+    uint32_t split = ~0u;
 };
 constexpr uint32_t kRowNormMaxDim = 8192;
 

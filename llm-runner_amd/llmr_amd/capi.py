@@ -144,6 +144,8 @@ _SIGS = {
                                           ctypes.c_float]),
     "llmr_batch_layernorm": (ctypes.c_int, [_vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                             ctypes.c_float]),
+    "llmr_batch_layernorm_split": (ctypes.c_int, [_vp, _vp, _u32, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32,
+                                                  _u32, _u32, ctypes.c_float]),
     "llmr_qkv_heads": (ctypes.c_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, ctypes.c_float, _vp, _vp,
                                       _vp, _vp, _vp, _u32, _u32, _u32]),
     "llmr_gated_residual": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32,
@@ -319,6 +321,11 @@ class Context:
     def batch_layernorm(self, x, x_stride, scale, shift, out, otype, out_stride, dim, rows, eps):
         check(lib().llmr_batch_layernorm(self._h, x, x_stride, scale, shift, out, otype, out_stride, dim,
                                          rows, float(eps)))
+
+    def batch_layernorm_split(self, x, x_stride, scale, shift, split_row, scale2, shift2, out, otype, out_stride,
+                              dim, rows, eps):
+        check(lib().llmr_batch_layernorm_split(self._h, x, x_stride, scale, shift, split_row, scale2, shift2, out,
+                                               otype, out_stride, dim, rows, float(eps)))
 
     def qkv_heads(self, qkv, qkv_stride, rows, n_heads, q_norm, k_norm, eps, cos_t, sin_t, q, k, v, otype,
                   seq_len, row0):

@@ -722,6 +722,18 @@ class FluxDiT:
         dispatch_batch_matmul_multi(self.g, jobs, N, K, epilogue, split, images=images, next_images=nxt,
                                     heads=heads)
 
+    def _layernorm2(self, scale_t, shift_t, scale_i, shift_i) -> None:
+        """LayerNorm + modulation of the joint hidden rows into xa: the text
+        rows with the text stream's vectors, the image rows with the image
+        stream's, in one launch (two where n_txt % 4 != 0)."""
+        nt, g = self.cfg.n_txt, self.g
+        if nt % 4 == 0:
+            glue.batch_layernorm_split(self.hidden, self.xa, self.LN_EPS, nt, (scale_t, shift_t), (scale_i, shift_i),
+                                       g=g)
+            return
+        for sl, sc, sh in ((slice(0, nt), scale_t, shift_t), (slice(nt, None), scale_i, shift_i)):
+            glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=sc, mod_shift=sh, g=g)
+
     def _heads(self, norms) -> QkvHeads:
         """The joint Q/K/V as the QKV projections' head routing; norms: per job
         (q_norm, k_norm, first sequence row)."""
@@ -752,9 +764,7 @@ class FluxDiT:
                               gates[1], None if out2 is None else out2[im])]
 
         # LayerNorm + modulation of each stream                      (flux_dit.c3:761-779)
-        for sl, mod in ((ts, mt), (im, mi)):
-            glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[1], mod_shift=mod[0],
-                                 g=g)
+        self._layernorm2(mt[1], mt[0], mi[1], mi[0])
         # Q | K | V of both streams, head norm + RoPE into the joint Q/K/V (text
         # rows first) on the projections' result                 (flux_dit.c3:786-863)
         self._multi(jobs(w.txt_qkv, w.img_qkv, d, self.xa, None), 3 * d, d,
@@ -766,9 +776,7 @@ class FluxDiT:
                     capi.EPI_GATED_RESIDUAL)
         # MLP: LayerNorm + modulation, up + gelu (swiglu: gate and up, silu(gate) * up), down,
         # hidden += gate2 * down (flux_dit.c3:902-967)
-        for sl, mod in ((ts, mt), (im, mi)):
-            glue.batch_layernorm(self.hidden[sl], self.xa[sl], self.LN_EPS, mod_scale=mod[4], mod_shift=mod[3],
-                                 g=g)
+        self._layernorm2(mt[4], mt[3], mi[4], mi[3])
         if c.mlp_act == "swiglu":
             self._multi(jobs(w.txt_mlp0, w.img_mlp0, d, self.xa, self.o, out2=self.fa), 2 * m, d,
                         capi.EPI_SPLIT_SWIGLU, split=0)

@@ -77,6 +77,26 @@ def batch_layernorm(x: torch.Tensor, out: torch.Tensor, eps: float, mod_scale: t
     return out
 
 
+def batch_layernorm_split(x: torch.Tensor, out: torch.Tensor, eps: float, split_row: int, mods, mods2,
+                          g: RenderGraph | None = None) -> torch.Tensor:
+    """batch_layernorm of rows from two streams in one launch: rows
+    [0, split_row) modulated by mods = (mod_scale, mod_shift), the rest by
+    mods2 (either vector may be None; split_row % 4 == 0); the rows equal
+    two batch_layernorm calls' (the Flux double block's text and image
+    LayerNorms, dependencies/flux.c3l/flux_dit.c3:761-779)."""
+    g = g or default_graph()
+    rows, dim = x.shape
+    if out.shape != x.shape:
+        raise ValueError("out must have x's shape")
+    xp, xs = _rows(x, "x", torch.float32)
+    op, os_ = _rows(out, "out")
+    g.bind_stream()
+    g.ctx.batch_layernorm_split(xp, xs, _vec(mods[0], "mod_scale", dim), _vec(mods[1], "mod_shift", dim), split_row,
+                                _vec(mods2[0], "mod_scale2", dim), _vec(mods2[1], "mod_shift2", dim), op, _otype(out),
+                                os_, dim, rows, eps)
+    return out
+
+
 def qkv_heads(qkv: torch.Tensor, n_heads: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
               row0: int = 0, q_norm: torch.Tensor | None = None, k_norm: torch.Tensor | None = None,
               eps: float = 1e-6, rope: tuple | None = None, g: RenderGraph | None = None) -> None:

@@ -62,6 +62,34 @@ def test_layernorm_adaln_on_row_range(orc, dev, dtype):
     assert (out[:nt].float() == 7.0).all()  # rows outside the range untouched
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_layernorm_split_equals_two_calls(orc, dev, dtype):
+    """llmr_batch_layernorm_split (the Flux double block's text and image
+    LayerNorms in one launch): rows below split_row with the first
+    modulation pair, the rest with the second (here scale only, no shift),
+    bit for bit the two batch_layernorm calls, and the oracle's LayerNorm +
+    modulation; a split_row that is not a multiple of 4, or past n_rows, is
+    refused."""
+    from llmr_amd import capi, glue
+    r = _rng(13)
+    S, nt, dim = 303, 44, 3072  # 259 image rows: the last workgroup of four rows is part-filled
+    h = (r.standard_normal((S, dim)) * 3 + 1.5).astype(np.float32)
+    sc, sh, sc2 = ((0.3 * r.standard_normal(dim)).astype(np.float32) for _ in range(3))
+    h_t = _dev(h, dev)
+    one = torch.full((S, dim), 7.0, dtype=dtype, device=dev)
+    two = torch.full((S, dim), 7.0, dtype=dtype, device=dev)
+    glue.batch_layernorm_split(h_t, one, 1e-6, nt, (_dev(sc, dev), _dev(sh, dev)), (_dev(sc2, dev), None))
+    glue.batch_layernorm(h_t[:nt], two[:nt], 1e-6, mod_scale=_dev(sc, dev), mod_shift=_dev(sh, dev))
+    glue.batch_layernorm(h_t[nt:], two[nt:], 1e-6, mod_scale=_dev(sc2, dev))
+    torch.cuda.synchronize()
+    assert torch.equal(one, two)
+    _close(one[:nt], orc.modulate(orc.batch_layernorm(h[:nt], 1e-6), sc, sh), dtype, atol=1e-5)
+    _close(one[nt:], orc.modulate(orc.batch_layernorm(h[nt:], 1e-6), sc2), dtype, atol=1e-5)
+    for bad in (nt + 2, S + 4):
+        with pytest.raises(capi.LlmrError, match="split_row"):
+            glue.batch_layernorm_split(h_t, one, 1e-6, bad, (None, None), (None, None))
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_qkv_heads_joint_rows(orc, dev, dtype):
     """Image rows of a linear1-shaped buffer (stride > 3*H*128) into rows
