@@ -626,6 +626,20 @@ LLMR_API int llmr_gated_residual(llmr_context* ctx, float* residual, uint32_t re
                                  uint32_t input_stride, const float* norm_weight, const float* gate,
                                  uint32_t gate_mode, uint32_t dim, uint32_t n_rows, float eps);
 
+/* llmr_gated_residual, then in the same pass over the rows
+ * llmr_batch_rmsnorm of the updated residual with next_weight (non-null),
+ * next_scale and next_shift (each may be null) and next_eps into out (of
+ * out_type): the Z-Image block's attention post-norm + gated residual and
+ * its FFN pre-norm (dependencies/zimage.c3l/dit.c3:1495-1503 then
+ * 1545-1554), bit for bit those two calls, reading and writing the residual
+ * rows once. dim <= 4096. No reference counterpart as a single dispatch. */
+LLMR_API int llmr_gated_residual_rmsnorm(llmr_context* ctx, float* residual, uint32_t residual_stride,
+                                         const float* input, uint32_t input_stride, const float* norm_weight,
+                                         const float* gate, uint32_t gate_mode, const float* next_weight,
+                                         const float* next_scale, const float* next_shift, void* out,
+                                         uint32_t out_type, uint32_t out_stride, uint32_t dim, uint32_t n_rows,
+                                         float eps, float next_eps);
+
 /* dst[r, dst_col + c] = f(src[r, src_col + c]) for c < n_cols with
  *   LLMR_ACT_COPY      x                         (a cast / column copy)
  *   LLMR_ACT_SILU      x / (1 + exp(-x))

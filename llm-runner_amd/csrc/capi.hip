@@ -872,6 +872,34 @@ int llmr_gated_residual(llmr_context* ctx, float* residual, uint32_t residual_st
     return launched(llmr::launch_residual(a, gate_mode == LLMR_GATE_TANH, ctx->cur), "gated_residual");
 }
 
+int llmr_gated_residual_rmsnorm(llmr_context* ctx, float* residual, uint32_t residual_stride, const float* input,
+                                uint32_t input_stride, const float* norm_weight, const float* gate, uint32_t gate_mode,
+                                const float* next_weight, const float* next_scale, const float* next_shift, void* out,
+                                uint32_t out_type, uint32_t out_stride, uint32_t dim, uint32_t n_rows, float eps,
+                                float next_eps) {
+    if (int r = check_ctx(ctx)) return r;
+    if (gate_mode > LLMR_GATE_TANH) return fail(LLMR_ERR_INVALID_ARG, "unknown gate mode %u", gate_mode);
+    if (!is_act_type(out_type)) return fail(LLMR_ERR_UNSUPPORTED, "output type %u not supported", out_type);
+    if (int r = check_dim(dim)) return r;
+    if (dim > 4096) return fail(LLMR_ERR_INVALID_ARG, "gated_residual_rmsnorm needs dim <= 4096 (got %u)", dim);
+    if (!(eps >= 0.0f) || !std::isfinite(eps) || !(next_eps >= 0.0f) || !std::isfinite(next_eps))
+        return fail(LLMR_ERR_INVALID_ARG, "eps and next_eps must be finite and >= 0");
+    if (n_rows == 0) return ok();
+    if (int r = check_rows(residual, "residual", residual_stride, dim)) return r;
+    if (int r = check_rows(input, "input", input_stride, dim)) return r;
+    if (int r = check_rows(out, "out", out_stride, dim)) return r;
+    if (int r = check_vec(norm_weight, "norm_weight", false)) return r;
+    if (int r = check_vec(gate, "gate", gate_mode != LLMR_GATE_NONE)) return r;
+    if (int r = check_vec(next_weight, "next_weight", true)) return r;
+    if (int r = check_vec(next_scale, "next_scale", false)) return r;
+    if (int r = check_vec(next_shift, "next_shift", false)) return r;
+    llmr::ResidualArgs a{residual, input, norm_weight, gate_mode == LLMR_GATE_NONE ? nullptr : gate,
+                         residual_stride, input_stride, n_rows, dim, eps,
+                         next_weight, next_scale, next_shift, out, out_stride, next_eps, (uint32_t)ctx->num_cus};
+    return launched(llmr::launch_residual_norm(a, gate_mode == LLMR_GATE_TANH, out_type, ctx->cur),
+                    "gated_residual_rmsnorm");
+}
+
 int llmr_activation(llmr_context* ctx, const float* src, uint32_t src_stride, uint32_t src_col, uint32_t src2_col,
                     void* dst, uint32_t dst_type, uint32_t dst_stride, uint32_t dst_col, uint32_t n_rows,
                     uint32_t n_cols, uint32_t act) {

@@ -274,6 +274,95 @@ __global__ void __launch_bounds__(256) residual_kernel(ResidualArgs a) {
     }
 }
 
+// The same update, then the updated row's RMSNorm (weight next_w) * (1 +
+// next_scale) + next_shift into out: the post-norm residual of one half of
+// a Z-Image block and the next half's pre-norm (dit.c3:1495-1503 then
+// 1545-1554) in one pass over the rows. The arithmetic is residual_kernel's,
+// then row_norm_kernel's (RMS) on the updated row in registers, in the same
+// order, so the results equal the two launches bit for bit.
+template <bool NORM, bool TANH, uint32_t OT, int NV>
+__global__ void __launch_bounds__(256) residual_norm_kernel(ResidualArgs a) {
+    // x's norm weights, the gate (tanh(gate) for TANH), next_w and
+    // 1 + next_scale, staged once per workgroup; the workgroups then take
+    // groups of four rows in turn (a persistent grid of two per CU: one
+    // workgroup of four rows each would run 4352 rows in 2.1 rounds of
+    // three, and stage the vectors 1088 times)
+    __shared__ f32x4 vec_lds[4][NV * 64];
+#pragma unroll
+    for (int j = 0; j < NV / 4; ++j) {
+        const uint32_t k = threadIdx.x + 256u * j, c = 4u * k;
+        const f32x4 z{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (NORM) vec_lds[0][k] = c < a.dim ? ld4(a.norm_w + c) : z;
+        if (a.gate) {
+            const f32x4 g = c < a.dim ? ld4(a.gate + c) : z;
+            if constexpr (TANH) vec_lds[1][k] = f32x4{tanhf(g.x), tanhf(g.y), tanhf(g.z), tanhf(g.w)};
+            else vec_lds[1][k] = g;
+        }
+        vec_lds[2][k] = c < a.dim ? ld4(a.next_w + c) : z;
+        if (a.next_scale) vec_lds[3][k] = c < a.dim ? 1.0f + ld4(a.next_scale + c) : z;
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t quads = (a.rows + 3u) / 4u;
+    for (uint32_t q = blockIdx.x; q < quads; q += gridDim.x) {
+        const uint32_t row = q * 4u + (threadIdx.x >> 6);
+        if (row >= a.rows) break;  // the last quad only: no later one for this wave
+        const float* xr = a.x + (size_t)row * a.x_stride;
+        float* hr = a.h + (size_t)row * a.h_stride;
+        f32x4 v[NV], hv[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = 4u * lane + 256u * i;
+            v[i] = c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = 4u * lane + 256u * i;
+            hv[i] = c < a.dim ? ld4(hr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        float s = 0.0f;
+        if constexpr (NORM) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i)
+                s += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+        }
+        float rms = 1.0f;
+        if constexpr (NORM) rms = 1.0f / __builtin_sqrtf(wave_sum(s) / (float)a.dim + a.eps);
+        float s2 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = 4u * lane + 256u * i;
+            if (c < a.dim) {
+                f32x4 y = v[i];
+                if constexpr (NORM) y = (y * rms) * vec_lds[0][lane + 64u * i];
+                if (a.gate) {
+                    const f32x4 g = vec_lds[1][lane + 64u * i];
+                    if constexpr (TANH) {
+                        y = (1.0f * g) * y;
+                        y = __builtin_elementwise_min(__builtin_elementwise_max(y, f32x4(-1e10f)), f32x4(1e10f));
+                    } else {
+                        y = g * y;
+                    }
+                }
+                hv[i] = hv[i] + y;
+                *(f32x4*)(hr + c) = hv[i];
+            }
+            s2 += (hv[i].x * hv[i].x + hv[i].y * hv[i].y) + (hv[i].z * hv[i].z + hv[i].w * hv[i].w);
+        }
+        const float r2 = 1.0f / __builtin_sqrtf(wave_sum(s2) / (float)a.dim + a.next_eps);
+        char* orow = (char*)a.out + (size_t)row * a.out_stride * (OT == kGgmlF32 ? 4u : 2u);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = 4u * lane + 256u * i;
+            if (c >= a.dim) continue;
+            f32x4 y = (hv[i] * r2) * vec_lds[2][lane + 64u * i];
+            if (a.next_scale) y = y * vec_lds[3][lane + 64u * i];
+            if (a.next_shift) y = y + ld4(a.next_shift + c);
+            store4<OT>(orow, c, y);
+        }
+    }
+}
+
 // --- act_cols ----------------------------------------------------------------
 // dst[r, dst_col + c] = f(src[r, src_col + c] (, src[r, src2_col + c])) for
 // c < cols, four columns per thread:
@@ -411,6 +500,33 @@ hipError_t launch_qkv_heads(const QkvHeadsArgs& a, uint32_t otype, hipStream_t s
         default: hipLaunchKernelGGL(qkv_heads_kernel<kGgmlBF16>, grid, block, 0, st, a); break;
     }
     return hipGetLastError();
+}
+
+template <bool NORM, bool TANH, uint32_t OT>
+hipError_t launch_residual_norm_t(const ResidualArgs& a, hipStream_t st) {
+    const dim3 grid(min((a.rows + 3u) / 4u, 2u * a.grid_cus)), block(256);
+    const uint32_t nv = (a.dim + 255u) / 256u;
+    if (nv <= 4) hipLaunchKernelGGL((residual_norm_kernel<NORM, TANH, OT, 4>), grid, block, 0, st, a);
+    else if (nv <= 8) hipLaunchKernelGGL((residual_norm_kernel<NORM, TANH, OT, 8>), grid, block, 0, st, a);
+    else if (nv <= 16) hipLaunchKernelGGL((residual_norm_kernel<NORM, TANH, OT, 16>), grid, block, 0, st, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+template <uint32_t OT>
+hipError_t launch_residual_norm_o(const ResidualArgs& a, bool tanh_gate, hipStream_t st) {
+    if (a.norm_w)
+        return tanh_gate ? launch_residual_norm_t<true, true, OT>(a, st) : launch_residual_norm_t<true, false, OT>(a, st);
+    return tanh_gate ? launch_residual_norm_t<false, true, OT>(a, st) : launch_residual_norm_t<false, false, OT>(a, st);
+}
+
+hipError_t launch_residual_norm(const ResidualArgs& a, bool tanh_gate, uint32_t otype, hipStream_t st) {
+    if (a.rows == 0) return hipSuccess;
+    switch (otype) {
+        case kGgmlF32: return launch_residual_norm_o<kGgmlF32>(a, tanh_gate, st);
+        case kGgmlF16: return launch_residual_norm_o<kGgmlF16>(a, tanh_gate, st);
+        default: return launch_residual_norm_o<kGgmlBF16>(a, tanh_gate, st);
+    }
 }
 
 hipError_t launch_residual(const ResidualArgs& a, bool tanh_gate, hipStream_t st) {

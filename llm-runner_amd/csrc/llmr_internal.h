@@ -228,7 +228,20 @@ struct ResidualArgs {
     const float* gate;      // [dim] or null: plain add
     uint32_t h_stride, x_stride, rows, dim;
     float eps;
+    // launch_residual_norm: the updated rows' RMSNorm (weight next_w, eps
+    // next_eps) * (1 + next_scale) + next_shift (either may be null) into out
+    const float* next_w = nullptr;
+    const float* next_scale = nullptr;
+    const float* next_shift = nullptr;
+    void* out = nullptr;    // [rows, out_stride] of the output type
+    uint32_t out_stride = 0;
+    float next_eps = 0.0f;
+    uint32_t grid_cus = 0;  // the device's CUs (the persistent grid: two workgroups each)
 };
+// The residual update, then the updated rows' RMSNorm + modulation in the
+// same pass (a.out, a.next_w non-null): bit for bit launch_residual followed
+// by launch_row_norm (RMSNorm) of the residual.
+hipError_t launch_residual_norm(const ResidualArgs& a, bool tanh_gate, uint32_t otype, hipStream_t st);
 
 constexpr int kActCopy = 0, kActSilu = 1, kActGelu = 2, kActSiluMul = 3;
 struct ActColsArgs {

@@ -150,6 +150,8 @@ _SIGS = {
                                       _vp, _vp, _vp, _u32, _u32, _u32]),
     "llmr_gated_residual": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _u32, _u32,
                                            ctypes.c_float]),
+    "llmr_gated_residual_rmsnorm": (ctypes.c_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _vp, _vp, _vp, _vp,
+                                                   _u32, _u32, _u32, _u32, ctypes.c_float, ctypes.c_float]),
     "llmr_activation": (ctypes.c_int, [_vp, _vp, _u32, _u32, _u32, _vp, _u32, _u32, _u32, _u32, _u32, _u32]),
     "llmr_timestep_embed": (ctypes.c_int, [_vp, _vp, _u32, ctypes.c_float]),
     "llmr_patchify": (ctypes.c_int, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32]),
@@ -335,6 +337,12 @@ class Context:
     def gated_residual(self, h, h_stride, x, x_stride, norm_w, gate, mode, dim, rows, eps):
         check(lib().llmr_gated_residual(self._h, h, h_stride, x, x_stride, norm_w, gate, mode, dim, rows,
                                         float(eps)))
+
+    def gated_residual_rmsnorm(self, h, h_stride, x, x_stride, norm_w, gate, mode, next_w, next_scale, next_shift,
+                               out, otype, out_stride, dim, rows, eps, next_eps):
+        check(lib().llmr_gated_residual_rmsnorm(self._h, h, h_stride, x, x_stride, norm_w, gate, mode, next_w,
+                                                next_scale, next_shift, out, otype, out_stride, dim, rows,
+                                                float(eps), float(next_eps)))
 
     def activation(self, src, src_stride, src_col, src2_col, dst, dtype, dst_stride, dst_col, rows, cols, act):
         check(lib().llmr_activation(self._h, src, src_stride, src_col, src2_col, dst, dtype, dst_stride,

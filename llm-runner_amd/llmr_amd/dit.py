@@ -155,9 +155,13 @@ class ZImageBlock:
                                       FlashAttentionPC(HEAD_DIM, H, S, 1.0 / math.sqrt(HEAD_DIM)))
         # D: O-proj; hidden += tanh(gate_msa) * rmsnorm(o-proj)        (dit.c3:1488-1503)
         mm([MatmulJob(wo, _t(self.xa), self.t, S)], dim, dim)
-        glue.gated_residual(hidden, self.t, w.adaln[1], capi.GATE_TANH, w.attn_norm2, eps, g=g)
-        # E: FFN pre-norm, * (1 + scale_mlp)                           (dit.c3:1545-1554)
-        glue.batch_rmsnorm(hidden, w.ffn_norm1, self.xa, eps, mod_scale=w.adaln[2], g=g)
+        # E: FFN pre-norm, * (1 + scale_mlp), in the same pass         (dit.c3:1545-1554)
+        if dim <= 4096:
+            glue.gated_residual_rmsnorm(hidden, self.t, w.adaln[1], capi.GATE_TANH, w.attn_norm2, eps, w.ffn_norm1,
+                                        self.xa, eps, mod_scale=w.adaln[2], g=g)
+        else:
+            glue.gated_residual(hidden, self.t, w.adaln[1], capi.GATE_TANH, w.attn_norm2, eps, g=g)
+            glue.batch_rmsnorm(hidden, w.ffn_norm1, self.xa, eps, mod_scale=w.adaln[2], g=g)
         # F: SwiGLU in-projection, down-projection                     (dit.c3:1562-1596)
         if w.w_gate_up is not None:
             # gate | up in one weight: silu(gate) * up straight into the

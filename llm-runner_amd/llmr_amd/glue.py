@@ -139,6 +139,29 @@ def gated_residual(residual: torch.Tensor, inp: torch.Tensor, gate: torch.Tensor
     return residual
 
 
+def gated_residual_rmsnorm(residual: torch.Tensor, inp: torch.Tensor, gate: torch.Tensor | None, mode: int,
+                           norm_weight: torch.Tensor | None, eps: float, next_weight: torch.Tensor,
+                           out: torch.Tensor, next_eps: float, mod_scale: torch.Tensor | None = None,
+                           mod_shift: torch.Tensor | None = None, g: RenderGraph | None = None) -> torch.Tensor:
+    """gated_residual, then batch_rmsnorm of the updated residual (next_weight,
+    mod_scale, mod_shift, next_eps) into out, in one pass: the Z-Image
+    block's attention post-norm + gated residual and its FFN pre-norm
+    (dependencies/zimage.c3l/dit.c3:1495-1503, 1545-1554); bit for bit the
+    two calls. dim <= 4096."""
+    g = g or default_graph()
+    rows, dim = residual.shape
+    if inp.shape != residual.shape or out.shape != residual.shape:
+        raise ValueError("input and out must have the residual's shape")
+    hp, hs = _rows(residual, "residual", torch.float32)
+    xp, xs = _rows(inp, "input", torch.float32)
+    op, os_ = _rows(out, "out")
+    g.bind_stream()
+    g.ctx.gated_residual_rmsnorm(hp, hs, xp, xs, _vec(norm_weight, "norm_weight", dim), _vec(gate, "gate", dim),
+                                 mode, _vec(next_weight, "next_weight", dim), _vec(mod_scale, "mod_scale", dim),
+                                 _vec(mod_shift, "mod_shift", dim), op, _otype(out), os_, dim, rows, eps, next_eps)
+    return out
+
+
 def activation(src: torch.Tensor, dst: torch.Tensor, act: int, src2: torch.Tensor | None = None,
                g: RenderGraph | None = None) -> torch.Tensor:
     """dst = act(src) (ACT_SILU_MUL: silu(src) * src2), dst in its own dtype; src and src2 are

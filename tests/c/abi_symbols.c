@@ -38,6 +38,7 @@ static const struct {
     {"llmr_weight_image_bytes", (void (*)(void))(uintptr_t)llmr_weight_image_bytes},
     {"llmr_swiglu_weight_image_bytes", (void (*)(void))(uintptr_t)llmr_swiglu_weight_image_bytes},
     {"llmr_batch_layernorm_split", (void (*)(void))(uintptr_t)llmr_batch_layernorm_split},
+    {"llmr_gated_residual_rmsnorm", (void (*)(void))(uintptr_t)llmr_gated_residual_rmsnorm},
     {"llmr_build_weight_image", (void (*)(void))(uintptr_t)llmr_build_weight_image},
     {"llmr_batch_matmul_swiglu", (void (*)(void))(uintptr_t)llmr_batch_matmul_swiglu},
     {"llmr_batch_matmul_swiglu_pc", (void (*)(void))(uintptr_t)llmr_batch_matmul_swiglu_pc},

@@ -156,6 +156,46 @@ def test_gated_residual_modes(orc, dev, mode, norm):
     np.testing.assert_array_equal(got[:nt], h[:nt])
 
 
+@pytest.mark.parametrize("mode,norm,dim,dtype,shift", [
+    (2, True, 3840, torch.bfloat16, False),   # the Z-Image block's form (scale only)
+    (1, False, 1000, torch.float16, True),    # a ragged width (NV 4), linear gate, scale and shift
+    (0, True, 2048, torch.float32, False),    # plain add
+])
+def test_gated_residual_rmsnorm_equals_two_calls(orc, dev, mode, norm, dim, dtype, shift):
+    """llmr_gated_residual_rmsnorm: the residual update and the updated rows'
+    RMSNorm + modulation in one pass, bit for bit gated_residual followed by
+    batch_rmsnorm (both outputs: the residual and the normalized rows), and
+    the oracle's RMSNorm + modulation of the updated rows; a dim above 4096
+    is refused."""
+    from llmr_amd import capi, glue
+    r = _rng(30 + mode)
+    S, nt = 203, 40  # 163 rows: a workgroup of four rows is part-filled
+    h = r.standard_normal((S, dim)).astype(np.float32)
+    x = r.standard_normal((S - nt, dim)).astype(np.float32) * 2
+    gate = r.standard_normal(dim).astype(np.float32)
+    nw, fw = ((1 + 0.1 * r.standard_normal(dim)).astype(np.float32) for _ in range(2))
+    sc, sh = ((0.3 * r.standard_normal(dim)).astype(np.float32) for _ in range(2))
+    ha, hb = _dev(h, dev), _dev(h, dev)
+    oa = torch.full((S - nt, dim), 7.0, dtype=dtype, device=dev)
+    ob = torch.full((S - nt, dim), 7.0, dtype=dtype, device=dev)
+    gt = _dev(gate, dev) if mode else None
+    nwt = _dev(nw, dev) if norm else None
+    sht = _dev(sh, dev) if shift else None
+    glue.gated_residual_rmsnorm(ha[nt:], _dev(x, dev), gt, mode, nwt, 1e-5, _dev(fw, dev), oa, 1e-6,
+                                mod_scale=_dev(sc, dev), mod_shift=sht)
+    glue.gated_residual(hb[nt:], _dev(x, dev), gt, mode, nwt, 1e-5)
+    glue.batch_rmsnorm(hb[nt:], _dev(fw, dev), ob, 1e-6, mod_scale=_dev(sc, dev), mod_shift=sht)
+    torch.cuda.synchronize()
+    assert torch.equal(ha, hb) and torch.equal(oa, ob)
+    h1 = ha[nt:].cpu().numpy()
+    ref = orc.modulate(orc.batch_rmsnorm(h1, fw, 1e-6), sc, sh if shift else None)
+    _close(oa, ref, dtype, atol=1e-5)
+    np.testing.assert_array_equal(ha[:nt].cpu().numpy(), h[:nt])
+    with pytest.raises(capi.LlmrError, match="4096"):
+        w = torch.zeros(4, 4104, device=dev)
+        glue.gated_residual_rmsnorm(w, w, None, 0, None, 1e-5, w[0], torch.zeros_like(w), 1e-5)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_activation_concat_gelu_silu_mul(orc, dev, dtype):
     """The single-stream concat: attention output -> cat[:, :d], gelu(linear1
