@@ -869,6 +869,7 @@ int llmr_gated_residual(llmr_context* ctx, float* residual, uint32_t residual_st
     if (int r = check_vec(gate, "gate", gate_mode != LLMR_GATE_NONE)) return r;
     llmr::ResidualArgs a{residual, input, norm_weight, gate_mode == LLMR_GATE_NONE ? nullptr : gate,
                          residual_stride, input_stride, n_rows, dim, eps};
+    a.grid_cus = (uint32_t)ctx->num_cus;
     return launched(llmr::launch_residual(a, gate_mode == LLMR_GATE_TANH, ctx->cur), "gated_residual");
 }
 

@@ -1589,7 +1589,8 @@ hipError_t run_job_fallback(uint32_t wtype, uint32_t xtype, uint32_t N, uint32_t
     hipError_t e = launch_batch_matmul(j.w, wtype, j.x, xtype, t, N, K, j.M, j.row_offset, num_cus, gemm_ws, st);
     if (e != hipSuccess) return e;
     if (epi.kind == kEpiResidual) {
-        const ResidualArgs r{j.y, t, nullptr, j.gate, epi.ldy, N, j.M, N, 0.0f};
+        ResidualArgs r{j.y, t, nullptr, j.gate, epi.ldy, N, j.M, N, 0.0f};
+        r.grid_cus = (uint32_t)num_cus;
         return launch_residual(r, false, st);
     }
     if (const GemmHeads* h = epi.heads) {  // columns [0, split) into the heads

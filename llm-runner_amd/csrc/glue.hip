@@ -26,6 +26,15 @@
 namespace llmr {
 namespace {
 
+// Workgroups of a persistent row-group kernel: two per CU (cus 0: one per
+// group of four rows). Measured on the Z-Image residual kernels (4352 rows,
+// 1088 groups): 512 workgroups of two or three groups beat 363 of three
+// (more rows in flight) and 1088 of one (the vectors staged 1088 times).
+inline uint32_t persistent_grid(uint32_t rows, uint32_t cus) {
+    const uint32_t quads = (rows + 3u) / 4u;
+    return cus ? min(quads, 2u * cus) : quads;
+}
+
 // --- output conversion -------------------------------------------------------
 
 template <uint32_t OT>
@@ -218,21 +227,11 @@ __global__ void __launch_bounds__(256) qkv_heads_kernel(QkvHeadsArgs a) {
 
 template <bool NORM, bool TANH, int NV>
 __global__ void __launch_bounds__(256) residual_kernel(ResidualArgs a) {
-    // the norm weights and the gate (tanh(gate) for TANH), computed once for
-    // the workgroup's four rows into LDS (element 4k .. 4k+3 at k)
+    // the norm weights and the gate (tanh(gate) for TANH), staged once per
+    // workgroup (element 4k .. 4k+3 at k); a persistent grid of two
+    // workgroups per CU walks the groups of four rows
     __shared__ f32x4 vec_lds[2][NV * 64];
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
-    const bool live = row < a.rows;
-    const float* xr = a.x + (size_t)(live ? row : 0u) * a.x_stride;
-    float* hr = a.h + (size_t)(live ? row : 0u) * a.h_stride;
-    f32x4 v[NV];
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const uint32_t c = 4u * lane + 256u * i;
-        v[i] = live && c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
     if (NORM || a.gate) {  // uniform over the workgroup
 #pragma unroll
         for (int j = 0; j < NV / 4; ++j) {
@@ -246,31 +245,49 @@ __global__ void __launch_bounds__(256) residual_kernel(ResidualArgs a) {
         }
         __syncthreads();
     }
-    if (!live) return;
-    if constexpr (NORM) {
+    const uint32_t quads = (a.rows + 3u) / 4u;
+    for (uint32_t q = blockIdx.x; q < quads; q += gridDim.x) {
+        const uint32_t row = q * 4u + (threadIdx.x >> 6);
+        if (row >= a.rows) break;  // the last group only
+        const float* xr = a.x + (size_t)row * a.x_stride;
+        float* hr = a.h + (size_t)row * a.h_stride;
+        f32x4 v[NV], hv[NV];
 #pragma unroll
-        for (int i = 0; i < NV; ++i)
-            s += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
-    }
-    float rms = 1.0f;
-    if constexpr (NORM) rms = 1.0f / __builtin_sqrtf(wave_sum(s) / (float)a.dim + a.eps);
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const uint32_t c = 4u * lane + 256u * i;
-        if (c >= a.dim) continue;
-        f32x4 y = v[i];
-        if constexpr (NORM) y = (y * rms) * vec_lds[0][lane + 64u * i];
-        if (a.gate) {
-            const f32x4 g = vec_lds[1][lane + 64u * i];
-            if constexpr (TANH) {
-                const f32x4 tg = g;
-                y = (1.0f * tg) * y;
-                y = __builtin_elementwise_min(__builtin_elementwise_max(y, f32x4(-1e10f)), f32x4(1e10f));
-            } else {
-                y = g * y;
-            }
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = 4u * lane + 256u * i;
+            v[i] = c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        *(f32x4*)(hr + c) = ld4(hr + c) + y;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = 4u * lane + 256u * i;
+            hv[i] = c < a.dim ? ld4(hr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        float s = 0.0f;
+        if constexpr (NORM) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i)
+                s += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+        }
+        float rms = 1.0f;
+        if constexpr (NORM) rms = 1.0f / __builtin_sqrtf(wave_sum(s) / (float)a.dim + a.eps);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = 4u * lane + 256u * i;
+            if (c >= a.dim) continue;
+            f32x4 y = v[i];
+            if constexpr (NORM) y = (y * rms) * vec_lds[0][lane + 64u * i];
+            if (a.gate) {
+                const f32x4 g = vec_lds[1][lane + 64u * i];
+                if constexpr (TANH) {
+                    const f32x4 tg = g;
+                    y = (1.0f * tg) * y;
+                    y = __builtin_elementwise_min(__builtin_elementwise_max(y, f32x4(-1e10f)), f32x4(1e10f));
+                } else {
+                    y = g * y;
+                }
+            }
+            *(f32x4*)(hr + c) = hv[i] + y;
+        }
     }
 }
 
@@ -459,7 +476,7 @@ hipError_t launch_row_norm_t(const RowNormArgs& a, bool ln, hipStream_t st) {
 
 template <bool NORM, bool TANH>
 hipError_t launch_residual_t(const ResidualArgs& a, hipStream_t st) {
-    const dim3 grid((a.rows + 3u) / 4u), block(256);
+    const dim3 grid(persistent_grid(a.rows, a.grid_cus)), block(256);
     const uint32_t nv = (a.dim + 255u) / 256u;
     if (nv <= 4) hipLaunchKernelGGL((residual_kernel<NORM, TANH, 4>), grid, block, 0, st, a);
     else if (nv <= 8) hipLaunchKernelGGL((residual_kernel<NORM, TANH, 8>), grid, block, 0, st, a);
@@ -504,7 +521,7 @@ hipError_t launch_qkv_heads(const QkvHeadsArgs& a, uint32_t otype, hipStream_t s
 
 template <bool NORM, bool TANH, uint32_t OT>
 hipError_t launch_residual_norm_t(const ResidualArgs& a, hipStream_t st) {
-    const dim3 grid(min((a.rows + 3u) / 4u, 2u * a.grid_cus)), block(256);
+    const dim3 grid(persistent_grid(a.rows, a.grid_cus)), block(256);
     const uint32_t nv = (a.dim + 255u) / 256u;
     if (nv <= 4) hipLaunchKernelGGL((residual_norm_kernel<NORM, TANH, OT, 4>), grid, block, 0, st, a);
     else if (nv <= 8) hipLaunchKernelGGL((residual_norm_kernel<NORM, TANH, OT, 8>), grid, block, 0, st, a);
