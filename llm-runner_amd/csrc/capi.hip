@@ -796,7 +796,7 @@ int row_norm_common(llmr_context* ctx, bool ln, const float* x, uint32_t x_strid
     if (int r = check_vec(mod_scale2, "mod_scale2", false)) return r;
     if (int r = check_vec(mod_shift2, "mod_shift2", false)) return r;
     llmr::RowNormArgs a{x, weight, mod_scale, mod_shift, out, x_stride, out_stride, n_rows, dim, eps,
-                        mod_scale2, mod_shift2, split};
+                        mod_scale2, mod_shift2, split, (uint32_t)ctx->num_cus};
     return launched(llmr::launch_row_norm(a, ln, out_type, ctx->cur), ln ? "batch_layernorm" : "batch_rmsnorm");
 }
 

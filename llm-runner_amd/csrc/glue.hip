@@ -88,68 +88,87 @@ __device__ __forceinline__ f32x4 ld4(const float* p) { return *(const f32x4*)p; 
 
 template <bool LN, uint32_t OT, int NV>
 __global__ void __launch_bounds__(256) row_norm_kernel(RowNormArgs a) {
-    // the modulation vectors, staged once for the workgroup's four rows
-    // (element 4k .. 4k+3 at k): the lanes keep only the row in registers
-    __shared__ f32x4 mod_lds[2][NV * 64];
+    // The vectors of one side of the split (1 + scale, shift; RMSNorm: its
+    // weight too), staged once per workgroup (element 4k .. 4k+3 at k); the
+    // workgroups of a side walk its groups of four rows. LayerNorm launches
+    // one workgroup per group (with two staged vectors they fit one round,
+    // five per CU, at the Flux shapes), RMSNorm a persistent grid of two per
+    // CU (three vectors of d = 3840: one group each ran in two rounds and
+    // staged the vectors per group).
+    constexpr int kW = LN ? -1 : 0, kS = LN ? 0 : 1, kH = LN ? 1 : 2;
+    __shared__ f32x4 vec_lds[LN ? 2 : 3][NV * 64];
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
-    // the workgroup's four rows lie on one side of the split (a multiple of 4)
-    const bool second = blockIdx.x * 4u >= a.split;
+    // side one: groups [0, qa) (all of them without a split; split % 4 == 0)
+    const uint32_t quads = (a.rows + 3u) / 4u, qa = a.split >= a.rows ? quads : a.split / 4u;
+    const uint32_t ga = a.grid_a, G = gridDim.x;
+    const bool second = blockIdx.x >= ga;
     const float* const scale = second ? a.scale2 : a.scale;
     const float* const shift = second ? a.shift2 : a.shift;
-    const bool live = row < a.rows;
-    const float* xr = a.x + (size_t)(live ? row : 0u) * a.x_stride;
-    f32x4 v[NV];
-    float s = 0.0f;
+    const uint32_t q0 = second ? qa + (blockIdx.x - ga) : blockIdx.x, qend = second ? quads : qa;
+    const uint32_t qstep = second ? G - ga : ga;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const uint32_t c = 4u * lane + 256u * i;
-        v[i] = live && c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NV / 4; ++j) {
+        const uint32_t k = threadIdx.x + 256u * j, c = 4u * k;
+        const f32x4 z{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (!LN) vec_lds[kW][k] = c < a.dim ? ld4(a.w + c) : z;
+        if (scale) vec_lds[kS][k] = c < a.dim ? 1.0f + ld4(scale + c) : z;
+        if (shift) vec_lds[kH][k] = c < a.dim ? ld4(shift + c) : z;
     }
-    if (scale || shift) {  // uniform over the workgroup
-#pragma unroll
-        for (int j = 0; j < NV / 4; ++j) {
-            const uint32_t k = threadIdx.x + 256u * j, c = 4u * k;
-            mod_lds[0][k] = scale && c < a.dim ? ld4(scale + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            mod_lds[1][k] = shift && c < a.dim ? ld4(shift + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-        __syncthreads();
-    }
-    if (!live) return;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        if constexpr (LN) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-        else s += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
-    }
-    s = wave_sum(s);
-    float mean = 0.0f, r;
-    if constexpr (LN) {
-        mean = s / (float)a.dim;
-        float q = 0.0f;
+    __syncthreads();
+    auto one_row = [&](uint32_t row) __attribute__((always_inline)) {
+        const float* xr = a.x + (size_t)row * a.x_stride;
+        f32x4 v[NV];
+        float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const uint32_t c = 4u * lane + 256u * i;
-            if (c < a.dim) {
-                const f32x4 d = v[i] - mean;
-                q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
-            }
+            v[i] = c < a.dim ? ld4(xr + c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        q = wave_sum(q);
-        r = 1.0f / __builtin_sqrtf(q / (float)a.dim + a.eps);
-    } else {
-        r = 1.0f / __builtin_sqrtf(s / (float)a.dim + a.eps);
-    }
-    char* orow = (char*)a.out + (size_t)row * a.out_stride * (OT == kGgmlF32 ? 4u : 2u);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const uint32_t c = 4u * lane + 256u * i;
-        if (c >= a.dim) continue;
-        f32x4 y;
-        if constexpr (LN) y = (v[i] - mean) * r;
-        else y = (v[i] * r) * ld4(a.w + c);
-        if (scale) y = y * (1.0f + mod_lds[0][lane + 64u * i]);
-        if (shift) y = y + mod_lds[1][lane + 64u * i];
-        store4<OT>(orow, c, y);
+        for (int i = 0; i < NV; ++i) {
+            if constexpr (LN) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+            else s += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+        }
+        s = wave_sum(s);
+        float mean = 0.0f, r;
+        if constexpr (LN) {
+            mean = s / (float)a.dim;
+            float qs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const uint32_t c = 4u * lane + 256u * i;
+                if (c < a.dim) {
+                    const f32x4 d = v[i] - mean;
+                    qs += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+                }
+            }
+            qs = wave_sum(qs);
+            r = 1.0f / __builtin_sqrtf(qs / (float)a.dim + a.eps);
+        } else {
+            r = 1.0f / __builtin_sqrtf(s / (float)a.dim + a.eps);
+        }
+        char* orow = (char*)a.out + (size_t)row * a.out_stride * (OT == kGgmlF32 ? 4u : 2u);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t c = 4u * lane + 256u * i;
+            if (c >= a.dim) continue;
+            f32x4 y;
+            if constexpr (LN) y = (v[i] - mean) * r;
+            else y = (v[i] * r) * vec_lds[kW][lane + 64u * i];
+            if (scale) y = y * vec_lds[kS][lane + 64u * i];
+            if (shift) y = y + vec_lds[kH][lane + 64u * i];
+            store4<OT>(orow, c, y);
+        }
+    };
+    if constexpr (LN) {  // one group per workgroup: no loop (it cost 19 registers and a round)
+        const uint32_t row = q0 * 4u + (threadIdx.x >> 6);
+        if (q0 < qend && row < a.rows) one_row(row);
+    } else {
+        for (uint32_t q = q0; q < qend; q += qstep) {
+            const uint32_t row = q * 4u + (threadIdx.x >> 6);
+            if (row >= a.rows) break;  // the last group only
+            one_row(row);
+        }
     }
 }
 
@@ -456,8 +475,17 @@ __global__ void __launch_bounds__(256) unpatchify_kernel(const float* in, float*
 // --- dispatch helpers ----------------------------------------------------------
 
 template <uint32_t OT>
-hipError_t launch_row_norm_t(const RowNormArgs& a, bool ln, hipStream_t st) {
-    const dim3 grid((a.rows + 3u) / 4u), block(256);
+hipError_t launch_row_norm_t(RowNormArgs a, bool ln, hipStream_t st) {
+    // LayerNorm: one workgroup per group of four rows; RMSNorm: two per CU.
+    // The workgroups are split between the sides in proportion to their
+    // groups (each side at least one when it has rows).
+    const uint32_t quads = (a.rows + 3u) / 4u, qa = a.split >= a.rows ? quads : a.split / 4u, qb = quads - qa;
+    const uint32_t G = ln ? quads : persistent_grid(a.rows, a.grid_cus);
+    uint32_t ga = qb == 0 ? G : qa == 0 ? 0u : (uint32_t)(((uint64_t)G * qa + quads / 2u) / quads);
+    if (qa > 0 && ga == 0) ga = 1;
+    if (qb > 0 && ga == G) ga = G - 1u;
+    a.grid_a = ga;
+    const dim3 grid(G), block(256);
     const uint32_t nv = (a.dim + 255u) / 256u;
 #define LLMR_ROW_NORM(NVV)                                                                              \
     if (nv <= NVV) {                                                                                    \

@@ -205,6 +205,8 @@ struct RowNormArgs {
     const float* scale2 = nullptr;
     const float* shift2 = nullptr;
     uint32_t split = ~0u;
+    uint32_t grid_cus = 0;  // the device's CUs (RMSNorm's persistent grid: two workgroups each)
+    uint32_t grid_a = 0;    // set by the launcher: workgroups of the first side
 };
 constexpr uint32_t kRowNormMaxDim = 8192;
 
