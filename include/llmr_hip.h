@@ -287,27 +287,32 @@ LLMR_API int llmr_build_weight_image(llmr_context* ctx, const void* weight, uint
  * columns. swiglu 0: rows [row_offset, row_offset + out_dim) (sized by
  * llmr_weight_image_bytes). swiglu 1: the SwiGLU arrangement of out_dim
  * outputs, gate rows [row_offset, row_offset + out_dim) and up rows
- * [row_offset + out_dim, row_offset + 2 out_dim) (sized by
- * llmr_swiglu_weight_image_bytes): what a SPLIT_SWIGLU job reads after the
- * plain image of its first `split` rows, at llmr_weight_image_bytes(split,
- * in_dim) into its image. */
+ * [row_offset + u, row_offset + u + out_dim) with u = up_offset, or out_dim
+ * when up_offset is 0 (sized by llmr_swiglu_weight_image_bytes): what a
+ * SPLIT_SWIGLU job reads after the plain image of its first `split` rows,
+ * at llmr_weight_image_bytes(split, in_dim) into its image. A part of an
+ * image is an image too: the rows [256 p0, 256 p1) of a plain image (row
+ * offset + 256 p0) start p0 panels into it, the outputs [128 p0, 128 p1)
+ * of a SwiGLU image of f outputs (row offset + 128 p0, up_offset f) p0
+ * panels in, a panel being llmr_weight_image_bytes(256, in_dim) bytes. */
 typedef struct llmr_next_weight_image {
     const void* weight;
     uint32_t out_dim;
     uint32_t in_dim;     /* % 64 == 0 */
     uint32_t row_offset;
     uint32_t swiglu;
+    uint32_t up_offset;  /* swiglu 1 only; 0: out_dim */
     void* image;         /* 256-byte aligned */
     size_t image_bytes;
 } llmr_next_weight_image;
 
-/* The weight images of the GEMM groups a caller issues next (the next
- * group's, or the next two groups'): `count` (1 to 4) images of weights of
- * weight_type, for the same input_type as the call that builds them. */
+/* The weight images of the GEMM groups a caller issues next: `count` (1 to
+ * 8) images or image parts of weights of weight_type, for the same
+ * input_type as the call that builds them. */
 typedef struct llmr_next_weight_images {
     uint32_t weight_type;
     uint32_t count;
-    llmr_next_weight_image image[4];
+    llmr_next_weight_image image[8];
 } llmr_next_weight_images;
 
 /* llmr_batch_matmul_multi, plus:

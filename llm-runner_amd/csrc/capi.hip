@@ -517,12 +517,18 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
             if (m.in_dim % 64 || m.out_dim == 0)
                 return fail(LLMR_ERR_INVALID_ARG, "next image %u: in_dim %% 64 == 0 and out_dim > 0 needed", i);
             if (m.swiglu > 1) return fail(LLMR_ERR_INVALID_ARG, "next image %u: swiglu must be 0 or 1", i);
+            if (m.up_offset && !m.swiglu)
+                return fail(LLMR_ERR_INVALID_ARG, "next image %u: up_offset needs swiglu 1", i);
+            if (m.swiglu && m.up_offset && m.up_offset < m.out_dim)
+                return fail(LLMR_ERR_INVALID_ARG, "next image %u: up_offset below out_dim (the up rows overlap the gate "
+                            "rows)", i);
             const size_t need = llmr::w16_image_bytes(m.out_dim, m.in_dim, m.swiglu != 0);
             if (m.image_bytes < need)
                 return fail(LLMR_ERR_INVALID_ARG, "next image %u holds %zu bytes, needs %zu", i, m.image_bytes,
                             need);
             if (int r = check_weight(m.weight, next->weight_type, m.in_dim)) return r;
-            if ((uint64_t)m.row_offset + (m.swiglu ? 2ull : 1ull) * m.out_dim > 0xffffffffull)
+            const uint64_t up = m.swiglu ? (m.up_offset ? m.up_offset : m.out_dim) : 0u;
+            if ((uint64_t)m.row_offset + up + m.out_dim > 0xffffffffull)
                 return fail(LLMR_ERR_INVALID_ARG, "next image %u: its last row overflows 32 bits", i);
             if (!m.image || !aligned(m.image, 256))
                 return fail(LLMR_ERR_INVALID_ARG, "next image %u must be non-null and 256-byte aligned", i);
@@ -539,6 +545,7 @@ static int batch_matmul_multi_impl(llmr_context* ctx, uint32_t wtype, uint32_t x
             nx.N[i] = m.out_dim;
             nx.K[i] = m.in_dim;
             nx.sw[i] = m.swiglu;
+            nx.up[i] = m.up_offset;
         }
         nx.count = next->count;
         nx.wtype = next->weight_type;

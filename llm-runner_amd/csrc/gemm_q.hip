@@ -1678,7 +1678,7 @@ static void next_image_rows(const NextImageSet& nx, uint32_t i, const void*& g, 
     }
     const uint64_t rb = row_bytes_of(nx.wtype, nx.K[i]);
     g = (const uint8_t*)nx.w[i] + (uint64_t)nx.row_offset[i] * rb;
-    u = (const uint8_t*)g + (uint64_t)nx.N[i] * rb;
+    u = (const uint8_t*)g + (uint64_t)(nx.up[i] ? nx.up[i] : nx.N[i]) * rb;
 }
 
 // Later groups' images: the items [0, fused) came from the GEMM's idle

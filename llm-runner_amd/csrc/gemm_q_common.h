@@ -28,10 +28,10 @@ struct PersistProblem {
 // i's item u at first[i] + u; the first `items` of them here, the rest by
 // w16_image_kernel after the GEMM).
 struct NextImages {
-    const uint8_t* W[4];   // raw weight blocks, row row_offset[i] is feature 0
-    const uint8_t* W2[4];  // non-null: a SwiGLU-arranged image, W[i] its gate rows, W2[i] its up rows
-    uint8_t* img[4];
-    uint32_t row_offset[4], N[4], K[4], first[4];
+    const uint8_t* W[8];   // raw weight blocks, row row_offset[i] is feature 0
+    const uint8_t* W2[8];  // non-null: a SwiGLU-arranged image, W[i] its gate rows, W2[i] its up rows
+    uint8_t* img[8];
+    uint32_t row_offset[8], N[8], K[8], first[8];
     uint32_t count, wtype;
     uint32_t items;       // items built by the GEMM's idle workgroups (0: none)
 };

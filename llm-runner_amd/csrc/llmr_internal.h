@@ -143,12 +143,13 @@ uint32_t w16_image_items(uint32_t N, uint32_t K, bool sw = false);
 // they are complete when the next call on the stream starts. Image i: the
 // plain image of rows [row_offset, + N) of w (sw 0), or the SwiGLU
 // arrangement of N outputs whose gate rows are [row_offset, + N) and up
-// rows [row_offset + N, + N) (sw 1).
-constexpr uint32_t kMaxNextImages = 4;
+// rows [row_offset + up, + N) (sw 1; up: up[i], or N when that is 0).
+constexpr uint32_t kMaxNextImages = 8;
 struct NextImageSet {
     const void* w[kMaxNextImages];
     void* img[kMaxNextImages];
     uint32_t row_offset[kMaxNextImages], N[kMaxNextImages], K[kMaxNextImages], sw[kMaxNextImages];
+    uint32_t up[kMaxNextImages];
     uint32_t count, wtype;
 };
 // Items of the images, numbered across them in order (image i's item u =

@@ -57,13 +57,13 @@ class MatmulEpilogue(ctypes.Structure):
 class NextWeightImage(ctypes.Structure):
     """llmr_next_weight_image: one weight image a call builds for a later call."""
     _fields_ = [("weight", ctypes.c_void_p), ("out_dim", ctypes.c_uint32), ("in_dim", ctypes.c_uint32),
-                ("row_offset", ctypes.c_uint32), ("swiglu", ctypes.c_uint32), ("image", ctypes.c_void_p),
-                ("image_bytes", ctypes.c_size_t)]
+                ("row_offset", ctypes.c_uint32), ("swiglu", ctypes.c_uint32), ("up_offset", ctypes.c_uint32),
+                ("image", ctypes.c_void_p), ("image_bytes", ctypes.c_size_t)]
 
 
 class NextWeightImages(ctypes.Structure):
-    """llmr_next_weight_images: weight images of later GEMM groups (1 to 4)."""
-    _fields_ = [("weight_type", ctypes.c_uint32), ("count", ctypes.c_uint32), ("image", NextWeightImage * 4)]
+    """llmr_next_weight_images: weight images of later GEMM groups (1 to 8)."""
+    _fields_ = [("weight_type", ctypes.c_uint32), ("count", ctypes.c_uint32), ("image", NextWeightImage * 8)]
 
 
 EPI_STORE, EPI_GATED_RESIDUAL, EPI_SPLIT_GELU, EPI_SPLIT_SWIGLU = 0, 1, 2, 3

@@ -35,7 +35,7 @@ import torch
 
 from . import capi, glue, workloads
 from .gguf import GGML_Q4_K, GGML_Q8_0
-from .ops import _TORCH_GGML, FlashAttentionPC, MatmulJob, NextImages, QkvHeads, RenderGraph, Tensor, \
+from .ops import _TORCH_GGML, FlashAttentionPC, MatmulJob, NextImage, NextImages, QkvHeads, RenderGraph, Tensor, \
     build_next_images, default_graph, dispatch_batch_matmul, dispatch_batch_matmul_multi, \
     dispatch_batch_matmul_swiglu, dispatch_flash_attention, dispatch_flash_attention_rows, \
     split_swiglu_image_bytes, weight_image_bytes
@@ -448,28 +448,32 @@ class _ImageChain:
     each: one or two Q4_K/Q8_0 weights of one shape N x K, rows from 0, the
     token counts of its jobs and, for a SPLIT_SWIGLU group, its split (a
     weight's image then the plain image of its first split rows followed by
-    the SwiGLU image of its (N - split) / 2 outputs: two next images), built
-    ahead image by image: each of group k's images by call k - 1, or by call
-    k - 2 when that call's idle workgroups (those without a tile in its
-    GEMM's last round) have room for all of its items after what the call
-    builds before it. A call's NextImages are built as far as its idle
-    workgroups reach and the rest right after it; the first group's are
-    built before it. Three buffers rotate (group k in buffer k % 3: at most
-    two groups are built ahead of the one running, none into the buffer it
-    reads). The room is estimated here from the launch's tile count; a wrong
-    estimate only moves items into the image launch after the GEMM. The
-    results are those of dispatch_batch_matmul_multi without images, bit
-    for bit. A group's weights may be None at construction (the shapes
-    alone plan the chain); bind() then sets them before start()."""
+    the SwiGLU image of its (N - split) / 2 outputs: two images), built
+    ahead. Call k builds what is left of group k + 1's images (its GEMM's
+    idle workgroups, those without a tile in its last round, as far as they
+    reach, the rest right after it), then, while its idle room lasts, parts
+    of group k + 2's and k + 3's images in order: whole 256-row panels (128
+    outputs of a SwiGLU image) of one image, a next image each (at most
+    eight a call). The first group's images are built before it. Four
+    buffers rotate (group k in buffer k % 4: at most three groups are built
+    ahead of the one running, none into the buffer it reads). The room is
+    estimated here from the launch's tile count; a wrong estimate only moves
+    items into the image launch after the GEMM. The results are those of
+    dispatch_batch_matmul_multi without images, bit for bit. A group's
+    weights may be None at construction (the shapes alone plan the chain);
+    bind() then sets them before start()."""
+
+    NBUF = 4        # buffers (groups built ahead: NBUF - 1)
+    MAX_PARTS = 8   # next images a call takes
 
     def __init__(self, groups, input_dtype: int, device, cus: int, wtype: int = GGML_Q4_K):
-        if any(self._entries(gr) > 4 for gr in groups):
-            raise ValueError("a group's images must fit one call's four next images")
+        if any(self._entries(gr) > self.MAX_PARTS for gr in groups):
+            raise ValueError("a group's images must fit one call's next images")
         self.groups, self.xtype = list(groups), input_dtype
         per = max(len(gr[0]) * self._image_bytes(gr) for gr in groups)
-        self.bufs = [torch.empty(per, dtype=torch.uint8, device=device) for _ in range(3)]
-        self.builds = self.plan(groups, cus, wtype)  # call k -> the (group, image) pairs it builds
-        self.images = None
+        self.bufs = [torch.empty(per, dtype=torch.uint8, device=device) for _ in range(self.NBUF)]
+        self.builds = self.plan(groups, cus, wtype)  # call k -> the (group, image, p0, p1) parts it builds
+        self.bound = False
         if all(w is not None for gr in groups for w in gr[0]):
             self.bind([gr[0] for gr in groups])
         self.k = 0
@@ -480,62 +484,84 @@ class _ImageChain:
         if len(weights) != len(self.groups) or any(len(w) != len(gr[0]) for w, gr in zip(weights, self.groups)):
             raise ValueError("one weight list per group, as many weights as planned")
         self.groups = [(list(w),) + tuple(gr[1:]) for w, gr in zip(weights, self.groups)]
-        self.images = [self._next(k).entries for k in range(len(self.groups))]  # group k's NextImage entries
+        self.nexts = [self._parts(c) for c in range(len(self.groups))]  # call c's NextImages (or None)
+        self.bound = True
 
     @classmethod
     def plan(cls, groups, cus: int, wtype: int = GGML_Q4_K):
-        """For each call k, the images (group j, image e) it builds, in order:
-        those of group k + 1 that call k - 1 did not build, then group k + 2's
-        in order while all items of the next one fit in what is left of the
-        call's room and a next image of the call's four is left."""
+        """For each call c, the image parts (group j, image e, panels [p0, p1))
+        it builds, in order: what is left of group c + 1's images, then parts
+        of group c + 2's and c + 3's images in order while whole panels fit
+        in what is left of the call's room and a next image is left."""
         n = len(groups)
         builds = [[] for _ in range(n)]
-        done = [0] * n  # images of each group assigned so far (in order)
+        done = [[0] * cls._entries(gr) for gr in groups]  # panels of each image assigned so far
         for c in range(n - 1):
-            room, slots = cls._room(groups[c], cus, wtype), 4
-            for j in (c + 1, c + 2):
-                if j >= n:
-                    break
-                items = cls._entry_items(groups[j])
-                while done[j] < len(items):
-                    if j > c + 1 and (items[done[j]] > room or slots == 0):
-                        break
-                    builds[c].append((j, done[j]))
-                    room -= items[done[j]]
+            room, slots = cls._room(groups[c], cus, wtype), cls.MAX_PARTS
+            later = False
+            for j in range(c + 1, min(n, c + cls.NBUF)):
+                ents = cls._entry_panels(groups[j])
+                per = cls._stage_groups(groups[j])  # items of one panel
+                for e, panels in enumerate(ents):
+                    p0 = done[j][e]
+                    if p0 == panels:
+                        continue
+                    if j == c + 1:  # the next group: all of what is left
+                        p1 = panels
+                    else:
+                        if not later:  # a margin for the groups after next
+                            room = room * 3 // 4
+                            later = True
+                        if slots == 0 or room < per:
+                            break
+                        p1 = min(panels, p0 + room // per)
+                    builds[c].append((j, e, p0, p1))
+                    room -= (p1 - p0) * per
                     slots -= 1
-                    done[j] += 1
+                    done[j][e] = p1
+                    if p1 < panels:  # the room ran out inside this image
+                        break
+                else:
+                    continue
+                break
         return builds
 
     @staticmethod
     def _split(group):
         return group[4] if len(group) > 4 else None
 
+    @staticmethod
+    def _stage_groups(group) -> int:
+        """Items of one panel: its K stages in groups of four."""
+        return -(-(group[2] // 64) // 4)
+
     @classmethod
-    def _entry_items(cls, group) -> list:
-        """Image items ((256-row panel, 4 K stages) each) of the group's next
-        images in order: one image per weight; a split SwiGLU weight's plain
-        rows (when split > 0), then its SwiGLU rows."""
-        ws, N, K = group[:3]
-        stages = -(-(K // 64) // 4)
+    def _entry_panels(cls, group) -> list:
+        """Panels of the group's images in order: one image per weight; a split
+        SwiGLU weight's plain rows (256 a panel, when split > 0), then its
+        SwiGLU rows (128 outputs a panel)."""
+        ws, N = group[0], group[1]
         split = cls._split(group)
         if split is None:
-            return [-(-N // 256) * stages] * len(ws)
-        one = ([split // 256 * stages] if split else []) + [-(-((N - split) // 2) // 128) * stages]
+            return [-(-N // 256)] * len(ws)
+        one = ([split // 256] if split else []) + [-(-((N - split) // 2) // 128)]
         return one * len(ws)
 
     @classmethod
+    def _entry_items(cls, group) -> list:
+        """Image items ((panel, 4 K stages) each) of the group's images."""
+        per = cls._stage_groups(group)
+        return [p * per for p in cls._entry_panels(group)]
+
+    @classmethod
     def _entries(cls, group) -> int:
-        """Next images of a group."""
-        return len(cls._entry_items(group))
+        """Images of a group."""
+        return len(cls._entry_panels(group))
 
     @classmethod
     def _panels(cls, group) -> int:
-        """256-row panels of one weight's image (SwiGLU: 128 outputs each),
-        also the GEMM's column tiles."""
-        N, split = group[1], cls._split(group)
-        if split is None:
-            return -(-N // 256)
-        return split // 256 + -(-((N - split) // 2) // 128)
+        """Panels of one weight's image, also the GEMM's column tiles."""
+        return sum(cls._entry_panels(group)) // len(group[0])
 
     @classmethod
     def _image_bytes(cls, group) -> int:
@@ -560,22 +586,40 @@ class _ImageChain:
 
     def _views(self, k: int):
         n = self._image_bytes(self.groups[k])
-        return [self.bufs[k % 3][i * n:(i + 1) * n] for i in range(len(self.groups[k][0]))]
+        return [self.bufs[k % self.NBUF][i * n:(i + 1) * n] for i in range(len(self.groups[k][0]))]
 
-    def _next(self, k: int) -> NextImages:
-        ws, N, K = self.groups[k][:3]
-        split = self._split(self.groups[k])
-        if split is None:
-            return NextImages.group(ws, N, K, self._views(k), (0,) * len(ws))
-        return NextImages.split_swiglu(ws, split, (N - split) // 2, K, self._views(k), (0,) * len(ws))
+    def _part(self, j: int, e: int, p0: int, p1: int) -> NextImage:
+        """Panels [p0, p1) of group j's image e as a next image."""
+        gr = self.groups[j]
+        ws, N, K = gr[:3]
+        split = self._split(gr)
+        per_w = 1 if split is None or split == 0 else 2  # images per weight
+        w, kind = divmod(e, per_w)
+        view = self._views(j)[w]
+        panel = weight_image_bytes(256, K)  # bytes of one panel (either arrangement)
+        if split is None or (split and kind == 0):  # plain rows
+            rows = N if split is None else split
+            n = min(256 * p1, rows) - 256 * p0
+            return NextImage(ws[w], n, K, view[p0 * panel:p1 * panel], 256 * p0)
+        f = (N - split) // 2
+        base = weight_image_bytes(split, K) if split else 0
+        n = min(128 * p1, f) - 128 * p0
+        return NextImage(ws[w], n, K, view[base + p0 * panel:base + p1 * panel], split + 128 * p0, True, f)
+
+    def _parts(self, c: int):
+        if not self.builds[c]:
+            return None
+        return NextImages([self._part(j, e, p0, p1) for j, e, p0, p1 in self.builds[c]])
 
     def start(self, g: RenderGraph) -> None:
         """Before the first group: its images."""
-        if self.images is None:
+        if not self.bound:
             raise RuntimeError("weight-image chain started before its weights were bound")
         self.k = 0
         self.active = True
-        build_next_images(g, NextImages(self.images[0]), self.xtype)
+        gr = self.groups[0]
+        build_next_images(g, NextImages([self._part(0, e, 0, p) for e, p in enumerate(self._entry_panels(gr))]),
+                          self.xtype)
 
     def take(self, jobs, N: int, K: int):
         """(images, next_images) for the next group's call, whose jobs must be
@@ -586,12 +630,9 @@ class _ImageChain:
         if (gN, gK) != (N, K) or [w.ptr() for w in ws] != [j.weight.ptr() for j in jobs]:
             self.active = False
             raise RuntimeError(f"weight-image chain out of step: group {k} holds other weights than this call's")
-        nxt = None
-        if self.builds[k]:
-            nxt = NextImages([self.images[j][e] for j, e in self.builds[k]])
         self.k += 1
         self.active = self.k < len(self.groups)
-        return self._views(k), nxt
+        return self._views(k), self.nexts[k]
 
 
 class FluxDiT:

@@ -308,25 +308,29 @@ class NextImage:
     row_offset + out_dim) of `weight` (a quantized Tensor) with in_dim
     columns, into `image` (a device tensor of weight_image_bytes); swiglu:
     the SwiGLU arrangement of out_dim outputs whose gate rows start at
-    row_offset and up rows at row_offset + out_dim (swiglu_weight_image_bytes)."""
+    row_offset and up rows up_offset rows later (0: out_dim;
+    swiglu_weight_image_bytes)."""
     weight: Tensor
     out_dim: int
     in_dim: int
     image: object
     row_offset: int = 0
     swiglu: bool = False
+    up_offset: int = 0
 
     def nbytes(self) -> int:
         return (swiglu_weight_image_bytes if self.swiglu else weight_image_bytes)(self.out_dim, self.in_dim)
 
     def rows(self) -> int:
-        return self.row_offset + (2 if self.swiglu else 1) * self.out_dim
+        if not self.swiglu:
+            return self.row_offset + self.out_dim
+        return self.row_offset + (self.up_offset or self.out_dim) + self.out_dim
 
 
 @dataclasses.dataclass
 class NextImages:
     """Weight images of the GEMM groups issued next (llmr_next_weight_images):
-    1 to 4 NextImage entries, weights of one type."""
+    1 to 8 NextImage entries, weights of one type."""
     entries: list
 
     @classmethod
@@ -354,12 +358,12 @@ class NextImages:
 
 def _next_images_struct(next_images: NextImages) -> capi.NextWeightImages:
     es = next_images.entries
-    if not 1 <= len(es) <= 4:
-        raise ValueError("next_images: one to four images")
+    if not 1 <= len(es) <= 8:
+        raise ValueError("next_images: one to eight images")
     if len(es) != len(set(e.image.data_ptr() for e in es)):
         raise ValueError("next_images: one buffer per image")
     nt = es[0].weight.dtype
-    arr = (capi.NextWeightImage * 4)()
+    arr = (capi.NextWeightImage * 8)()
     for i, e in enumerate(es):
         _dev(e.weight, "next weight")
         nbytes = e.nbytes()
@@ -367,7 +371,7 @@ def _next_images_struct(next_images: NextImages) -> capi.NextWeightImages:
             raise ValueError("next weights: one type, covering the image's rows x in_dim")
         if not e.image.is_cuda or e.image.numel() * e.image.element_size() < nbytes:
             raise ValueError(f"next images must be device tensors of at least {nbytes} bytes")
-        arr[i] = capi.NextWeightImage(e.weight.ptr(), e.out_dim, e.in_dim, e.row_offset, int(e.swiglu),
+        arr[i] = capi.NextWeightImage(e.weight.ptr(), e.out_dim, e.in_dim, e.row_offset, int(e.swiglu), e.up_offset,
                                       e.image.data_ptr(), e.image.numel() * e.image.element_size())
     return capi.NextWeightImages(nt, len(es), arr)
 

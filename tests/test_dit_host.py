@@ -30,28 +30,37 @@ def test_image_chain_refuses_out_of_step_calls():
     assert not chain.active
 
 
-def _check_plan(groups, cus):
-    """Each image of each group after the first built by call k - 1 or
-    k - 2 and by no other, never into the buffer the building call reads
-    (k % 3); at most four images a call; a call builds group k + 2's images
-    only after all of group k + 1's, and only within its room. Returns the
-    plan, (group, image) -> call, and the items a call leaves to the image
-    launch after its GEMM."""
+def _check_plan(groups, cus, wtype=None):
+    """Every panel of every image of each group after the first built
+    exactly once, by call k - 1, k - 2 or k - 3 (never into the buffer the
+    building call reads: group k in buffer k % 4); at most eight parts a
+    call; group k + 1's parts first, and the parts of the groups after it
+    only within three quarters of what is left of the call's room. Returns
+    the plan and the items each call leaves to the image launch after its
+    GEMM."""
     C = dit._ImageChain
-    builds = C.plan(groups, cus)
-    by = {}
-    for c, es in enumerate(builds):
-        assert len(es) <= 4, c
-        assert es == sorted(es), c
-        for j, e in es:
-            assert (j, e) not in by and j - c in (1, 2) and j % 3 != c % 3, (c, j, e)
-            by[(j, e)] = c
-        if any(j == c + 2 for j, _ in es):
-            assert sum(C._entry_items(groups[j])[e] for j, e in es) <= C._room(groups[c], cus), c
-    assert sorted(by) == [(j, e) for j in range(1, len(groups)) for e in range(C._entries(groups[j]))]
-    left = [max(0, sum(C._entry_items(groups[j])[e] for j, e in es) - C._room(groups[c], cus))
-            for c, es in enumerate(builds)]
-    return builds, by, left
+    kw = {} if wtype is None else {"wtype": wtype}
+    builds = C.plan(groups, cus, **kw)
+    seen = {}
+    left = []
+    for c, parts in enumerate(builds):
+        assert len(parts) <= C.MAX_PARTS, c
+        room = C._room(groups[c], cus, **kw)
+        nxt = sum((p1 - p0) * C._stage_groups(groups[j]) for j, e, p0, p1 in parts if j == c + 1)
+        later = sum((p1 - p0) * C._stage_groups(groups[j]) for j, e, p0, p1 in parts if j > c + 1)
+        assert later <= max(0, room - nxt) * 3 // 4, c
+        js = [j for j, _, _, _ in parts]
+        assert js == sorted(js) and all(1 <= j - c <= C.NBUF - 1 for j in js), (c, parts)
+        for j, e, p0, p1 in parts:
+            assert j % C.NBUF != c % C.NBUF and 0 <= p0 < p1 <= C._entry_panels(groups[j])[e], (c, j, e)
+            for p in range(p0, p1):
+                assert (j, e, p) not in seen, (c, j, e, p)
+                seen[(j, e, p)] = c
+        left.append(max(0, nxt + later - room))
+    want = {(j, e, p) for j in range(1, len(groups)) for e, n in enumerate(C._entry_panels(groups[j]))
+            for p in range(n)}
+    assert set(seen) == want
+    return builds, left
 
 
 def _flux_groups(act):
@@ -73,47 +82,58 @@ def _flux_groups(act):
 def test_image_chain_plan_flux_step():
     """The plan over a Flux-dev step's GEMM groups on 256 CUs keeps the
     chain's rules and leaves no item to an image launch: the double block's
-    QKV builds the projection's and the MLP-in's images, the MLP-in the
-    MLP-out's and the next QKV's text image, linear2 the next linear1's and
-    linear2's."""
+    QKV builds the projection's images and, in three quarters of what is
+    left of its room, the MLP-in's text image and half its image-row one;
+    the projection the rest of that and three panels of the MLP-out's."""
     groups = _flux_groups("gelu")
-    builds, _, left = _check_plan(groups, 256)
+    builds, left = _check_plan(groups, 256)
     assert sum(left) == 0
-    assert builds[0] == [(1, 0), (1, 1), (2, 0), (2, 1)] and builds[1] == []
-    assert builds[2] == [(3, 0), (3, 1), (4, 0)] and builds[3] == [(4, 1), (5, 0), (5, 1)]
-    s0 = 19 * 4
-    assert builds[s0] == [] and builds[s0 + 1] == [(s0 + 2, 0), (s0 + 3, 0)]
+    assert builds[0] == [(1, 0, 0, 12), (1, 1, 0, 12), (2, 0, 0, 48), (2, 1, 0, 24)]
+    assert builds[1] == [(2, 1, 24, 48), (3, 0, 0, 3)]
 
 
 def test_image_chain_plan_flux2_step():
     """The Flux.2 form: the MLP-in's images (SwiGLU only) and linear1's
     (plain Q | K | V rows, then the SwiGLU rows: two images of one weight)
-    take part. The double block's MLP-in is twice as wide, so the QKV no
-    longer builds it beside the projection; linear2 still builds the next
-    linear1 and linear2 (three images)."""
+    take part, and a call with room left after the next group builds parts
+    of the two groups after it (within three quarters of that room): the
+    MLP-out begins the next block's MLP-in (42 of its text image's 96
+    panels), so from the second double block on 624 items a block are left
+    to launches (the first block 1344), against 1056 a block when only the
+    next two groups' whole images were planned."""
     C = dit._ImageChain
     groups = _flux_groups("swiglu")
     assert C._entries(groups[2]) == 2 and C._entries(groups[76]) == 2
     # the split SwiGLU weight's panels: 36 plain + 96 of 128 outputs
     assert C._panels(groups[76]) == 132 and C._entry_items(groups[76]) == [36 * 12, 96 * 12]
-    builds, _, left = _check_plan(groups, 256)
-    # the QKV builds the MLP-in's text image beside the projection's; the
-    # projection (room 480) and the MLP-in (room 768) leave 672 and 384
-    # items a double block to image launches, the single blocks none
-    assert builds[0] == [(1, 0), (1, 1), (2, 0)] and builds[1] == [(2, 1)] and builds[2] == [(3, 0), (3, 1)]
-    assert left[:4] == [0, 672, 384, 0] and sum(left) == 19 * (672 + 384)
-    s0 = 19 * 4
-    assert builds[s0] == [(s0 + 1, 0), (s0 + 2, 0)] and builds[s0 + 1] == [(s0 + 2, 1), (s0 + 3, 0)]
+    builds, left = _check_plan(groups, 256)
+    assert left[:8] == [0, 960, 384, 0, 0, 240, 384, 0] and sum(left) == 1344 + 18 * 624
+    assert builds[3] == [(4, 0, 0, 36), (4, 1, 0, 36), (5, 0, 0, 12), (5, 1, 0, 12), (6, 0, 0, 42)]
+    assert builds[4] == [(6, 0, 42, 96), (6, 1, 0, 36)]
 
 
-def test_image_chain_plan_four_images():
-    """A call builds no more than the four images a call takes: of two split
-    SwiGLU weights' four images after a group whose room would hold them
-    all, the last is left to the next call."""
-    groups = [([0, 1], 1024, 1024, (300,)), ([0], 1024, 1024, (256,)), ([0, 1], 2048, 1024, (256,), 512),
+def test_image_chain_plan_zimage_block():
+    """The Z-Image block's four Q8_0 GEMMs (QKV, O-proj, SwiGLU, down):
+    with one item per eight K stages of room the QKV and the O-proj build
+    a few items of the next image each and the SwiGLU (176 idle
+    workgroups) the down projection's whole image."""
+    from llmr_amd.gguf import GGML_Q8_0
+    d, f, S = 3840, 10240, 4352
+    groups = [([0], 3 * d, d, (S,)), ([0], d, d, (S,)), ([0], 2 * f, d, (S,), 0), ([0], d, f, (S,))]
+    builds, left = _check_plan(groups, 256, GGML_Q8_0)
+    assert builds[:3] == [[(1, 0, 0, 15)], [(2, 0, 0, 80)], [(3, 0, 0, 15)]]
+    assert left[2] == 0 and left[0] > 0 and left[1] > 0
+
+
+def test_image_chain_plan_eight_images():
+    """A call builds no more than the eight next images a call takes: of four
+    split SwiGLU weights' eight images after a group whose room would hold
+    them all, the last is left to the next call."""
+    groups = [([0, 1], 1024, 1024, (300,)), ([0], 1024, 1024, (256,)), ([0, 1, 2, 3], 2048, 1024, (256,), 512),
               ([0], 1024, 1024, (256,))]
     C = dit._ImageChain
-    assert C._entries(groups[2]) == 4
+    assert C._entries(groups[2]) == 8
     assert C._items(groups[1]) + C._items(groups[2]) <= C._room(groups[0], 256)
-    builds, _, _ = _check_plan(groups, 256)
-    assert builds[0] == [(1, 0), (2, 0), (2, 1), (2, 2)] and builds[1] == [(2, 3), (3, 0)]
+    builds, _ = _check_plan(groups, 256)
+    assert len(builds[0]) == 8 and builds[0][0] == (1, 0, 0, 4) and builds[0][-1] == (2, 6, 0, 2)
+    assert builds[1][0] == (2, 7, 0, 6)  # f = 768 outputs: six panels

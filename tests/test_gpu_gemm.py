@@ -843,25 +843,31 @@ def test_weight_image_entry_points_reject_bad_arguments(dev):
     with pytest.raises(capi.LlmrError, match="256-byte aligned"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, [img.data_ptr() + 16])
     img2 = torch.zeros(nb, dtype=torch.uint8, device=dev)
-    one = capi.NextWeightImage(w.ptr(), N, K, 0, 0, img.data_ptr(), nb)
-    nxt = capi.NextWeightImages(12, 5, (capi.NextWeightImage * 4)(one, one, one, one))
+    one = capi.NextWeightImage(w.ptr(), N, K, 0, 0, 0, img.data_ptr(), nb)
+    nxt = capi.NextWeightImages(12, 9, (capi.NextWeightImage * 8)(*([one] * 8)))
     with pytest.raises(capi.LlmrError, match="count"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
     nxt.count = 2  # images 0 and 1 in one buffer
     with pytest.raises(capi.LlmrError, match="same buffer"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
-    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, 0, img2.data_ptr(), nb - 1)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, 0, 0, img2.data_ptr(), nb - 1)
     with pytest.raises(capi.LlmrError, match="needs"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
     # a SwiGLU image of N outputs: twice the panels of the plain one
     assert ops.swiglu_weight_image_bytes(N, K) > nb
-    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, 1, img2.data_ptr(), nb)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, 1, 0, img2.data_ptr(), nb)
     with pytest.raises(capi.LlmrError, match="needs"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
-    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, 2, img2.data_ptr(), nb)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, K, 0, 2, 0, img2.data_ptr(), nb)
     with pytest.raises(capi.LlmrError, match="swiglu must be 0 or 1"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
-    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, 256 + 32, 0, 0, img2.data_ptr(), nb)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N // 2, K, 0, 0, N // 2, img2.data_ptr(), nb)
+    with pytest.raises(capi.LlmrError, match="up_offset needs swiglu"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N // 4, K, 0, 1, N // 8, img2.data_ptr(), nb)
+    with pytest.raises(capi.LlmrError, match="up_offset below out_dim"):
+        ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
+    nxt.image[1] = capi.NextWeightImage(w.ptr(), N, 256 + 32, 0, 0, 0, img2.data_ptr(), nb)
     with pytest.raises(capi.LlmrError, match="in_dim"):
         ctx.batch_matmul_multi_images(12, 30, N, K, [job], epi, None, nxt)
     nxt.count = 1
@@ -982,3 +988,45 @@ def test_multi_next_swiglu_images(dev, wtype, xtype, Ms, N, K):
     torch.cuda.synchronize()
     assert torch.equal(ys[0], ys[1]) and torch.equal(y2s[0], y2s[1])
     assert torch.isfinite(y2s[0].float()).all() and y2s[0].float().abs().max() > 0
+
+
+@pytest.mark.parametrize("wtype,xtype", [(12, 30), (8, 1)])
+def test_next_image_parts_assemble_whole_images(dev, wtype, xtype):
+    """Next images that are parts of an image (whole panels: rows [256 p0,
+    256 p1) of a plain image at row offset + 256 p0, outputs [128 p0, 128
+    p1) of a SwiGLU image at its gate rows + 128 p0 with up_offset the
+    image's output count), built by a GEMM call (as far as its idle
+    workgroups reach, the rest after it), land where the whole image has
+    those panels: byte for byte the whole images built by a call without
+    jobs. Ragged last panels on both."""
+    import torch
+    from llmr_amd import gguf, ops, synth
+    g = ops.default_graph()
+    Ms, N, K = (4608,), 3328, 512  # 234 tiles: room for 44 items
+    _, xs, wts = _multi_setup(dev, wtype, Ms, N, K, xtype, 73)
+    K2, ro = 768, 16
+    f, n = 264, 640  # SwiGLU outputs (3 panels of 128), plain rows (3 panels of 256)
+
+    def qw(seed, rows):
+        blk = gguf.quantize(synth.normal(73, seed, rows * K2, 0.02), wtype)
+        return ops.Tensor.quantized(torch.from_numpy(blk).to(dev), wtype, rows, K2)
+    wsw, wpl = qw(40, ro + 2 * f), qw(41, ro + n)
+    panel = ops.weight_image_bytes(256, K2)
+    whole = [torch.zeros(ops.swiglu_weight_image_bytes(f, K2), dtype=torch.uint8, device=dev),
+             torch.zeros(ops.weight_image_bytes(n, K2), dtype=torch.uint8, device=dev)]
+    parts = [torch.zeros_like(t) for t in whole]
+    ops.build_next_images(g, ops.NextImages([ops.NextImage(wsw, f, K2, whole[0], ro, True),
+                                             ops.NextImage(wpl, n, K2, whole[1], ro)]), xtype)
+    nxt = ops.NextImages([
+        ops.NextImage(wsw, 128, K2, parts[0][:panel], ro, True, f),
+        ops.NextImage(wpl, 256, K2, parts[1][:panel], ro),
+        ops.NextImage(wsw, f - 128, K2, parts[0][panel:], ro + 128, True, f),
+        ops.NextImage(wpl, n - 256, K2, parts[1][panel:], ro + 256)])
+    out = torch.zeros(sum(Ms), N, device=dev)
+    print(f"next image parts: w{wtype} x{xtype}", flush=True)
+    ops.dispatch_batch_matmul_multi(g, [ops.MatmulJob(wts[0], ops.Tensor.from_torch(xs[0]), out, Ms[0], 0)], N, K,
+                                    next_images=nxt)
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert torch.equal(parts[i], whole[i]), i
+    assert whole[0].any() and whole[1].any()
