@@ -136,8 +136,8 @@ hipError_t launch_w16_image(const void* w, const void* w2, uint32_t wtype, uint3
 // Work items (256-row panel x 4 stages) of a weight image (sw: the SwiGLU
 // arrangement of N outputs, 128 outputs a panel).
 uint32_t w16_image_items(uint32_t N, uint32_t K, bool sw = false);
-// Weight images of the GEMM group that follows a launch_batch_matmul_multi
-// call and the one after (up to four images, each its own shape, for the
+// Weight images of the GEMM groups that follow a launch_batch_matmul_multi
+// call (up to eight images or image parts, each its own shape, for the
 // call's 16-bit input type): built in part by the two-pass GEMM's
 // workgroups that are idle in its last round, the rest right after it, so
 // they are complete when the next call on the stream starts. Image i: the
