@@ -137,3 +137,29 @@ def test_image_chain_plan_eight_images():
     builds, _ = _check_plan(groups, 256)
     assert len(builds[0]) == 8 and builds[0][0] == (1, 0, 0, 4) and builds[0][-1] == (2, 6, 0, 2)
     assert builds[1][0] == (2, 7, 0, 6)  # f = 768 outputs: six panels
+
+
+def test_image_chain_plan_random_groups():
+    """The planner's rules (_check_plan) over 300 random group sequences:
+    one or two weights (up to four for split SwiGLU groups of one
+    projection), N and K multiples of 64 of a few hundred to several
+    thousand, plain or split SwiGLU groups (split 0 or a multiple of 256),
+    one or two jobs of 1-5000 tokens, 80-304 CUs, Q4_K and Q8_0 rooms."""
+    import random
+    from llmr_amd.gguf import GGML_Q4_K, GGML_Q8_0
+    rnd = random.Random(20261202)
+    C = dit._ImageChain
+    for _ in range(300):
+        groups = []
+        for _ in range(rnd.randint(2, 14)):
+            K = 64 * rnd.randint(1, 120)
+            Ms = tuple(rnd.randint(1, 5000) for _ in range(rnd.randint(1, 2)))
+            if rnd.random() < 0.3:  # split SwiGLU: split rows plain, then 2 f SwiGLU rows
+                split = 256 * rnd.randint(0, 12)
+                f = 8 * rnd.randint(1, 600)
+                nw = rnd.randint(1, 4 if split == 0 else 2)
+                groups.append(([0] * nw, split + 2 * f, K, Ms, split))
+            else:
+                groups.append(([0] * rnd.randint(1, 2), 64 * rnd.randint(1, 300), K, Ms))
+        assert all(C._entries(gr) <= C.MAX_PARTS for gr in groups)
+        _check_plan(groups, rnd.choice((80, 104, 256, 304)), rnd.choice((GGML_Q4_K, GGML_Q8_0)))
