@@ -1030,3 +1030,51 @@ def test_next_image_parts_assemble_whole_images(dev, wtype, xtype):
     for i in range(2):
         assert torch.equal(parts[i], whole[i]), i
     assert whole[0].any() and whole[1].any()
+
+
+def test_next_image_parts_random(dev):
+    """Eight seeded random cases of image parts as next images of one GEMM
+    call: a plain and a SwiGLU image of random ragged sizes, row offsets and
+    K, each cut at a random panel into two parts listed in random order,
+    equal the whole images byte for byte (both weight types)."""
+    import random
+    import torch
+    from llmr_amd import gguf, ops, synth
+    rnd = random.Random(1202)
+    g = ops.default_graph()
+    Ms, N, K = (4608,), 3328, 512
+    for case in range(8):
+        wtype = rnd.choice((8, 12))
+        xtype = rnd.choice((1, 30))
+        _, xs, wts = _multi_setup(dev, wtype, Ms, N, K, xtype, 90 + case)
+        K2 = 256 * rnd.randint(1, 4)
+        f, n = 8 * rnd.randint(17, 80), 8 * rnd.randint(33, 160)  # > one panel each
+        ro_s, ro_p = 8 * rnd.randint(0, 4), 8 * rnd.randint(0, 4)
+
+        def qw(seed, rows):
+            blk = gguf.quantize(synth.normal(90 + case, seed, rows * K2, 0.02), wtype)
+            return ops.Tensor.quantized(torch.from_numpy(blk).to(dev), wtype, rows, K2)
+        wsw, wpl = qw(40, ro_s + 2 * f + 8), qw(41, ro_p + n + 8)
+        panel = ops.weight_image_bytes(256, K2)
+        whole = [torch.zeros(ops.swiglu_weight_image_bytes(f, K2), dtype=torch.uint8, device=dev),
+                 torch.zeros(ops.weight_image_bytes(n, K2), dtype=torch.uint8, device=dev)]
+        parts = [torch.zeros_like(t) for t in whole]
+        ops.build_next_images(g, ops.NextImages([ops.NextImage(wsw, f, K2, whole[0], ro_s, True),
+                                                 ops.NextImage(wpl, n, K2, whole[1], ro_p)]), xtype)
+        ps = rnd.randint(1, -(-f // 128) - 1)  # the SwiGLU image's cut (panels of 128 outputs)
+        pp = rnd.randint(1, -(-n // 256) - 1) if n > 256 else 1
+        es = [ops.NextImage(wsw, 128 * ps, K2, parts[0][:ps * panel], ro_s, True, f),
+              ops.NextImage(wsw, f - 128 * ps, K2, parts[0][ps * panel:], ro_s + 128 * ps, True, f)]
+        if 256 * pp < n:
+            es += [ops.NextImage(wpl, 256 * pp, K2, parts[1][:pp * panel], ro_p),
+                   ops.NextImage(wpl, n - 256 * pp, K2, parts[1][pp * panel:], ro_p + 256 * pp)]
+        else:
+            es.append(ops.NextImage(wpl, n, K2, parts[1], ro_p))
+        rnd.shuffle(es)
+        out = torch.zeros(sum(Ms), N, device=dev)
+        print(f"parts case {case}: w{wtype} x{xtype} K2 {K2} f {f} cut {ps} n {n} cut {pp}", flush=True)
+        ops.dispatch_batch_matmul_multi(g, [ops.MatmulJob(wts[0], ops.Tensor.from_torch(xs[0]), out, Ms[0], 0)], N,
+                                        K, next_images=ops.NextImages(es))
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(parts[i], whole[i]), (case, i)
