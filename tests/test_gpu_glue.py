@@ -291,3 +291,53 @@ def test_synth_q4k_distribution(orc, dev):
     w = orc.dequant_q4k(blk.cpu().numpy())
     assert np.isfinite(w).all()
     assert abs(w.mean()) < 1e-4 and abs(w.std() / 0.02 - 1) < 0.02
+
+
+def test_glue_fusions_random(dev):
+    """Twelve seeded random cases each of the split LayerNorm (split_row a
+    multiple of 4 up to n_rows, width up to 8192) and the fused residual +
+    RMSNorm (width up to 4096, every gate mode, with and without the
+    post-norm, scale and shift present or not), against their two-call
+    forms bit for bit, over ragged row counts and output types."""
+    import random
+    from llmr_amd import glue
+    rnd = random.Random(1203)
+    r = _rng(40)
+    dts = (torch.float32, torch.float16, torch.bfloat16)
+    for case in range(12):
+        dim, rows = 4 * rnd.randint(1, 2048), rnd.randint(1, 700)
+        split = 4 * rnd.randint(0, rows // 4)
+        dt = rnd.choice(dts)
+        h = _dev((r.standard_normal((rows, dim)) * 2 + 0.5).astype(np.float32), dev)
+        vecs = [_dev((0.3 * r.standard_normal(dim)).astype(np.float32), dev) if rnd.random() < 0.7 else None
+                for _ in range(4)]
+        a = torch.full((rows, dim), 7.0, dtype=dt, device=dev)
+        b = torch.full((rows, dim), 7.0, dtype=dt, device=dev)
+        print(f"split layernorm case {case}: rows {rows} dim {dim} split {split} {dt}", flush=True)
+        glue.batch_layernorm_split(h, a, 1e-6, split, (vecs[0], vecs[1]), (vecs[2], vecs[3]))
+        if split:
+            glue.batch_layernorm(h[:split], b[:split], 1e-6, mod_scale=vecs[0], mod_shift=vecs[1])
+        if split < rows:
+            glue.batch_layernorm(h[split:], b[split:], 1e-6, mod_scale=vecs[2], mod_shift=vecs[3])
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), case
+    for case in range(12):
+        dim, rows = 4 * rnd.randint(1, 1024), rnd.randint(1, 700)
+        mode, norm = rnd.randint(0, 2), rnd.random() < 0.5
+        dt = rnd.choice(dts)
+        h = r.standard_normal((rows, dim)).astype(np.float32)
+        x = _dev((2 * r.standard_normal((rows, dim))).astype(np.float32), dev)
+        gate = _dev(r.standard_normal(dim).astype(np.float32), dev) if mode else None
+        nw, fw = (_dev((1 + 0.1 * r.standard_normal(dim)).astype(np.float32), dev) for _ in range(2))
+        sc = _dev((0.3 * r.standard_normal(dim)).astype(np.float32), dev) if rnd.random() < 0.7 else None
+        sh = _dev((0.3 * r.standard_normal(dim)).astype(np.float32), dev) if rnd.random() < 0.5 else None
+        ha, hb = _dev(h, dev), _dev(h, dev)
+        oa = torch.full((rows, dim), 7.0, dtype=dt, device=dev)
+        ob = torch.full((rows, dim), 7.0, dtype=dt, device=dev)
+        print(f"residual rmsnorm case {case}: rows {rows} dim {dim} mode {mode} norm {norm} {dt}", flush=True)
+        glue.gated_residual_rmsnorm(ha, x, gate, mode, nw if norm else None, 1e-5, fw, oa, 1e-6, mod_scale=sc,
+                                    mod_shift=sh)
+        glue.gated_residual(hb, x, gate, mode, nw if norm else None, 1e-5)
+        glue.batch_rmsnorm(hb, fw, ob, 1e-6, mod_scale=sc, mod_shift=sh)
+        torch.cuda.synchronize()
+        assert torch.equal(ha, hb) and torch.equal(oa, ob), case
